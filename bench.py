@@ -1,0 +1,210 @@
+"""Benchmark of the random-walk hot path on one MI355X.
+
+Default workload: uniform random walk on an R-MAT
+graph with 2^20 nodes and 2^24 edge samples (a,b,c,d = .57,.19,.19,.05,
+deduplicated, int64 CSR), 10 walks per node (10,485,760 walks), walk_length
+80, rand = Philox float32 uniforms [N, 80] (seed 2).  One step = one
+random_walk() call over the whole batch, inputs resident in HBM.
+
+Prints ONE JSON line with walk-steps/s, the roofline of the walk kernel (HBM
+random gather: one 64-B line per dependent read, streams at their byte
+count) and a CPU baseline (the oracle's single-threaded restatement of the
+reference's eval_cpu loop, timed on a bounded sample of the same walks).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5]
+"""
+from __future__ import annotations
+
+import argparse
+import hashlib
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+METRIC = "walk steps/sec at 1 MI355X + achieved GB/s vs random-gather roofline"
+PEAK_HBM_GBS = 8000.0
+LINE = 64  # bytes charged per dependent random read
+
+CONFIGS = {
+    # name: (description, kind, graph builder args, walks per node, L, extra)
+    "c2": ("R-MAT 2^20 uniform walk, 10 walks/node, L=80", "uniform",
+           dict(scale=20, samples=1 << 24, symmetrize=False), 10, 80, {}),
+    "c3": ("node2vec p=0.5 q=2 on symmetrized R-MAT 2^20, 4 walks/node, L=40", "node2vec",
+           dict(scale=20, samples=1 << 24, symmetrize=True), 4, 40, dict(p=0.5, q=2.0, seed=3)),
+    "c4": ("R-MAT 2^24 uniform walk, 1 walk/node, L=20", "uniform",
+           dict(scale=24, samples=1 << 28, symmetrize=False), 1, 20, {}),
+}
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def kernel_source_hash() -> str:
+    path = os.path.join(REPO, "mlx_cluster_amd", "csrc", "mlxc_walk.hip")
+    return hashlib.sha256(open(path, "rb").read()).hexdigest()[:16]
+
+
+def traffic_from_profile(name: str):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary of the
+    same kernel source (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-
+    kernel calibration), or None when no summary for this source exists."""
+    path = os.path.join(REPO, "profiles", f"{name}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    d = json.load(open(path))
+    if d.get("kernel_source_sha256_16") != kernel_source_hash():
+        return None
+    return d.get("hbm_bytes_per_launch")
+
+
+def uniform_counts(torch, rowptr, walks):
+    """Moving steps M (from a node with deg > 0) and sink walks Z (walks that
+    meet a deg-0 node before their last step) of a finished uniform walk."""
+    L = walks.shape[1] - 1
+    M = 0
+    sunk = torch.zeros(walks.shape[0], dtype=torch.bool, device=walks.device)
+    for l in range(L):
+        u = walks[:, l]
+        deg = rowptr[u + 1] - rowptr[u]
+        M += int((deg > 0).sum())
+        sunk |= deg == 0
+    return M, int(sunk.sum())
+
+
+def cpu_baseline_uniform(np, oracle, rowptr_h, col_h, start, rand, L, target_s=12.0):
+    """Single-threaded oracle walk on an evenly strided sample of walks."""
+    N = start.shape[0]
+    probe = min(N, 20_000)
+    idx = np.linspace(0, N - 1, probe).astype(np.int64)
+    t0 = time.perf_counter()
+    oracle.uniform_walk(rowptr_h, col_h, start[idx], rand[idx], L)
+    rate = probe * L / (time.perf_counter() - t0)
+    walks = int(min(N, max(probe, target_s * rate / L)))
+    idx = np.linspace(0, N - 1, walks).astype(np.int64)
+    s, r = start[idx], rand[idx]
+    t0 = time.perf_counter()
+    _, _, st, _ = oracle.uniform_walk(rowptr_h, col_h, s, r, L)
+    dt = time.perf_counter() - t0
+    assert st == 0
+    return walks * L / dt, walks, dt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the walks need no cross-GPU exchange and this build "
+              "runs on a single MI355X (see DESIGN.md for how the path shards). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import mlx_cluster_amd as mc
+    from mlx_cluster_amd import synth
+
+    desc, kind, gargs, per_node, L, extra = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"config {args.config}: {desc} on {torch.cuda.get_device_name(dev)}")
+    rowptr, col = synth.rmat_csr(gargs["scale"], gargs["samples"], seed=0, device=dev,
+                                 symmetrize=gargs["symmetrize"])
+    V = rowptr.numel() - 1
+    E = col.numel()
+    N = per_node * V
+    start = torch.arange(N, device=dev, dtype=torch.int64) % V
+    torch.cuda.synchronize()
+    log(f"graph V={V} E={E}; walks N={N} L={L}")
+
+    if kind == "uniform":
+        rand = mc.philox_uniform((N, L), 2, device=dev)
+        step = lambda: mc.random_walk(rowptr, col, start, rand, L)
+    else:
+        rand = None
+        step = lambda: mc.rejection_sampling(rowptr, col, start, L, extra["p"], extra["q"],
+                                             seed=extra["seed"], rows_sorted=True)
+
+    for _ in range(args.warmup):
+        out = step()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)  # the walk kernels launch on this stream
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for ev0, ev1 in events:
+        ev0.record(stream)
+        out = step()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
+    ms_per_step = wall / args.steps * 1e3
+    steps_per_launch = N * L
+    value = steps_per_launch / (ms_per_step / 1e3)
+    log(f"{ms_per_step:.3f} ms/step wall, {kernel_ms:.3f} ms/launch (events)")
+
+    # Roofline bytes of one launch (64-B line per dependent random read).
+    if kind == "uniform":
+        M, Z = uniform_counts(torch, rowptr, out)
+        roof_bytes = LINE * (M + Z) + LINE * M + 4 * M + 8 * N * (L + 1) + 8 * N
+        units = dict(moving_steps=M, sink_walks=Z)
+    else:
+        roof_bytes = None
+        units = {}
+    achieved = roof_bytes / (kernel_ms / 1e3) / 1e9 if roof_bytes else None
+    traffic = traffic_from_profile(f"{kind}_walk_{args.config}")
+    roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": (achieved / PEAK_HBM_GBS) if achieved else None, "traffic": traffic,
+                "algorithmic_bytes_per_launch": roof_bytes, "kernel_ms": kernel_ms, **units}
+
+    # Sampled bit-exact parity against the oracle, and the CPU baseline.
+    import oracle
+    rowptr_h, col_h = rowptr.cpu().numpy(), col.cpu().numpy()
+    g = torch.Generator().manual_seed(1)
+    sample = torch.randint(0, N, (2000,), generator=g).to(dev)
+    if kind == "uniform":
+        ref, _, st, _ = oracle.uniform_walk(rowptr_h, col_h, start[sample].cpu().numpy(),
+                                            rand[sample].cpu().numpy(), L)
+    else:
+        ref = None
+    parity = None if ref is None else bool(np.array_equal(out[sample].cpu().numpy(), ref))
+    cpu = None
+    if not args.no_cpu_baseline and kind == "uniform":
+        rate, walks, dt = cpu_baseline_uniform(np, oracle, rowptr_h, col_h, start.cpu().numpy(),
+                                               rand.cpu().numpy(), L, args.cpu_seconds)
+        cpu = {"value": rate, "unit": "walk-steps/s", "cores": 1, "kind": "port",
+               "sample": f"{walks} of {N} walks (evenly strided) x {L} steps, {dt:.1f} s, "
+                         f"oracle/walk_oracle.c uniform walk, 1 thread"}
+        log(f"cpu baseline {rate:.3e} steps/s over {walks} walks")
+
+    line = {
+        "metric": METRIC, "value": value, "unit": "walk-steps/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int64",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}: {desc}", "num_nodes": V, "num_edges": E,
+                   "num_walks": N, "walk_length": L, "walk_steps_per_launch": steps_per_launch,
+                   "parity_sample_bit_exact": parity},
+        "roofline": roofline, "cpu_baseline": cpu,
+    }
+    if cpu:
+        line["speedup_vs_cpu_baseline"] = value / cpu["value"]
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,135 @@
+/*
+ * mlxc — C ABI of the MI355X random-walk library (libmlxc.so).
+ *
+ * The drop-in boundary for the random-walk hot path of vinayhpandya/mlx_cluster.
+ * Plain pointers and sizes only.  Every pointer argument named d_* is a
+ * device pointer (HIP/torch allocation on the current device); `stream` is a
+ * hipStream_t (NULL = the legacy default stream).  All walk entry points are
+ * asynchronous on `stream`: they enqueue work and return.
+ *
+ * Return codes: 0 on success, a negative MLXC_ERR_* code otherwise; the
+ * message of the calling thread's last failure is in mlxc_last_error().
+ *
+ * Ownership: the caller allocates every buffer (inputs, outputs and the small
+ * status/work buffers).  The library never allocates or frees device memory.
+ */
+#ifndef MLXC_H
+#define MLXC_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLXC_OK 0
+#define MLXC_ERR_INVALID_ARGUMENT (-1)
+#define MLXC_ERR_HIP (-2)
+
+/* Size in int64 words of the device workspace `d_work` that every walk entry
+ * point takes.  The call zeroes it on `stream` before its kernel runs; after
+ * the call has completed, word 0 holds the MLXC_STATUS_* bits of that call
+ * (the other words are internal: the walk-queue counter). */
+#define MLXC_WORK_WORDS 4
+
+/* Bits a walk kernel ORs into d_work[0] when the graph or the starts are
+ * malformed (the reference reads out of bounds in these cases; these kernels
+ * never do — the affected walk stops and its remaining entries repeat its
+ * last node). */
+#define MLXC_STATUS_BAD_NODE 1 /* a start or col value outside [0, num_nodes) */
+#define MLXC_STATUS_BAD_ROW 2  /* rowptr[v] / rowptr[v+1] outside [0, num_edges] or decreasing */
+
+/* Acceptance rules of mlxc_rejection_sampling. */
+#define MLXC_RULE_REF_CHAIN 0      /* BiasedRandomWalk.cpp:86-91, reproduced term for term */
+#define MLXC_RULE_NODE2VEC_EXACT 1 /* analytic node2vec: accept iff r < prob_d(t, x)      */
+
+/* Bits written by mlxc_csr_check. */
+#define MLXC_CSR_BAD_ROWPTR 1   /* rowptr[0] != 0, rowptr[V] != E, or decreasing */
+#define MLXC_CSR_BAD_COL 2      /* a col value outside [0, V) */
+#define MLXC_CSR_UNSORTED 4     /* some row is not sorted ascending */
+
+/* Trial cap of one biased step (the reference loops without bound,
+ * BiasedRandomWalk.cpp:80): after this many rejections the last candidate is
+ * kept. */
+#define MLXC_MAX_TRIALS 65536
+
+/* Library version, major*10000 + minor*100 + patch. */
+int mlxc_version(void);
+
+/* Message of the calling thread's most recent failed call ("" if none). */
+const char* mlxc_last_error(void);
+
+/*
+ * Uniform random walk.
+ * Replaces: RandomWalk::eval_cpu / eval_gpu and the op random_walk(rowptr,
+ *   col, start, rand, walk_length) —
+ *   /root/reference/random_walks/RandomWalk.cpp:18-62 (CPU), :73-108 (GPU
+ *   dispatch), :138-148 (op); /root/reference/random_walks/RandomWalk.h:56-61;
+ *   binding /root/reference/bindings.cpp:12-33.
+ *
+ * d_rowptr  int64 [num_nodes + 1]     d_col  int64 [num_edges]
+ * d_start   int64 [num_walks]         d_rand float32 [num_walks * walk_length]
+ * d_n_out   int64 [num_walks * (walk_length + 1)]  (row-major [N, L+1])
+ * d_e_out   int64 [num_walks * walk_length] or NULL (edge ids, -1 = stayed)
+ * d_work    int64 [MLXC_WORK_WORDS] device workspace (see above).
+ *
+ * Step l of walk n at node v: deg = rowptr[v+1] - rowptr[v]; deg == 0 keeps
+ * v; otherwise e = rowptr[v] + (int64)(rand[n*L + l] * (float)deg) in IEEE
+ * float32 (truncated; clamped to [0, deg-1]) and v = col[e].
+ */
+int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes,
+                     const int64_t* d_col, int64_t num_edges,
+                     const int64_t* d_start, int64_t num_walks,
+                     const float* d_rand, int32_t walk_length,
+                     int64_t* d_n_out, int64_t* d_e_out, int64_t* d_work,
+                     void* stream);
+
+/*
+ * node2vec walk by rejection sampling.
+ * Replaces: BiasedRandomWalk::eval_cpu and the op rejection_sampling(rowptr,
+ *   col, start, walk_length, p, q) —
+ *   /root/reference/random_walks/BiasedRandomWalk.cpp:30-102 (CPU; its GPU
+ *   path :150-155 only throws), :183-193 (op);
+ *   /root/reference/random_walks/BiasedRandomWalk.h:58-64;
+ *   binding /root/reference/bindings.cpp:35-63.
+ *
+ * The reference draws from libc rand(); this entry point draws from the
+ * counter-based stream Philox4x32-10(key = seed; counter = (walk lo, walk hi,
+ * step, trial)): word 0 picks the candidate as in mlxc_random_walk, word 1
+ * gives r = (x1 >> 8) * 2^-24 for the acceptance test against the FP64
+ * constants of BiasedRandomWalk.cpp:52-55.  rows_sorted != 0 promises that
+ * every row of col is sorted ascending (binary-search neighbour test);
+ * rows_sorted == 0 scans rows linearly, as the reference does.
+ */
+int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes,
+                            const int64_t* d_col, int64_t num_edges,
+                            const int64_t* d_start, int64_t num_walks,
+                            int32_t walk_length, double p, double q,
+                            uint64_t seed, int32_t rule, int32_t rows_sorted,
+                            int64_t* d_n_out, int64_t* d_e_out, int64_t* d_work,
+                            void* stream);
+
+/*
+ * Validates a CSR graph on the device and reports MLXC_CSR_* bits in
+ * *h_flags (host pointer).  Synchronises `stream`.  d_work: int64
+ * [MLXC_WORK_WORDS] device workspace supplied by the caller.
+ * No reference counterpart: the reference validates nothing (its
+ * is_neighbor, BiasedRandomWalk.cpp:20-28, works on unsorted rows); this
+ * picks the neighbour-test strategy for mlxc_rejection_sampling.
+ */
+int mlxc_csr_check(const int64_t* d_rowptr, int64_t num_nodes,
+                   const int64_t* d_col, int64_t num_edges,
+                   int64_t* d_work, int32_t* h_flags, void* stream);
+
+/*
+ * Uniform float32 fill from Philox4x32-10: out[i] = (w >> 8) * 2^-24 with w
+ * word (i % 4) of Philox(key = seed; counter = (i/4 lo, i/4 hi, 0, 0)).
+ * Stands in for mx.random.uniform, which makes the reference tests' rand
+ * tensor (/root/reference/tests/test_random_walk.py:31).
+ */
+int mlxc_philox_uniform(float* d_out, int64_t n, uint64_t seed, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,84 @@
+"""ctypes binding of libmlxc.so, the HIP library declared in include/mlxc.h.
+
+The library is loaded after torch, so it shares torch's HIP runtime (both
+resolve the soname libamdhip64.so.7 to the copy torch has already loaded).
+There is no fallback: if the library is missing the import fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must be loaded first: provides the HIP runtime)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmlxc.so")
+
+MLXC_OK = 0
+MLXC_ERR_INVALID_ARGUMENT = -1
+MLXC_ERR_HIP = -2
+MLXC_WORK_WORDS = 4
+MLXC_STATUS_BAD_NODE = 1
+MLXC_STATUS_BAD_ROW = 2
+MLXC_RULE_REF_CHAIN = 0
+MLXC_RULE_NODE2VEC_EXACT = 1
+MLXC_CSR_BAD_ROWPTR = 1
+MLXC_CSR_BAD_COL = 2
+MLXC_CSR_UNSORTED = 4
+MLXC_MAX_TRIALS = 65536
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_u64 = ctypes.c_uint64
+_dbl = ctypes.c_double
+_ptr = ctypes.c_void_p
+
+# name -> (restype, argtypes); every function include/mlxc.h declares.
+SIGNATURES = {
+    "mlxc_version": (ctypes.c_int, []),
+    "mlxc_last_error": (ctypes.c_char_p, []),
+    "mlxc_random_walk": (
+        ctypes.c_int,
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _ptr, _ptr],
+    ),
+    "mlxc_rejection_sampling": (
+        ctypes.c_int,
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _dbl, _dbl, _u64, _i32, _i32,
+         _ptr, _ptr, _ptr, _ptr],
+    ),
+    "mlxc_csr_check": (ctypes.c_int, [_ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr]),
+    "mlxc_philox_uniform": (ctypes.c_int, [_ptr, _i64, _u64, _ptr]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Returns the loaded library, loading it on first use."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built; run `python -m mlx_cluster_amd.build_lib` "
+            "(this package has no CPU fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    msg = load().mlxc_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    if rc == MLXC_OK:
+        return
+    msg = last_error()
+    if rc == MLXC_ERR_INVALID_ARGUMENT:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")

@@ -1,0 +1,49 @@
+"""Builds libmlxc.so (HIP kernels + C ABI) in-tree for gfx950.
+
+Usage: python -m mlx_cluster_amd.build_lib   (or build() from __graft_entry__)
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+SRC = os.path.join(PKG_DIR, "csrc", "mlxc_walk.hip")
+OUT = os.path.join(PKG_DIR, "libmlxc.so")
+INCLUDE = os.path.join(REPO_DIR, "include")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = os.environ.get("MLXC_OFFLOAD_ARCH", "gfx950")
+
+# -ffp-contract=off: the walk's index is an IEEE float32 product that must
+# round exactly as the reference's scalar code; no fused or reassociated math.
+# -packed-fp32-ops off: keep the compiler from emitting packed FP32 forms.
+FLAGS = [
+    "-O3",
+    "-std=c++17",
+    f"--offload-arch={ARCH}",
+    "-fPIC",
+    "-shared",
+    "-ffp-contract=off",
+    "-fno-fast-math",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None, out: str = OUT) -> str:
+    cmd = [HIPCC, *FLAGS, *(extra_flags or []), "-I", INCLUDE, SRC, "-o", out + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"hipcc failed building {out}")
+    os.replace(out + ".tmp", out)
+    return out
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

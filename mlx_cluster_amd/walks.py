@@ -1,0 +1,275 @@
+"""Python surface of the random-walk path, mirroring mlx_cluster's.
+
+Reference interface (vinayhpandya/mlx_cluster):
+  random_walk(rowptr, col, start, rand, walk_length, *, stream=None)
+      /root/reference/bindings.cpp:12-33, op at
+      /root/reference/random_walks/RandomWalk.cpp:138-148
+  rejection_sampling(rowptr, col, start, walk_length, p, q, *, stream=None)
+      /root/reference/bindings.cpp:35-63, op at
+      /root/reference/random_walks/BiasedRandomWalk.cpp:183-193
+
+Same names, positional order and keyword-only `stream`.  Arrays are torch
+tensors on a ROCm device (numpy arrays and CPU tensors are copied to the
+current device).  Both functions return the node sequences, an int64 tensor
+[num_walks, walk_length + 1], as the reference ops do (they discard the edge
+output, RandomWalk.cpp:147); `return_edges=True` also returns the edge ids.
+
+Every walk runs in the HIP library libmlxc.so; there is no CPU path.
+"""
+from __future__ import annotations
+
+import numbers
+from typing import Optional, Tuple, Union
+
+import numpy as np
+import torch
+
+from . import _lib
+
+TensorLike = Union[torch.Tensor, np.ndarray]
+
+_RULES = {"ref_chain": _lib.MLXC_RULE_REF_CHAIN, "node2vec": _lib.MLXC_RULE_NODE2VEC_EXACT}
+
+
+# ---------------------------------------------------------------- helpers
+
+def _resolve_device(stream, tensors) -> torch.device:
+    if isinstance(stream, torch.cuda.Stream):
+        return stream.device
+    for t in tensors:
+        if isinstance(t, torch.Tensor) and t.is_cuda:
+            return t.device
+    if not torch.cuda.is_available():
+        raise RuntimeError("mlx_cluster_amd needs a ROCm GPU; none is visible")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _stream_handle(stream, device: torch.device) -> int:
+    """hipStream_t for `stream`: None -> torch's current stream on device."""
+    _check_stream_arg(stream)
+    if stream is None:
+        return torch.cuda.current_stream(device).cuda_stream
+    if isinstance(stream, torch.cuda.Stream):
+        return stream.cuda_stream
+    return torch.cuda.current_stream(torch.device(stream)).cuda_stream
+
+
+def _as_tensor(x: TensorLike, dtype: torch.dtype, name: str) -> torch.Tensor:
+    """Type checks (no device work): numpy arrays are wrapped, dtypes must match."""
+    if isinstance(x, np.ndarray):
+        x = torch.from_numpy(x)
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor or numpy.ndarray, got {type(x)!r}")
+    if x.dtype != dtype:
+        raise TypeError(f"{name} must have dtype {dtype}, got {x.dtype}")
+    return x
+
+
+def _on(x: torch.Tensor, device: torch.device) -> torch.Tensor:
+    if x.device != device:
+        x = x.to(device)
+    return x.contiguous()
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _graph(rowptr, col, start):
+    rowptr = _as_tensor(rowptr, torch.int64, "rowptr")
+    col = _as_tensor(col, torch.int64, "col")
+    start = _as_tensor(start, torch.int64, "start")
+    if rowptr.dim() != 1 or rowptr.numel() < 1:
+        raise ValueError("rowptr must be 1-D with num_nodes + 1 >= 1 entries")
+    if col.dim() != 1:
+        raise ValueError("col must be 1-D")
+    return rowptr, col, start.reshape(-1)
+
+
+def _check_stream_arg(stream) -> None:
+    if isinstance(stream, (str, torch.device)) and torch.device(stream).type == "cpu":
+        raise ValueError(
+            "stream='cpu': this build evaluates walks on the GPU only "
+            "(the reference's CPU evaluation is not part of it)")
+    if stream is not None and not isinstance(stream, (str, torch.device, torch.cuda.Stream)):
+        raise TypeError(f"stream must be None, a torch.cuda.Stream or a device, got {type(stream)!r}")
+
+
+def _walk_length(walk_length) -> int:
+    if isinstance(walk_length, bool) or not isinstance(walk_length, numbers.Integral):
+        raise TypeError("walk_length must be an int")
+    walk_length = int(walk_length)
+    if walk_length < 0:
+        raise ValueError("walk_length must be >= 0")
+    if walk_length > 2**31 - 2:
+        raise ValueError("walk_length too large")
+    return walk_length
+
+
+def _raise_status(work: torch.Tensor, stream, what: str) -> None:
+    if isinstance(stream, torch.cuda.Stream):
+        stream.synchronize()  # the kernel ran there, not on torch's current stream
+    bits = int(work[0].item())
+    if bits == 0:
+        return
+    reasons = []
+    if bits & _lib.MLXC_STATUS_BAD_NODE:
+        reasons.append("a start or col entry is outside [0, num_nodes)")
+    if bits & _lib.MLXC_STATUS_BAD_ROW:
+        reasons.append("rowptr is malformed (an entry outside [0, num_edges] or decreasing)")
+    raise ValueError(f"{what}: " + "; ".join(reasons))
+
+
+# ------------------------------------------------------------------- API
+
+def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike, rand: TensorLike,
+                walk_length: int, *, stream=None, return_edges: bool = False,
+                check: bool = True
+                ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """Uniform random walks over a CSR graph.
+
+    Mirrors mlx_cluster.random_walk (/root/reference/bindings.cpp:12-33;
+    semantics /root/reference/random_walks/RandomWalk.cpp:41-60).
+
+    Args:
+        rowptr: int64 [num_nodes + 1] CSR row pointer.
+        col: int64 [num_edges] CSR column indices.
+        start: int64 [num_walks] start nodes (any shape; flattened).
+        rand: float32 with num_walks * walk_length uniforms in [0, 1); walk n
+            reads rand.view(-1)[n * walk_length + l] at step l.
+        walk_length: steps per walk (>= 0).
+        stream: None (torch's current stream), a torch.cuda.Stream or a
+            device.  'cpu' raises: this build has no CPU evaluation.
+        return_edges: also return the edge ids [num_walks, walk_length]
+            (-1 where the walk stayed in a node of out-degree 0), the
+            reference's discarded second output (RandomWalk.cpp:58).
+        check: synchronise and raise ValueError if a start/col index or a
+            rowptr entry was out of range (the reference reads out of bounds
+            there).  With check=False the call stays asynchronous.
+
+    Returns:
+        int64 [num_walks, walk_length + 1] node sequences (and edge ids).
+    """
+    L = _walk_length(walk_length)
+    _check_stream_arg(stream)
+    rowptr, col, start = _graph(rowptr, col, start)
+    rand = _as_tensor(rand, torch.float32, "rand")
+    N = start.numel()
+    if rand.numel() != N * L:
+        raise ValueError(f"rand must hold num_walks * walk_length = {N * L} values, got {rand.numel()}")
+    device = _resolve_device(stream, (rowptr, col, start, rand))
+    handle = _stream_handle(stream, device)
+    rowptr, col, start, rand = (_on(t, device) for t in (rowptr, col, start, rand))
+    n_out = torch.empty((N, L + 1), dtype=torch.int64, device=device)
+    e_out = torch.empty((N, L), dtype=torch.int64, device=device) if return_edges else None
+    work = torch.empty(_lib.MLXC_WORK_WORDS, dtype=torch.int64, device=device)
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        rc = lib.mlxc_random_walk(_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(),
+                                  _ptr(start), N, _ptr(rand), L, _ptr(n_out),
+                                  _ptr(e_out) if return_edges else None, work.data_ptr(), handle)
+    _lib.check(rc, "random_walk")
+    if check:
+        _raise_status(work, stream, "random_walk")
+    return (n_out, e_out) if return_edges else n_out
+
+
+def csr_check(rowptr: TensorLike, col: TensorLike, *, stream=None) -> int:
+    """MLXC_CSR_* bits of a CSR graph, computed on the device (synchronous)."""
+    _check_stream_arg(stream)
+    rowptr, col, _ = _graph(rowptr, col, torch.empty(0, dtype=torch.int64))
+    device = _resolve_device(stream, (rowptr, col))
+    handle = _stream_handle(stream, device)
+    rowptr, col = _on(rowptr, device), _on(col, device)
+    work = torch.empty(_lib.MLXC_WORK_WORDS, dtype=torch.int64, device=device)
+    flags = _lib.ctypes.c_int32(0)
+    with torch.cuda.device(device):
+        rc = _lib.load().mlxc_csr_check(_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(),
+                                        work.data_ptr(), _lib.ctypes.addressof(flags), handle)
+    _lib.check(rc, "csr_check")
+    return int(flags.value)
+
+
+def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
+                       walk_length: int, p: float, q: float, *, stream=None,
+                       seed: Optional[int] = None, rule: str = "ref_chain",
+                       rows_sorted: Optional[bool] = None, return_edges: bool = False,
+                       check: bool = True
+                       ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """node2vec random walks by rejection sampling.
+
+    Mirrors mlx_cluster.rejection_sampling (/root/reference/bindings.cpp:35-63;
+    semantics /root/reference/random_walks/BiasedRandomWalk.cpp:52-100),
+    which has no GPU implementation in the reference (:150-155).
+
+    Args:
+        rowptr, col, start, walk_length: as in random_walk.
+        p: return parameter (likelihood of revisiting the previous node).
+        q: in-out parameter (breadth- versus depth-first).
+        stream: as in random_walk.
+        seed: key of the Philox4x32-10 stream the walk draws from (the
+            reference uses libc rand()).  None draws one from torch's default
+            CPU generator, so torch.manual_seed makes runs repeatable.
+        rule: 'ref_chain' reproduces the reference's acceptance chain
+            (BiasedRandomWalk.cpp:86-91) term for term; 'node2vec' is the
+            analytic node2vec rule (accept with probability 1/p, 1 or 1/q,
+            normalised).  They agree whenever q >= max(p, 1).
+        rows_sorted: whether every CSR row is sorted ascending (binary-search
+            neighbour test).  None checks the graph on the device first, which
+            also rejects malformed graphs with ValueError.
+        return_edges, check: as in random_walk.
+    """
+    L = _walk_length(walk_length)
+    p, q = float(p), float(q)
+    if not (np.isfinite(p) and np.isfinite(q) and p > 0 and q > 0):
+        raise ValueError("p and q must be finite and > 0")
+    if rule not in _RULES:
+        raise ValueError(f"rule must be one of {sorted(_RULES)}")
+    _check_stream_arg(stream)
+    rowptr, col, start = _graph(rowptr, col, start)
+    device = _resolve_device(stream, (rowptr, col, start))
+    handle = _stream_handle(stream, device)
+    rowptr, col, start = (_on(t, device) for t in (rowptr, col, start))
+    if seed is None:
+        seed = int(torch.randint(0, 2**62, (1,)).item())
+    seed = int(seed) & (2**64 - 1)
+    if rows_sorted is None:
+        flags = csr_check(rowptr, col, stream=stream)
+        if flags & _lib.MLXC_CSR_BAD_ROWPTR:
+            raise ValueError("rejection_sampling: rowptr is malformed")
+        if flags & _lib.MLXC_CSR_BAD_COL:
+            raise ValueError("rejection_sampling: a col entry is outside [0, num_nodes)")
+        rows_sorted = not (flags & _lib.MLXC_CSR_UNSORTED)
+    N = start.numel()
+    n_out = torch.empty((N, L + 1), dtype=torch.int64, device=device)
+    e_out = torch.empty((N, L), dtype=torch.int64, device=device) if return_edges else None
+    work = torch.empty(_lib.MLXC_WORK_WORDS, dtype=torch.int64, device=device)
+    with torch.cuda.device(device):
+        rc = _lib.load().mlxc_rejection_sampling(
+            _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,
+            p, q, seed, _RULES[rule], 1 if rows_sorted else 0, _ptr(n_out),
+            _ptr(e_out) if return_edges else None, work.data_ptr(), handle)
+    _lib.check(rc, "rejection_sampling")
+    if check:
+        _raise_status(work, stream, "rejection_sampling")
+    return (n_out, e_out) if return_edges else n_out
+
+
+def philox_uniform(shape, seed: int, *, device=None, stream=None) -> torch.Tensor:
+    """float32 tensor of Philox4x32-10 uniforms in [0, 1 - 2^-24].
+
+    Element i (row-major) is (w >> 8) * 2^-24 with w word i % 4 of
+    Philox(key = seed, counter = (i // 4, 0)).  A seeded stand-in for the
+    mx.random.uniform call that makes the reference tests' rand tensor
+    (/root/reference/tests/test_random_walk.py:31).
+    """
+    if isinstance(shape, numbers.Integral):
+        shape = (int(shape),)
+    _check_stream_arg(stream)
+    dev = torch.device(device) if device is not None else _resolve_device(stream, ())
+    handle = _stream_handle(stream, dev)
+    out = torch.empty(tuple(shape), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.load().mlxc_philox_uniform(_ptr(out), out.numel(), int(seed) & (2**64 - 1), handle)
+    _lib.check(rc, "philox_uniform")
+    return out

@@ -1,0 +1,162 @@
+"""numpy wrapper of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: the checker the HIP path is compared with.  Only
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use it;
+the product (mlx_cluster_amd) never imports it.
+
+Functions follow the reference's CPU evaluation:
+  uniform_walk   -> /root/reference/random_walks/RandomWalk.cpp:41-60
+  node2vec_walk  -> /root/reference/random_walks/BiasedRandomWalk.cpp:20-28,52-100
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
+
+RULE_REF_CHAIN = 0
+RULE_NODE2VEC_EXACT = 1
+MAX_TRIALS = 65536
+
+
+class Counts(ctypes.Structure):
+    _fields_ = [("moving_steps", ctypes.c_int64), ("sink_walks", ctypes.c_int64),
+                ("trials", ctypes.c_int64), ("member_tests", ctypes.c_int64),
+                ("member_lines", ctypes.c_int64)]
+
+    def as_dict(self):
+        return {k: int(getattr(self, k)) for k, _ in self._fields_}
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        lib = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        i64, i32, u64, u32, dbl = (ctypes.c_int64, ctypes.c_int32, ctypes.c_uint64,
+                                   ctypes.c_uint32, ctypes.c_double)
+        lib.oracle_philox4x32_10.argtypes = [P, P, P]
+        lib.oracle_u32_to_unit_float.argtypes = [u32]
+        lib.oracle_u32_to_unit_float.restype = ctypes.c_float
+        lib.oracle_philox_uniform_fill.argtypes = [P, i64, u64]
+        lib.oracle_node2vec_trial0_u0.argtypes = [P, i64, i32, u64]
+        lib.oracle_pick_index.argtypes = [ctypes.c_float, i64]
+        lib.oracle_pick_index.restype = i64
+        lib.oracle_uniform_walk.argtypes = [P, i64, P, i64, P, i64, P, i32, P, P, P]
+        lib.oracle_uniform_walk.restype = ctypes.c_int
+        lib.oracle_node2vec_probs.argtypes = [dbl, dbl, P]
+        lib.oracle_node2vec_walk.argtypes = [P, i64, P, i64, P, i64, i32, dbl, dbl, u64, i32,
+                                             i32, P, P, P]
+        lib.oracle_node2vec_walk.restype = ctypes.c_int
+        lib.oracle_node2vec_walk_libc.argtypes = [P, i64, P, i64, P, i64, i32, dbl, dbl, u32,
+                                                  i32, P, P]
+        lib.oracle_node2vec_walk_libc.restype = ctypes.c_int
+        lib.oracle_csr_flags.argtypes = [P, i64, P, i64]
+        lib.oracle_csr_flags.restype = i32
+        _lib = lib
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _i64(a):
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int64))
+
+
+def philox4x32_10(ctr, key) -> np.ndarray:
+    c = np.ascontiguousarray(ctr, dtype=np.uint32)
+    k = np.ascontiguousarray(key, dtype=np.uint32)
+    out = np.zeros(4, dtype=np.uint32)
+    _load().oracle_philox4x32_10(_p(c), _p(k), _p(out))
+    return out
+
+
+def u32_to_unit_float(x: int) -> float:
+    return float(np.float32(_load().oracle_u32_to_unit_float(int(x))))
+
+
+def philox_uniform(n: int, seed: int) -> np.ndarray:
+    out = np.empty(int(n), dtype=np.float32)
+    _load().oracle_philox_uniform_fill(_p(out), int(n), int(seed) & (2**64 - 1))
+    return out
+
+
+def node2vec_trial0_u0(num_walks: int, walk_length: int, seed: int) -> np.ndarray:
+    out = np.empty((int(num_walks), int(walk_length)), dtype=np.float32)
+    _load().oracle_node2vec_trial0_u0(_p(out), int(num_walks), int(walk_length),
+                                      int(seed) & (2**64 - 1))
+    return out
+
+
+def pick_index(r: float, deg: int) -> int:
+    return int(_load().oracle_pick_index(float(np.float32(r)), int(deg)))
+
+
+def uniform_walk(rowptr, col, start, rand, walk_length, *, with_edges=False):
+    """Returns (n_out [N, L+1], e_out [N, L] or None, status, counts dict)."""
+    rowptr, col, start = _i64(rowptr), _i64(col), _i64(start).reshape(-1)
+    rand = np.ascontiguousarray(np.asarray(rand, dtype=np.float32)).reshape(-1)
+    N, L = start.size, int(walk_length)
+    assert rand.size == N * L
+    n_out = np.empty((N, L + 1), dtype=np.int64)
+    e_out = np.empty((N, L), dtype=np.int64) if with_edges else None
+    counts = Counts()
+    st = _load().oracle_uniform_walk(_p(rowptr), rowptr.size - 1, _p(col), col.size, _p(start),
+                                     N, _p(rand), L, _p(n_out), _p(e_out),
+                                     ctypes.byref(counts))
+    return n_out, e_out, st, counts.as_dict()
+
+
+def node2vec_probs(p: float, q: float) -> np.ndarray:
+    out = np.zeros(3, dtype=np.float64)
+    _load().oracle_node2vec_probs(float(p), float(q), _p(out))
+    return out
+
+
+def node2vec_walk(rowptr, col, start, walk_length, p, q, seed, *, rule=RULE_REF_CHAIN,
+                  rows_sorted=True, with_edges=False):
+    """Returns (n_out, e_out or None, status, counts dict)."""
+    rowptr, col, start = _i64(rowptr), _i64(col), _i64(start).reshape(-1)
+    N, L = start.size, int(walk_length)
+    n_out = np.empty((N, L + 1), dtype=np.int64)
+    e_out = np.empty((N, L), dtype=np.int64) if with_edges else None
+    counts = Counts()
+    st = _load().oracle_node2vec_walk(_p(rowptr), rowptr.size - 1, _p(col), col.size, _p(start),
+                                      N, L, float(p), float(q), int(seed) & (2**64 - 1),
+                                      int(rule), 1 if rows_sorted else 0, _p(n_out), _p(e_out),
+                                      ctypes.byref(counts))
+    return n_out, e_out, st, counts.as_dict()
+
+
+def node2vec_walk_libc(rowptr, col, start, walk_length, p, q, libc_seed, *,
+                       rule=RULE_REF_CHAIN):
+    rowptr, col, start = _i64(rowptr), _i64(col), _i64(start).reshape(-1)
+    N, L = start.size, int(walk_length)
+    n_out = np.empty((N, L + 1), dtype=np.int64)
+    st = _load().oracle_node2vec_walk_libc(_p(rowptr), rowptr.size - 1, _p(col), col.size,
+                                           _p(start), N, L, float(p), float(q),
+                                           int(libc_seed) & 0xFFFFFFFF, int(rule), _p(n_out),
+                                           None)
+    return n_out, st
+
+
+def csr_flags(rowptr, col) -> int:
+    rowptr, col = _i64(rowptr), _i64(col)
+    return int(_load().oracle_csr_flags(_p(rowptr), rowptr.size - 1, _p(col), col.size))

@@ -1,0 +1,99 @@
+"""The C-ABI library loads and exports what include/mlxc.h declares.
+
+CPU-only: argument errors are rejected on the host before any HIP call, so
+they can be exercised without a GPU.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+from mlx_cluster_amd import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "mlxc.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mlxc_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_path():
+    names = declared_functions()
+    assert {"mlxc_random_walk", "mlxc_rejection_sampling", "mlxc_version",
+            "mlxc_last_error"} <= set(names)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert sorted(_lib.SIGNATURES) == declared_functions()
+
+
+def test_header_constants_match_binding():
+    text = open(HEADER).read()
+    for name in ["MLXC_OK", "MLXC_ERR_INVALID_ARGUMENT", "MLXC_ERR_HIP", "MLXC_WORK_WORDS",
+                 "MLXC_STATUS_BAD_NODE", "MLXC_STATUS_BAD_ROW", "MLXC_RULE_REF_CHAIN",
+                 "MLXC_RULE_NODE2VEC_EXACT", "MLXC_CSR_BAD_ROWPTR", "MLXC_CSR_BAD_COL",
+                 "MLXC_CSR_UNSORTED", "MLXC_MAX_TRIALS"]:
+        m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
+        assert m, name
+        assert int(m.group(1)) == getattr(_lib, name), name
+
+
+def test_version():
+    assert _lib.load().mlxc_version() == 100
+
+
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("args,msg", [
+    ((FAKE, -1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, FAKE, None), "num_nodes"),
+    ((FAKE, 1, FAKE, -1, FAKE, 1, FAKE, 1, FAKE, None, FAKE, None), "num_edges"),
+    ((FAKE, 1, FAKE, 0, FAKE, -1, FAKE, 1, FAKE, None, FAKE, None), "num_walks"),
+    ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, -2, FAKE, None, FAKE, None), "walk_length"),
+    ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, None, None), "work"),
+    ((None, 1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, FAKE, None), "NULL"),
+    ((FAKE, 1, FAKE, 0, FAKE, 1, None, 3, FAKE, None, FAKE, None), "rand"),
+    ((FAKE, 1, FAKE, 0, FAKE, 2**62, FAKE, 8, FAKE, None, FAKE, None), "overflows"),
+])
+def test_random_walk_rejects_bad_arguments(args, msg):
+    lib = _lib.load()
+    assert lib.mlxc_random_walk(*args) == _lib.MLXC_ERR_INVALID_ARGUMENT
+    assert msg in _lib.last_error()
+
+
+@pytest.mark.parametrize("p,q,rule,msg", [
+    (0.0, 1.0, 0, "p and q"), (1.0, -1.0, 0, "p and q"), (float("inf"), 1.0, 0, "p and q"),
+    (1.0, float("nan"), 0, "p and q"), (1.0, 1.0, 7, "rule"),
+])
+def test_rejection_sampling_rejects_bad_arguments(p, q, rule, msg):
+    lib = _lib.load()
+    rc = lib.mlxc_rejection_sampling(FAKE, 1, FAKE, 0, FAKE, 0, 3, p, q, 1, rule, 1, FAKE, None,
+                                     FAKE, None)
+    assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT
+    assert msg in _lib.last_error()
+
+
+def test_other_entry_points_reject_bad_arguments():
+    lib = _lib.load()
+    assert lib.mlxc_philox_uniform(FAKE, -1, 0, None) == _lib.MLXC_ERR_INVALID_ARGUMENT
+    assert lib.mlxc_philox_uniform(None, 0, 0, None) == _lib.MLXC_OK  # empty is a no-op
+    flags = ctypes.c_int32(0)
+    assert lib.mlxc_csr_check(FAKE, -1, FAKE, 0, FAKE, ctypes.addressof(flags), None) \
+        == _lib.MLXC_ERR_INVALID_ARGUMENT
+    assert lib.mlxc_csr_check(FAKE, 1, FAKE, 0, FAKE, None, None) \
+        == _lib.MLXC_ERR_INVALID_ARGUMENT
+
+
+def test_python_check_maps_codes():
+    with pytest.raises(ValueError):
+        _lib.load().mlxc_philox_uniform(FAKE, -1, 0, None)
+        _lib.check(_lib.MLXC_ERR_INVALID_ARGUMENT, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.MLXC_ERR_HIP, "x")

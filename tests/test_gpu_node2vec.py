@@ -1,0 +1,133 @@
+"""Parity of the HIP node2vec walk (libmlxc.so) with the CPU oracle.
+
+Bit-exact on the shared Philox stream for both acceptance rules, plus
+distribution checks against the closed-form transition weights.
+"""
+import numpy as np
+import pytest
+import torch
+from scipy import stats
+
+import mlx_cluster_amd as mc
+import oracle
+from mlx_cluster_amd import synth
+from tests.graphs import csr, undirected
+from tests.test_oracle import class_counts, three_class_graph
+
+pytestmark = pytest.mark.gpu
+
+RULE_NAME = {oracle.RULE_REF_CHAIN: "ref_chain", oracle.RULE_NODE2VEC_EXACT: "node2vec"}
+
+
+def gpu_walk(rowptr, col, start, L, p, q, seed, rule, cuda, **kw):
+    t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.int64)).to(cuda)
+    n, e = mc.rejection_sampling(t(rowptr), t(col), t(start), L, p, q, seed=seed,
+                                 rule=RULE_NAME[rule], return_edges=True, **kw)
+    return n.cpu().numpy(), e.cpu().numpy()
+
+
+def assert_parity(rowptr, col, start, L, p, q, seed, rule, cuda, sorted_rows=True, **kw):
+    n_ref, e_ref, st, counts = oracle.node2vec_walk(rowptr, col, start, L, p, q, seed, rule=rule,
+                                                    rows_sorted=sorted_rows, with_edges=True)
+    assert st == 0
+    n, e = gpu_walk(rowptr, col, start, L, p, q, seed, rule, cuda, **kw)
+    np.testing.assert_array_equal(n, n_ref)
+    np.testing.assert_array_equal(e, e_ref)
+    return n, counts
+
+
+def test_fixture_c1(c1, cuda):
+    names = sorted({k[4:-6] for k in c1 if k.startswith("n2v_") and k.endswith("_nodes")})
+    assert len(names) == 5
+    for name in names:
+        p, q, rule, seed = c1[f"n2v_{name}_params"]
+        n, e = gpu_walk(c1["rowptr"], c1["col"], c1["start"], int(c1["walk_length"]), p, q,
+                        int(seed), int(rule), cuda)
+        np.testing.assert_array_equal(n, c1[f"n2v_{name}_nodes"])
+        np.testing.assert_array_equal(e, c1[f"n2v_{name}_edges"])
+
+
+@pytest.mark.parametrize("p,q", [(0.5, 2.0), (4.0, 0.25), (1.0, 3.0), (2.0, 0.5)])
+@pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
+def test_rmat_symmetrized(p, q, rule, cuda):
+    rowptr, col = synth.rmat_csr(12, 40_000, seed=11, symmetrize=True)
+    rowptr, col = rowptr.numpy(), col.numpy()
+    V = rowptr.size - 1
+    start = np.arange(2 * V) % V
+    assert_parity(rowptr, col, start, 20, p, q, 1234, rule, cuda)
+
+
+@pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
+def test_unsorted_rows_use_linear_scan(rule, cuda):
+    rng = np.random.default_rng(2)
+    rowptr, col = undirected(500, rng.integers(0, 500, (4000, 2)), sort=False)
+    assert oracle.csr_flags(rowptr, col) & 4  # rows really are unsorted
+    assert mc.csr_check(rowptr, col) == oracle.csr_flags(rowptr, col)
+    start = np.arange(1000) % 500
+    assert_parity(rowptr, col, start, 15, 0.5, 2.0, 5, rule, cuda, sorted_rows=False)
+
+
+def test_p1_q1_equals_uniform_walk(cuda):
+    rowptr, col = synth.rmat_csr(12, 40_000, seed=12)
+    V = rowptr.numel() - 1
+    start = torch.arange(V) % V
+    L = 16
+    n, _ = gpu_walk(rowptr.numpy(), col.numpy(), start.numpy(), L, 1.0, 1.0, 99,
+                    oracle.RULE_REF_CHAIN, cuda)
+    rand = torch.from_numpy(oracle.node2vec_trial0_u0(V, L, 99))
+    u = mc.random_walk(rowptr.to(cuda), col.to(cuda), start.to(cuda), rand.to(cuda), L)
+    np.testing.assert_array_equal(n, u.cpu().numpy())
+
+
+@pytest.mark.parametrize("N,L", [(0, 4), (1, 1), (3, 0), (300, 2), (1025, 7)])
+def test_ragged_sizes(N, L, cuda):
+    rowptr, col = undirected(64, np.random.default_rng(N).integers(0, 64, (200, 2)))
+    start = np.arange(N) % 64
+    assert_parity(rowptr, col, start, L, 0.7, 1.5, N + L, oracle.RULE_NODE2VEC_EXACT, cuda)
+
+
+@pytest.mark.parametrize("p,q,rule", [(0.5, 2.0, oracle.RULE_NODE2VEC_EXACT),
+                                      (4.0, 0.25, oracle.RULE_NODE2VEC_EXACT),
+                                      (4.0, 0.25, oracle.RULE_REF_CHAIN)])
+def test_transition_chi_square(p, q, rule, cuda):
+    K, M = 3, 4
+    (rowptr, col), a, b = three_class_graph(K, M)
+    N = 1_000_000
+    n, _ = gpu_walk(rowptr, col, np.zeros(N, np.int64), 2, p, q, 2024, rule, cuda)
+    p0, p1, p2 = oracle.node2vec_probs(p, q)
+    w = (p0, p1, p2) if rule == oracle.RULE_NODE2VEC_EXACT else (max(p0, p2), max(p1, p2), p2)
+    expect = np.array([w[0], K * w[1], M * w[2]])
+    expect = expect / expect.sum() * N
+    assert stats.chisquare(class_counts(n, a, b), expect).pvalue > 0.01
+
+
+def test_hub_graph_parity(cuda):
+    """Small version of configuration 5: BA-style graph with hubs (long rows,
+    many membership tests), p=4, q=0.25, both rules."""
+    rowptr, col = synth.ba_hub_csr(20_000, 5, 4, 5_000, seed=3)
+    rowptr, col = rowptr.numpy(), col.numpy()
+    start = np.arange(20_000)
+    for rule in (oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT):
+        _, counts = assert_parity(rowptr, col, start, 12, 4.0, 0.25, 55, rule, cuda)
+        if rule == oracle.RULE_NODE2VEC_EXACT:
+            assert counts["member_tests"] > 0
+
+
+def test_csr_check_matches_oracle(cuda):
+    rowptr, col = csr(4, [(0, 1), (0, 3), (2, 1)])
+    cases = [(rowptr, col), (rowptr, np.array([3, 1, 1])), (rowptr, np.array([1, 9, 1])),
+             (np.array([0, 2, 1, 3, 3]), col), (np.array([0, 2, 2, 3, 4]), col)]
+    for rp, cl in cases:
+        assert mc.csr_check(rp, cl) == oracle.csr_flags(rp, cl)
+    with pytest.raises(ValueError, match="outside"):
+        mc.rejection_sampling(rowptr, np.array([1, 9, 1]), np.array([0]), 3, 1.0, 1.0)
+    with pytest.raises(ValueError, match="rowptr"):
+        mc.rejection_sampling(np.array([0, 2, 1, 3, 3]), col, np.array([0]), 3, 1.0, 1.0)
+
+
+def test_seed_none_follows_torch_manual_seed(c1, cuda):
+    torch.manual_seed(3)
+    a = mc.rejection_sampling(c1["rowptr"], c1["col"], c1["start"], 5, 1.0, 3.0)
+    torch.manual_seed(3)
+    b = mc.rejection_sampling(c1["rowptr"], c1["col"], c1["start"], 5, 1.0, 3.0)
+    assert torch.equal(a, b)

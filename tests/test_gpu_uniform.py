@@ -1,0 +1,162 @@
+"""Parity of the HIP uniform walk (libmlxc.so) with the CPU oracle.
+
+Bit-exact: node sequences and edge ids must equal the oracle's restatement of
+RandomWalk.cpp:41-60 for the same rand tensor.
+"""
+import numpy as np
+import pytest
+import torch
+
+import mlx_cluster_amd as mc
+import oracle
+from mlx_cluster_amd import synth
+from tests.graphs import csr, undirected, uniform_transitions_ok
+
+pytestmark = pytest.mark.gpu
+
+
+def run_both(rowptr, col, start, rand, L, cuda):
+    rowptr, col, start = (np.asarray(a, dtype=np.int64) for a in (rowptr, col, start))
+    rand = np.asarray(rand, dtype=np.float32).reshape(start.size, L)
+    n_ref, e_ref, st, _ = oracle.uniform_walk(rowptr, col, start, rand, L, with_edges=True)
+    assert st == 0
+    n, e = mc.random_walk(torch.from_numpy(rowptr).to(cuda), torch.from_numpy(col).to(cuda),
+                          torch.from_numpy(start).to(cuda), torch.from_numpy(rand).to(cuda), L,
+                          return_edges=True)
+    return n.cpu().numpy(), e.cpu().numpy(), n_ref, e_ref
+
+
+def assert_parity(rowptr, col, start, rand, L, cuda):
+    n, e, n_ref, e_ref = run_both(rowptr, col, start, rand, L, cuda)
+    np.testing.assert_array_equal(n, n_ref)
+    np.testing.assert_array_equal(e, e_ref)
+    return n
+
+
+def test_fixture_c1(c1, cuda):
+    rowptr, col, start, rand = (torch.from_numpy(c1[k]).to(cuda)
+                                for k in ("rowptr", "col", "start", "rand"))
+    L = int(c1["walk_length"])
+    n, e = mc.random_walk(rowptr, col, start, rand, L, return_edges=True)
+    np.testing.assert_array_equal(n.cpu().numpy(), c1["uniform_nodes"])
+    np.testing.assert_array_equal(e.cpu().numpy(), c1["uniform_edges"])
+    # default call returns the node sequences only, as the reference op does
+    n2 = mc.random_walk(rowptr, col, start, rand, L)
+    assert n2.shape == (2000, L + 1) and n2.dtype == torch.int64
+    assert torch.equal(n2, n)
+
+
+def test_hand_graphs(cuda):
+    rowptr, col = csr(3, [(0, 1), (1, 2), (2, 0)])
+    n = assert_parity(rowptr, col, [0, 2], np.full((2, 4), 0.7), 4, cuda)
+    assert n.tolist() == [[0, 1, 2, 0, 1], [2, 0, 1, 2, 0]]
+    rowptr, col = csr(4, [(0, 1), (1, 3)])  # sink 3, isolated 2
+    n = assert_parity(rowptr, col, [0, 2], np.full((2, 5), 0.5), 5, cuda)
+    assert n.tolist() == [[0, 1, 3, 3, 3, 3], [2, 2, 2, 2, 2, 2]]
+    rowptr, col = csr(2, [(0, 0), (0, 1), (1, 0)])  # self-loop
+    n = assert_parity(rowptr, col, [0, 0], [[0.1, 0.1], [0.75, 0.1]], 2, cuda)
+    assert n.tolist() == [[0, 0, 0], [0, 1, 0]]
+    rowptr, col = undirected(5, [(0, 1), (0, 2), (0, 3), (0, 4)])
+    r = np.array([[k / 4 + 0.01, 0.3] for k in range(4)], np.float32)
+    n = assert_parity(rowptr, col, [0, 0, 0, 0], r, 2, cuda)
+    assert n[:, 1].tolist() == [1, 2, 3, 4]
+
+
+def test_out_of_range_rand_is_clamped_like_oracle(cuda):
+    rowptr, col = csr(4, [(0, 1), (0, 2), (0, 3), (1, 0), (2, 0), (3, 0)])
+    r = np.array([[1.0, 0.5], [2.5, 0.5], [-0.5, 0.5], [np.nan, 0.5], [np.inf, 0.5],
+                  [1 - 2 ** -24, 0.5]], np.float32)
+    n = assert_parity(rowptr, col, [0] * 6, r, 2, cuda)
+    assert n[:, 1].tolist() == [3, 3, 1, 1, 3, 3]
+
+
+@pytest.mark.parametrize("N,L", [(0, 5), (1, 1), (7, 0), (255, 3), (257, 17), (5000, 40),
+                                 (70_001, 9)])
+def test_ragged_sizes(N, L, cuda):
+    rowptr, col = synth.rmat_csr(10, 6000, seed=N + L)
+    V = rowptr.numel() - 1
+    start = (np.arange(N) * 7919) % V
+    rand = oracle.philox_uniform(N * L, seed=N * 31 + L)
+    assert_parity(rowptr.numpy(), col.numpy(), start, rand, L, cuda)
+
+
+def test_rmat_scale16_with_sinks(cuda):
+    rowptr, col = synth.rmat_csr(16, 1 << 20, seed=3)
+    rowptr, col = rowptr.numpy(), col.numpy()
+    assert (np.diff(rowptr) == 0).sum() > 1000  # many absorbing nodes
+    V = rowptr.size - 1
+    start = np.arange(4 * V) % V
+    L = 30
+    rand = oracle.philox_uniform(start.size * L, seed=77)
+    n = assert_parity(rowptr, col, start, rand, L, cuda)
+    assert uniform_transitions_ok(rowptr, col, start, rand, n) == 0
+
+
+def test_philox_uniform_matches_oracle(cuda):
+    for n, seed in [(1, 0), (3, 5), (4, 5), (1001, 2**63 + 12345), (1 << 18, 9)]:
+        got = mc.philox_uniform(n, seed, device=cuda).cpu().numpy()
+        np.testing.assert_array_equal(got, oracle.philox_uniform(n, seed))
+
+
+def test_repeatable_and_side_stream(cuda):
+    rowptr, col = synth.rmat_csr(12, 40_000, seed=5, device=cuda)
+    V = rowptr.numel() - 1
+    start = torch.arange(3 * V, device=cuda) % V
+    rand = mc.philox_uniform((start.numel(), 25), 4, device=cuda)
+    a = mc.random_walk(rowptr, col, start, rand, 25)
+    s = torch.cuda.Stream(device=cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+    b = mc.random_walk(rowptr, col, start, rand, 25, stream=s)
+    torch.cuda.current_stream(cuda).wait_stream(s)
+    assert torch.equal(a, b)
+
+
+def test_numpy_inputs_are_copied(c1, cuda):
+    n = mc.random_walk(c1["rowptr"], c1["col"], c1["start"], c1["rand"], int(c1["walk_length"]))
+    assert n.is_cuda
+    np.testing.assert_array_equal(n.cpu().numpy(), c1["uniform_nodes"])
+
+
+def test_bad_graph_raises(cuda):
+    rowptr, col = csr(3, [(0, 1), (1, 2)])
+    rand = np.zeros((1, 3), np.float32)
+    with pytest.raises(ValueError, match="outside"):
+        mc.random_walk(rowptr, col, np.array([5]), rand, 3)
+    with pytest.raises(ValueError, match="outside"):
+        mc.random_walk(rowptr, np.array([7, 2]), np.array([0]), rand, 3)
+    with pytest.raises(ValueError, match="rowptr"):
+        mc.random_walk(np.array([0, 2, 1, 2]), col, np.array([0]), rand, 3)
+    with pytest.raises(ValueError, match="rowptr"):
+        mc.random_walk(np.array([0, 1, 9, 2]), col, np.array([0]), rand, 3)
+
+
+def test_c2_full_size_properties(cuda):
+    """Configuration 2 at full size (R-MAT 2^20, 10 walks per node, L=80):
+    every one of the 838,860,800 steps is checked against numpy-free torch
+    float32 arithmetic on the device, and a sample of walks bit-exactly
+    against the oracle."""
+    rowptr, col = synth.rmat_csr(20, 1 << 24, seed=0, device=cuda)
+    V = rowptr.numel() - 1
+    N, L = 10 * V, 80
+    start = torch.arange(N, device=cuda) % V
+    rand = mc.philox_uniform((N, L), 2, device=cuda)
+    n = mc.random_walk(rowptr, col, start, rand, L)
+    assert torch.equal(n[:, 0], start)
+    bad = 0
+    for l in range(L):
+        u, v = n[:, l], n[:, l + 1]
+        rs = rowptr[u]
+        deg = rowptr[u + 1] - rs
+        prod = rand[:, l] * deg.to(torch.float32)
+        idx = torch.minimum(prod.to(torch.int64), (deg - 1).clamp_min(0))
+        moving = deg > 0
+        expect = torch.where(moving, col[torch.where(moving, rs + idx, 0)], u)
+        bad += int((expect != v).sum())
+    assert bad == 0
+    g = torch.Generator().manual_seed(0)
+    sample = torch.randint(0, N, (4000,), generator=g).to(cuda)
+    rp, cl = rowptr.cpu().numpy(), col.cpu().numpy()
+    n_ref, _, st, _ = oracle.uniform_walk(rp, cl, start[sample].cpu().numpy(),
+                                          rand[sample].cpu().numpy(), L)
+    assert st == 0
+    np.testing.assert_array_equal(n[sample].cpu().numpy(), n_ref)
