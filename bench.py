@@ -102,6 +102,8 @@ def main():
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 1 GiB device-to-device copy (rocprof counter scale)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the walks need no cross-GPU exchange and this build "
@@ -115,9 +117,20 @@ def main():
     import mlx_cluster_amd as mc
     from mlx_cluster_amd import synth
 
-    desc, kind, gargs, per_node, L, extra = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        # A plain copy of known size: 1 GiB read + 1 GiB written per launch.
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_each_way": src.numel() * 4,
+                          "launches": args.warmup + args.steps}), flush=True)
+        return
+
+    desc, kind, gargs, per_node, L, extra = CONFIGS[args.config]
     log(f"config {args.config}: {desc} on {torch.cuda.get_device_name(dev)}")
     rowptr, col = synth.rmat_csr(gargs["scale"], gargs["samples"], seed=0, device=dev,
                                  symmetrize=gargs["symmetrize"])

@@ -11,7 +11,10 @@ import os
 
 import torch  # noqa: F401  (must be loaded first: provides the HIP runtime)
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmlxc.so")
+# MLXC_LIB selects another build of the same library (for example one
+# compiled with different tuning macros); the default is the in-tree build.
+LIB_PATH = os.environ.get("MLXC_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "libmlxc.so")
 
 MLXC_OK = 0
 MLXC_ERR_INVALID_ARGUMENT = -1

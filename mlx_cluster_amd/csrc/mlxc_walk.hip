@@ -285,6 +285,229 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
     if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
 }
 
+// ------------------------------------------------- uniform walk, windowed
+
+// Per-lane register windows for the two streams of the uniform walk.
+//
+// The rand stream: walk n reads rand[n*L + l] at step l, so a lane walks
+// through its own row 4 bytes at a time while its 63 neighbours do the same
+// 4*L bytes apart.  Read one float at a time, nearly every step misses L2 and
+// costs a 128-byte line.  Instead each slot keeps the next RW floats of its
+// row in registers, loaded as one aligned RW*4-byte block, so the stream
+// costs one line per RW steps.
+//
+// The output: walk n writes n_out[n*(L+1) + j] for j = 0..L, one 8-byte entry
+// per step.  Scattered 8-byte stores reach memory as partial 32-byte writes.
+// Each slot buffers its entries in an 8-entry window aligned to 64 bytes of
+// the output and writes a full window with four 16-byte stores; walks that
+// sink in a node of out-degree 0 write their constant tail in whole 64-byte
+// blocks.
+template <int RW>
+struct RandWindow {
+    float w[RW];
+    int valid;  // w[0 .. valid-1] are the next uniforms of the walk
+};
+
+template <int RW>
+__device__ __forceinline__ void rw_shift1(RandWindow<RW>& r) {
+#pragma unroll
+    for (int i = 0; i + 1 < RW; ++i) r.w[i] = r.w[i + 1];
+}
+
+// Loads the aligned block holding rand[f] and shifts it so w[0] = rand[f].
+template <int RW>
+__device__ __forceinline__ void rw_load(RandWindow<RW>& r, const float* __restrict__ rand,
+                                        int64_t f, int64_t total) {
+    const int64_t base = f & ~static_cast<int64_t>(RW - 1);
+    if (base + RW <= total) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const f32x4* p = reinterpret_cast<const f32x4*>(rand + base);
+#pragma unroll
+        for (int i = 0; i < RW / 4; ++i) {
+            const f32x4 x = __builtin_nontemporal_load(p + i);
+            r.w[4 * i] = x.x;
+            r.w[4 * i + 1] = x.y;
+            r.w[4 * i + 2] = x.z;
+            r.w[4 * i + 3] = x.w;
+        }
+    } else {  // last block of the array: element loads inside [0, total)
+#pragma unroll
+        for (int i = 0; i < RW; ++i)
+            r.w[i] = (base + i < total) ? __builtin_nontemporal_load(rand + base + i) : 0.0f;
+    }
+    const int k = static_cast<int>(f - base);
+    // shift left by k in log2(RW) conditional steps
+#pragma unroll
+    for (int bit = RW / 2; bit >= 1; bit >>= 1) {
+        if (k & bit) {
+#pragma unroll
+            for (int i = 0; i < RW; ++i) r.w[i] = (i + bit < RW) ? r.w[i + bit] : 0.0f;
+        }
+    }
+    r.valid = RW - k;
+}
+
+struct OutWindow {
+    int64_t w[8];  // w[8-count .. 7] hold the newest entries; w[7] is entry g
+    int count;
+};
+
+// Writes the buffered entries, the newest of which is output index g.
+__device__ __forceinline__ void ow_flush(OutWindow& o, int64_t* __restrict__ out, int64_t g) {
+    if (o.count == 8 && ((g + 1) & 7) == 0) {
+        int64_t* p = out + (g - 7);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
+            i64x2 x = {o.w[2 * i], o.w[2 * i + 1]};
+            *reinterpret_cast<i64x2*>(p + 2 * i) = x;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (i >= 8 - o.count) out[g - 7 + i] = o.w[i];
+    }
+    o.count = 0;
+}
+
+// Appends the entry for output index g; writes the window when g closes a
+// 64-byte block.
+__device__ __forceinline__ void ow_push(OutWindow& o, int64_t* __restrict__ out, int64_t g,
+                                        int64_t x) {
+#pragma unroll
+    for (int i = 0; i < 7; ++i) o.w[i] = o.w[i + 1];
+    o.w[7] = x;
+    o.count = o.count < 8 ? o.count + 1 : 8;
+    if (((g + 1) & 7) == 0) ow_flush(o, out, g);
+}
+
+// Output indices g .. g_last (inclusive) all hold x; the window holds the
+// entries before g.  Ends with everything written.
+__device__ __forceinline__ void ow_fill(OutWindow& o, int64_t* __restrict__ out, int64_t g,
+                                        int64_t g_last, int64_t x) {
+    while (g <= g_last && (g & 7) != 0) ow_push(o, out, g++, x);
+    if (o.count) ow_flush(o, out, g - 1);
+    typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
+    const i64x2 xx = {x, x};
+    for (; g + 7 <= g_last; g += 8) {
+        i64x2* p = reinterpret_cast<i64x2*>(out + g);
+        p[0] = xx;
+        p[1] = xx;
+        p[2] = xx;
+        p[3] = xx;
+    }
+    for (; g <= g_last; ++g) out[g] = x;
+}
+
+// Uniform walk with register windows (requires 16-byte aligned rand and
+// n_out; no edge output).  W walk slots per lane, walks from the wave queue.
+template <int W, int RW>
+__global__ __launch_bounds__(kBlock) void uniform_walk_win_kernel(WalkArgs a) {
+    const int64_t L = a.walk_length;
+    const int64_t L1 = L + 1;
+    const int64_t N = a.num_walks;
+    const int64_t rtotal = N * L;
+    unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.work + 1);
+    WaveQueue q{0, 0};
+    int64_t n[W], v[W], l[W];
+    RandWindow<RW> rw[W];
+    OutWindow ow[W];
+    uint32_t status = 0;
+
+#pragma unroll
+    for (int s = 0; s < W; ++s) {
+        n[s] = -1;
+        l[s] = L;
+        v[s] = 0;
+        rw[s].valid = 0;
+        ow[s].count = 0;
+    }
+
+    while (true) {
+        bool unretired = false;
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            const bool need = (n[s] < N) && (l[s] >= L);
+            const int64_t id = queue_take(q, need, counter);
+            if (need) {
+                n[s] = id;
+                if (id < N) {
+                    const int64_t s0 = a.start[id];
+                    v[s] = s0;
+                    l[s] = 0;
+                    rw[s].valid = 0;
+                    ow[s].count = 0;
+                    ow_push(ow[s], a.n_out, id * L1, s0);
+                    if (!node_ok(s0, a.num_nodes)) {
+                        status |= MLXC_STATUS_BAD_NODE;
+                        ow_fill(ow[s], a.n_out, id * L1 + 1, id * L1 + L, s0);
+                        l[s] = L;
+                    } else if (L == 0) {
+                        ow_flush(ow[s], a.n_out, id * L1);
+                    }
+                }
+            }
+            unretired |= (n[s] < N);
+        }
+        if (!__any(unretired)) break;
+
+        // Phase 1: rowptr pair of every live slot, and a new rand block where
+        // the window has run dry.
+        RowBounds rb[W];
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            const bool live = (n[s] < N) && (l[s] < L);
+            rb[s] = {0, 0};
+            if (live) {
+                rb[s] = load_row(a.rowptr, v[s]);
+                if (rw[s].valid == 0) rw_load(rw[s], a.rand, n[s] * L + l[s], rtotal);
+            }
+        }
+        // Phase 2: candidate edge and its target.
+        int64_t x[W];
+        bool moved[W];
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            const bool live = (n[s] < N) && (l[s] < L);
+            x[s] = v[s];
+            moved[s] = false;
+            if (live) {
+                const int64_t deg = rb[s].end - rb[s].begin;
+                if (!row_ok(rb[s], a.num_edges)) {
+                    status |= MLXC_STATUS_BAD_ROW;
+                } else if (deg > 0) {
+                    x[s] = a.col[rb[s].begin + pick_index(rw[s].w[0], deg)];
+                    moved[s] = true;
+                }
+            }
+        }
+        // Phase 3: buffer the new node, advance, finish sunk / broken walks.
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            const bool live = (n[s] < N) && (l[s] < L);
+            if (!live) continue;
+            const int64_t g = n[s] * L1 + l[s] + 1;  // output index of this step
+            bool stop = !moved[s];
+            if (moved[s] && !node_ok(x[s], a.num_nodes)) {
+                status |= MLXC_STATUS_BAD_NODE;
+                stop = true;
+            }
+            v[s] = x[s];
+            l[s] += 1;
+            rw_shift1(rw[s]);
+            rw[s].valid -= 1;
+            if (stop) {
+                ow_fill(ow[s], a.n_out, g, n[s] * L1 + L, x[s]);
+                l[s] = L;
+            } else {
+                ow_push(ow[s], a.n_out, g, x[s]);
+                if (l[s] == L && ow[s].count) ow_flush(ow[s], a.n_out, g);
+            }
+        }
+    }
+    if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
+}
+
 // ---------------------------------------------------------- node2vec walk
 
 struct N2VArgs {
@@ -552,16 +775,29 @@ int zero_work(int64_t* d_work, hipStream_t stream) {
     return MLXC_OK;
 }
 
-constexpr int kUniformSlots = 2;  // walks in flight per lane
+#ifndef MLXC_UNIFORM_SLOTS
+#define MLXC_UNIFORM_SLOTS 2   // walks in flight per lane
+#endif
+#ifndef MLXC_RAND_WINDOW
+#define MLXC_RAND_WINDOW 16    // uniforms per rand block (4-byte floats)
+#endif
 
-template <bool kEdges>
-int launch_uniform(const WalkArgs& a, hipStream_t stream) {
-    auto kernel = uniform_walk_kernel<kUniformSlots, kEdges>;
+template <typename Kernel>
+int launch_persistent(Kernel kernel, const WalkArgs& a, int slots, hipStream_t stream) {
     int grid = 0;
-    if (int rc = persistent_grid(kernel, a.num_walks, kUniformSlots, grid)) return rc;
+    if (int rc = persistent_grid(kernel, a.num_walks, slots, grid)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
+}
+
+int launch_uniform(const WalkArgs& a, hipStream_t stream) {
+    constexpr int W = MLXC_UNIFORM_SLOTS;
+    const bool aligned = (reinterpret_cast<uintptr_t>(a.rand) % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(a.n_out) % 16 == 0);
+    if (a.e_out) return launch_persistent(uniform_walk_kernel<W, true>, a, W, stream);
+    if (!aligned) return launch_persistent(uniform_walk_kernel<W, false>, a, W, stream);
+    return launch_persistent(uniform_walk_win_kernel<W, MLXC_RAND_WINDOW>, a, W, stream);
 }
 
 template <int kRule, bool kSorted, bool kEdges>
@@ -607,7 +843,7 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* 
     if (num_walks == 0) return MLXC_OK;
     WalkArgs a{d_rowptr, d_col, d_start, d_rand, d_n_out, d_e_out, d_work,
                num_nodes, num_edges, num_walks, walk_length};
-    return d_e_out ? launch_uniform<true>(a, s) : launch_uniform<false>(a, s);
+    return launch_uniform(a, s);
 }
 
 int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
