@@ -94,6 +94,37 @@ def cpu_baseline_uniform(np, oracle, rowptr_h, col_h, start, rand, L, target_s=1
     return walks * L / dt, walks, dt
 
 
+def gather_ceiling(torch, dev):
+    """Random-gather ceiling: out[i] = table[idx[i]] with 2^26 independent
+    uniform int64 indices (torch.take), for tables from 32 MiB (L2/MALL
+    resident) to 8 GiB (HBM).  Reports gathered lines/s and the equivalent
+    GB/s at 64 and 128 bytes per line; the idx and out streams are included
+    in the time, not in the line count."""
+    res = []
+    n = 1 << 26
+    for mib in (32, 128, 256, 1024, 8192):
+        table = torch.arange(mib << 17, dtype=torch.int64, device=dev)
+        g = torch.Generator(device=dev).manual_seed(mib)
+        idx = torch.randint(0, table.numel(), (n,), generator=g, device=dev)
+        out = torch.take(table, idx)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        reps = 10
+        for _ in range(reps):
+            torch.take(table, idx, out=out) if hasattr(torch, "take") else None
+        ev[1].record()
+        torch.cuda.synchronize()
+        ms = ev[0].elapsed_time(ev[1]) / reps
+        lines = n / (ms / 1e3)
+        res.append({"table_MiB": mib, "ms": ms, "gathers_per_s": lines,
+                    "GBs_at_64B": lines * 64 / 1e9, "GBs_at_128B": lines * 128 / 1e9,
+                    "stream_GBs": n * 16 / (ms / 1e3) / 1e9})
+        log(f"gather table {mib} MiB: {ms:.3f} ms, {lines:.3e} gathers/s")
+        del table, idx, out
+    return {"gather_ceiling": res}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,6 +135,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (rocprof counter scale)")
+    ap.add_argument("--gather-ceiling", action="store_true",
+                    help="measure independent random 8-byte gathers over tables of several sizes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the walks need no cross-GPU exchange and this build "
@@ -128,6 +161,10 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes_each_way": src.numel() * 4,
                           "launches": args.warmup + args.steps}), flush=True)
+        return
+
+    if args.gather_ceiling:
+        print(json.dumps(gather_ceiling(torch, dev)), flush=True)
         return
 
     desc, kind, gargs, per_node, L, extra = CONFIGS[args.config]
@@ -170,11 +207,15 @@ def main():
     value = steps_per_launch / (ms_per_step / 1e3)
     log(f"{ms_per_step:.3f} ms/step wall, {kernel_ms:.3f} ms/launch (events)")
 
-    # Roofline bytes of one launch (64-B line per dependent random read).
+    # Algorithmic bytes of one launch: one 64-B line per dependent random
+    # read of the reference loop (rowptr pair and col, RandomWalk.cpp:45-54),
+    # streams at their byte count.  M = steps from a node with deg > 0,
+    # Z = walks that meet a deg-0 node (one rowptr read to find it).
     if kind == "uniform":
         M, Z = uniform_counts(torch, rowptr, out)
         roof_bytes = LINE * (M + Z) + LINE * M + 4 * M + 8 * N * (L + 1) + 8 * N
-        units = dict(moving_steps=M, sink_walks=Z)
+        units = dict(moving_steps=M, sink_walks=Z,
+                     bytes_formula="64*(M+Z) + 64*M + 4*M + 8*N*(L+1) + 8*N")
     else:
         roof_bytes = None
         units = {}
@@ -182,7 +223,9 @@ def main():
     traffic = traffic_from_profile(f"{kind}_walk_{args.config}")
     roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": (achieved / PEAK_HBM_GBS) if achieved else None, "traffic": traffic,
-                "algorithmic_bytes_per_launch": roof_bytes, "kernel_ms": kernel_ms, **units}
+                "algorithmic_bytes_per_launch": roof_bytes,
+                "kernel_ms": kernel_ms, "kernel_ms_source": "HIP events around each call on its stream",
+                **units}
 
     # Sampled bit-exact parity against the oracle, and the CPU baseline.
     import oracle

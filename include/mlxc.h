@@ -16,6 +16,7 @@
 #ifndef MLXC_H
 #define MLXC_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -26,16 +27,23 @@ extern "C" {
 #define MLXC_ERR_INVALID_ARGUMENT (-1)
 #define MLXC_ERR_HIP (-2)
 
-/* Size in int64 words of the device workspace `d_work` that every walk entry
- * point takes.  The call zeroes it on `stream` before its kernel runs; after
- * the call has completed, word 0 holds the MLXC_STATUS_* bits of that call
- * (the other words are internal: the walk-queue counter). */
+/* Device workspace.  Every walk entry point takes `d_workspace` (16-byte
+ * aligned, at least MLXC_WORK_WORDS int64 words) and its size in bytes.  The
+ * call zeroes the first MLXC_WORK_WORDS words on `stream` before its kernels
+ * run; after the call has completed, word 0 holds the MLXC_STATUS_* bits of
+ * that call (the other words are internal: the walk-queue counter).  A
+ * workspace of mlxc_walk_workspace_bytes(num_nodes, num_edges, num_walks)
+ * bytes also holds a per-call copy of the graph laid out as 16-byte edge
+ * records (target node, target row begin, target degree) and one such record
+ * per walk start, which lets the uniform walk take one dependent read per
+ * step instead of two; with a smaller workspace the walk reads the CSR arrays
+ * directly.  Same results either way. */
 #define MLXC_WORK_WORDS 4
 
-/* Bits a walk kernel ORs into d_work[0] when the graph or the starts are
- * malformed (the reference reads out of bounds in these cases; these kernels
- * never do — the affected walk stops and its remaining entries repeat its
- * last node). */
+/* Bits a walk kernel ORs into workspace word 0 when the graph or the starts
+ * are malformed (the reference reads out of bounds in these cases; these
+ * kernels never do — the affected walk stops and its remaining output
+ * entries are unspecified). */
 #define MLXC_STATUS_BAD_NODE 1 /* a start or col value outside [0, num_nodes) */
 #define MLXC_STATUS_BAD_ROW 2  /* rowptr[v] / rowptr[v+1] outside [0, num_edges] or decreasing */
 
@@ -59,6 +67,14 @@ int mlxc_version(void);
 /* Message of the calling thread's most recent failed call ("" if none). */
 const char* mlxc_last_error(void);
 
+/* Workspace bytes that enable the edge-record layout for num_walks walks
+ * over a graph with num_nodes nodes and num_edges CSR entries:
+ * 256 + 16 * (num_edges + num_walks) when num_nodes and num_edges are below
+ * 2^31, else the minimum MLXC_WORK_WORDS * 8.  No reference counterpart (the
+ * reference allocates its outputs inside eval, RandomWalk.cpp:28-29, and uses
+ * no scratch). */
+size_t mlxc_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks);
+
 /*
  * Uniform random walk.
  * Replaces: RandomWalk::eval_cpu / eval_gpu and the op random_walk(rowptr,
@@ -71,7 +87,7 @@ const char* mlxc_last_error(void);
  * d_start   int64 [num_walks]         d_rand float32 [num_walks * walk_length]
  * d_n_out   int64 [num_walks * (walk_length + 1)]  (row-major [N, L+1])
  * d_e_out   int64 [num_walks * walk_length] or NULL (edge ids, -1 = stayed)
- * d_work    int64 [MLXC_WORK_WORDS] device workspace (see above).
+ * d_workspace, workspace_bytes: device workspace (see above).
  *
  * Step l of walk n at node v: deg = rowptr[v+1] - rowptr[v]; deg == 0 keeps
  * v; otherwise e = rowptr[v] + (int64)(rand[n*L + l] * (float)deg) in IEEE
@@ -81,8 +97,8 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes,
                      const int64_t* d_col, int64_t num_edges,
                      const int64_t* d_start, int64_t num_walks,
                      const float* d_rand, int32_t walk_length,
-                     int64_t* d_n_out, int64_t* d_e_out, int64_t* d_work,
-                     void* stream);
+                     int64_t* d_n_out, int64_t* d_e_out,
+                     void* d_workspace, size_t workspace_bytes, void* stream);
 
 /*
  * node2vec walk by rejection sampling.
@@ -106,20 +122,21 @@ int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes,
                             const int64_t* d_start, int64_t num_walks,
                             int32_t walk_length, double p, double q,
                             uint64_t seed, int32_t rule, int32_t rows_sorted,
-                            int64_t* d_n_out, int64_t* d_e_out, int64_t* d_work,
-                            void* stream);
+                            int64_t* d_n_out, int64_t* d_e_out,
+                            void* d_workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Validates a CSR graph on the device and reports MLXC_CSR_* bits in
- * *h_flags (host pointer).  Synchronises `stream`.  d_work: int64
- * [MLXC_WORK_WORDS] device workspace supplied by the caller.
+ * *h_flags (host pointer).  Synchronises `stream`.  d_workspace: at least
+ * MLXC_WORK_WORDS int64 words of device memory supplied by the caller.
  * No reference counterpart: the reference validates nothing (its
  * is_neighbor, BiasedRandomWalk.cpp:20-28, works on unsorted rows); this
  * picks the neighbour-test strategy for mlxc_rejection_sampling.
  */
 int mlxc_csr_check(const int64_t* d_rowptr, int64_t num_nodes,
                    const int64_t* d_col, int64_t num_edges,
-                   int64_t* d_work, int32_t* h_flags, void* stream);
+                   void* d_workspace, size_t workspace_bytes, int32_t* h_flags,
+                   void* stream);
 
 /*
  * Uniform float32 fill from Philox4x32-10: out[i] = (w >> 8) * 2^-24 with w

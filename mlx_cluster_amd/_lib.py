@@ -34,21 +34,23 @@ _i32 = ctypes.c_int32
 _u64 = ctypes.c_uint64
 _dbl = ctypes.c_double
 _ptr = ctypes.c_void_p
+_size = ctypes.c_size_t
 
 # name -> (restype, argtypes); every function include/mlxc.h declares.
 SIGNATURES = {
     "mlxc_version": (ctypes.c_int, []),
     "mlxc_last_error": (ctypes.c_char_p, []),
+    "mlxc_walk_workspace_bytes": (_size, [_i64, _i64, _i64]),
     "mlxc_random_walk": (
         ctypes.c_int,
-        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _ptr, _ptr],
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _ptr, _size, _ptr],
     ),
     "mlxc_rejection_sampling": (
         ctypes.c_int,
         [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _dbl, _dbl, _u64, _i32, _i32,
-         _ptr, _ptr, _ptr, _ptr],
+         _ptr, _ptr, _ptr, _size, _ptr],
     ),
-    "mlxc_csr_check": (ctypes.c_int, [_ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr]),
+    "mlxc_csr_check": (ctypes.c_int, [_ptr, _i64, _ptr, _i64, _ptr, _size, _ptr, _ptr]),
     "mlxc_philox_uniform": (ctypes.c_int, [_ptr, _i64, _u64, _ptr]),
 }
 

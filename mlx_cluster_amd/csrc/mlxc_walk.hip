@@ -301,7 +301,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
 // Each slot buffers its entries in an 8-entry window aligned to 64 bytes of
 // the output and writes a full window with four 16-byte stores; walks that
 // sink in a node of out-degree 0 write their constant tail in whole 64-byte
-// blocks.
+// blocks.  The stores are non-temporal: the output is never read back, and
+// streaming it past the caches keeps them for the graph.
 template <int RW>
 struct RandWindow {
     float w[RW];
@@ -347,33 +348,39 @@ __device__ __forceinline__ void rw_load(RandWindow<RW>& r, const float* __restri
     r.valid = RW - k;
 }
 
-struct OutWindow {
-    int64_t w[8];  // w[8-count .. 7] hold the newest entries; w[7] is entry g
+// T is the type the entries are buffered in (int32_t when node ids fit);
+// they are written as int64.
+template <typename T>
+struct OutWin {
+    T w[8];  // w[8-count .. 7] hold the newest entries; w[7] is entry g
     int count;
 };
+typedef OutWin<int64_t> OutWindow;
 
 // Writes the buffered entries, the newest of which is output index g.
-__device__ __forceinline__ void ow_flush(OutWindow& o, int64_t* __restrict__ out, int64_t g) {
+template <typename T>
+__device__ __forceinline__ void ow_flush(OutWin<T>& o, int64_t* __restrict__ out, int64_t g) {
     if (o.count == 8 && ((g + 1) & 7) == 0) {
         int64_t* p = out + (g - 7);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
-            i64x2 x = {o.w[2 * i], o.w[2 * i + 1]};
-            *reinterpret_cast<i64x2*>(p + 2 * i) = x;
+            i64x2 x = {static_cast<int64_t>(o.w[2 * i]), static_cast<int64_t>(o.w[2 * i + 1])};
+            __builtin_nontemporal_store(x, reinterpret_cast<i64x2*>(p + 2 * i));
         }
     } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            if (i >= 8 - o.count) out[g - 7 + i] = o.w[i];
+            if (i >= 8 - o.count)
+                __builtin_nontemporal_store(static_cast<int64_t>(o.w[i]), out + g - 7 + i);
     }
     o.count = 0;
 }
 
 // Appends the entry for output index g; writes the window when g closes a
 // 64-byte block.
-__device__ __forceinline__ void ow_push(OutWindow& o, int64_t* __restrict__ out, int64_t g,
-                                        int64_t x) {
+template <typename T>
+__device__ __forceinline__ void ow_push(OutWin<T>& o, int64_t* __restrict__ out, int64_t g, T x) {
 #pragma unroll
     for (int i = 0; i < 7; ++i) o.w[i] = o.w[i + 1];
     o.w[7] = x;
@@ -383,20 +390,22 @@ __device__ __forceinline__ void ow_push(OutWindow& o, int64_t* __restrict__ out,
 
 // Output indices g .. g_last (inclusive) all hold x; the window holds the
 // entries before g.  Ends with everything written.
-__device__ __forceinline__ void ow_fill(OutWindow& o, int64_t* __restrict__ out, int64_t g,
-                                        int64_t g_last, int64_t x) {
+template <typename T>
+__device__ __forceinline__ void ow_fill(OutWin<T>& o, int64_t* __restrict__ out, int64_t g,
+                                        int64_t g_last, T x) {
     while (g <= g_last && (g & 7) != 0) ow_push(o, out, g++, x);
     if (o.count) ow_flush(o, out, g - 1);
     typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
-    const i64x2 xx = {x, x};
+    const int64_t x64 = static_cast<int64_t>(x);
+    const i64x2 xx = {x64, x64};
     for (; g + 7 <= g_last; g += 8) {
         i64x2* p = reinterpret_cast<i64x2*>(out + g);
-        p[0] = xx;
-        p[1] = xx;
-        p[2] = xx;
-        p[3] = xx;
+        __builtin_nontemporal_store(xx, p);
+        __builtin_nontemporal_store(xx, p + 1);
+        __builtin_nontemporal_store(xx, p + 2);
+        __builtin_nontemporal_store(xx, p + 3);
     }
-    for (; g <= g_last; ++g) out[g] = x;
+    for (; g <= g_last; ++g) __builtin_nontemporal_store(x64, out + g);
 }
 
 // Uniform walk with register windows (requires 16-byte aligned rand and
@@ -503,6 +512,270 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_win_kernel(WalkArgs a) {
                 ow_push(ow[s], a.n_out, g, x[s]);
                 if (l[s] == L && ow[s].count) ow_flush(ow[s], a.n_out, g);
             }
+        }
+    }
+    if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
+}
+
+// ------------------------------------------- uniform walk, edge records
+
+// One record per CSR entry e, written by edge_record_kernel at the start of
+// each call: the target node col[e] together with its row bounds.  A walk at
+// node v with row [begin, begin + deg) picks e and reads record e: one
+// dependent 16-byte read per step gives the next node and everything needed
+// for the step after it, where the plain CSR needs two (rowptr[v], then
+// col[e]).  The walk's random reads, which bound it, halve; the records cost
+// 16 bytes per edge of HBM and one pass over the graph per call.
+struct __attribute__((aligned(16))) EdgeRecord {
+    int32_t node;   // col[e]
+    int32_t begin;  // rowptr[col[e]]
+    int32_t deg;    // rowptr[col[e] + 1] - rowptr[col[e]]; < 0 marks a malformed entry
+    int32_t pad;
+};
+constexpr int32_t kRecBadNode = -1;  // col[e] outside [0, num_nodes)
+constexpr int32_t kRecBadRow = -2;   // row of col[e] outside [0, num_edges] or decreasing
+constexpr size_t kRecordOffset = 256;  // bytes of workspace before the records
+
+__global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __restrict__ rowptr,
+                                                             const int64_t* __restrict__ col,
+                                                             int64_t num_nodes, int64_t num_edges,
+                                                             EdgeRecord* __restrict__ rec) {
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; e < num_edges;
+         e += stride) {
+        const int64_t c = col[e];
+        i32x4 r = {static_cast<int32_t>(c), 0, kRecBadNode, 0};
+        if (node_ok(c, num_nodes)) {
+            const RowBounds rb = load_row(rowptr, c);
+            if (row_ok(rb, num_edges)) {
+                r.y = static_cast<int32_t>(rb.begin);
+                r.z = static_cast<int32_t>(rb.end - rb.begin);
+            } else {
+                r.z = kRecBadRow;
+            }
+        }
+        *reinterpret_cast<i32x4*>(rec + e) = r;
+    }
+}
+
+// Loads the aligned rand block holding rand[f] without shifting it.
+template <int RW>
+__device__ __forceinline__ void rw_load_block(RandWindow<RW>& r, const float* __restrict__ rand,
+                                              int64_t f, int64_t total) {
+    const int64_t base = f & ~static_cast<int64_t>(RW - 1);
+    if (base + RW <= total) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const f32x4* p = reinterpret_cast<const f32x4*>(rand + base);
+#pragma unroll
+        for (int i = 0; i < RW / 4; ++i) {
+            const f32x4 x = __builtin_nontemporal_load(p + i);
+            r.w[4 * i] = x.x;
+            r.w[4 * i + 1] = x.y;
+            r.w[4 * i + 2] = x.z;
+            r.w[4 * i + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < RW; ++i)
+            r.w[i] = (base + i < total) ? __builtin_nontemporal_load(rand + base + i) : 0.0f;
+    }
+}
+
+// First index of the rand block that serves rand[f]: the aligned block, or for
+// the array's last partial block the last RW values (total must be a multiple
+// of 4 and at least RW, so every block is 16-byte aligned and in bounds).
+template <int RW>
+__device__ __forceinline__ int64_t rw_block_base(int64_t f, int64_t total) {
+    const int64_t base = f & ~static_cast<int64_t>(RW - 1);
+    return base + RW <= total ? base : total - RW;
+}
+
+template <int RW>
+__device__ __forceinline__ void rw_load_at(RandWindow<RW>& r, const float* __restrict__ rand,
+                                           int64_t base) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4* p = reinterpret_cast<const f32x4*>(rand + base);
+#pragma unroll
+    for (int i = 0; i < RW / 4; ++i) {
+        const f32x4 x = __builtin_nontemporal_load(p + i);
+        r.w[4 * i] = x.x;
+        r.w[4 * i + 1] = x.y;
+        r.w[4 * i + 2] = x.z;
+        r.w[4 * i + 3] = x.w;
+    }
+}
+
+template <int RW>
+__device__ __forceinline__ void rw_shift_by(RandWindow<RW>& r, int k) {
+#pragma unroll
+    for (int bit = RW / 2; bit >= 1; bit >>= 1) {
+        if (k & bit) {
+#pragma unroll
+            for (int i = 0; i < RW; ++i) r.w[i] = (i + bit < RW) ? r.w[i + bit] : 0.0f;
+        }
+    }
+}
+
+// Start records: walk n's start node in the edge-record format, so a slot
+// beginning a walk and a slot taking a step both issue the same single 16-byte
+// read.  Written by walk_init_kernel (one coalesced pass over start).
+__global__ __launch_bounds__(kBlock) void walk_init_kernel(const int64_t* __restrict__ rowptr,
+                                                           const int64_t* __restrict__ start,
+                                                           int64_t num_nodes, int64_t num_edges,
+                                                           int64_t num_walks,
+                                                           EdgeRecord* __restrict__ init) {
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; n < num_walks;
+         n += stride) {
+        const int64_t v = start[n];
+        i32x4 r = {static_cast<int32_t>(v), 0, kRecBadNode, 0};
+        if (node_ok(v, num_nodes)) {
+            const RowBounds rb = load_row(rowptr, v);
+            if (row_ok(rb, num_edges)) {
+                r.y = static_cast<int32_t>(rb.begin);
+                r.z = static_cast<int32_t>(rb.end - rb.begin);
+            } else {
+                r.z = kRecBadRow;
+            }
+        }
+        *reinterpret_cast<i32x4*>(init + n) = r;
+    }
+}
+
+// Slot phases of the record walk.
+enum : int {
+    kSlotIdle = 0,   // wants a walk id
+    kSlotStart = 1,  // reads the start record of walk n (and its first rand block)
+    kSlotWalk = 2,   // reads the record of the chosen edge
+    kSlotDone = 3,   // the queue is exhausted
+};
+
+// Uniform walk over edge records (requires 16-byte aligned rand and n_out,
+// num_nodes and num_edges below 2^31, num_walks * walk_length a multiple of
+// 4 and at least RW; no edge output).
+//
+// Loop invariant: every live slot issues exactly one dependent 16-byte read
+// per iteration (a start record or an edge record), plus at most one
+// independent rand block, and the wave waits once.  The rand value for a step
+// is taken from the window in the iteration before the read it addresses, so
+// a new rand block always travels together with a record read and never costs
+// a round trip of its own.  Output stores issued after the wait overlap the
+// next iteration's read.
+template <int W, int RW>
+__global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
+                                                                  const EdgeRecord* __restrict__ recs,
+                                                                  const EdgeRecord* __restrict__ init) {
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const int64_t L = a.walk_length;
+    const int64_t L1 = L + 1;
+    const int64_t N = a.num_walks;
+    const int64_t rtotal = N * L;
+    unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.work + 1);
+    WaveQueue q{0, 0};
+    int phase[W];
+    int64_t n[W], l[W], e[W];  // e: record index read this iteration (kSlotWalk)
+    int64_t fr[W];             // rand index whose block the next read brings along
+    bool need_block[W];        // ... if set
+    RandWindow<RW> rw[W];
+    OutWin<int32_t> ow[W];
+    uint32_t status = 0;
+
+#pragma unroll
+    for (int s = 0; s < W; ++s) {
+        phase[s] = kSlotIdle;
+        n[s] = 0;
+        l[s] = 0;
+        e[s] = 0;
+        fr[s] = 0;
+        need_block[s] = false;
+        rw[s].valid = 0;
+        ow[s].count = 0;
+    }
+
+    while (true) {
+        // 1. One record read per live slot (idle slots read init[0], so the
+        // load is unconditional and nothing merges with it before the wait in
+        // step 3), and the rand blocks due.
+        int ph[W];  // phase at issue: only these slots consume in step 3
+        i32x4 rec[W];
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            ph[s] = phase[s];
+            const EdgeRecord* p = ph[s] == kSlotStart ? init + n[s]
+                                  : ph[s] == kSlotWalk ? recs + e[s]
+                                                       : init;
+            rec[s] = *reinterpret_cast<const i32x4*>(p);
+        }
+#pragma unroll
+        for (int s = 0; s < W; ++s)
+            if (need_block[s]) rw_load_at(rw[s], a.rand, rw_block_base<RW>(fr[s], rtotal));
+
+        // 2. While the reads are in flight, idle slots draw walk ids from the
+        // wave queue; they issue their start reads next iteration.
+        bool alive = false;
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            const bool need = phase[s] == kSlotIdle;
+            const int64_t id = queue_take(q, need, counter);
+            if (need) {
+                n[s] = id;
+                l[s] = 0;
+                phase[s] = id < N ? kSlotStart : kSlotDone;
+                fr[s] = id * L;  // the first step's uniform
+            }
+            alive |= phase[s] != kSlotDone;
+        }
+        if (!__any(alive)) break;  // every slot done: nothing was read above
+
+        // 3. Consume: buffer the node, finish or pick the next edge.
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            if (ph[s] != kSlotStart && ph[s] != kSlotWalk) {
+                // a slot that just drew a walk reads its start record and
+                // first rand block next iteration
+                need_block[s] = phase[s] == kSlotStart && L > 0;
+                continue;
+            }
+            const int64_t g0 = n[s] * L1;  // output index of the walk's start node
+            const int64_t g = g0 + l[s] + (ph[s] == kSlotWalk ? 1 : 0);
+            if (need_block[s]) {
+                // block holding rand[fr]: shift it so w[0] is that value
+                const int k = static_cast<int>(fr[s] - rw_block_base<RW>(fr[s], rtotal));
+                rw_shift_by(rw[s], k);
+                rw[s].valid = RW - k;
+                need_block[s] = false;
+            }
+            const int32_t node = rec[s].x, begin = rec[s].y, deg = rec[s].z;
+            bool fill = false, flush = false;
+            if (deg < 0) {
+                // malformed start or graph entry: stop (outputs unspecified)
+                status |= deg == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
+                if (ph[s] == kSlotStart) ow[s].count = 0;
+                ow_fill(ow[s], a.n_out, g, g0 + L, node);
+                phase[s] = kSlotIdle;
+                continue;
+            }
+            if (ph[s] == kSlotStart) ow[s].count = 0;
+            ow_push(ow[s], a.n_out, g, node);
+            if (ph[s] == kSlotWalk) l[s] += 1;
+            if (l[s] == L) flush = true;
+            else if (deg == 0) fill = true;  // absorbing node: the walk stays
+            if (fill) {
+                ow_fill(ow[s], a.n_out, g + 1, g0 + L, node);
+            } else if (flush) {
+                if (ow[s].count) ow_flush(ow[s], a.n_out, g);
+            } else {
+                // step l (0-based) leaves this node with uniform rand[n*L + l]
+                e[s] = begin + pick_index(rw[s].w[0], deg);
+                rw_shift1(rw[s]);
+                rw[s].valid -= 1;
+                need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
+                fr[s] = n[s] * L + l[s] + 1;
+                phase[s] = kSlotWalk;
+            }
+            if (fill || flush) phase[s] = kSlotIdle;
         }
     }
     if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
@@ -753,12 +1026,16 @@ int persistent_grid(Kernel kernel, int64_t num_walks, int walks_per_lane, int& g
 
 int check_common(const int64_t* rowptr, int64_t num_nodes, const int64_t* col, int64_t num_edges,
                  const int64_t* start, int64_t num_walks, int32_t walk_length,
-                 const int64_t* n_out, const int64_t* work) {
+                 const int64_t* n_out, const void* work, size_t work_bytes) {
     if (num_nodes < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_nodes must be >= 0");
     if (num_edges < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_edges must be >= 0");
     if (num_walks < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_walks must be >= 0");
     if (walk_length < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "walk_length must be >= 0");
-    if (!work) return fail(MLXC_ERR_INVALID_ARGUMENT, "work must not be NULL");
+    if (!work) return fail(MLXC_ERR_INVALID_ARGUMENT, "workspace must not be NULL");
+    if (work_bytes < MLXC_WORK_WORDS * sizeof(int64_t))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "workspace must hold at least MLXC_WORK_WORDS int64 words");
+    if (reinterpret_cast<uintptr_t>(work) % 16 != 0)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
     if (num_walks > 0) {
         if (!rowptr || !start || !n_out)
             return fail(MLXC_ERR_INVALID_ARGUMENT, "rowptr, start and n_out must not be NULL");
@@ -776,7 +1053,7 @@ int zero_work(int64_t* d_work, hipStream_t stream) {
 }
 
 #ifndef MLXC_UNIFORM_SLOTS
-#define MLXC_UNIFORM_SLOTS 2   // walks in flight per lane
+#define MLXC_UNIFORM_SLOTS 1   // walks in flight per lane
 #endif
 #ifndef MLXC_RAND_WINDOW
 #define MLXC_RAND_WINDOW 16    // uniforms per rand block (4-byte floats)
@@ -791,12 +1068,51 @@ int launch_persistent(Kernel kernel, const WalkArgs& a, int slots, hipStream_t s
     return MLXC_OK;
 }
 
-int launch_uniform(const WalkArgs& a, hipStream_t stream) {
+bool records_fit(int64_t num_nodes, int64_t num_edges) {
+    return num_nodes <= INT32_MAX && num_edges <= INT32_MAX;
+}
+
+size_t record_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks) {
+    if (!records_fit(num_nodes, num_edges) || num_walks < 0)
+        return MLXC_WORK_WORDS * sizeof(int64_t);
+    return kRecordOffset + static_cast<size_t>(num_edges + num_walks) * sizeof(EdgeRecord);
+}
+
+int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes,
+                   hipStream_t stream) {
     constexpr int W = MLXC_UNIFORM_SLOTS;
     const bool aligned = (reinterpret_cast<uintptr_t>(a.rand) % 16 == 0) &&
                          (reinterpret_cast<uintptr_t>(a.n_out) % 16 == 0);
     if (a.e_out) return launch_persistent(uniform_walk_kernel<W, true>, a, W, stream);
     if (!aligned) return launch_persistent(uniform_walk_kernel<W, false>, a, W, stream);
+    const int64_t rtotal = a.num_walks * a.walk_length;
+    if (records_fit(a.num_nodes, a.num_edges) && rtotal % 4 == 0 && rtotal >= MLXC_RAND_WINDOW &&
+        workspace_bytes >= record_workspace_bytes(a.num_nodes, a.num_edges, a.num_walks)) {
+        EdgeRecord* recs = reinterpret_cast<EdgeRecord*>(static_cast<char*>(workspace) + kRecordOffset);
+        EdgeRecord* init = recs + a.num_edges;
+        DeviceInfo info;
+        if (int rc = device_info(info)) return rc;
+        const int64_t cap = static_cast<int64_t>(info.cus) * 16;
+        if (a.num_edges > 0) {
+            int64_t grid = (a.num_edges + kBlock - 1) / kBlock;
+            if (grid > cap) grid = cap;
+            hipLaunchKernelGGL(edge_record_kernel, dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0,
+                               stream, a.rowptr, a.col, a.num_nodes, a.num_edges, recs);
+            MLXC_HIP_TRY(hipGetLastError());
+        }
+        int64_t igrid = (a.num_walks + kBlock - 1) / kBlock;
+        if (igrid > cap) igrid = cap;
+        hipLaunchKernelGGL(walk_init_kernel, dim3(static_cast<unsigned>(igrid)), dim3(kBlock), 0,
+                           stream, a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks, init);
+        MLXC_HIP_TRY(hipGetLastError());
+        auto kernel = uniform_walk_rec_kernel<W, MLXC_RAND_WINDOW>;
+        int grid = 0;
+        if (int rc = persistent_grid(kernel, a.num_walks, W, grid)) return rc;
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a,
+                           static_cast<const EdgeRecord*>(recs), static_cast<const EdgeRecord*>(init));
+        MLXC_HIP_TRY(hipGetLastError());
+        return MLXC_OK;
+    }
     return launch_persistent(uniform_walk_win_kernel<W, MLXC_RAND_WINDOW>, a, W, stream);
 }
 
@@ -829,13 +1145,19 @@ int mlxc_version(void) { return 100; }
 
 const char* mlxc_last_error(void) { return g_last_error.c_str(); }
 
+size_t mlxc_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks) {
+    if (num_nodes < 0 || num_edges < 0) return MLXC_WORK_WORDS * sizeof(int64_t);
+    return record_workspace_bytes(num_nodes, num_edges, num_walks);
+}
+
 int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
                      int64_t num_edges, const int64_t* d_start, int64_t num_walks,
                      const float* d_rand, int32_t walk_length, int64_t* d_n_out,
-                     int64_t* d_e_out, int64_t* d_work, void* stream) {
+                     int64_t* d_e_out, void* d_workspace, size_t workspace_bytes, void* stream) {
     if (int rc = check_common(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
-                              walk_length, d_n_out, d_work))
+                              walk_length, d_n_out, d_workspace, workspace_bytes))
         return rc;
+    int64_t* d_work = static_cast<int64_t*>(d_workspace);
     if (num_walks > 0 && walk_length > 0 && !d_rand)
         return fail(MLXC_ERR_INVALID_ARGUMENT, "rand must not be NULL");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -843,17 +1165,19 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* 
     if (num_walks == 0) return MLXC_OK;
     WalkArgs a{d_rowptr, d_col, d_start, d_rand, d_n_out, d_e_out, d_work,
                num_nodes, num_edges, num_walks, walk_length};
-    return launch_uniform(a, s);
+    return launch_uniform(a, d_workspace, workspace_bytes, s);
 }
 
 int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
                             int64_t num_edges, const int64_t* d_start, int64_t num_walks,
                             int32_t walk_length, double p, double q, uint64_t seed,
                             int32_t rule, int32_t rows_sorted, int64_t* d_n_out,
-                            int64_t* d_e_out, int64_t* d_work, void* stream) {
+                            int64_t* d_e_out, void* d_workspace, size_t workspace_bytes,
+                            void* stream) {
     if (int rc = check_common(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
-                              walk_length, d_n_out, d_work))
+                              walk_length, d_n_out, d_workspace, workspace_bytes))
         return rc;
+    int64_t* d_work = static_cast<int64_t*>(d_workspace);
     if (!(p > 0.0) || !(q > 0.0) || !std::isfinite(p) || !std::isfinite(q))
         return fail(MLXC_ERR_INVALID_ARGUMENT, "p and q must be finite and > 0");
     if (rule != MLXC_RULE_REF_CHAIN && rule != MLXC_RULE_NODE2VEC_EXACT)
@@ -878,11 +1202,15 @@ int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const in
 }
 
 int mlxc_csr_check(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
-                   int64_t num_edges, int64_t* d_work, int32_t* h_flags, void* stream) {
+                   int64_t num_edges, void* d_workspace, size_t workspace_bytes, int32_t* h_flags,
+                   void* stream) {
     if (num_nodes < 0 || num_edges < 0)
         return fail(MLXC_ERR_INVALID_ARGUMENT, "num_nodes and num_edges must be >= 0");
-    if (!d_rowptr || !d_work || !h_flags || (num_edges > 0 && !d_col))
+    if (!d_rowptr || !d_workspace || !h_flags || (num_edges > 0 && !d_col))
         return fail(MLXC_ERR_INVALID_ARGUMENT, "NULL pointer argument");
+    if (workspace_bytes < MLXC_WORK_WORDS * sizeof(int64_t))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "workspace must hold at least MLXC_WORK_WORDS int64 words");
+    int64_t* d_work = static_cast<int64_t*>(d_workspace);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (int rc = zero_work(d_work, s)) return rc;
     DeviceInfo info;

@@ -106,6 +106,12 @@ def _walk_length(walk_length) -> int:
     return walk_length
 
 
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Device workspace of at least nbytes (int64 words, so 16-byte aligned
+    from torch's allocator); torch's caching allocator recycles it."""
+    return torch.empty((int(nbytes) + 7) // 8, dtype=torch.int64, device=device)
+
+
 def _raise_status(work: torch.Tensor, stream, what: str) -> None:
     if isinstance(stream, torch.cuda.Stream):
         stream.synchronize()  # the kernel ran there, not on torch's current stream
@@ -162,12 +168,13 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike, rand: Te
     rowptr, col, start, rand = (_on(t, device) for t in (rowptr, col, start, rand))
     n_out = torch.empty((N, L + 1), dtype=torch.int64, device=device)
     e_out = torch.empty((N, L), dtype=torch.int64, device=device) if return_edges else None
-    work = torch.empty(_lib.MLXC_WORK_WORDS, dtype=torch.int64, device=device)
     lib = _lib.load()
+    work = _workspace(lib.mlxc_walk_workspace_bytes(rowptr.numel() - 1, col.numel(), N), device)
     with torch.cuda.device(device):
         rc = lib.mlxc_random_walk(_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(),
                                   _ptr(start), N, _ptr(rand), L, _ptr(n_out),
-                                  _ptr(e_out) if return_edges else None, work.data_ptr(), handle)
+                                  _ptr(e_out) if return_edges else None, work.data_ptr(),
+                                  work.numel() * 8, handle)
     _lib.check(rc, "random_walk")
     if check:
         _raise_status(work, stream, "random_walk")
@@ -181,11 +188,12 @@ def csr_check(rowptr: TensorLike, col: TensorLike, *, stream=None) -> int:
     device = _resolve_device(stream, (rowptr, col))
     handle = _stream_handle(stream, device)
     rowptr, col = _on(rowptr, device), _on(col, device)
-    work = torch.empty(_lib.MLXC_WORK_WORDS, dtype=torch.int64, device=device)
+    work = _workspace(_lib.MLXC_WORK_WORDS * 8, device)
     flags = _lib.ctypes.c_int32(0)
     with torch.cuda.device(device):
         rc = _lib.load().mlxc_csr_check(_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(),
-                                        work.data_ptr(), _lib.ctypes.addressof(flags), handle)
+                                        work.data_ptr(), work.numel() * 8,
+                                        _lib.ctypes.addressof(flags), handle)
     _lib.check(rc, "csr_check")
     return int(flags.value)
 
@@ -243,12 +251,12 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     N = start.numel()
     n_out = torch.empty((N, L + 1), dtype=torch.int64, device=device)
     e_out = torch.empty((N, L), dtype=torch.int64, device=device) if return_edges else None
-    work = torch.empty(_lib.MLXC_WORK_WORDS, dtype=torch.int64, device=device)
+    work = _workspace(_lib.MLXC_WORK_WORDS * 8, device)
     with torch.cuda.device(device):
         rc = _lib.load().mlxc_rejection_sampling(
             _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,
             p, q, seed, _RULES[rule], 1 if rows_sorted else 0, _ptr(n_out),
-            _ptr(e_out) if return_edges else None, work.data_ptr(), handle)
+            _ptr(e_out) if return_edges else None, work.data_ptr(), work.numel() * 8, handle)
     _lib.check(rc, "rejection_sampling")
     if check:
         _raise_status(work, stream, "rejection_sampling")

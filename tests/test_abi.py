@@ -52,15 +52,21 @@ def test_version():
 FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
 
 
+WS = 64  # workspace bytes passed with FAKE
+
+
 @pytest.mark.parametrize("args,msg", [
-    ((FAKE, -1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, FAKE, None), "num_nodes"),
-    ((FAKE, 1, FAKE, -1, FAKE, 1, FAKE, 1, FAKE, None, FAKE, None), "num_edges"),
-    ((FAKE, 1, FAKE, 0, FAKE, -1, FAKE, 1, FAKE, None, FAKE, None), "num_walks"),
-    ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, -2, FAKE, None, FAKE, None), "walk_length"),
-    ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, None, None), "work"),
-    ((None, 1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, FAKE, None), "NULL"),
-    ((FAKE, 1, FAKE, 0, FAKE, 1, None, 3, FAKE, None, FAKE, None), "rand"),
-    ((FAKE, 1, FAKE, 0, FAKE, 2**62, FAKE, 8, FAKE, None, FAKE, None), "overflows"),
+    ((FAKE, -1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, FAKE, WS, None), "num_nodes"),
+    ((FAKE, 1, FAKE, -1, FAKE, 1, FAKE, 1, FAKE, None, FAKE, WS, None), "num_edges"),
+    ((FAKE, 1, FAKE, 0, FAKE, -1, FAKE, 1, FAKE, None, FAKE, WS, None), "num_walks"),
+    ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, -2, FAKE, None, FAKE, WS, None), "walk_length"),
+    ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, None, WS, None), "workspace"),
+    ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, FAKE, 16, None), "MLXC_WORK_WORDS"),
+    ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, ctypes.c_void_p(0x1008), WS, None),
+     "aligned"),
+    ((None, 1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, FAKE, WS, None), "NULL"),
+    ((FAKE, 1, FAKE, 0, FAKE, 1, None, 3, FAKE, None, FAKE, WS, None), "rand"),
+    ((FAKE, 1, FAKE, 0, FAKE, 2**62, FAKE, 8, FAKE, None, FAKE, WS, None), "overflows"),
 ])
 def test_random_walk_rejects_bad_arguments(args, msg):
     lib = _lib.load()
@@ -75,7 +81,7 @@ def test_random_walk_rejects_bad_arguments(args, msg):
 def test_rejection_sampling_rejects_bad_arguments(p, q, rule, msg):
     lib = _lib.load()
     rc = lib.mlxc_rejection_sampling(FAKE, 1, FAKE, 0, FAKE, 0, 3, p, q, 1, rule, 1, FAKE, None,
-                                     FAKE, None)
+                                     FAKE, WS, None)
     assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT
     assert msg in _lib.last_error()
 
@@ -85,10 +91,22 @@ def test_other_entry_points_reject_bad_arguments():
     assert lib.mlxc_philox_uniform(FAKE, -1, 0, None) == _lib.MLXC_ERR_INVALID_ARGUMENT
     assert lib.mlxc_philox_uniform(None, 0, 0, None) == _lib.MLXC_OK  # empty is a no-op
     flags = ctypes.c_int32(0)
-    assert lib.mlxc_csr_check(FAKE, -1, FAKE, 0, FAKE, ctypes.addressof(flags), None) \
+    assert lib.mlxc_csr_check(FAKE, -1, FAKE, 0, FAKE, WS, ctypes.addressof(flags), None) \
         == _lib.MLXC_ERR_INVALID_ARGUMENT
-    assert lib.mlxc_csr_check(FAKE, 1, FAKE, 0, FAKE, None, None) \
+    assert lib.mlxc_csr_check(FAKE, 1, FAKE, 0, FAKE, WS, None, None) \
         == _lib.MLXC_ERR_INVALID_ARGUMENT
+    assert lib.mlxc_csr_check(FAKE, 1, FAKE, 0, FAKE, 8, ctypes.addressof(flags), None) \
+        == _lib.MLXC_ERR_INVALID_ARGUMENT
+
+
+def test_workspace_size_query():
+    lib = _lib.load()
+    assert lib.mlxc_walk_workspace_bytes(10, 100, 7) == 256 + 16 * 107
+    assert lib.mlxc_walk_workspace_bytes(10, 0, 0) == 256
+    assert lib.mlxc_walk_workspace_bytes(2**31, 5, 1) == 32
+    assert lib.mlxc_walk_workspace_bytes(5, 2**31, 1) == 32
+    assert lib.mlxc_walk_workspace_bytes(-1, 5, 1) == 32
+    assert lib.mlxc_walk_workspace_bytes(5, 5, -1) == 32
 
 
 def test_python_check_maps_codes():

@@ -160,3 +160,50 @@ def test_c2_full_size_properties(cuda):
                                           rand[sample].cpu().numpy(), L)
     assert st == 0
     np.testing.assert_array_equal(n[sample].cpu().numpy(), n_ref)
+
+
+def _abi_walk(rowptr, col, start, rand_t, L, n_out_t, *, e_out=None, ws_bytes=None):
+    """Calls mlxc_random_walk directly so each kernel path can be selected:
+    edge records (full workspace), CSR reads (minimal workspace), and the
+    unwindowed kernel (edge output or unaligned buffers)."""
+    from mlx_cluster_amd import _lib
+    lib = _lib.load()
+    V, E = rowptr.numel() - 1, col.numel()
+    if ws_bytes is None:
+        ws_bytes = lib.mlxc_walk_workspace_bytes(V, E, start.numel())
+    ws = torch.empty((ws_bytes + 7) // 8, dtype=torch.int64, device=rowptr.device)
+    rc = lib.mlxc_random_walk(rowptr.data_ptr(), V, col.data_ptr(), E, start.data_ptr(),
+                              start.numel(), rand_t, L, n_out_t,
+                              None if e_out is None else e_out.data_ptr(), ws.data_ptr(),
+                              ws_bytes, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    assert int(ws[0].item()) == 0
+
+
+@pytest.mark.parametrize("N,L", [(1, 1), (33, 5), (1000, 16), (4097, 23), (20_000, 80)])
+def test_all_kernel_paths_agree(N, L, cuda):
+    rowptr, col = synth.rmat_csr(12, 30_000, seed=N, device=cuda)
+    V = rowptr.numel() - 1
+    start = (torch.arange(N, device=cuda) * 131) % V
+    rand = mc.philox_uniform(N * L + 1, 17, device=cuda)
+    ref, _, st, _ = oracle.uniform_walk(rowptr.cpu().numpy(), col.cpu().numpy(),
+                                        start.cpu().numpy(), rand[:N * L].cpu().numpy(), L)
+    assert st == 0
+    outs = {}
+    for name, kw in [("records", {}), ("csr", dict(ws_bytes=32))]:
+        out = torch.full((N, L + 1), -7, dtype=torch.int64, device=cuda)
+        _abi_walk(rowptr, col, start, rand.data_ptr(), L, out.data_ptr(), **kw)
+        outs[name] = out
+    e = torch.empty((N, L), dtype=torch.int64, device=cuda)
+    out = torch.full((N, L + 1), -7, dtype=torch.int64, device=cuda)
+    _abi_walk(rowptr, col, start, rand.data_ptr(), L, out.data_ptr(), e_out=e)
+    outs["edges"] = out
+    # unaligned rand (4-byte offset) and unaligned n_out (8-byte offset)
+    rand_u = mc.philox_uniform(N * L + 1, 0, device=cuda)
+    rand_u[1:] = rand[:N * L]
+    big = torch.full((N * (L + 1) + 1,), -7, dtype=torch.int64, device=cuda)
+    _abi_walk(rowptr, col, start, rand_u.data_ptr() + 4, L, big.data_ptr() + 8)
+    outs["unaligned"] = big[1:].view(N, L + 1)
+    for name, o in outs.items():
+        np.testing.assert_array_equal(o.cpu().numpy(), ref, err_msg=name)
