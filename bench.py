@@ -45,8 +45,12 @@ def log(*a):
 
 
 def kernel_source_hash() -> str:
-    path = os.path.join(REPO, "mlx_cluster_amd", "csrc", "mlxc_walk.hip")
-    return hashlib.sha256(open(path, "rb").read()).hexdigest()[:16]
+    """sha256[:16] over every source file of libmlxc.so."""
+    from mlx_cluster_amd.build_lib import source_files
+    h = hashlib.sha256()
+    for path in source_files():
+        h.update(open(path, "rb").read())
+    return h.hexdigest()[:16]
 
 
 def traffic_from_profile(name: str):
@@ -123,6 +127,38 @@ def gather_ceiling(torch, dev):
         log(f"gather table {mib} MiB: {ms:.3f} ms, {lines:.3e} gathers/s")
         del table, idx, out
     return {"gather_ceiling": res}
+
+
+def node2vec_bytes(np, oracle, rowptr_h, col_h, start_h, L, extra, walks=200_000):
+    """SURVEY 8(d) node2vec bytes, 64*(S_move+Z) + 64*T + 64*(Q+P) + 8*N*(L+1) + 8*N, with
+    the counts from the oracle over an evenly strided sample of walks scaled to N."""
+    N = start_h.shape[0]
+    idx = np.linspace(0, N - 1, min(N, walks)).astype(np.int64)
+    _, _, st, c = oracle.node2vec_walk(rowptr_h, col_h, start_h[idx], L, extra["p"], extra["q"],
+                                       extra["seed"], rule=0, rows_sorted=True)
+    f = N / idx.size
+    S, Z, T = c["moving_steps"] * f, c["sink_walks"] * f, c["trials"] * f
+    Q, P = c["member_tests"] * f, c["member_lines"] * f
+    b = LINE * (S + Z) + LINE * T + LINE * (Q + P) + 8 * N * (L + 1) + 8 * N
+    return int(b), dict(moving_steps=int(S), sink_walks=int(Z), trials=int(T),
+                        member_tests=int(Q), member_lines=int(P), counts_sample_walks=int(idx.size),
+                        bytes_formula="64*(S+Z) + 64*T + 64*(Q+P) + 8*N*(L+1) + 8*N")
+
+
+def cpu_baseline_node2vec(np, oracle, rowptr_h, col_h, start, L, extra, target_s=12.0):
+    N = start.shape[0]
+    probe = min(N, 5_000)
+    idx = np.linspace(0, N - 1, probe).astype(np.int64)
+    t0 = time.perf_counter()
+    oracle.node2vec_walk_libc(rowptr_h, col_h, start[idx], L, extra["p"], extra["q"], 1)
+    rate = probe * L / (time.perf_counter() - t0)
+    walks = int(min(N, max(probe, target_s * rate / L)))
+    idx = np.linspace(0, N - 1, walks).astype(np.int64)
+    t0 = time.perf_counter()
+    _, st = oracle.node2vec_walk_libc(rowptr_h, col_h, start[idx], L, extra["p"], extra["q"], 1)
+    dt = time.perf_counter() - t0
+    assert st == 0
+    return walks * L / dt, walks, dt
 
 
 def main():
@@ -207,6 +243,11 @@ def main():
     value = steps_per_launch / (ms_per_step / 1e3)
     log(f"{ms_per_step:.3f} ms/step wall, {kernel_ms:.3f} ms/launch (events)")
 
+    import oracle
+    rowptr_h, col_h = rowptr.cpu().numpy(), col.cpu().numpy()
+    g = torch.Generator().manual_seed(1)
+    sample = torch.randint(0, N, (2000,), generator=g).to(dev)
+
     # Algorithmic bytes of one launch: one 64-B line per dependent random
     # read of the reference loop (rowptr pair and col, RandomWalk.cpp:45-54),
     # streams at their byte count.  M = steps from a node with deg > 0,
@@ -217,8 +258,10 @@ def main():
         units = dict(moving_steps=M, sink_walks=Z,
                      bytes_formula="64*(M+Z) + 64*M + 4*M + 8*N*(L+1) + 8*N")
     else:
-        roof_bytes = None
-        units = {}
+        # node2vec: the work depends on rejections, so it is counted by the
+        # oracle on an evenly strided sample of walks and scaled to N.
+        roof_bytes, units = node2vec_bytes(np, oracle, rowptr_h, col_h, start.cpu().numpy(), L,
+                                           extra)
     achieved = roof_bytes / (kernel_ms / 1e3) / 1e9 if roof_bytes else None
     traffic = traffic_from_profile(f"{kind}_walk_{args.config}")
     roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -228,16 +271,19 @@ def main():
                 **units}
 
     # Sampled bit-exact parity against the oracle, and the CPU baseline.
-    import oracle
-    rowptr_h, col_h = rowptr.cpu().numpy(), col.cpu().numpy()
-    g = torch.Generator().manual_seed(1)
-    sample = torch.randint(0, N, (2000,), generator=g).to(dev)
     if kind == "uniform":
         ref, _, st, _ = oracle.uniform_walk(rowptr_h, col_h, start[sample].cpu().numpy(),
                                             rand[sample].cpu().numpy(), L)
+        got = out[sample].cpu().numpy()
     else:
-        ref = None
-    parity = None if ref is None else bool(np.array_equal(out[sample].cpu().numpy(), ref))
+        # walk ids index the Philox stream: check a contiguous block of
+        # walks [s0, s0 + 2000) with the oracle told its first walk id
+        s0 = int(sample[0].item()) % max(1, N - 2000)
+        ref, _, st, _ = oracle.node2vec_walk(rowptr_h, col_h, start[s0:s0 + 2000].cpu().numpy(),
+                                             L, extra["p"], extra["q"], extra["seed"], rule=0,
+                                             rows_sorted=True, first_walk=s0)
+        got = out[s0:s0 + 2000].cpu().numpy()
+    parity = bool(st == 0 and np.array_equal(got, ref))
     cpu = None
     if not args.no_cpu_baseline and kind == "uniform":
         rate, walks, dt = cpu_baseline_uniform(np, oracle, rowptr_h, col_h, start.cpu().numpy(),
@@ -245,6 +291,14 @@ def main():
         cpu = {"value": rate, "unit": "walk-steps/s", "cores": 1, "kind": "port",
                "sample": f"{walks} of {N} walks (evenly strided) x {L} steps, {dt:.1f} s, "
                          f"oracle/walk_oracle.c uniform walk, 1 thread"}
+        log(f"cpu baseline {rate:.3e} steps/s over {walks} walks")
+    elif not args.no_cpu_baseline:
+        rate, walks, dt = cpu_baseline_node2vec(np, oracle, rowptr_h, col_h, start.cpu().numpy(),
+                                                L, extra, args.cpu_seconds)
+        cpu = {"value": rate, "unit": "walk-steps/s", "cores": 1, "kind": "port",
+               "sample": f"{walks} of {N} walks (evenly strided) x {L} steps, {dt:.1f} s, "
+                         f"oracle/walk_oracle.c node2vec walk with libc rand() and linear "
+                         f"is_neighbor scans as in the reference, 1 thread"}
         log(f"cpu baseline {rate:.3e} steps/s over {walks} walks")
 
     line = {

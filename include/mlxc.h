@@ -32,12 +32,11 @@ extern "C" {
  * call zeroes the first MLXC_WORK_WORDS words on `stream` before its kernels
  * run; after the call has completed, word 0 holds the MLXC_STATUS_* bits of
  * that call (the other words are internal: the walk-queue counter).  A
- * workspace of mlxc_walk_workspace_bytes(num_nodes, num_edges, num_walks)
- * bytes also holds a per-call copy of the graph laid out as 16-byte edge
- * records (target node, target row begin, target degree) and one such record
- * per walk start, which lets the uniform walk take one dependent read per
- * step instead of two; with a smaller workspace the walk reads the CSR arrays
- * directly.  Same results either way. */
+ * workspace of the size the *_workspace_bytes queries return also holds
+ * per-call layouts of the graph and the starts (16-byte records: node, row
+ * begin, row degree) that cut the dependent reads per step; with a smaller
+ * workspace the kernels read the CSR arrays directly.  Same results either
+ * way. */
 #define MLXC_WORK_WORDS 4
 
 /* Bits a walk kernel ORs into workspace word 0 when the graph or the starts
@@ -67,13 +66,19 @@ int mlxc_version(void);
 /* Message of the calling thread's most recent failed call ("" if none). */
 const char* mlxc_last_error(void);
 
-/* Workspace bytes that enable the edge-record layout for num_walks walks
- * over a graph with num_nodes nodes and num_edges CSR entries:
- * 256 + 16 * (num_edges + num_walks) when num_nodes and num_edges are below
- * 2^31, else the minimum MLXC_WORK_WORDS * 8.  No reference counterpart (the
- * reference allocates its outputs inside eval, RandomWalk.cpp:28-29, and uses
- * no scratch). */
-size_t mlxc_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks);
+/* Workspace bytes that let mlxc_random_walk use its fastest layout for this
+ * call: 256 + 16 * (num_edges + num_walks) when the call takes at least
+ * 4 * num_edges steps (per-call edge records), else 256 + 16 * num_walks
+ * (start records only); MLXC_WORK_WORDS * 8 when num_nodes or num_edges is
+ * 2^31 or more.  No reference counterpart (the reference allocates inside
+ * eval, RandomWalk.cpp:28-29). */
+size_t mlxc_random_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges,
+                                        int64_t num_walks, int32_t walk_length);
+
+/* Workspace bytes for mlxc_rejection_sampling's fastest layout (same
+ * conventions).  No reference counterpart. */
+size_t mlxc_rejection_sampling_workspace_bytes(int64_t num_nodes, int64_t num_edges,
+                                               int64_t num_walks, int32_t walk_length);
 
 /*
  * Uniform random walk.

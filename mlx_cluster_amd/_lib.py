@@ -40,7 +40,8 @@ _size = ctypes.c_size_t
 SIGNATURES = {
     "mlxc_version": (ctypes.c_int, []),
     "mlxc_last_error": (ctypes.c_char_p, []),
-    "mlxc_walk_workspace_bytes": (_size, [_i64, _i64, _i64]),
+    "mlxc_random_walk_workspace_bytes": (_size, [_i64, _i64, _i64, _i32]),
+    "mlxc_rejection_sampling_workspace_bytes": (_size, [_i64, _i64, _i64, _i32]),
     "mlxc_random_walk": (
         ctypes.c_int,
         [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _ptr, _size, _ptr],

@@ -10,7 +10,9 @@ import sys
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
-SRC = os.path.join(PKG_DIR, "csrc", "mlxc_walk.hip")
+CSRC = os.path.join(PKG_DIR, "csrc")
+SOURCES = [os.path.join(CSRC, f) for f in
+           ("mlxc_api.hip", "prep_kernels.hip", "uniform_walk.hip", "node2vec_walk.hip")]
 OUT = os.path.join(PKG_DIR, "libmlxc.so")
 INCLUDE = os.path.join(REPO_DIR, "include")
 
@@ -34,7 +36,8 @@ FLAGS = [
 
 
 def build(verbose: bool = False, extra_flags: list[str] | None = None, out: str = OUT) -> str:
-    cmd = [HIPCC, *FLAGS, *(extra_flags or []), "-I", INCLUDE, SRC, "-o", out + ".tmp"]
+    cmd = [HIPCC, *FLAGS, *(extra_flags or []), "-I", INCLUDE, "-I", CSRC, *SOURCES,
+           "-o", out + ".tmp"]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -43,6 +46,12 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, out: str 
         raise RuntimeError(f"hipcc failed building {out}")
     os.replace(out + ".tmp", out)
     return out
+
+
+def source_files() -> list[str]:
+    """Every file the library is built from (kernels, headers, C ABI)."""
+    return sorted([os.path.join(CSRC, f) for f in os.listdir(CSRC)] +
+                  [os.path.join(INCLUDE, "mlxc.h")])
 
 
 if __name__ == "__main__":

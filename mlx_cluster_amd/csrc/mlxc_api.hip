@@ -1,0 +1,169 @@
+// The C ABI of libmlxc.so (include/mlxc.h): argument validation, workspace
+// reset and dispatch to the kernel launchers.  Every entry point checks its
+// arguments on the host before touching the device and reports failures as
+// a negative code plus a thread-local message.
+#include <climits>
+#include <cmath>
+#include <mutex>
+#include <string>
+
+#include "walk_host.h"
+
+namespace mlxc {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int device_info(DeviceInfo& info) {
+    static std::mutex mu;
+    static DeviceInfo cache[64];
+    int dev = 0;
+    MLXC_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return fail(MLXC_ERR_HIP, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (cache[dev].cus == 0) {
+        int cus = 0;
+        MLXC_HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        cache[dev].cus = cus;
+    }
+    info = cache[dev];
+    return MLXC_OK;
+}
+
+namespace {
+
+int check_workspace(const void* work, size_t work_bytes) {
+    if (!work) return fail(MLXC_ERR_INVALID_ARGUMENT, "workspace must not be NULL");
+    if (work_bytes < MLXC_WORK_WORDS * sizeof(int64_t))
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "workspace must hold at least MLXC_WORK_WORDS int64 words");
+    if (reinterpret_cast<uintptr_t>(work) % 16 != 0)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    return MLXC_OK;
+}
+
+int check_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col, int64_t num_edges,
+               const int64_t* start, int64_t num_walks, int32_t walk_length, const int64_t* n_out,
+               const void* work, size_t work_bytes) {
+    if (num_nodes < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_nodes must be >= 0");
+    if (num_edges < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_edges must be >= 0");
+    if (num_walks < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_walks must be >= 0");
+    if (walk_length < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "walk_length must be >= 0");
+    if (int rc = check_workspace(work, work_bytes)) return rc;
+    if (num_walks > 0) {
+        if (!rowptr || !start || !n_out)
+            return fail(MLXC_ERR_INVALID_ARGUMENT, "rowptr, start and n_out must not be NULL");
+        if (num_edges > 0 && !col) return fail(MLXC_ERR_INVALID_ARGUMENT, "col must not be NULL");
+        if (num_walks > INT64_MAX / (static_cast<int64_t>(walk_length) + 1))
+            return fail(MLXC_ERR_INVALID_ARGUMENT, "num_walks * (walk_length + 1) overflows int64");
+    }
+    return MLXC_OK;
+}
+
+}  // namespace
+}  // namespace mlxc
+
+using namespace mlxc;
+
+extern "C" {
+
+int mlxc_version(void) { return 100; }
+
+const char* mlxc_last_error(void) { return g_last_error.c_str(); }
+
+size_t mlxc_random_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
+                                        int32_t walk_length) {
+    return uniform_workspace_bytes(num_nodes, num_edges, num_walks, walk_length);
+}
+
+size_t mlxc_rejection_sampling_workspace_bytes(int64_t num_nodes, int64_t num_edges,
+                                               int64_t num_walks, int32_t walk_length) {
+    return node2vec_workspace_bytes(num_nodes, num_edges, num_walks, walk_length);
+}
+
+int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
+                     int64_t num_edges, const int64_t* d_start, int64_t num_walks,
+                     const float* d_rand, int32_t walk_length, int64_t* d_n_out,
+                     int64_t* d_e_out, void* d_workspace, size_t workspace_bytes, void* stream) {
+    if (int rc = check_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
+                            walk_length, d_n_out, d_workspace, workspace_bytes))
+        return rc;
+    if (num_walks > 0 && walk_length > 0 && !d_rand)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "rand must not be NULL");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int64_t* d_work = static_cast<int64_t*>(d_workspace);
+    if (int rc = launch_zero_work(d_work, s)) return rc;
+    if (num_walks == 0) return MLXC_OK;
+    const WalkArgs a{d_rowptr, d_col, d_start, d_rand, d_n_out, d_e_out, d_work,
+                     num_nodes, num_edges, num_walks, walk_length};
+    return launch_uniform(a, d_workspace, workspace_bytes, s);
+}
+
+int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
+                            int64_t num_edges, const int64_t* d_start, int64_t num_walks,
+                            int32_t walk_length, double p, double q, uint64_t seed,
+                            int32_t rule, int32_t rows_sorted, int64_t* d_n_out,
+                            int64_t* d_e_out, void* d_workspace, size_t workspace_bytes,
+                            void* stream) {
+    if (int rc = check_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
+                            walk_length, d_n_out, d_workspace, workspace_bytes))
+        return rc;
+    if (!(p > 0.0) || !(q > 0.0) || !std::isfinite(p) || !std::isfinite(q))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "p and q must be finite and > 0");
+    if (rule != MLXC_RULE_REF_CHAIN && rule != MLXC_RULE_NODE2VEC_EXACT)
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "rule must be MLXC_RULE_REF_CHAIN or MLXC_RULE_NODE2VEC_EXACT");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int64_t* d_work = static_cast<int64_t*>(d_workspace);
+    if (int rc = launch_zero_work(d_work, s)) return rc;
+    if (num_walks == 0) return MLXC_OK;
+    // Acceptance constants exactly as BiasedRandomWalk.cpp:52-55, in FP64.
+    const double max_prob = std::fmax(std::fmax(1. / p, 1.), 1. / q);
+    N2VParams prm;
+    prm.prob0 = 1. / p / max_prob;
+    prm.prob1 = 1. / max_prob;
+    prm.prob2 = 1. / q / max_prob;
+    prm.key0 = static_cast<uint32_t>(seed);
+    prm.key1 = static_cast<uint32_t>(seed >> 32);
+    prm.rule = rule;
+    prm.rows_sorted = rows_sorted != 0;
+    const WalkArgs a{d_rowptr, d_col, d_start, nullptr, d_n_out, d_e_out, d_work,
+                     num_nodes, num_edges, num_walks, walk_length};
+    return launch_node2vec(a, prm, d_workspace, workspace_bytes, s);
+}
+
+int mlxc_csr_check(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
+                   int64_t num_edges, void* d_workspace, size_t workspace_bytes, int32_t* h_flags,
+                   void* stream) {
+    if (num_nodes < 0 || num_edges < 0)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "num_nodes and num_edges must be >= 0");
+    if (!d_rowptr || !h_flags || (num_edges > 0 && !d_col))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "NULL pointer argument");
+    if (int rc = check_workspace(d_workspace, workspace_bytes)) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int64_t* d_work = static_cast<int64_t*>(d_workspace);
+    if (int rc = launch_zero_work(d_work, s)) return rc;
+    if (int rc = launch_csr_check(d_rowptr, num_nodes, d_col, num_edges, d_work, s)) return rc;
+    int64_t host[3] = {0, 0, 0};
+    MLXC_HIP_TRY(hipMemcpyAsync(host, d_work, sizeof(host), hipMemcpyDeviceToHost, s));
+    MLXC_HIP_TRY(hipStreamSynchronize(s));
+    int32_t flags = static_cast<int32_t>(host[0]);
+    if (!(flags & MLXC_CSR_BAD_ROWPTR) && host[1] != host[2]) flags |= MLXC_CSR_UNSORTED;
+    *h_flags = flags;
+    return MLXC_OK;
+}
+
+int mlxc_philox_uniform(float* d_out, int64_t n, uint64_t seed, void* stream) {
+    if (n < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "n must be >= 0");
+    if (n == 0) return MLXC_OK;
+    if (!d_out) return fail(MLXC_ERR_INVALID_ARGUMENT, "out must not be NULL");
+    return launch_philox_fill(d_out, n, seed, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

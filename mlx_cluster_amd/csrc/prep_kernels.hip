@@ -1,0 +1,187 @@
+// Per-call preparation kernels: workspace reset, edge records, start
+// records, CSR validation and seeded uniform fills.
+#include "walk_host.h"
+
+namespace mlxc {
+
+__global__ void zero_words_kernel(int64_t* p, int n) {
+    const int i = threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+// Edge records (see EdgeRecord); optionally also col as int32 (col32 may be
+// null), the neighbour-search array of the node2vec walk.
+__global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __restrict__ rowptr,
+                                                             const int64_t* __restrict__ col,
+                                                             int64_t num_nodes, int64_t num_edges,
+                                                             EdgeRecord* __restrict__ rec,
+                                                             int32_t* __restrict__ col32) {
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; e < num_edges;
+         e += stride) {
+        const int64_t c = col[e];
+        i32x4 r = {static_cast<int32_t>(c), 0, kRecBadNode, 0};
+        if (node_ok(c, num_nodes)) {
+            const RowBounds rb = load_row(rowptr, c);
+            if (row_ok(rb, num_edges)) {
+                r.y = static_cast<int32_t>(rb.begin);
+                r.z = static_cast<int32_t>(rb.end - rb.begin);
+            } else {
+                r.z = kRecBadRow;
+            }
+        }
+        *reinterpret_cast<i32x4*>(rec + e) = r;
+        if (col32) col32[e] = r.x;
+    }
+}
+
+// Start records: walk n's start node in the edge-record format, so a slot
+// beginning a walk and a slot taking a step both issue the same single 16-byte
+// read.  Written by walk_init_kernel (one coalesced pass over start).
+__global__ __launch_bounds__(kBlock) void walk_init_kernel(const int64_t* __restrict__ rowptr,
+                                                           const int64_t* __restrict__ start,
+                                                           int64_t num_nodes, int64_t num_edges,
+                                                           int64_t num_walks,
+                                                           EdgeRecord* __restrict__ init) {
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; n < num_walks;
+         n += stride) {
+        const int64_t v = start[n];
+        i32x4 r = {static_cast<int32_t>(v), 0, kRecBadNode, 0};
+        if (node_ok(v, num_nodes)) {
+            const RowBounds rb = load_row(rowptr, v);
+            if (row_ok(rb, num_edges)) {
+                r.y = static_cast<int32_t>(rb.begin);
+                r.z = static_cast<int32_t>(rb.end - rb.begin);
+            } else {
+                r.z = kRecBadRow;
+            }
+        }
+        *reinterpret_cast<i32x4*>(init + n) = r;
+    }
+}
+
+__device__ __forceinline__ int64_t wave_sum(int64_t x) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
+    return x;
+}
+
+// work[0] |= MLXC_CSR_BAD_ROWPTR / MLXC_CSR_BAD_COL bits; work[1] counts
+// positions i >= 1 with col[i] < col[i-1]; work[2] counts those positions
+// that start a non-empty row.  Rows are sorted iff work[1] == work[2].
+__global__ __launch_bounds__(kBlock) void csr_check_kernel(const int64_t* __restrict__ rowptr,
+                                                           int64_t V,
+                                                           const int64_t* __restrict__ col,
+                                                           int64_t E, int64_t* work) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    uint32_t bits = 0;
+    int64_t desc = 0, start_desc = 0;
+    if (gid == 0 && (rowptr[0] != 0 || rowptr[V] != E)) bits |= MLXC_CSR_BAD_ROWPTR;
+    for (int64_t v = gid; v < V; v += stride) {
+        const int64_t rs = rowptr[v], re = rowptr[v + 1];
+        if (re < rs) bits |= MLXC_CSR_BAD_ROWPTR;
+        if (rs >= 1 && re > rs && re <= E && col[rs] < col[rs - 1]) ++start_desc;
+    }
+    for (int64_t i = gid; i < E; i += stride) {
+        const int64_t c = col[i];
+        if (!node_ok(c, V)) bits |= MLXC_CSR_BAD_COL;
+        if (i >= 1 && c < col[i - 1]) ++desc;
+    }
+    const int64_t d = wave_sum(desc), sd = wave_sum(start_desc);
+    const uint64_t any_bits = __ballot(bits != 0);
+    uint32_t wave_bits = bits;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) wave_bits |= __shfl_xor(wave_bits, off, kWave);
+    if (__lane_id() == 0) {
+        if (any_bits) atomicOr(reinterpret_cast<unsigned long long*>(work), static_cast<unsigned long long>(wave_bits));
+        if (d) atomicAdd(reinterpret_cast<unsigned long long*>(work + 1), static_cast<unsigned long long>(d));
+        if (sd) atomicAdd(reinterpret_cast<unsigned long long*>(work + 2), static_cast<unsigned long long>(sd));
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void philox_fill_kernel(float* __restrict__ out, int64_t n,
+                                                             uint32_t k0, uint32_t k1) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    const int64_t blocks = (n + 3) >> 2;
+    for (int64_t j = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; j < blocks; j += stride) {
+        uint32_t c0 = static_cast<uint32_t>(j), c1 = static_cast<uint32_t>(static_cast<uint64_t>(j) >> 32);
+        uint32_t c2 = 0, c3 = 0;
+        philox4x32_10(c0, c1, c2, c3, k0, k1);
+        const int64_t i = j << 2;
+        if (i + 3 < n) {
+            out[i] = unit_float(c0);
+            out[i + 1] = unit_float(c1);
+            out[i + 2] = unit_float(c2);
+            out[i + 3] = unit_float(c3);
+        } else {
+            const uint32_t w[4] = {c0, c1, c2, c3};
+            for (int k = 0; k < 4 && i + k < n; ++k) out[i + k] = unit_float(w[k]);
+        }
+    }
+}
+
+// ------------------------------------------------------------- launchers
+
+int stream_grid(int64_t items, int blocks_per_cu, int& grid) {
+    DeviceInfo info;
+    if (int rc = device_info(info)) return rc;
+    int64_t g = (items + kBlock - 1) / kBlock;
+    const int64_t cap = static_cast<int64_t>(info.cus) * blocks_per_cu;
+    if (g > cap) g = cap;
+    grid = static_cast<int>(g < 1 ? 1 : g);
+    return MLXC_OK;
+}
+
+int launch_zero_work(int64_t* d_work, hipStream_t stream) {
+    hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(kWave), 0, stream, d_work, MLXC_WORK_WORDS);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
+                        int64_t num_edges, EdgeRecord* recs, int32_t* col32, hipStream_t stream) {
+    if (num_edges == 0) return MLXC_OK;
+    int grid = 0;
+    if (int rc = stream_grid(num_edges, 16, grid)) return rc;
+    hipLaunchKernelGGL(edge_record_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col,
+                       num_nodes, num_edges, recs, col32);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
+                     int64_t num_edges, int64_t num_walks, EdgeRecord* init, hipStream_t stream) {
+    if (num_walks == 0) return MLXC_OK;
+    int grid = 0;
+    if (int rc = stream_grid(num_walks, 16, grid)) return rc;
+    hipLaunchKernelGGL(walk_init_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, start,
+                       num_nodes, num_edges, num_walks, init);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
+                     int64_t num_edges, int64_t* d_work, hipStream_t stream) {
+    int grid = 0;
+    if (int rc = stream_grid(num_nodes > num_edges ? num_nodes : num_edges, 8, grid)) return rc;
+    hipLaunchKernelGGL(csr_check_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, num_nodes,
+                       col, num_edges, d_work);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int launch_philox_fill(float* out, int64_t n, uint64_t seed, hipStream_t stream) {
+    if (n == 0) return MLXC_OK;
+    int grid = 0;
+    if (int rc = stream_grid((n + 3) / 4, 16, grid)) return rc;
+    hipLaunchKernelGGL(philox_fill_kernel, dim3(grid), dim3(kBlock), 0, stream, out, n,
+                       static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32));
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+}  // namespace mlxc

@@ -1,0 +1,507 @@
+// Uniform random walk kernels (RandomWalk.cpp:41-60) and their launcher.
+//
+// The walk is a chain of dependent random reads, so throughput comes from
+// the number of chains in flight and the number of reads per step, not from
+// arithmetic.  Every lane runs a small state machine over W walk slots; a
+// slot whose walk ends (or is absorbed by a node of out-degree 0) takes the
+// next walk from a per-wavefront queue refilled by one global atomic per
+// kQueueChunk walks, so lanes never idle while walks remain and the kernel's
+// tail is about one walk long.  Grids are the device's resident capacity.
+#include "walk_host.h"
+
+namespace mlxc {
+
+// Uniform walk without register windows: W walk slots per lane, walks from
+// the wave queue, 8-byte loads and stores.  Serves the cases the windowed
+// kernels do not: the edge-id output and buffers that are not 16-byte
+// aligned.
+template <int W, bool kEdges>
+__global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
+    const int64_t L = a.walk_length;
+    const int64_t N = a.num_walks;
+    unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.work + 1);
+    WaveQueue q{0, 0};
+    int64_t n[W], v[W], l[W];
+    uint32_t status = 0;
+
+#pragma unroll
+    for (int s = 0; s < W; ++s) { n[s] = -1; l[s] = L; v[s] = 0; }
+
+    while (true) {
+        // Acquire walks for empty slots; write their first column.
+        bool unretired = false;
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            const bool need = (n[s] < N) && (l[s] >= L);  // slot idle (or never used)
+            const int64_t id = queue_take(q, need, counter);
+            if (need) {
+                n[s] = id;  // id >= N ends the slot for good
+                if (id < N) {
+                    const int64_t s0 = a.start[id];
+                    a.n_out[id * (L + 1)] = s0;
+                    v[s] = s0;
+                    l[s] = 0;
+                    if (!node_ok(s0, a.num_nodes)) {
+                        status |= MLXC_STATUS_BAD_NODE;
+                        for (int64_t j = 1; j <= L; ++j) a.n_out[id * (L + 1) + j] = s0;
+                        if (kEdges)
+                            for (int64_t j = 0; j < L; ++j) a.e_out[id * L + j] = -1;
+                        l[s] = L;
+                    }
+                }
+            }
+            unretired |= (n[s] < N);
+        }
+        // The whole wave leaves together, once every slot of every lane has
+        // drawn an id past the end; until then idle lanes keep voting.
+        if (!__any(unretired)) break;
+
+        // Phase 1: rowptr pair and the step's uniform, for every live slot.
+        RowBounds rb[W];
+        float r[W];
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            const bool live = (n[s] < N) && (l[s] < L);
+            rb[s] = {0, 0};
+            r[s] = 0.0f;
+            if (live) {
+                rb[s] = load_row(a.rowptr, v[s]);
+                r[s] = __builtin_nontemporal_load(a.rand + n[s] * L + l[s]);
+            }
+        }
+        // Phase 2: candidate edge and its target, for every moving slot.
+        int64_t e[W], x[W];
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            const bool live = (n[s] < N) && (l[s] < L);
+            e[s] = -1;
+            x[s] = v[s];
+            if (live) {
+                const int64_t deg = rb[s].end - rb[s].begin;
+                if (!row_ok(rb[s], a.num_edges)) {
+                    status |= MLXC_STATUS_BAD_ROW;
+                } else if (deg > 0) {
+                    e[s] = rb[s].begin + pick_index(r[s], deg);
+                    x[s] = a.col[e[s]];
+                }
+            }
+        }
+        // Phase 3: store, advance, and finish sunk / broken walks.
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            const bool live = (n[s] < N) && (l[s] < L);
+            if (!live) continue;
+            int64_t* out = a.n_out + n[s] * (L + 1);
+            const bool moved = e[s] >= 0;
+            bool stop = !moved;  // deg == 0 (absorbing) or malformed row
+            out[l[s] + 1] = x[s];
+            if (kEdges) a.e_out[n[s] * L + l[s]] = e[s];
+            l[s] += 1;
+            if (moved && !node_ok(x[s], a.num_nodes)) {
+                status |= MLXC_STATUS_BAD_NODE;
+                stop = true;
+            }
+            v[s] = x[s];
+            if (stop) {
+                for (int64_t j = l[s] + 1; j <= L; ++j) out[j] = x[s];
+                if (kEdges)
+                    for (int64_t j = l[s]; j < L; ++j) a.e_out[n[s] * L + j] = -1;
+                l[s] = L;
+            }
+        }
+    }
+    if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
+}
+
+// Slot phases of the windowed walks.
+enum : int {
+    kSlotIdle = 0,   // wants a walk id
+    kSlotStart = 1,  // reads the start record of walk n (and its first rand block)
+    kSlotWalk = 2,   // record walk: reads the record of the chosen edge
+    kSlotCol = 3,    // CSR walk: reads col[e] of the chosen edge
+    kSlotRow = 4,    // CSR walk: reads rowptr[v], rowptr[v+1] of the new node
+    kSlotDone = 5,   // the queue is exhausted
+};
+
+// Uniform walk over edge records (requires 16-byte aligned rand and n_out,
+// num_nodes and num_edges below 2^31, num_walks * walk_length a multiple of
+// 4 and at least RW; no edge output).
+//
+// Loop invariant: every live slot issues exactly one dependent 16-byte read
+// per iteration (a start record or an edge record), plus at most one
+// independent rand block, and the wave waits once.  The rand value for a step
+// is taken from the window in the iteration before the read it addresses, so
+// a new rand block always travels together with a record read and never costs
+// a round trip of its own.  Output stores issued after the wait overlap the
+// next iteration's read.
+template <int W, int RW>
+__global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
+                                                                  const EdgeRecord* __restrict__ recs,
+                                                                  const EdgeRecord* __restrict__ init) {
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const int64_t L = a.walk_length;
+    const int64_t L1 = L + 1;
+    const int64_t N = a.num_walks;
+    const int64_t rtotal = N * L;
+    unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.work + 1);
+    WaveQueue q{0, 0};
+    int phase[W];
+    int64_t n[W], l[W], e[W];  // e: record index read this iteration (kSlotWalk)
+    int64_t fr[W];             // rand index whose block the next read brings along
+    bool need_block[W];        // ... if set
+    RandWindow<RW> rw[W];
+    OutWin<int32_t> ow[W];
+    uint32_t status = 0;
+
+#pragma unroll
+    for (int s = 0; s < W; ++s) {
+        phase[s] = kSlotIdle;
+        n[s] = 0;
+        l[s] = 0;
+        e[s] = 0;
+        fr[s] = 0;
+        need_block[s] = false;
+        rw[s].valid = 0;
+        ow[s].count = 0;
+    }
+
+    while (true) {
+        // 1. One record read per live slot (idle slots read init[0], so the
+        // load is unconditional and nothing merges with it before the wait in
+        // step 3), and the rand blocks due.
+        int ph[W];  // phase at issue: only these slots consume in step 3
+        i32x4 rec[W];
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            ph[s] = phase[s];
+            const EdgeRecord* p = ph[s] == kSlotStart ? init + n[s]
+                                  : ph[s] == kSlotWalk ? recs + e[s]
+                                                       : init;
+            rec[s] = *reinterpret_cast<const i32x4*>(p);
+        }
+#pragma unroll
+        for (int s = 0; s < W; ++s)
+            if (need_block[s]) rw_load_at(rw[s], a.rand, rw_block_base<RW>(fr[s], rtotal));
+
+        // 2. While the reads are in flight, idle slots draw walk ids from the
+        // wave queue; they issue their start reads next iteration.
+        bool alive = false;
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            const bool need = phase[s] == kSlotIdle;
+            const int64_t id = queue_take(q, need, counter);
+            if (need) {
+                n[s] = id;
+                l[s] = 0;
+                phase[s] = id < N ? kSlotStart : kSlotDone;
+                fr[s] = id * L;  // the first step's uniform
+            }
+            alive |= phase[s] != kSlotDone;
+        }
+        if (!__any(alive)) break;  // every slot done: nothing was read above
+
+        // 3. Consume: buffer the node, finish or pick the next edge.
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            if (ph[s] != kSlotStart && ph[s] != kSlotWalk) {
+                // a slot that just drew a walk reads its start record and
+                // first rand block next iteration
+                need_block[s] = phase[s] == kSlotStart && L > 0;
+                continue;
+            }
+            const int64_t g0 = n[s] * L1;  // output index of the walk's start node
+            const int64_t g = g0 + l[s] + (ph[s] == kSlotWalk ? 1 : 0);
+            if (need_block[s]) {
+                // block holding rand[fr]: shift it so w[0] is that value
+                const int k = static_cast<int>(fr[s] - rw_block_base<RW>(fr[s], rtotal));
+                rw_shift_by(rw[s], k);
+                rw[s].valid = RW - k;
+                need_block[s] = false;
+            }
+            const int32_t node = rec[s].x, begin = rec[s].y, deg = rec[s].z;
+            bool fill = false, flush = false;
+            if (deg < 0) {
+                // malformed start or graph entry: stop (outputs unspecified)
+                status |= deg == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
+                if (ph[s] == kSlotStart) ow[s].count = 0;
+                ow_fill(ow[s], a.n_out, g, g0 + L, node);
+                phase[s] = kSlotIdle;
+                continue;
+            }
+            if (ph[s] == kSlotStart) ow[s].count = 0;
+            ow_push(ow[s], a.n_out, g, node);
+            if (ph[s] == kSlotWalk) l[s] += 1;
+            if (l[s] == L) flush = true;
+            else if (deg == 0) fill = true;  // absorbing node: the walk stays
+            if (fill) {
+                ow_fill(ow[s], a.n_out, g + 1, g0 + L, node);
+            } else if (flush) {
+                if (ow[s].count) ow_flush(ow[s], a.n_out, g);
+            } else {
+                // step l (0-based) leaves this node with uniform rand[n*L + l]
+                e[s] = begin + pick_index(rw[s].w[0], deg);
+                rw_shift1(rw[s]);
+                rw[s].valid -= 1;
+                need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
+                fr[s] = n[s] * L + l[s] + 1;
+                phase[s] = kSlotWalk;
+            }
+            if (fill || flush) phase[s] = kSlotIdle;
+        }
+    }
+    if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
+}
+
+// Uniform walk over the CSR arrays, for calls whose edge records would not
+// pay for themselves (few steps per edge) or do not fit int32.  Same loop
+// shape as the record walk — one dependent read per slot per iteration, one
+// wait — but a step costs two reads: col[e] of the chosen edge, then the row
+// of the new node.  Start records (walk_init_kernel) give the first row.
+// Requirements as for the record walk except num_edges may be any size the
+// int32 start records hold (num_nodes, num_edges below 2^31).
+template <int W, int RW>
+__global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
+                                                                  const EdgeRecord* __restrict__ init) {
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4), aligned(8)));
+    const int64_t L = a.walk_length;
+    const int64_t L1 = L + 1;
+    const int64_t N = a.num_walks;
+    const int64_t rtotal = N * L;
+    unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.work + 1);
+    WaveQueue q{0, 0};
+    int phase[W];
+    int64_t n[W], l[W], e[W], v[W], fr[W];
+    bool need_block[W];
+    RandWindow<RW> rw[W];
+    OutWin<int32_t> ow[W];
+    uint32_t status = 0;
+
+#pragma unroll
+    for (int s = 0; s < W; ++s) {
+        phase[s] = kSlotIdle;
+        n[s] = 0;
+        l[s] = 0;
+        e[s] = 0;
+        v[s] = 0;
+        fr[s] = 0;
+        need_block[s] = false;
+        rw[s].valid = 0;
+        ow[s].count = 0;
+    }
+
+    while (true) {
+        // 1. Reads: a 16-byte start record or rowptr pair (one instruction;
+        // idle slots read init[0]), an 8-byte col entry, and due rand blocks.
+        int ph[W];
+        i32x4 row[W];
+        int64_t cv[W];
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            ph[s] = phase[s];
+            const i32x4* p = ph[s] == kSlotRow ? reinterpret_cast<const i32x4*>(a.rowptr + v[s])
+                             : ph[s] == kSlotStart ? reinterpret_cast<const i32x4*>(init + n[s])
+                                                   : reinterpret_cast<const i32x4*>(init);
+            row[s] = *p;
+            if (ph[s] == kSlotCol) cv[s] = a.col[e[s]];
+        }
+#pragma unroll
+        for (int s = 0; s < W; ++s)  // a block due after a pick travels with the col read
+            if (need_block[s] && ph[s] != kSlotRow)
+                rw_load_at(rw[s], a.rand, rw_block_base<RW>(fr[s], rtotal));
+
+        // 2. Idle slots draw walk ids while the reads are in flight.
+        bool alive = false;
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            const bool need = phase[s] == kSlotIdle;
+            const int64_t id = queue_take(q, need, counter);
+            if (need) {
+                n[s] = id;
+                l[s] = 0;
+                phase[s] = id < N ? kSlotStart : kSlotDone;
+                fr[s] = id * L;
+            }
+            alive |= phase[s] != kSlotDone;
+        }
+        if (!__any(alive)) break;
+
+        // 3. Consume.
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            if (ph[s] == kSlotIdle || ph[s] == kSlotDone) {
+                need_block[s] = phase[s] == kSlotStart && L > 0;
+                continue;
+            }
+            if (need_block[s] && ph[s] != kSlotCol) {
+                const int k = static_cast<int>(fr[s] - rw_block_base<RW>(fr[s], rtotal));
+                rw_shift_by(rw[s], k);
+                rw[s].valid = RW - k;
+                need_block[s] = false;
+            }
+            const int64_t g0 = n[s] * L1;
+            int64_t begin = 0, deg = 0;
+            bool pick = false, stop = false;
+            if (ph[s] == kSlotStart) {
+                ow[s].count = 0;
+                v[s] = row[s].x;
+                ow_push(ow[s], a.n_out, g0, row[s].x);
+                if (row[s].z < 0) {
+                    status |= row[s].z == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
+                    ow_fill(ow[s], a.n_out, g0 + 1, g0 + L, row[s].x);
+                    stop = true;
+                } else if (L == 0) {
+                    ow_flush(ow[s], a.n_out, g0);
+                    stop = true;
+                } else {
+                    begin = row[s].y;
+                    deg = row[s].z;
+                    pick = true;
+                }
+            } else if (ph[s] == kSlotCol) {
+                const int64_t g = g0 + l[s] + 1;
+                if (!node_ok(cv[s], a.num_nodes)) {
+                    status |= MLXC_STATUS_BAD_NODE;
+                    ow_fill(ow[s], a.n_out, g, g0 + L, static_cast<int32_t>(v[s]));
+                    stop = true;
+                } else {
+                    v[s] = cv[s];
+                    l[s] += 1;
+                    ow_push(ow[s], a.n_out, g, static_cast<int32_t>(cv[s]));
+                    if (l[s] == L) {
+                        if (ow[s].count) ow_flush(ow[s], a.n_out, g);
+                        stop = true;
+                    } else {
+                        phase[s] = kSlotRow;
+                    }
+                }
+            } else {  // kSlotRow
+                const RowBounds rb = {
+                    static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(row[s].y)) << 32) |
+                                         static_cast<uint32_t>(row[s].x)),
+                    static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(row[s].w)) << 32) |
+                                         static_cast<uint32_t>(row[s].z))};
+                if (!row_ok(rb, a.num_edges)) {
+                    status |= MLXC_STATUS_BAD_ROW;
+                    ow_fill(ow[s], a.n_out, g0 + l[s] + 1, g0 + L, static_cast<int32_t>(v[s]));
+                    stop = true;
+                } else {
+                    begin = rb.begin;
+                    deg = rb.end - rb.begin;
+                    pick = true;
+                }
+            }
+            if (pick) {
+                if (deg == 0) {  // absorbing node: the walk stays
+                    ow_fill(ow[s], a.n_out, g0 + l[s] + 1, g0 + L, static_cast<int32_t>(v[s]));
+                    stop = true;
+                } else {
+                    e[s] = begin + pick_index(rw[s].w[0], deg);
+                    rw_shift1(rw[s]);
+                    rw[s].valid -= 1;
+                    need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
+                    fr[s] = n[s] * L + l[s] + 1;
+                    phase[s] = kSlotCol;
+                }
+            }
+            if (stop) phase[s] = kSlotIdle;
+        }
+    }
+    if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
+}
+
+// ------------------------------------------------------------- launcher
+
+#ifndef MLXC_UNIFORM_SLOTS
+#define MLXC_UNIFORM_SLOTS 1   // walks in flight per lane
+#endif
+#ifndef MLXC_RAND_WINDOW
+#define MLXC_RAND_WINDOW 16    // uniforms per rand block (4-byte floats)
+#endif
+
+namespace {
+
+enum class UniformMode { kRecords, kCsr, kPlain };
+
+// Edge records cost one random read per edge to build; they pay off when the
+// call takes several steps per edge.
+bool records_pay_off(int64_t num_edges, int64_t num_walks, int32_t walk_length) {
+    return num_walks * static_cast<int64_t>(walk_length) >= 4 * num_edges;
+}
+
+size_t record_bytes(int64_t num_edges, int64_t num_walks) {
+    return kRecordOffset + static_cast<size_t>(num_edges + num_walks) * sizeof(EdgeRecord);
+}
+
+size_t init_bytes(int64_t num_walks) {
+    return kRecordOffset + static_cast<size_t>(num_walks) * sizeof(EdgeRecord);
+}
+
+UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes) {
+    const int64_t rtotal = a.num_walks * a.walk_length;
+    const bool streams_ok = reinterpret_cast<uintptr_t>(a.rand) % 16 == 0 &&
+                            reinterpret_cast<uintptr_t>(a.n_out) % 16 == 0 && rtotal % 4 == 0 &&
+                            rtotal >= MLXC_RAND_WINDOW;
+    if (a.e_out || !streams_ok || !records_fit(a.num_nodes, a.num_edges)) return UniformMode::kPlain;
+    if (records_pay_off(a.num_edges, a.num_walks, a.walk_length) &&
+        workspace_bytes >= record_bytes(a.num_edges, a.num_walks))
+        return UniformMode::kRecords;
+    if (workspace_bytes >= init_bytes(a.num_walks)) return UniformMode::kCsr;
+    return UniformMode::kPlain;
+}
+
+template <typename Kernel, typename... Extra>
+int launch_walk_kernel(Kernel kernel, int slots, const WalkArgs& a, hipStream_t stream,
+                       Extra... extra) {
+    int grid = 0;
+    if (int rc = persistent_grid(kernel, a.num_walks, slots, grid)) return rc;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a, extra...);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+}  // namespace
+
+size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
+                               int32_t walk_length) {
+    const size_t minimum = MLXC_WORK_WORDS * sizeof(int64_t);
+    if (num_nodes < 0 || num_edges < 0 || num_walks < 0 || walk_length < 0 ||
+        !records_fit(num_nodes, num_edges))
+        return minimum;
+    return records_pay_off(num_edges, num_walks, walk_length) ? record_bytes(num_edges, num_walks)
+                                                              : init_bytes(num_walks);
+}
+
+int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes,
+                   hipStream_t stream) {
+    constexpr int W = MLXC_UNIFORM_SLOTS;
+    constexpr int RW = MLXC_RAND_WINDOW;
+    EdgeRecord* recs = reinterpret_cast<EdgeRecord*>(static_cast<char*>(workspace) + kRecordOffset);
+    switch (uniform_mode(a, workspace_bytes)) {
+    case UniformMode::kRecords: {
+        EdgeRecord* init = recs + a.num_edges;
+        if (int rc = launch_edge_records(a.rowptr, a.col, a.num_nodes, a.num_edges, recs, nullptr,
+                                         stream))
+            return rc;
+        if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
+                                      init, stream))
+            return rc;
+        return launch_walk_kernel(uniform_walk_rec_kernel<W, RW>, W, a, stream,
+                                  static_cast<const EdgeRecord*>(recs),
+                                  static_cast<const EdgeRecord*>(init));
+    }
+    case UniformMode::kCsr: {
+        EdgeRecord* init = recs;
+        if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
+                                      init, stream))
+            return rc;
+        return launch_walk_kernel(uniform_walk_csr_kernel<W, RW>, W, a, stream,
+                                  static_cast<const EdgeRecord*>(init));
+    }
+    case UniformMode::kPlain:
+        break;
+    }
+    if (a.e_out) return launch_walk_kernel(uniform_walk_kernel<2, true>, 2, a, stream);
+    return launch_walk_kernel(uniform_walk_kernel<2, false>, 2, a, stream);
+}
+
+}  // namespace mlxc

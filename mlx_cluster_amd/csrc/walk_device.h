@@ -1,0 +1,302 @@
+// Device-side building blocks of the random-walk kernels (gfx950): the
+// Philox4x32-10 generator, the reference's float32 index rule, CSR row reads
+// with bounds checks, the per-wavefront walk queue, the per-lane register
+// windows for the rand and output streams, and the edge-record layout.
+//
+// Reference semantics (vinayhpandya/mlx_cluster):
+//   uniform walk   /root/reference/random_walks/RandomWalk.cpp:41-60
+//   node2vec walk  /root/reference/random_walks/BiasedRandomWalk.cpp:20-28,52-100
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "mlxc.h"
+
+namespace mlxc {
+
+constexpr int kBlock = 256;           // 4 wavefronts of 64
+constexpr int kWave = 64;
+constexpr int64_t kQueueChunk = 256;  // walks taken per global atomic
+
+// ------------------------------------------------------------------ Philox
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy
+// as 1, 2, 3", SC'11): ten rounds of two 32x32->64 multiplies with a Weyl
+// key schedule.
+__device__ __forceinline__ void philox4x32_10(uint32_t& c0, uint32_t& c1, uint32_t& c2,
+                                              uint32_t& c3, uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int round = 0; round < 10; ++round) {
+        const uint32_t lo0 = 0xD2511F53u * c0;
+        const uint32_t hi0 = __umulhi(0xD2511F53u, c0);
+        const uint32_t lo1 = 0xCD9E8D57u * c2;
+        const uint32_t hi1 = __umulhi(0xCD9E8D57u, c2);
+        const uint32_t n0 = hi1 ^ c1 ^ k0;
+        const uint32_t n2 = hi0 ^ c3 ^ k1;
+        c0 = n0;
+        c1 = lo1;
+        c2 = n2;
+        c3 = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+}
+
+// 24 random bits -> float in [0, 1 - 2^-24]; both steps are exact.
+__device__ __forceinline__ float unit_float(uint32_t x) {
+    return static_cast<float>(x >> 8) * 0x1p-24f;
+}
+
+// --------------------------------------------------------- index selection
+
+// RandomWalk.cpp:51-53: idx = (int64_t)(r * (row_end - row_start)) with r a
+// float, i.e. the degree is rounded to float32, multiplied in float32 (RN)
+// and truncated.  Clamped to [0, deg-1]: for r in [0,1) and deg <= 2^24 the
+// clamp never fires; it keeps out-of-range r (and deg > 2^24, where
+// (float)deg can round up) inside the row instead of reading past it.
+__device__ __forceinline__ int64_t pick_index(float r, int64_t deg) {
+    if (deg <= (int64_t{1} << 24)) {
+        const float fdeg = static_cast<float>(static_cast<int32_t>(deg));  // exact
+        const float p = __fmul_rn(r, fdeg);
+        if (!(p >= 0.0f)) return 0;        // negative or NaN
+        if (p >= fdeg) return deg - 1;     // r >= 1
+        return static_cast<int64_t>(static_cast<int32_t>(p));
+    }
+    const float fdeg = static_cast<float>(deg);
+    const float p = __fmul_rn(r, fdeg);
+    if (!(p >= 0.0f)) return 0;
+    if (p >= 9.0e18f) return deg - 1;
+    const int64_t idx = static_cast<int64_t>(p);
+    return idx < deg ? idx : deg - 1;
+}
+
+// rowptr[v], rowptr[v+1] as one 16-byte load (8-byte aligned).
+struct RowBounds {
+    int64_t begin, end;
+};
+
+__device__ __forceinline__ RowBounds load_row(const int64_t* __restrict__ rowptr, int64_t v) {
+    typedef int64_t i64x2 __attribute__((ext_vector_type(2), aligned(8)));
+    const i64x2 b = *reinterpret_cast<const i64x2*>(rowptr + v);
+    return {b.x, b.y};
+}
+
+__device__ __forceinline__ bool node_ok(int64_t v, int64_t num_nodes) {
+    return static_cast<uint64_t>(v) < static_cast<uint64_t>(num_nodes);
+}
+
+__device__ __forceinline__ bool row_ok(RowBounds r, int64_t num_edges) {
+    return r.begin >= 0 && r.end >= r.begin && r.end <= num_edges;
+}
+
+// ------------------------------------------------------------ walk queue
+
+// Per-wavefront queue of walk ids.  Lanes that need a walk vote; the wave
+// hands out consecutive ids from its current chunk and takes a new chunk of
+// kQueueChunk ids from the global counter with one atomic when the chunk runs
+// dry.  All values here are wave-uniform.
+struct WaveQueue {
+    int64_t next, end;
+};
+
+__device__ __forceinline__ int64_t wave_bcast(int64_t x) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ int lane_rank(uint64_t mask) {
+    // number of set bits of mask below this lane
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+// Returns the walk id for lanes with need == true (others get -1).
+__device__ __forceinline__ int64_t queue_take(WaveQueue& q, bool need,
+                                              unsigned long long* counter) {
+    const uint64_t mask = __ballot(need);
+    if (mask == 0) return -1;
+    const int cnt = __popcll(mask);
+    const int rank = lane_rank(mask);
+    const int64_t avail = q.end - q.next;
+    int64_t id;
+    if (cnt <= avail) {
+        id = q.next + rank;
+        q.next += cnt;
+    } else {
+        // The lowest active lane takes the chunk; readfirstlane returns that
+        // same lane's value, whatever the exec mask.
+        const uint64_t active = __ballot(true);
+        int64_t base = 0;
+        if (__lane_id() == __ffsll(static_cast<long long>(active)) - 1)
+            base = static_cast<int64_t>(atomicAdd(counter, static_cast<unsigned long long>(kQueueChunk)));
+        base = wave_bcast(base);
+        id = rank < avail ? q.next + rank : base + (rank - avail);
+        q.next = base + (cnt - avail);
+        q.end = base + kQueueChunk;
+    }
+    return need ? id : -1;
+}
+
+// Arguments shared by the walk kernels.
+struct WalkArgs {
+    const int64_t* rowptr;
+    const int64_t* col;
+    const int64_t* start;
+    const float* rand;
+    int64_t* n_out;
+    int64_t* e_out;
+    int64_t* work;  // [0] status bits, [1] walk-queue counter
+    int64_t num_nodes;
+    int64_t num_edges;
+    int64_t num_walks;
+    int32_t walk_length;
+};
+
+// ------------------------------------------------- stream windows
+
+// Per-lane register windows for the two streams of the uniform walk.
+//
+// The rand stream: walk n reads rand[n*L + l] at step l, so a lane walks
+// through its own row 4 bytes at a time while its 63 neighbours do the same
+// 4*L bytes apart.  Read one float at a time, nearly every step misses L2 and
+// costs a 128-byte line.  Instead each slot keeps the next RW floats of its
+// row in registers, loaded as one aligned RW*4-byte block, so the stream
+// costs one line per RW steps.
+//
+// The output: walk n writes n_out[n*(L+1) + j] for j = 0..L, one 8-byte entry
+// per step.  Scattered 8-byte stores reach memory as partial 32-byte writes.
+// Each slot buffers its entries in an 8-entry window aligned to 64 bytes of
+// the output and writes a full window with four 16-byte stores; walks that
+// sink in a node of out-degree 0 write their constant tail in whole 64-byte
+// blocks.  The stores are non-temporal: the output is never read back, and
+// streaming it past the caches keeps them for the graph.
+template <int RW>
+struct RandWindow {
+    float w[RW];
+    int valid;  // w[0 .. valid-1] are the next uniforms of the walk
+};
+
+template <int RW>
+__device__ __forceinline__ void rw_shift1(RandWindow<RW>& r) {
+#pragma unroll
+    for (int i = 0; i + 1 < RW; ++i) r.w[i] = r.w[i + 1];
+}
+
+// First index of the rand block that serves rand[f]: the aligned block, or for
+// the array's last partial block the last RW values (total must be a multiple
+// of 4 and at least RW, so every block is 16-byte aligned and in bounds).
+template <int RW>
+__device__ __forceinline__ int64_t rw_block_base(int64_t f, int64_t total) {
+    const int64_t base = f & ~static_cast<int64_t>(RW - 1);
+    return base + RW <= total ? base : total - RW;
+}
+
+template <int RW>
+__device__ __forceinline__ void rw_load_at(RandWindow<RW>& r, const float* __restrict__ rand,
+                                           int64_t base) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4* p = reinterpret_cast<const f32x4*>(rand + base);
+#pragma unroll
+    for (int i = 0; i < RW / 4; ++i) {
+        const f32x4 x = __builtin_nontemporal_load(p + i);
+        r.w[4 * i] = x.x;
+        r.w[4 * i + 1] = x.y;
+        r.w[4 * i + 2] = x.z;
+        r.w[4 * i + 3] = x.w;
+    }
+}
+
+template <int RW>
+__device__ __forceinline__ void rw_shift_by(RandWindow<RW>& r, int k) {
+#pragma unroll
+    for (int bit = RW / 2; bit >= 1; bit >>= 1) {
+        if (k & bit) {
+#pragma unroll
+            for (int i = 0; i < RW; ++i) r.w[i] = (i + bit < RW) ? r.w[i + bit] : 0.0f;
+        }
+    }
+}
+
+// T is the type the entries are buffered in (int32_t when node ids fit);
+// they are written as int64.
+template <typename T>
+struct OutWin {
+    T w[8];  // w[8-count .. 7] hold the newest entries; w[7] is entry g
+    int count;
+};
+typedef OutWin<int64_t> OutWindow;
+
+// Writes the buffered entries, the newest of which is output index g.
+template <typename T>
+__device__ __forceinline__ void ow_flush(OutWin<T>& o, int64_t* __restrict__ out, int64_t g) {
+    if (o.count == 8 && ((g + 1) & 7) == 0) {
+        int64_t* p = out + (g - 7);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
+            i64x2 x = {static_cast<int64_t>(o.w[2 * i]), static_cast<int64_t>(o.w[2 * i + 1])};
+            __builtin_nontemporal_store(x, reinterpret_cast<i64x2*>(p + 2 * i));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (i >= 8 - o.count)
+                __builtin_nontemporal_store(static_cast<int64_t>(o.w[i]), out + g - 7 + i);
+    }
+    o.count = 0;
+}
+
+// Appends the entry for output index g; writes the window when g closes a
+// 64-byte block.
+template <typename T>
+__device__ __forceinline__ void ow_push(OutWin<T>& o, int64_t* __restrict__ out, int64_t g, T x) {
+#pragma unroll
+    for (int i = 0; i < 7; ++i) o.w[i] = o.w[i + 1];
+    o.w[7] = x;
+    o.count = o.count < 8 ? o.count + 1 : 8;
+    if (((g + 1) & 7) == 0) ow_flush(o, out, g);
+}
+
+// Output indices g .. g_last (inclusive) all hold x; the window holds the
+// entries before g.  Ends with everything written.
+template <typename T>
+__device__ __forceinline__ void ow_fill(OutWin<T>& o, int64_t* __restrict__ out, int64_t g,
+                                        int64_t g_last, T x) {
+    while (g <= g_last && (g & 7) != 0) ow_push(o, out, g++, x);
+    if (o.count) ow_flush(o, out, g - 1);
+    typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
+    const int64_t x64 = static_cast<int64_t>(x);
+    const i64x2 xx = {x64, x64};
+    for (; g + 7 <= g_last; g += 8) {
+        i64x2* p = reinterpret_cast<i64x2*>(out + g);
+        __builtin_nontemporal_store(xx, p);
+        __builtin_nontemporal_store(xx, p + 1);
+        __builtin_nontemporal_store(xx, p + 2);
+        __builtin_nontemporal_store(xx, p + 3);
+    }
+    for (; g <= g_last; ++g) __builtin_nontemporal_store(x64, out + g);
+}
+
+// ----------------------------------------------------------- edge records
+
+// One record per CSR entry e, written by edge_record_kernel at the start of
+// each call: the target node col[e] together with its row bounds.  A walk at
+// node v with row [begin, begin + deg) picks e and reads record e: one
+// dependent 16-byte read per step gives the next node and everything needed
+// for the step after it, where the plain CSR needs two (rowptr[v], then
+// col[e]).  The walk's random reads, which bound it, halve; the records cost
+// 16 bytes per edge of HBM and one pass over the graph per call.
+struct __attribute__((aligned(16))) EdgeRecord {
+    int32_t node;   // col[e]
+    int32_t begin;  // rowptr[col[e]]
+    int32_t deg;    // rowptr[col[e] + 1] - rowptr[col[e]]; < 0 marks a malformed entry
+    int32_t pad;
+};
+constexpr int32_t kRecBadNode = -1;  // col[e] outside [0, num_nodes)
+constexpr int32_t kRecBadRow = -2;   // row of col[e] outside [0, num_edges] or decreasing
+constexpr size_t kRecordOffset = 256;  // bytes of workspace before the records
+
+}  // namespace mlxc

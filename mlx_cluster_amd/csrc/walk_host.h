@@ -1,0 +1,88 @@
+// Host-side internals shared by the translation units of libmlxc.so: error
+// reporting, device properties, grid sizing and the launchers each file
+// provides.  Nothing here is part of the C ABI (include/mlxc.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "mlxc.h"
+#include "walk_device.h"
+
+namespace mlxc {
+
+// Records msg as the calling thread's last error and returns code.
+int fail(int code, const std::string& msg);
+
+#define MLXC_HIP_TRY(expr)                                                                   \
+    do {                                                                                     \
+        hipError_t err_ = (expr);                                                            \
+        if (err_ != hipSuccess)                                                              \
+            return ::mlxc::fail(MLXC_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(err_)); \
+    } while (0)
+
+struct DeviceInfo {
+    int cus = 0;  // compute units of the current device
+};
+
+// Properties of the current device (cached per device).
+int device_info(DeviceInfo& info);
+
+// Grid for a grid-stride kernel over `items`: enough blocks to cover them,
+// at most blocks_per_cu per compute unit.
+int stream_grid(int64_t items, int blocks_per_cu, int& grid);
+
+// Persistent grid: the blocks that stay resident on the device, but no more
+// than the walks can feed (each block serves slots * kBlock walks at once).
+template <typename Kernel>
+int persistent_grid(Kernel kernel, int64_t num_walks, int slots, int& grid) {
+    DeviceInfo info;
+    if (int rc = device_info(info)) return rc;
+    int per_cu = 0;
+    MLXC_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kBlock, 0));
+    if (per_cu < 1) per_cu = 1;
+    const int64_t resident = static_cast<int64_t>(info.cus) * per_cu;
+    const int64_t per_block = static_cast<int64_t>(slots) * kBlock;
+    const int64_t feedable = (num_walks + per_block - 1) / per_block;
+    grid = static_cast<int>(feedable < resident ? feedable : resident);
+    if (grid < 1) grid = 1;
+    return MLXC_OK;
+}
+
+// Node ids and edge offsets fit the int32 fields of the record layouts.
+inline bool records_fit(int64_t num_nodes, int64_t num_edges) {
+    return num_nodes <= INT32_MAX && num_edges <= INT32_MAX;
+}
+
+// ---- prep_kernels.hip
+int launch_zero_work(int64_t* d_work, hipStream_t stream);
+int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
+                        int64_t num_edges, EdgeRecord* recs, int32_t* col32, hipStream_t stream);
+int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
+                     int64_t num_edges, int64_t num_walks, EdgeRecord* init, hipStream_t stream);
+int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
+                     int64_t num_edges, int64_t* d_work, hipStream_t stream);
+int launch_philox_fill(float* out, int64_t n, uint64_t seed, hipStream_t stream);
+
+// ---- uniform_walk.hip
+size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
+                               int32_t walk_length);
+int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes,
+                   hipStream_t stream);
+
+// ---- node2vec_walk.hip
+struct N2VParams {
+    double prob0, prob1, prob2;  // acceptance constants, BiasedRandomWalk.cpp:52-55
+    uint32_t key0, key1;         // Philox key (the seed)
+    int32_t rule;                // MLXC_RULE_*
+    bool rows_sorted;
+};
+size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
+                                int32_t walk_length);
+int launch_node2vec(const WalkArgs& a, const N2VParams& p, void* workspace,
+                    size_t workspace_bytes, hipStream_t stream);
+
+}  // namespace mlxc

@@ -169,7 +169,8 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike, rand: Te
     n_out = torch.empty((N, L + 1), dtype=torch.int64, device=device)
     e_out = torch.empty((N, L), dtype=torch.int64, device=device) if return_edges else None
     lib = _lib.load()
-    work = _workspace(lib.mlxc_walk_workspace_bytes(rowptr.numel() - 1, col.numel(), N), device)
+    work = _workspace(lib.mlxc_random_walk_workspace_bytes(rowptr.numel() - 1, col.numel(), N, L),
+                      device)
     with torch.cuda.device(device):
         rc = lib.mlxc_random_walk(_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(),
                                   _ptr(start), N, _ptr(rand), L, _ptr(n_out),
@@ -251,9 +252,11 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     N = start.numel()
     n_out = torch.empty((N, L + 1), dtype=torch.int64, device=device)
     e_out = torch.empty((N, L), dtype=torch.int64, device=device) if return_edges else None
-    work = _workspace(_lib.MLXC_WORK_WORDS * 8, device)
+    lib = _lib.load()
+    work = _workspace(lib.mlxc_rejection_sampling_workspace_bytes(rowptr.numel() - 1, col.numel(),
+                                                                  N, L), device)
     with torch.cuda.device(device):
-        rc = _lib.load().mlxc_rejection_sampling(
+        rc = lib.mlxc_rejection_sampling(
             _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,
             p, q, seed, _RULES[rule], 1 if rows_sorted else 0, _ptr(n_out),
             _ptr(e_out) if return_edges else None, work.data_ptr(), work.numel() * 8, handle)

@@ -60,8 +60,8 @@ def _load():
         lib.oracle_uniform_walk.argtypes = [P, i64, P, i64, P, i64, P, i32, P, P, P]
         lib.oracle_uniform_walk.restype = ctypes.c_int
         lib.oracle_node2vec_probs.argtypes = [dbl, dbl, P]
-        lib.oracle_node2vec_walk.argtypes = [P, i64, P, i64, P, i64, i32, dbl, dbl, u64, i32,
-                                             i32, P, P, P]
+        lib.oracle_node2vec_walk.argtypes = [P, i64, P, i64, P, i64, i64, i32, dbl, dbl, u64,
+                                             i32, i32, P, P, P]
         lib.oracle_node2vec_walk.restype = ctypes.c_int
         lib.oracle_node2vec_walk_libc.argtypes = [P, i64, P, i64, P, i64, i32, dbl, dbl, u32,
                                                   i32, P, P]
@@ -131,15 +131,17 @@ def node2vec_probs(p: float, q: float) -> np.ndarray:
 
 
 def node2vec_walk(rowptr, col, start, walk_length, p, q, seed, *, rule=RULE_REF_CHAIN,
-                  rows_sorted=True, with_edges=False):
-    """Returns (n_out, e_out or None, status, counts dict)."""
+                  rows_sorted=True, with_edges=False, first_walk=0):
+    """Returns (n_out, e_out or None, status, counts dict).  Walk n draws from
+    the Philox stream of walk index first_walk + n."""
     rowptr, col, start = _i64(rowptr), _i64(col), _i64(start).reshape(-1)
     N, L = start.size, int(walk_length)
     n_out = np.empty((N, L + 1), dtype=np.int64)
     e_out = np.empty((N, L), dtype=np.int64) if with_edges else None
     counts = Counts()
     st = _load().oracle_node2vec_walk(_p(rowptr), rowptr.size - 1, _p(col), col.size, _p(start),
-                                      N, L, float(p), float(q), int(seed) & (2**64 - 1),
+                                      N, int(first_walk), L, float(p), float(q),
+                                      int(seed) & (2**64 - 1),
                                       int(rule), 1 if rows_sorted else 0, _p(n_out), _p(e_out),
                                       ctypes.byref(counts))
     return n_out, e_out, st, counts.as_dict()

@@ -199,7 +199,7 @@ static int accept_candidate(int32_t rule, const double probs[3], double r,
 
 int oracle_node2vec_walk(const int64_t* rowptr, int64_t num_nodes,
                          const int64_t* col, int64_t num_edges,
-                         const int64_t* start, int64_t num_walks,
+                         const int64_t* start, int64_t num_walks, int64_t first_walk,
                          int32_t walk_length, double p, double q,
                          uint64_t seed, int32_t rule, int32_t rows_sorted,
                          int64_t* n_out, int64_t* e_out, oracle_counts* counts) {
@@ -223,7 +223,7 @@ int oracle_node2vec_walk(const int64_t* rowptr, int64_t num_nodes,
             else if (re - rs == 0) { sunk = 1; c.sink_walks++; }     /* :61-63 */
             else {                                                   /* :64-66 */
                 float u0, u1;
-                n2v_uniforms(seed, n, 0, 0u, &u0, &u1);
+                n2v_uniforms(seed, first_walk + n, 0, 0u, &u0, &u1);
                 e = rs + oracle_pick_index(u0, re - rs);
                 v = col[e];
                 c.moving_steps++;
@@ -250,7 +250,7 @@ int oracle_node2vec_walk(const int64_t* rowptr, int64_t num_nodes,
                     c.moving_steps++;
                     for (uint32_t trial = 0;; ++trial) {
                         float u0, u1;
-                        n2v_uniforms(seed, n, (int32_t)l, trial, &u0, &u1);
+                        n2v_uniforms(seed, first_walk + n, (int32_t)l, trial, &u0, &u1);
                         e = rs + oracle_pick_index(u0, re - rs);     /* :81 */
                         x = col[e];                                  /* :82 */
                         c.trials++;

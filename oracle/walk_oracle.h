@@ -72,12 +72,14 @@ int oracle_uniform_walk(const int64_t* rowptr, int64_t num_nodes,
 void oracle_node2vec_probs(double p, double q, double probs[3]);
 
 /* node2vec walk by rejection sampling, BiasedRandomWalk.cpp:57-100, driven
- * by the Philox stream u0/u1(seed; walk, step, trial).  Rows are searched
- * with a linear scan when rows_sorted == 0 (BiasedRandomWalk.cpp:20-28) and
- * with lower_bound otherwise (same answer on sorted rows). */
+ * by the Philox stream u0/u1(seed; walk, step, trial) where walk n of this
+ * call has stream index first_walk + n (so any block of a larger call can be
+ * recomputed).  Rows are searched with a linear scan when rows_sorted == 0
+ * (BiasedRandomWalk.cpp:20-28) and with lower_bound otherwise (same answer on
+ * sorted rows). */
 int oracle_node2vec_walk(const int64_t* rowptr, int64_t num_nodes,
                          const int64_t* col, int64_t num_edges,
-                         const int64_t* start, int64_t num_walks,
+                         const int64_t* start, int64_t num_walks, int64_t first_walk,
                          int32_t walk_length, double p, double q,
                          uint64_t seed, int32_t rule, int32_t rows_sorted,
                          int64_t* n_out, int64_t* e_out, oracle_counts* counts);

@@ -100,13 +100,15 @@ def test_other_entry_points_reject_bad_arguments():
 
 
 def test_workspace_size_query():
-    lib = _lib.load()
-    assert lib.mlxc_walk_workspace_bytes(10, 100, 7) == 256 + 16 * 107
-    assert lib.mlxc_walk_workspace_bytes(10, 0, 0) == 256
-    assert lib.mlxc_walk_workspace_bytes(2**31, 5, 1) == 32
-    assert lib.mlxc_walk_workspace_bytes(5, 2**31, 1) == 32
-    assert lib.mlxc_walk_workspace_bytes(-1, 5, 1) == 32
-    assert lib.mlxc_walk_workspace_bytes(5, 5, -1) == 32
+    q = _lib.load().mlxc_random_walk_workspace_bytes
+    assert q(10, 100, 100, 4) == 256 + 16 * 200   # 400 steps >= 4 * 100 edges: records
+    assert q(10, 100, 99, 4) == 256 + 16 * 99     # 396 steps < 400: start records only
+    assert q(10, 0, 0, 0) == 256 + 16 * 0
+    assert q(2**31, 5, 1, 1) == 32
+    assert q(5, 2**31, 1, 1) == 32
+    assert q(-1, 5, 1, 1) == 32
+    assert q(5, 5, -1, 1) == 32
+    assert q(5, 5, 1, -1) == 32
 
 
 def test_python_check_maps_codes():

@@ -164,13 +164,14 @@ def test_c2_full_size_properties(cuda):
 
 def _abi_walk(rowptr, col, start, rand_t, L, n_out_t, *, e_out=None, ws_bytes=None):
     """Calls mlxc_random_walk directly so each kernel path can be selected:
-    edge records (full workspace), CSR reads (minimal workspace), and the
-    unwindowed kernel (edge output or unaligned buffers)."""
+    edge records (full workspace, many steps per edge), CSR reads with start
+    records (workspace for start records only), and the unwindowed kernel
+    (minimal workspace, edge output or unaligned buffers)."""
     from mlx_cluster_amd import _lib
     lib = _lib.load()
     V, E = rowptr.numel() - 1, col.numel()
     if ws_bytes is None:
-        ws_bytes = lib.mlxc_walk_workspace_bytes(V, E, start.numel())
+        ws_bytes = 256 + 16 * (E + start.numel())  # room for edge + start records
     ws = torch.empty((ws_bytes + 7) // 8, dtype=torch.int64, device=rowptr.device)
     rc = lib.mlxc_random_walk(rowptr.data_ptr(), V, col.data_ptr(), E, start.data_ptr(),
                               start.numel(), rand_t, L, n_out_t,
@@ -181,9 +182,13 @@ def _abi_walk(rowptr, col, start, rand_t, L, n_out_t, *, e_out=None, ws_bytes=No
     assert int(ws[0].item()) == 0
 
 
-@pytest.mark.parametrize("N,L", [(1, 1), (33, 5), (1000, 16), (4097, 23), (20_000, 80)])
+@pytest.mark.parametrize("N,L", [(1, 1), (33, 5), (257, 4), (1000, 16), (4096, 23),
+                                 (20_000, 80)])
 def test_all_kernel_paths_agree(N, L, cuda):
-    rowptr, col = synth.rmat_csr(12, 30_000, seed=N, device=cuda)
+    # small graph (E <= 300) so that most shapes take >= 4 * E steps: the
+    # full workspace then selects the edge-record walk; N * L not a multiple
+    # of 4 selects the unwindowed kernel whatever the workspace
+    rowptr, col = synth.rmat_csr(7, 300, seed=N, device=cuda)
     V = rowptr.numel() - 1
     start = (torch.arange(N, device=cuda) * 131) % V
     rand = mc.philox_uniform(N * L + 1, 17, device=cuda)
@@ -191,7 +196,8 @@ def test_all_kernel_paths_agree(N, L, cuda):
                                         start.cpu().numpy(), rand[:N * L].cpu().numpy(), L)
     assert st == 0
     outs = {}
-    for name, kw in [("records", {}), ("csr", dict(ws_bytes=32))]:
+    csr_ws = 256 + 16 * N
+    for name, kw in [("records", {}), ("csr", dict(ws_bytes=csr_ws)), ("plain", dict(ws_bytes=32))]:
         out = torch.full((N, L + 1), -7, dtype=torch.int64, device=cuda)
         _abi_walk(rowptr, col, start, rand.data_ptr(), L, out.data_ptr(), **kw)
         outs[name] = out
