@@ -146,7 +146,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
     unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.work + 1);
     WaveQueue q{0, 0};
     int phase[W];
-    int64_t n[W], l[W], e[W];  // e: record index read this iteration (kSlotWalk)
+    int64_t n[W];
+    int32_t l[W], e[W];        // e: record index read this iteration (kSlotWalk)
     int64_t fr[W];             // rand index whose block the next read brings along
     bool need_block[W];        // ... if set
     RandWindow<RW> rw[W];
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                 if (ow[s].count) ow_flush(ow[s], a.n_out, g);
             } else {
                 // step l (0-based) leaves this node with uniform rand[n*L + l]
-                e[s] = begin + pick_index(rw[s].w[0], deg);
+                e[s] = static_cast<int32_t>(begin + pick_index(rw[s].w[0], deg));
                 rw_shift1(rw[s]);
                 rw[s].valid -= 1;
                 need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
@@ -270,7 +271,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
     unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.work + 1);
     WaveQueue q{0, 0};
     int phase[W];
-    int64_t n[W], l[W], e[W], v[W], fr[W];
+    int64_t n[W], fr[W];
+    int32_t l[W], e[W], v[W];  // steps, edge and node ids fit in int32 here
     bool need_block[W];
     RandWindow<RW> rw[W];
     OutWin<int32_t> ow[W];
@@ -325,7 +327,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
         }
         if (!__any(alive)) break;
 
-        // 3. Consume.
+        // 3. Consume.  Each slot ends the iteration with at most one
+        // buffered entry, then at most one tail fill or flush.
 #pragma unroll
         for (int s = 0; s < W; ++s) {
             if (ph[s] == kSlotIdle || ph[s] == kSlotDone) {
@@ -339,40 +342,32 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                 need_block[s] = false;
             }
             const int64_t g0 = n[s] * L1;
-            int64_t begin = 0, deg = 0;
-            bool pick = false, stop = false;
+            int64_t g = g0 + l[s];  // output index of the last buffered entry
+            int64_t begin = 0, deg = -1;  // row to pick from (deg >= 0: pick)
+            bool push = false, fill = false, flush = false;
+            uint32_t bad = 0;
             if (ph[s] == kSlotStart) {
                 ow[s].count = 0;
                 v[s] = row[s].x;
-                ow_push(ow[s], a.n_out, g0, row[s].x);
+                push = true;
                 if (row[s].z < 0) {
-                    status |= row[s].z == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
-                    ow_fill(ow[s], a.n_out, g0 + 1, g0 + L, row[s].x);
-                    stop = true;
+                    bad = row[s].z == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
                 } else if (L == 0) {
-                    ow_flush(ow[s], a.n_out, g0);
-                    stop = true;
+                    flush = true;
                 } else {
                     begin = row[s].y;
                     deg = row[s].z;
-                    pick = true;
                 }
             } else if (ph[s] == kSlotCol) {
-                const int64_t g = g0 + l[s] + 1;
                 if (!node_ok(cv[s], a.num_nodes)) {
-                    status |= MLXC_STATUS_BAD_NODE;
-                    ow_fill(ow[s], a.n_out, g, g0 + L, static_cast<int32_t>(v[s]));
-                    stop = true;
+                    bad = MLXC_STATUS_BAD_NODE;
                 } else {
-                    v[s] = cv[s];
+                    v[s] = static_cast<int32_t>(cv[s]);
                     l[s] += 1;
-                    ow_push(ow[s], a.n_out, g, static_cast<int32_t>(cv[s]));
-                    if (l[s] == L) {
-                        if (ow[s].count) ow_flush(ow[s], a.n_out, g);
-                        stop = true;
-                    } else {
-                        phase[s] = kSlotRow;
-                    }
+                    g += 1;
+                    push = true;
+                    if (l[s] == L) flush = true;
+                    else phase[s] = kSlotRow;
                 }
             } else {  // kSlotRow
                 const RowBounds rb = {
@@ -381,29 +376,32 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                     static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(row[s].w)) << 32) |
                                          static_cast<uint32_t>(row[s].z))};
                 if (!row_ok(rb, a.num_edges)) {
-                    status |= MLXC_STATUS_BAD_ROW;
-                    ow_fill(ow[s], a.n_out, g0 + l[s] + 1, g0 + L, static_cast<int32_t>(v[s]));
-                    stop = true;
+                    bad = MLXC_STATUS_BAD_ROW;
                 } else {
                     begin = rb.begin;
                     deg = rb.end - rb.begin;
-                    pick = true;
                 }
             }
-            if (pick) {
-                if (deg == 0) {  // absorbing node: the walk stays
-                    ow_fill(ow[s], a.n_out, g0 + l[s] + 1, g0 + L, static_cast<int32_t>(v[s]));
-                    stop = true;
-                } else {
-                    e[s] = begin + pick_index(rw[s].w[0], deg);
-                    rw_shift1(rw[s]);
-                    rw[s].valid -= 1;
-                    need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
-                    fr[s] = n[s] * L + l[s] + 1;
-                    phase[s] = kSlotCol;
-                }
+            if (bad) {
+                status |= bad;
+                fill = true;  // stop the walk (outputs of a flagged call are unspecified)
+            } else if (deg == 0) {
+                fill = true;  // absorbing node: the walk stays
+            } else if (deg > 0) {
+                e[s] = static_cast<int32_t>(begin + pick_index(rw[s].w[0], deg));
+                rw_shift1(rw[s]);
+                rw[s].valid -= 1;
+                need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
+                fr[s] = n[s] * L + l[s] + 1;
+                phase[s] = kSlotCol;
             }
-            if (stop) phase[s] = kSlotIdle;
+            if (push) ow_push(ow[s], a.n_out, g, v[s]);
+            if (fill) {
+                ow_fill(ow[s], a.n_out, g + 1, g0 + L, v[s]);
+            } else if (flush && ow[s].count) {
+                ow_flush(ow[s], a.n_out, g);
+            }
+            if (fill || flush) phase[s] = kSlotIdle;
         }
     }
     if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
@@ -411,8 +409,15 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
 
 // ------------------------------------------------------------- launcher
 
-#ifndef MLXC_UNIFORM_SLOTS
-#define MLXC_UNIFORM_SLOTS 1   // walks in flight per lane
+// Walks in flight per lane.  The record walk is bound by the random-read
+// rate and runs best at the higher occupancy of one slot; the CSR walk (two
+// dependent reads per step, often over graphs of several GB) is latency-bound
+// and gains from a second slot.  Measured on MI355X, configurations 2 and 4.
+#ifndef MLXC_REC_SLOTS
+#define MLXC_REC_SLOTS 1
+#endif
+#ifndef MLXC_CSR_SLOTS
+#define MLXC_CSR_SLOTS 2
 #endif
 #ifndef MLXC_RAND_WINDOW
 #define MLXC_RAND_WINDOW 16    // uniforms per rand block (4-byte floats)
@@ -473,7 +478,6 @@ size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num
 
 int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes,
                    hipStream_t stream) {
-    constexpr int W = MLXC_UNIFORM_SLOTS;
     constexpr int RW = MLXC_RAND_WINDOW;
     EdgeRecord* recs = reinterpret_cast<EdgeRecord*>(static_cast<char*>(workspace) + kRecordOffset);
     switch (uniform_mode(a, workspace_bytes)) {
@@ -485,7 +489,8 @@ int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes,
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, stream))
             return rc;
-        return launch_walk_kernel(uniform_walk_rec_kernel<W, RW>, W, a, stream,
+        return launch_walk_kernel(uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW>, MLXC_REC_SLOTS, a,
+                                  stream,
                                   static_cast<const EdgeRecord*>(recs),
                                   static_cast<const EdgeRecord*>(init));
     }
@@ -494,7 +499,8 @@ int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes,
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, stream))
             return rc;
-        return launch_walk_kernel(uniform_walk_csr_kernel<W, RW>, W, a, stream,
+        return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW>, MLXC_CSR_SLOTS, a,
+                                  stream,
                                   static_cast<const EdgeRecord*>(init));
     }
     case UniformMode::kPlain:
