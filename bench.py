@@ -220,7 +220,7 @@ def main():
     else:
         rand = None
         step = lambda: mc.rejection_sampling(rowptr, col, start, L, extra["p"], extra["q"],
-                                             seed=extra["seed"], rows_sorted=True)
+                                             seed=extra["seed"])
 
     for _ in range(args.warmup):
         out = step()

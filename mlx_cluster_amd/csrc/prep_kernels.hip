@@ -10,12 +10,15 @@ __global__ void zero_words_kernel(int64_t* p, int n) {
 }
 
 // Edge records (see EdgeRecord); optionally also col as int32 (col32 may be
-// null), the neighbour-search array of the node2vec walk.
+// null) and every index_stride-th entry of it (index), the neighbour-search
+// arrays of the node2vec walk.
 __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __restrict__ rowptr,
                                                              const int64_t* __restrict__ col,
                                                              int64_t num_nodes, int64_t num_edges,
                                                              EdgeRecord* __restrict__ rec,
-                                                             int32_t* __restrict__ col32) {
+                                                             int32_t* __restrict__ col32,
+                                                             int32_t* __restrict__ index,
+                                                             int index_stride) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t e = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; e < num_edges;
@@ -32,7 +35,10 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
             }
         }
         *reinterpret_cast<i32x4*>(rec + e) = r;
-        if (col32) col32[e] = r.x;
+        if (col32) {
+            col32[e] = r.x;
+            if (e % index_stride == 0) index[e / index_stride] = r.x;
+        }
     }
 }
 
@@ -143,12 +149,13 @@ int launch_zero_work(int64_t* d_work, hipStream_t stream) {
 }
 
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
-                        int64_t num_edges, EdgeRecord* recs, int32_t* col32, hipStream_t stream) {
+                        int64_t num_edges, EdgeRecord* recs, int32_t* col32, int32_t* index,
+                        int index_stride, hipStream_t stream) {
     if (num_edges == 0) return MLXC_OK;
     int grid = 0;
     if (int rc = stream_grid(num_edges, 16, grid)) return rc;
     hipLaunchKernelGGL(edge_record_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col,
-                       num_nodes, num_edges, recs, col32);
+                       num_nodes, num_edges, recs, col32, index, index_stride);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

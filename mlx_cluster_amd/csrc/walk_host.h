@@ -59,8 +59,10 @@ inline bool records_fit(int64_t num_nodes, int64_t num_edges) {
 
 // ---- prep_kernels.hip
 int launch_zero_work(int64_t* d_work, hipStream_t stream);
+// col32 / index may be null (the uniform walk needs neither).
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
-                        int64_t num_edges, EdgeRecord* recs, int32_t* col32, hipStream_t stream);
+                        int64_t num_edges, EdgeRecord* recs, int32_t* col32, int32_t* index,
+                        int index_stride, hipStream_t stream);
 int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
                      int64_t num_edges, int64_t num_walks, EdgeRecord* init, hipStream_t stream);
 int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,

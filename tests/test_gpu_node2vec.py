@@ -20,9 +20,15 @@ RULE_NAME = {oracle.RULE_REF_CHAIN: "ref_chain", oracle.RULE_NODE2VEC_EXACT: "no
 
 
 def gpu_walk(rowptr, col, start, L, p, q, seed, rule, cuda, **kw):
+    """Runs both kernels: the record walk (node output only) and the direct
+    CSR walk (taken when edge ids are requested); their node outputs must
+    agree.  Returns (nodes, edges)."""
     t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.int64)).to(cuda)
-    n, e = mc.rejection_sampling(t(rowptr), t(col), t(start), L, p, q, seed=seed,
-                                 rule=RULE_NAME[rule], return_edges=True, **kw)
+    args = (t(rowptr), t(col), t(start), L, p, q)
+    n_rec = mc.rejection_sampling(*args, seed=seed, rule=RULE_NAME[rule], **kw)
+    n, e = mc.rejection_sampling(*args, seed=seed, rule=RULE_NAME[rule], return_edges=True, **kw)
+    np.testing.assert_array_equal(n_rec.cpu().numpy(), n.cpu().numpy(),
+                                  err_msg="record walk != CSR walk")
     return n.cpu().numpy(), e.cpu().numpy()
 
 
@@ -65,6 +71,18 @@ def test_unsorted_rows_use_linear_scan(rule, cuda):
     assert mc.csr_check(rowptr, col) == oracle.csr_flags(rowptr, col)
     start = np.arange(1000) % 500
     assert_parity(rowptr, col, start, 15, 0.5, 2.0, 5, rule, cuda, sorted_rows=False)
+    # the same graph declared sorted by the caller on sorted rows
+    srp, scol = undirected(500, rng.integers(0, 500, (4000, 2)))
+    assert_parity(srp, scol, start, 15, 0.5, 2.0, 5, rule, cuda, rows_sorted=True)
+
+
+def test_trial_cap_matches_oracle(cuda):
+    """p = q = 1e6 makes prob_2 = 1e-6: most steps hit the 65,536-trial cap
+    and keep their last candidate, identically in oracle and kernels."""
+    rowptr, col = undirected(40, [(i, (i * 7 + 3) % 40) for i in range(40)] +
+                             [(i, (i * 11 + 5) % 40) for i in range(40)])
+    start = np.arange(64) % 40
+    assert_parity(rowptr, col, start, 3, 1e6, 1e6, 8, oracle.RULE_NODE2VEC_EXACT, cuda)
 
 
 def test_p1_q1_equals_uniform_walk(cuda):
