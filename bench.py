@@ -34,10 +34,18 @@ CONFIGS = {
     "c2": ("R-MAT 2^20 uniform walk, 10 walks/node, L=80", "uniform",
            dict(scale=20, samples=1 << 24, symmetrize=False), 10, 80, {}),
     "c3": ("node2vec p=0.5 q=2 on symmetrized R-MAT 2^20, 4 walks/node, L=40", "node2vec",
-           dict(scale=20, samples=1 << 24, symmetrize=True), 4, 40, dict(p=0.5, q=2.0, seed=3)),
+           dict(scale=20, samples=1 << 24, symmetrize=True), 4, 40,
+           dict(p=0.5, q=2.0, seed=3, rule="ref_chain")),
     "c4": ("R-MAT 2^24 uniform walk, 1 walk/node, L=20", "uniform",
            dict(scale=24, samples=1 << 28, symmetrize=False), 1, 20, {}),
+    "c5": ("node2vec p=4 q=0.25 (reference chain) on BA 4M nodes m=20 + 64 hubs of 500K, "
+           "2 walks/node, L=30", "node2vec", dict(ba=(4_000_000, 20, 64, 500_000)), 2, 30,
+           dict(p=4.0, q=0.25, seed=5, rule="ref_chain")),
+    "c5x": ("node2vec p=4 q=0.25 (analytic rule) on BA 4M nodes m=20 + 64 hubs of 500K, "
+            "2 walks/node, L=30", "node2vec", dict(ba=(4_000_000, 20, 64, 500_000)), 2, 30,
+            dict(p=4.0, q=0.25, seed=5, rule="node2vec")),
 }
+RULE_ID = {"ref_chain": 0, "node2vec": 1}
 
 
 def log(*a):
@@ -135,7 +143,8 @@ def node2vec_bytes(np, oracle, rowptr_h, col_h, start_h, L, extra, walks=200_000
     N = start_h.shape[0]
     idx = np.linspace(0, N - 1, min(N, walks)).astype(np.int64)
     _, _, st, c = oracle.node2vec_walk(rowptr_h, col_h, start_h[idx], L, extra["p"], extra["q"],
-                                       extra["seed"], rule=0, rows_sorted=True)
+                                       extra["seed"], rule=RULE_ID[extra["rule"]],
+                                       rows_sorted=True)
     f = N / idx.size
     S, Z, T = c["moving_steps"] * f, c["sink_walks"] * f, c["trials"] * f
     Q, P = c["member_tests"] * f, c["member_lines"] * f
@@ -147,15 +156,17 @@ def node2vec_bytes(np, oracle, rowptr_h, col_h, start_h, L, extra, walks=200_000
 
 def cpu_baseline_node2vec(np, oracle, rowptr_h, col_h, start, L, extra, target_s=12.0):
     N = start.shape[0]
-    probe = min(N, 5_000)
+    probe = min(N, 2_000)
     idx = np.linspace(0, N - 1, probe).astype(np.int64)
+    rule = RULE_ID[extra["rule"]]
     t0 = time.perf_counter()
-    oracle.node2vec_walk_libc(rowptr_h, col_h, start[idx], L, extra["p"], extra["q"], 1)
+    oracle.node2vec_walk_libc(rowptr_h, col_h, start[idx], L, extra["p"], extra["q"], 1, rule=rule)
     rate = probe * L / (time.perf_counter() - t0)
     walks = int(min(N, max(probe, target_s * rate / L)))
     idx = np.linspace(0, N - 1, walks).astype(np.int64)
     t0 = time.perf_counter()
-    _, st = oracle.node2vec_walk_libc(rowptr_h, col_h, start[idx], L, extra["p"], extra["q"], 1)
+    _, st = oracle.node2vec_walk_libc(rowptr_h, col_h, start[idx], L, extra["p"], extra["q"], 1,
+                                      rule=rule)
     dt = time.perf_counter() - t0
     assert st == 0
     return walks * L / dt, walks, dt
@@ -205,8 +216,12 @@ def main():
 
     desc, kind, gargs, per_node, L, extra = CONFIGS[args.config]
     log(f"config {args.config}: {desc} on {torch.cuda.get_device_name(dev)}")
-    rowptr, col = synth.rmat_csr(gargs["scale"], gargs["samples"], seed=0, device=dev,
-                                 symmetrize=gargs["symmetrize"])
+    if "ba" in gargs:
+        nodes, m, hubs, hub_degree = gargs["ba"]
+        rowptr, col = synth.ba_hub_csr(nodes, m, hubs, hub_degree, seed=0, device=dev)
+    else:
+        rowptr, col = synth.rmat_csr(gargs["scale"], gargs["samples"], seed=0, device=dev,
+                                     symmetrize=gargs["symmetrize"])
     V = rowptr.numel() - 1
     E = col.numel()
     N = per_node * V
@@ -220,7 +235,7 @@ def main():
     else:
         rand = None
         step = lambda: mc.rejection_sampling(rowptr, col, start, L, extra["p"], extra["q"],
-                                             seed=extra["seed"])
+                                             seed=extra["seed"], rule=extra["rule"])
 
     for _ in range(args.warmup):
         out = step()
@@ -280,8 +295,9 @@ def main():
         # walks [s0, s0 + 2000) with the oracle told its first walk id
         s0 = int(sample[0].item()) % max(1, N - 2000)
         ref, _, st, _ = oracle.node2vec_walk(rowptr_h, col_h, start[s0:s0 + 2000].cpu().numpy(),
-                                             L, extra["p"], extra["q"], extra["seed"], rule=0,
-                                             rows_sorted=True, first_walk=s0)
+                                             L, extra["p"], extra["q"], extra["seed"],
+                                             rule=RULE_ID[extra["rule"]], rows_sorted=True,
+                                             first_walk=s0)
         got = out[s0:s0 + 2000].cpu().numpy()
     parity = bool(st == 0 and np.array_equal(got, ref))
     cpu = None

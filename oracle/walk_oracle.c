@@ -274,6 +274,14 @@ int oracle_node2vec_walk(const int64_t* rowptr, int64_t num_nodes,
     return status;
 }
 
+/* is_neighbor exactly as BiasedRandomWalk.cpp:20-28: a linear scan of
+ * row(v) for w. */
+static int is_neighbor_scan(const int64_t* rowptr, const int64_t* col, int64_t v, int64_t w) {
+    for (int64_t i = rowptr[v]; i < rowptr[v + 1]; ++i)
+        if (col[i] == w) return 1;
+    return 0;
+}
+
 int oracle_node2vec_walk_libc(const int64_t* rowptr, int64_t num_nodes,
                               const int64_t* col, int64_t num_edges,
                               const int64_t* start, int64_t num_walks,
@@ -316,9 +324,16 @@ int oracle_node2vec_walk_libc(const int64_t* rowptr, int64_t num_nodes,
                         x = col[e];
                         double r = ((double)rand() / (RAND_MAX));   /* :84 */
                         if (!node_ok(x, num_nodes)) { bad = 1; break; }
-                        if (accept_candidate(rule, probs, r, rowptr, col, num_edges, x, t, 0,
-                                             &c, &bad))
+                        if (rule == ORACLE_RULE_REF_CHAIN) {
+                            /* :86-91 evaluated as written: is_neighbor runs
+                             * whenever the first clause fails */
+                            if (x == t && r < probs[0]) break;
+                            else if (is_neighbor_scan(rowptr, col, x, t) && r < probs[1]) break;
+                            else if (r < probs[2]) break;
+                        } else if (accept_candidate(rule, probs, r, rowptr, col, num_edges, x, t,
+                                                    0, &c, &bad)) {
                             break;
+                        }
                         if (bad || trial + 1 >= ORACLE_MAX_TRIALS) break;
                     }
                 }

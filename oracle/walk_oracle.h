@@ -86,7 +86,10 @@ int oracle_node2vec_walk(const int64_t* rowptr, int64_t num_nodes,
 
 /* The same walk driven by libc rand() exactly as the reference draws it
  * (rand() % deg for the candidate, rand()/RAND_MAX for the test), for
- * distribution tests and the CPU timing baseline.  srand(libc_seed) first. */
+ * distribution tests and the CPU timing baseline.  srand(libc_seed) first.
+ * The reference chain is evaluated as written, with its linear is_neighbor
+ * scan on every trial whose first clause fails, so the timing is the
+ * reference's. */
 int oracle_node2vec_walk_libc(const int64_t* rowptr, int64_t num_nodes,
                               const int64_t* col, int64_t num_edges,
                               const int64_t* start, int64_t num_walks,
