@@ -50,6 +50,11 @@ extern "C" {
 #define MLXC_RULE_REF_CHAIN 0      /* BiasedRandomWalk.cpp:86-91, reproduced term for term */
 #define MLXC_RULE_NODE2VEC_EXACT 1 /* analytic node2vec: accept iff r < prob_d(t, x)      */
 
+/* Row order of the graph passed to mlxc_rejection_sampling. */
+#define MLXC_ROWS_UNSORTED 0  /* scan rows linearly, as the reference's is_neighbor does */
+#define MLXC_ROWS_SORTED 1    /* the caller promises every row is sorted ascending */
+#define MLXC_ROWS_DETECT 2    /* the call checks the rows on the device (and validates the CSR) */
+
 /* Bits written by mlxc_csr_check. */
 #define MLXC_CSR_BAD_ROWPTR 1   /* rowptr[0] != 0, rowptr[V] != E, or decreasing */
 #define MLXC_CSR_BAD_COL 2      /* a col value outside [0, V) */
@@ -118,15 +123,17 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes,
  * counter-based stream Philox4x32-10(key = seed; counter = (walk lo, walk hi,
  * step, trial)): word 0 picks the candidate as in mlxc_random_walk, word 1
  * gives r = (x1 >> 8) * 2^-24 for the acceptance test against the FP64
- * constants of BiasedRandomWalk.cpp:52-55.  rows_sorted != 0 promises that
- * every row of col is sorted ascending (binary-search neighbour test);
- * rows_sorted == 0 scans rows linearly, as the reference does.
+ * constants of BiasedRandomWalk.cpp:52-55.  `rows` is one of MLXC_ROWS_*:
+ * sorted rows are searched through a block index, unsorted rows scanned
+ * linearly as the reference does; MLXC_ROWS_DETECT decides on the device in
+ * the call's preparation pass, which also validates the whole CSR (status
+ * bits as for the walk).
  */
 int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes,
                             const int64_t* d_col, int64_t num_edges,
                             const int64_t* d_start, int64_t num_walks,
                             int32_t walk_length, double p, double q,
-                            uint64_t seed, int32_t rule, int32_t rows_sorted,
+                            uint64_t seed, int32_t rule, int32_t rows,
                             int64_t* d_n_out, int64_t* d_e_out,
                             void* d_workspace, size_t workspace_bytes, void* stream);
 

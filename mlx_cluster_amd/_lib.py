@@ -24,6 +24,9 @@ MLXC_STATUS_BAD_NODE = 1
 MLXC_STATUS_BAD_ROW = 2
 MLXC_RULE_REF_CHAIN = 0
 MLXC_RULE_NODE2VEC_EXACT = 1
+MLXC_ROWS_UNSORTED = 0
+MLXC_ROWS_SORTED = 1
+MLXC_ROWS_DETECT = 2
 MLXC_CSR_BAD_ROWPTR = 1
 MLXC_CSR_BAD_COL = 2
 MLXC_CSR_UNSORTED = 4

@@ -108,7 +108,7 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* 
 int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
                             int64_t num_edges, const int64_t* d_start, int64_t num_walks,
                             int32_t walk_length, double p, double q, uint64_t seed,
-                            int32_t rule, int32_t rows_sorted, int64_t* d_n_out,
+                            int32_t rule, int32_t rows, int64_t* d_n_out,
                             int64_t* d_e_out, void* d_workspace, size_t workspace_bytes,
                             void* stream) {
     if (int rc = check_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
@@ -119,6 +119,9 @@ int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const in
     if (rule != MLXC_RULE_REF_CHAIN && rule != MLXC_RULE_NODE2VEC_EXACT)
         return fail(MLXC_ERR_INVALID_ARGUMENT,
                     "rule must be MLXC_RULE_REF_CHAIN or MLXC_RULE_NODE2VEC_EXACT");
+    if (rows != MLXC_ROWS_UNSORTED && rows != MLXC_ROWS_SORTED && rows != MLXC_ROWS_DETECT)
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "rows must be MLXC_ROWS_UNSORTED, MLXC_ROWS_SORTED or MLXC_ROWS_DETECT");
     hipStream_t s = static_cast<hipStream_t>(stream);
     int64_t* d_work = static_cast<int64_t*>(d_workspace);
     if (int rc = launch_zero_work(d_work, s)) return rc;
@@ -132,7 +135,7 @@ int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const in
     prm.key0 = static_cast<uint32_t>(seed);
     prm.key1 = static_cast<uint32_t>(seed >> 32);
     prm.rule = rule;
-    prm.rows_sorted = rows_sorted != 0;
+    prm.rows = rows;
     const WalkArgs a{d_rowptr, d_col, d_start, nullptr, d_n_out, d_e_out, d_work,
                      num_nodes, num_edges, num_walks, walk_length};
     return launch_node2vec(a, prm, d_workspace, workspace_bytes, s);

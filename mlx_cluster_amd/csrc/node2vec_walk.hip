@@ -181,6 +181,7 @@ struct N2VRecArgs {
     const EdgeRecord* init;   // [num_walks]
     const int32_t* col32;     // [num_edges rounded up to kSearchBlock] col as int32
     const int32_t* index;     // [ceil(num_edges / kSearchBlock)] col32[kSearchBlock * j]
+    int32_t rows;             // MLXC_ROWS_*; DETECT reads the prep pass's counts in work[2..3]
     double prob0, prob1, prob2;
     uint32_t key0, key1;
 };
@@ -219,9 +220,11 @@ __device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, double r, bool 
 // waits once.  Sorted rows are searched through the block index (see
 // kSearchBlock); unsorted rows are scanned one entry per iteration, as the
 // reference scans them.
-template <int kRule, bool kSorted>
+template <int kRule>
 __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const bool sorted = a.rows == MLXC_ROWS_SORTED ||
+                        (a.rows == MLXC_ROWS_DETECT && a.w.work[2] == a.w.work[3]);
     const int64_t L = a.w.walk_length;
     const int64_t L1 = L + 1;
     const int64_t N = a.w.num_walks;
@@ -314,7 +317,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                 } else if (dx == 0) {
                     accept = n2v_resolve<kRule>(a, static_cast<double>(r), false);
                     next_trial = !accept;
-                } else if (!kSorted) {
+                } else if (!sorted) {
                     lo = bx;
                     hi = bx + dx;
                     phase = kN2vScan;
@@ -449,9 +452,9 @@ int dispatch_n2v(const N2VArgs& a, bool sorted, bool edges, hipStream_t stream) 
                  : launch_n2v<kRule, false, false>(a, stream);
 }
 
-template <int kRule, bool kSorted>
+template <int kRule>
 int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
-    auto kernel = node2vec_rec_kernel<kRule, kSorted>;
+    auto kernel = node2vec_rec_kernel<kRule>;
     int grid = 0;
     if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
@@ -496,8 +499,11 @@ int launch_node2vec(const WalkArgs& w, const N2VParams& p, void* workspace, size
         EdgeRecord* init = recs + w.num_edges;
         int32_t* col32 = reinterpret_cast<int32_t*>(base + lay.col32);
         int32_t* index = reinterpret_cast<int32_t*>(base + lay.index);
+        // one pass builds the search arrays and, for MLXC_ROWS_DETECT, checks
+        // the rows (the walk reads the result on the device: no host sync)
         if (int rc = launch_edge_records(w.rowptr, w.col, w.num_nodes, w.num_edges, recs, col32,
-                                         index, kSearchBlock, stream))
+                                         index, kSearchBlock,
+                                         p.rows == MLXC_ROWS_DETECT ? w.work : nullptr, stream))
             return rc;
         if (int rc = launch_walk_init(w.rowptr, w.start, w.num_nodes, w.num_edges, w.num_walks,
                                       init, stream))
@@ -511,13 +517,25 @@ int launch_node2vec(const WalkArgs& w, const N2VParams& p, void* workspace, size
         a.prob2 = p.prob2;
         a.key0 = p.key0;
         a.key1 = p.key1;
-        if (p.rule == MLXC_RULE_REF_CHAIN)
-            return p.rows_sorted ? launch_n2v_rec<MLXC_RULE_REF_CHAIN, true>(a, stream)
-                                 : launch_n2v_rec<MLXC_RULE_REF_CHAIN, false>(a, stream);
-        return p.rows_sorted ? launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, true>(a, stream)
-                             : launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, false>(a, stream);
+        a.rows = p.rows;
+        return p.rule == MLXC_RULE_REF_CHAIN ? launch_n2v_rec<MLXC_RULE_REF_CHAIN>(a, stream)
+                                             : launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT>(a, stream);
     }
-    // Edge output or graphs beyond int32: the direct CSR kernel.
+    // Edge output or graphs beyond int32: the direct CSR kernel, which needs
+    // the row order on the host.
+    bool sorted = p.rows == MLXC_ROWS_SORTED;
+    if (p.rows == MLXC_ROWS_DETECT) {
+        if (int rc = launch_csr_check(w.rowptr, w.num_nodes, w.col, w.num_edges, w.work, stream))
+            return rc;
+        int64_t host[3] = {0, 0, 0};
+        MLXC_HIP_TRY(hipMemcpyAsync(host, w.work, sizeof(host), hipMemcpyDeviceToHost, stream));
+        MLXC_HIP_TRY(hipStreamSynchronize(stream));
+        if (host[0] & MLXC_CSR_BAD_ROWPTR) return fail(MLXC_ERR_INVALID_ARGUMENT, "rowptr is malformed");
+        if (host[0] & MLXC_CSR_BAD_COL)
+            return fail(MLXC_ERR_INVALID_ARGUMENT, "a col entry is outside [0, num_nodes)");
+        sorted = host[1] == host[2];
+        if (int rc = launch_zero_work(w.work, stream)) return rc;
+    }
     N2VArgs a;
     a.w = w;
     a.prob0 = p.prob0;
@@ -527,8 +545,8 @@ int launch_node2vec(const WalkArgs& w, const N2VParams& p, void* workspace, size
     a.key1 = p.key1;
     const bool edges = w.e_out != nullptr;
     return p.rule == MLXC_RULE_REF_CHAIN
-               ? dispatch_n2v<MLXC_RULE_REF_CHAIN>(a, p.rows_sorted, edges, stream)
-               : dispatch_n2v<MLXC_RULE_NODE2VEC_EXACT>(a, p.rows_sorted, edges, stream);
+               ? dispatch_n2v<MLXC_RULE_REF_CHAIN>(a, sorted, edges, stream)
+               : dispatch_n2v<MLXC_RULE_NODE2VEC_EXACT>(a, sorted, edges, stream);
 }
 
 }  // namespace mlxc

@@ -9,21 +9,75 @@ __global__ void zero_words_kernel(int64_t* p, int n) {
     if (i < n) p[i] = 0;
 }
 
+__device__ __forceinline__ int64_t wave_sum(int64_t x) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
+    return x;
+}
+
+__device__ __forceinline__ uint32_t wave_or(uint32_t x) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) x |= __shfl_xor(x, off, kWave);
+    return x;
+}
+
+// CSR validation, accumulated per thread and reduced per wave.  Rows are
+// sorted iff every position i >= 1 with col[i] < col[i-1] starts a non-empty
+// row, i.e. iff desc == start_desc.
+struct CsrCheck {
+    bool bad_rowptr = false;  // rowptr[0] != 0, rowptr[V] != E, or decreasing
+    bool bad_col = false;     // a col value outside [0, V)
+    int64_t desc = 0;
+    int64_t start_desc = 0;
+
+    // node-parallel part: thread gid of a grid of `stride` threads
+    __device__ void nodes(const int64_t* rowptr, int64_t V, const int64_t* col, int64_t E,
+                          int64_t gid, int64_t stride) {
+        if (gid == 0 && (rowptr[0] != 0 || rowptr[V] != E)) bad_rowptr = true;
+        for (int64_t v = gid; v < V; v += stride) {
+            const int64_t rs = rowptr[v], re = rowptr[v + 1];
+            if (re < rs) bad_rowptr = true;
+            if (rs >= 1 && re > rs && re <= E && col[rs] < col[rs - 1]) ++start_desc;
+        }
+    }
+    // edge-parallel part: entry i holding c
+    __device__ void edge(const int64_t* col, int64_t V, int64_t i, int64_t c) {
+        if (!node_ok(c, V)) bad_col = true;
+        if (i >= 1 && c < col[i - 1]) ++desc;
+    }
+    // adds the wave's totals to the given words (lane 0 of each wave)
+    __device__ void flush(unsigned long long* bits_word, uint32_t rowptr_bit, uint32_t col_bit,
+                          unsigned long long* desc_word, unsigned long long* start_desc_word) {
+        const uint32_t bits = wave_or((bad_rowptr ? rowptr_bit : 0u) | (bad_col ? col_bit : 0u));
+        const int64_t d = wave_sum(desc), sd = wave_sum(start_desc);
+        if (__lane_id() == 0) {
+            if (bits) atomicOr(bits_word, static_cast<unsigned long long>(bits));
+            if (d) atomicAdd(desc_word, static_cast<unsigned long long>(d));
+            if (sd) atomicAdd(start_desc_word, static_cast<unsigned long long>(sd));
+        }
+    }
+};
+
 // Edge records (see EdgeRecord); optionally also col as int32 (col32 may be
 // null) and every index_stride-th entry of it (index), the neighbour-search
-// arrays of the node2vec walk.
+// arrays of the node2vec walk.  With a non-null work pointer the same pass
+// validates the whole CSR (status bits into work[0]) and counts the row
+// descents into work[2] / work[3], from which the node2vec walk decides
+// whether its rows are sorted.
 __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __restrict__ rowptr,
                                                              const int64_t* __restrict__ col,
                                                              int64_t num_nodes, int64_t num_edges,
                                                              EdgeRecord* __restrict__ rec,
                                                              int32_t* __restrict__ col32,
                                                              int32_t* __restrict__ index,
-                                                             int index_stride) {
+                                                             int index_stride, int64_t* work) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-    for (int64_t e = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; e < num_edges;
-         e += stride) {
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    CsrCheck check;
+    for (int64_t e = gid; e < num_edges; e += stride) {
         const int64_t c = col[e];
+        if (work) check.edge(col, num_nodes, e, c);
         i32x4 r = {static_cast<int32_t>(c), 0, kRecBadNode, 0};
         if (node_ok(c, num_nodes)) {
             const RowBounds rb = load_row(rowptr, c);
@@ -39,6 +93,11 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
             col32[e] = r.x;
             if (e % index_stride == 0) index[e / index_stride] = r.x;
         }
+    }
+    if (work) {
+        check.nodes(rowptr, num_nodes, col, num_edges, gid, stride);
+        unsigned long long* w = reinterpret_cast<unsigned long long*>(work);
+        check.flush(w, MLXC_STATUS_BAD_ROW, MLXC_STATUS_BAD_NODE, w + 2, w + 3);
     }
 }
 
@@ -69,12 +128,6 @@ __global__ __launch_bounds__(kBlock) void walk_init_kernel(const int64_t* __rest
     }
 }
 
-__device__ __forceinline__ int64_t wave_sum(int64_t x) {
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
-    return x;
-}
-
 // work[0] |= MLXC_CSR_BAD_ROWPTR / MLXC_CSR_BAD_COL bits; work[1] counts
 // positions i >= 1 with col[i] < col[i-1]; work[2] counts those positions
 // that start a non-empty row.  Rows are sorted iff work[1] == work[2].
@@ -84,29 +137,11 @@ __global__ __launch_bounds__(kBlock) void csr_check_kernel(const int64_t* __rest
                                                            int64_t E, int64_t* work) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    uint32_t bits = 0;
-    int64_t desc = 0, start_desc = 0;
-    if (gid == 0 && (rowptr[0] != 0 || rowptr[V] != E)) bits |= MLXC_CSR_BAD_ROWPTR;
-    for (int64_t v = gid; v < V; v += stride) {
-        const int64_t rs = rowptr[v], re = rowptr[v + 1];
-        if (re < rs) bits |= MLXC_CSR_BAD_ROWPTR;
-        if (rs >= 1 && re > rs && re <= E && col[rs] < col[rs - 1]) ++start_desc;
-    }
-    for (int64_t i = gid; i < E; i += stride) {
-        const int64_t c = col[i];
-        if (!node_ok(c, V)) bits |= MLXC_CSR_BAD_COL;
-        if (i >= 1 && c < col[i - 1]) ++desc;
-    }
-    const int64_t d = wave_sum(desc), sd = wave_sum(start_desc);
-    const uint64_t any_bits = __ballot(bits != 0);
-    uint32_t wave_bits = bits;
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) wave_bits |= __shfl_xor(wave_bits, off, kWave);
-    if (__lane_id() == 0) {
-        if (any_bits) atomicOr(reinterpret_cast<unsigned long long*>(work), static_cast<unsigned long long>(wave_bits));
-        if (d) atomicAdd(reinterpret_cast<unsigned long long*>(work + 1), static_cast<unsigned long long>(d));
-        if (sd) atomicAdd(reinterpret_cast<unsigned long long*>(work + 2), static_cast<unsigned long long>(sd));
-    }
+    CsrCheck check;
+    check.nodes(rowptr, V, col, E, gid, stride);
+    for (int64_t i = gid; i < E; i += stride) check.edge(col, V, i, col[i]);
+    unsigned long long* w = reinterpret_cast<unsigned long long*>(work);
+    check.flush(w, MLXC_CSR_BAD_ROWPTR, MLXC_CSR_BAD_COL, w + 1, w + 2);
 }
 
 __global__ __launch_bounds__(kBlock) void philox_fill_kernel(float* __restrict__ out, int64_t n,
@@ -150,12 +185,13 @@ int launch_zero_work(int64_t* d_work, hipStream_t stream) {
 
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                         int64_t num_edges, EdgeRecord* recs, int32_t* col32, int32_t* index,
-                        int index_stride, hipStream_t stream) {
-    if (num_edges == 0) return MLXC_OK;
+                        int index_stride, int64_t* check_work, hipStream_t stream) {
+    if (num_edges == 0 && !check_work) return MLXC_OK;
     int grid = 0;
-    if (int rc = stream_grid(num_edges, 16, grid)) return rc;
+    const int64_t items = check_work && num_nodes > num_edges ? num_nodes : num_edges;
+    if (int rc = stream_grid(items, 16, grid)) return rc;
     hipLaunchKernelGGL(edge_record_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col,
-                       num_nodes, num_edges, recs, col32, index, index_stride);
+                       num_nodes, num_edges, recs, col32, index, index_stride, check_work);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

@@ -484,7 +484,7 @@ int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes,
     case UniformMode::kRecords: {
         EdgeRecord* init = recs + a.num_edges;
         if (int rc = launch_edge_records(a.rowptr, a.col, a.num_nodes, a.num_edges, recs, nullptr,
-                                         nullptr, 1, stream))
+                                         nullptr, 1, nullptr, stream))
             return rc;
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, stream))

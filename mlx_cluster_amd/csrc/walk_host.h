@@ -59,10 +59,12 @@ inline bool records_fit(int64_t num_nodes, int64_t num_edges) {
 
 // ---- prep_kernels.hip
 int launch_zero_work(int64_t* d_work, hipStream_t stream);
-// col32 / index may be null (the uniform walk needs neither).
+// col32 / index may be null (the uniform walk needs neither); a non-null
+// check_work also validates the CSR and counts row descents (see
+// edge_record_kernel).
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                         int64_t num_edges, EdgeRecord* recs, int32_t* col32, int32_t* index,
-                        int index_stride, hipStream_t stream);
+                        int index_stride, int64_t* check_work, hipStream_t stream);
 int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
                      int64_t num_edges, int64_t num_walks, EdgeRecord* init, hipStream_t stream);
 int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
@@ -80,7 +82,7 @@ struct N2VParams {
     double prob0, prob1, prob2;  // acceptance constants, BiasedRandomWalk.cpp:52-55
     uint32_t key0, key1;         // Philox key (the seed)
     int32_t rule;                // MLXC_RULE_*
-    bool rows_sorted;
+    int32_t rows;                // MLXC_ROWS_*
 };
 size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
                                 int32_t walk_length);

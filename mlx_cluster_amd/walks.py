@@ -223,9 +223,11 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
             (BiasedRandomWalk.cpp:86-91) term for term; 'node2vec' is the
             analytic node2vec rule (accept with probability 1/p, 1 or 1/q,
             normalised).  They agree whenever q >= max(p, 1).
-        rows_sorted: whether every CSR row is sorted ascending (binary-search
-            neighbour test).  None checks the graph on the device first, which
-            also rejects malformed graphs with ValueError.
+        rows_sorted: whether every CSR row is sorted ascending (sorted rows
+            are searched, unsorted ones scanned as the reference does).  None
+            lets the call check the rows on the device as part of its
+            preparation pass, which also validates the whole graph (a
+            malformed graph raises ValueError when check=True).
         return_edges, check: as in random_walk.
     """
     L = _walk_length(walk_length)
@@ -242,13 +244,8 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     if seed is None:
         seed = int(torch.randint(0, 2**62, (1,)).item())
     seed = int(seed) & (2**64 - 1)
-    if rows_sorted is None:
-        flags = csr_check(rowptr, col, stream=stream)
-        if flags & _lib.MLXC_CSR_BAD_ROWPTR:
-            raise ValueError("rejection_sampling: rowptr is malformed")
-        if flags & _lib.MLXC_CSR_BAD_COL:
-            raise ValueError("rejection_sampling: a col entry is outside [0, num_nodes)")
-        rows_sorted = not (flags & _lib.MLXC_CSR_UNSORTED)
+    rows = (_lib.MLXC_ROWS_DETECT if rows_sorted is None else
+            _lib.MLXC_ROWS_SORTED if rows_sorted else _lib.MLXC_ROWS_UNSORTED)
     N = start.numel()
     n_out = torch.empty((N, L + 1), dtype=torch.int64, device=device)
     e_out = torch.empty((N, L), dtype=torch.int64, device=device) if return_edges else None
@@ -258,7 +255,7 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     with torch.cuda.device(device):
         rc = lib.mlxc_rejection_sampling(
             _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,
-            p, q, seed, _RULES[rule], 1 if rows_sorted else 0, _ptr(n_out),
+            p, q, seed, _RULES[rule], rows, _ptr(n_out),
             _ptr(e_out) if return_edges else None, work.data_ptr(), work.numel() * 8, handle)
     _lib.check(rc, "rejection_sampling")
     if check:

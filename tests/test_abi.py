@@ -38,7 +38,8 @@ def test_header_constants_match_binding():
     text = open(HEADER).read()
     for name in ["MLXC_OK", "MLXC_ERR_INVALID_ARGUMENT", "MLXC_ERR_HIP", "MLXC_WORK_WORDS",
                  "MLXC_STATUS_BAD_NODE", "MLXC_STATUS_BAD_ROW", "MLXC_RULE_REF_CHAIN",
-                 "MLXC_RULE_NODE2VEC_EXACT", "MLXC_CSR_BAD_ROWPTR", "MLXC_CSR_BAD_COL",
+                 "MLXC_RULE_NODE2VEC_EXACT", "MLXC_ROWS_UNSORTED", "MLXC_ROWS_SORTED",
+                 "MLXC_ROWS_DETECT", "MLXC_CSR_BAD_ROWPTR", "MLXC_CSR_BAD_COL",
                  "MLXC_CSR_UNSORTED", "MLXC_MAX_TRIALS"]:
         m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
         assert m, name
@@ -84,6 +85,13 @@ def test_rejection_sampling_rejects_bad_arguments(p, q, rule, msg):
                                      FAKE, WS, None)
     assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT
     assert msg in _lib.last_error()
+
+
+def test_rejection_sampling_rejects_bad_row_mode():
+    lib = _lib.load()
+    rc = lib.mlxc_rejection_sampling(FAKE, 1, FAKE, 0, FAKE, 0, 3, 1.0, 1.0, 1, 0, 3, FAKE, None,
+                                     FAKE, WS, None)
+    assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT and "rows" in _lib.last_error()
 
 
 def test_other_entry_points_reject_bad_arguments():
