@@ -33,6 +33,9 @@ CONFIGS = {
     # name: (description, kind, graph builder args, walks per node, L, extra)
     "c2": ("R-MAT 2^20 uniform walk, 10 walks/node, L=80", "uniform",
            dict(scale=20, samples=1 << 24, symmetrize=False), 10, 80, {}),
+    "c2s": ("R-MAT 2^20 uniform walk, 10 walks/node, L=80, uniforms generated in the kernel "
+            "(seed=2, the stream of c2's rand tensor)", "uniform_seeded",
+            dict(scale=20, samples=1 << 24, symmetrize=False), 10, 80, {}),
     "c3": ("node2vec p=0.5 q=2 on symmetrized R-MAT 2^20, 4 walks/node, L=40", "node2vec",
            dict(scale=20, samples=1 << 24, symmetrize=True), 4, 40,
            dict(p=0.5, q=2.0, seed=3, rule="ref_chain")),
@@ -229,7 +232,14 @@ def main():
     torch.cuda.synchronize()
     log(f"graph V={V} E={E}; walks N={N} L={L}")
 
-    if kind == "uniform":
+    seeded = kind == "uniform_seeded"
+    if seeded:
+        # the walks of c2 without the rand tensor; rand is materialised only
+        # for the parity sample and the CPU baseline, after timing
+        kind = "uniform"
+        rand = None
+        step = lambda: mc.random_walk(rowptr, col, start, None, L, seed=2)
+    elif kind == "uniform":
         rand = mc.philox_uniform((N, L), 2, device=dev)
         step = lambda: mc.random_walk(rowptr, col, start, rand, L)
     else:
@@ -269,9 +279,11 @@ def main():
     # Z = walks that meet a deg-0 node (one rowptr read to find it).
     if kind == "uniform":
         M, Z = uniform_counts(torch, rowptr, out)
-        roof_bytes = LINE * (M + Z) + LINE * M + 4 * M + 8 * N * (L + 1) + 8 * N
+        rand_bytes = 0 if seeded else 4 * M  # generated uniforms are not read
+        roof_bytes = LINE * (M + Z) + LINE * M + rand_bytes + 8 * N * (L + 1) + 8 * N
         units = dict(moving_steps=M, sink_walks=Z,
-                     bytes_formula="64*(M+Z) + 64*M + 4*M + 8*N*(L+1) + 8*N")
+                     bytes_formula=("64*(M+Z) + 64*M + 8*N*(L+1) + 8*N" if seeded else
+                                    "64*(M+Z) + 64*M + 4*M + 8*N*(L+1) + 8*N"))
     else:
         # node2vec: the work depends on rejections, so it is counted by the
         # oracle on an evenly strided sample of walks and scaled to N.
@@ -286,6 +298,8 @@ def main():
                 **units}
 
     # Sampled bit-exact parity against the oracle, and the CPU baseline.
+    if kind == "uniform" and rand is None:
+        rand = mc.philox_uniform((N, L), 2, device=dev)
     if kind == "uniform":
         ref, _, st, _ = oracle.uniform_walk(rowptr_h, col_h, start[sample].cpu().numpy(),
                                             rand[sample].cpu().numpy(), L)

@@ -111,6 +111,24 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes,
                      void* d_workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Uniform random walk that generates its uniforms instead of reading a rand
+ * tensor: the same walk as mlxc_random_walk with
+ *   rand[n*L + l] = (w >> 8) * 2^-24, w = word (i % 4) of
+ *   Philox4x32-10(key = seed; counter = (i/4 lo, i/4 hi, 0, 0)), i = n*L + l,
+ * i.e. bit-identical to mlxc_random_walk on the output of
+ * mlxc_philox_uniform(rand, num_walks * walk_length, seed).  Saves the
+ * 4-byte-per-step rand stream and the pass that writes it.
+ * Extends: the reference's rand input, made by mx.random.uniform before the
+ *   call (/root/reference/tests/test_random_walk.py:31-36).
+ */
+int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes,
+                            const int64_t* d_col, int64_t num_edges,
+                            const int64_t* d_start, int64_t num_walks,
+                            int32_t walk_length, uint64_t seed,
+                            int64_t* d_n_out, int64_t* d_e_out,
+                            void* d_workspace, size_t workspace_bytes, void* stream);
+
+/*
  * node2vec walk by rejection sampling.
  * Replaces: BiasedRandomWalk::eval_cpu and the op rejection_sampling(rowptr,
  *   col, start, walk_length, p, q) —

@@ -49,6 +49,10 @@ SIGNATURES = {
         ctypes.c_int,
         [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _ptr, _size, _ptr],
     ),
+    "mlxc_random_walk_seeded": (
+        ctypes.c_int,
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _u64, _ptr, _ptr, _ptr, _size, _ptr],
+    ),
     "mlxc_rejection_sampling": (
         ctypes.c_int,
         [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _dbl, _dbl, _u64, _i32, _i32,

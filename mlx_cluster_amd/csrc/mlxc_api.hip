@@ -101,8 +101,26 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* 
     if (int rc = launch_zero_work(d_work, s)) return rc;
     if (num_walks == 0) return MLXC_OK;
     const WalkArgs a{d_rowptr, d_col, d_start, d_rand, d_n_out, d_e_out, d_work,
-                     num_nodes, num_edges, num_walks, walk_length};
-    return launch_uniform(a, d_workspace, workspace_bytes, s);
+                     num_nodes, num_edges, num_walks, walk_length, 0u, 0u};
+    return launch_uniform(a, d_workspace, workspace_bytes, false, s);
+}
+
+int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
+                            int64_t num_edges, const int64_t* d_start, int64_t num_walks,
+                            int32_t walk_length, uint64_t seed, int64_t* d_n_out,
+                            int64_t* d_e_out, void* d_workspace, size_t workspace_bytes,
+                            void* stream) {
+    if (int rc = check_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
+                            walk_length, d_n_out, d_workspace, workspace_bytes))
+        return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int64_t* d_work = static_cast<int64_t*>(d_workspace);
+    if (int rc = launch_zero_work(d_work, s)) return rc;
+    if (num_walks == 0) return MLXC_OK;
+    const WalkArgs a{d_rowptr, d_col, d_start, nullptr, d_n_out, d_e_out, d_work,
+                     num_nodes, num_edges, num_walks, walk_length,
+                     static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32)};
+    return launch_uniform(a, d_workspace, workspace_bytes, true, s);
 }
 
 int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
@@ -137,7 +155,7 @@ int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const in
     prm.rule = rule;
     prm.rows = rows;
     const WalkArgs a{d_rowptr, d_col, d_start, nullptr, d_n_out, d_e_out, d_work,
-                     num_nodes, num_edges, num_walks, walk_length};
+                     num_nodes, num_edges, num_walks, walk_length, 0u, 0u};
     return launch_node2vec(a, prm, d_workspace, workspace_bytes, s);
 }
 

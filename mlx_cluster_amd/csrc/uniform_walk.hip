@@ -15,7 +15,7 @@ namespace mlxc {
 // the wave queue, 8-byte loads and stores.  Serves the cases the windowed
 // kernels do not: the edge-id output and buffers that are not 16-byte
 // aligned.
-template <int W, bool kEdges>
+template <int W, bool kEdges, bool kGen>
 __global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
     const int64_t L = a.walk_length;
     const int64_t N = a.num_walks;
@@ -66,7 +66,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
             r[s] = 0.0f;
             if (live) {
                 rb[s] = load_row(a.rowptr, v[s]);
-                r[s] = __builtin_nontemporal_load(a.rand + n[s] * L + l[s]);
+                r[s] = kGen ? philox_uniform_at(n[s] * L + l[s], a.key0, a.key1)
+                            : __builtin_nontemporal_load(a.rand + n[s] * L + l[s]);
             }
         }
         // Phase 2: candidate edge and its target, for every moving slot.
@@ -134,7 +135,7 @@ enum : int {
 // a new rand block always travels together with a record read and never costs
 // a round trip of its own.  Output stores issued after the wait overlap the
 // next iteration's read.
-template <int W, int RW>
+template <int W, int RW, bool kGen>
 __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                                                                   const EdgeRecord* __restrict__ recs,
                                                                   const EdgeRecord* __restrict__ init) {
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
         }
 #pragma unroll
         for (int s = 0; s < W; ++s)
-            if (need_block[s]) rw_load_at(rw[s], a.rand, rw_block_base<RW>(fr[s], rtotal));
+            if (need_block[s]) rw_fetch<RW, kGen>(rw[s], a, fr[s], rtotal);
 
         // 2. While the reads are in flight, idle slots draw walk ids from the
         // wave queue; they issue their start reads next iteration.
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
             const int64_t g = g0 + l[s] + (ph[s] == kSlotWalk ? 1 : 0);
             if (need_block[s]) {
                 // block holding rand[fr]: shift it so w[0] is that value
-                const int k = static_cast<int>(fr[s] - rw_block_base<RW>(fr[s], rtotal));
+                const int k = static_cast<int>(fr[s] - rw_base<RW, kGen>(fr[s], rtotal));
                 rw_shift_by(rw[s], k);
                 rw[s].valid = RW - k;
                 need_block[s] = false;
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
 // of the new node.  Start records (walk_init_kernel) give the first row.
 // Requirements as for the record walk except num_edges may be any size the
 // int32 start records hold (num_nodes, num_edges below 2^31).
-template <int W, int RW>
+template <int W, int RW, bool kGen>
 __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                                                                   const EdgeRecord* __restrict__ init) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4), aligned(8)));
@@ -309,7 +310,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
 #pragma unroll
         for (int s = 0; s < W; ++s)  // a block due after a pick travels with the col read
             if (need_block[s] && ph[s] != kSlotRow)
-                rw_load_at(rw[s], a.rand, rw_block_base<RW>(fr[s], rtotal));
+                rw_fetch<RW, kGen>(rw[s], a, fr[s], rtotal);
 
         // 2. Idle slots draw walk ids while the reads are in flight.
         bool alive = false;
@@ -336,7 +337,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                 continue;
             }
             if (need_block[s] && ph[s] != kSlotCol) {
-                const int k = static_cast<int>(fr[s] - rw_block_base<RW>(fr[s], rtotal));
+                const int k = static_cast<int>(fr[s] - rw_base<RW, kGen>(fr[s], rtotal));
                 rw_shift_by(rw[s], k);
                 rw[s].valid = RW - k;
                 need_block[s] = false;
@@ -441,11 +442,11 @@ size_t init_bytes(int64_t num_walks) {
     return kRecordOffset + static_cast<size_t>(num_walks) * sizeof(EdgeRecord);
 }
 
-UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes) {
+UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes, bool gen) {
     const int64_t rtotal = a.num_walks * a.walk_length;
-    const bool streams_ok = reinterpret_cast<uintptr_t>(a.rand) % 16 == 0 &&
-                            reinterpret_cast<uintptr_t>(a.n_out) % 16 == 0 && rtotal % 4 == 0 &&
-                            rtotal >= MLXC_RAND_WINDOW;
+    const bool rand_ok = gen || (reinterpret_cast<uintptr_t>(a.rand) % 16 == 0 && rtotal % 4 == 0 &&
+                                 rtotal >= MLXC_RAND_WINDOW);
+    const bool streams_ok = rand_ok && reinterpret_cast<uintptr_t>(a.n_out) % 16 == 0;
     if (a.e_out || !streams_ok || !records_fit(a.num_nodes, a.num_edges)) return UniformMode::kPlain;
     if (records_pay_off(a.num_edges, a.num_walks, a.walk_length) &&
         workspace_bytes >= record_bytes(a.num_edges, a.num_walks))
@@ -476,11 +477,14 @@ size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num
                                                               : init_bytes(num_walks);
 }
 
-int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes,
-                   hipStream_t stream) {
+namespace {
+
+template <bool kGen>
+int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
     constexpr int RW = MLXC_RAND_WINDOW;
     EdgeRecord* recs = reinterpret_cast<EdgeRecord*>(static_cast<char*>(workspace) + kRecordOffset);
-    switch (uniform_mode(a, workspace_bytes)) {
+    switch (uniform_mode(a, workspace_bytes, kGen)) {
     case UniformMode::kRecords: {
         EdgeRecord* init = recs + a.num_edges;
         if (int rc = launch_edge_records(a.rowptr, a.col, a.num_nodes, a.num_edges, recs, nullptr,
@@ -489,7 +493,7 @@ int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes,
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, stream))
             return rc;
-        return launch_walk_kernel(uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW>, MLXC_REC_SLOTS, a,
+        return launch_walk_kernel(uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen>, MLXC_REC_SLOTS, a,
                                   stream,
                                   static_cast<const EdgeRecord*>(recs),
                                   static_cast<const EdgeRecord*>(init));
@@ -499,15 +503,23 @@ int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes,
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, stream))
             return rc;
-        return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW>, MLXC_CSR_SLOTS, a,
+        return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW, kGen>, MLXC_CSR_SLOTS, a,
                                   stream,
                                   static_cast<const EdgeRecord*>(init));
     }
     case UniformMode::kPlain:
         break;
     }
-    if (a.e_out) return launch_walk_kernel(uniform_walk_kernel<2, true>, 2, a, stream);
-    return launch_walk_kernel(uniform_walk_kernel<2, false>, 2, a, stream);
+    if (a.e_out) return launch_walk_kernel(uniform_walk_kernel<2, true, kGen>, 2, a, stream);
+    return launch_walk_kernel(uniform_walk_kernel<2, false, kGen>, 2, a, stream);
+}
+
+}  // namespace
+
+int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes, bool generate,
+                   hipStream_t stream) {
+    return generate ? launch_uniform_impl<true>(a, workspace, workspace_bytes, stream)
+                    : launch_uniform_impl<false>(a, workspace, workspace_bytes, stream);
 }
 
 }  // namespace mlxc

@@ -153,6 +153,7 @@ struct WalkArgs {
     int64_t num_edges;
     int64_t num_walks;
     int32_t walk_length;
+    uint32_t key0, key1;  // Philox key (the seed) when the kernel generates its uniforms
 };
 
 // ------------------------------------------------- stream windows
@@ -207,6 +208,46 @@ __device__ __forceinline__ void rw_load_at(RandWindow<RW>& r, const float* __res
         r.w[4 * i + 2] = x.z;
         r.w[4 * i + 3] = x.w;
     }
+}
+
+// Uniform i of the seeded stream, in the layout of mlxc_philox_uniform:
+// word i % 4 of Philox(counter = (i / 4 lo, i / 4 hi, 0, 0), key).
+__device__ __forceinline__ float philox_uniform_at(int64_t i, uint32_t k0, uint32_t k1) {
+    const uint64_t j = static_cast<uint64_t>(i) >> 2;
+    uint32_t c0 = static_cast<uint32_t>(j), c1 = static_cast<uint32_t>(j >> 32), c2 = 0, c3 = 0;
+    philox4x32_10(c0, c1, c2, c3, k0, k1);
+    const int w = static_cast<int>(i & 3);
+    return unit_float(w == 0 ? c0 : w == 1 ? c1 : w == 2 ? c2 : c3);
+}
+
+// Generates the block of the seeded stream starting at base (a multiple of 4).
+template <int RW>
+__device__ __forceinline__ void rw_gen_at(RandWindow<RW>& r, int64_t base, uint32_t k0,
+                                          uint32_t k1) {
+#pragma unroll
+    for (int i = 0; i < RW / 4; ++i) {
+        const uint64_t j = (static_cast<uint64_t>(base) >> 2) + i;
+        uint32_t c0 = static_cast<uint32_t>(j), c1 = static_cast<uint32_t>(j >> 32), c2 = 0, c3 = 0;
+        philox4x32_10(c0, c1, c2, c3, k0, k1);
+        r.w[4 * i] = unit_float(c0);
+        r.w[4 * i + 1] = unit_float(c1);
+        r.w[4 * i + 2] = unit_float(c2);
+        r.w[4 * i + 3] = unit_float(c3);
+    }
+}
+
+// Block start for rand[f]: generated streams have no array end to respect.
+template <int RW, bool kGen>
+__device__ __forceinline__ int64_t rw_base(int64_t f, int64_t total) {
+    return kGen ? (f & ~static_cast<int64_t>(RW - 1)) : rw_block_base<RW>(f, total);
+}
+
+// Fills the window with the block that serves rand[f], read or generated.
+template <int RW, bool kGen>
+__device__ __forceinline__ void rw_fetch(RandWindow<RW>& r, const WalkArgs& a, int64_t f,
+                                         int64_t total) {
+    if (kGen) rw_gen_at(r, rw_base<RW, kGen>(f, total), a.key0, a.key1);
+    else rw_load_at(r, a.rand, rw_base<RW, kGen>(f, total));
 }
 
 template <int RW>

@@ -74,7 +74,9 @@ int launch_philox_fill(float* out, int64_t n, uint64_t seed, hipStream_t stream)
 // ---- uniform_walk.hip
 size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
                                int32_t walk_length);
-int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes,
+// generate: the kernels compute their uniforms from the Philox key in a
+// (key0, key1) instead of reading a.rand.
+int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes, bool generate,
                    hipStream_t stream);
 
 // ---- node2vec_walk.hip

@@ -128,9 +128,9 @@ def _raise_status(work: torch.Tensor, stream, what: str) -> None:
 
 # ------------------------------------------------------------------- API
 
-def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike, rand: TensorLike,
-                walk_length: int, *, stream=None, return_edges: bool = False,
-                check: bool = True
+def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
+                rand: Optional[TensorLike], walk_length: int, *, stream=None,
+                return_edges: bool = False, check: bool = True, seed: Optional[int] = None
                 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """Uniform random walks over a CSR graph.
 
@@ -142,7 +142,10 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike, rand: Te
         col: int64 [num_edges] CSR column indices.
         start: int64 [num_walks] start nodes (any shape; flattened).
         rand: float32 with num_walks * walk_length uniforms in [0, 1); walk n
-            reads rand.view(-1)[n * walk_length + l] at step l.
+            reads rand.view(-1)[n * walk_length + l] at step l.  None with
+            `seed` set: the kernels generate the uniforms themselves,
+            bit-identical to rand = philox_uniform((num_walks, walk_length),
+            seed), without the rand tensor's memory traffic.
         walk_length: steps per walk (>= 0).
         stream: None (torch's current stream), a torch.cuda.Stream or a
             device.  'cpu' raises: this build has no CPU evaluation.
@@ -152,6 +155,7 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike, rand: Te
         check: synchronise and raise ValueError if a start/col index or a
             rowptr entry was out of range (the reference reads out of bounds
             there).  With check=False the call stays asynchronous.
+        seed: key of the generated uniforms when rand is None.
 
     Returns:
         int64 [num_walks, walk_length + 1] node sequences (and edge ids).
@@ -159,23 +163,35 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike, rand: Te
     L = _walk_length(walk_length)
     _check_stream_arg(stream)
     rowptr, col, start = _graph(rowptr, col, start)
-    rand = _as_tensor(rand, torch.float32, "rand")
     N = start.numel()
-    if rand.numel() != N * L:
-        raise ValueError(f"rand must hold num_walks * walk_length = {N * L} values, got {rand.numel()}")
+    if rand is None:
+        if seed is None:
+            raise ValueError("rand is None: pass seed= to have the kernels generate the uniforms")
+        seed = int(seed) & (2**64 - 1)
+    else:
+        if seed is not None:
+            raise ValueError("pass either rand or seed, not both")
+        rand = _as_tensor(rand, torch.float32, "rand")
+        if rand.numel() != N * L:
+            raise ValueError(f"rand must hold num_walks * walk_length = {N * L} values, "
+                             f"got {rand.numel()}")
     device = _resolve_device(stream, (rowptr, col, start, rand))
     handle = _stream_handle(stream, device)
-    rowptr, col, start, rand = (_on(t, device) for t in (rowptr, col, start, rand))
+    rowptr, col, start = (_on(t, device) for t in (rowptr, col, start))
     n_out = torch.empty((N, L + 1), dtype=torch.int64, device=device)
     e_out = torch.empty((N, L), dtype=torch.int64, device=device) if return_edges else None
     lib = _lib.load()
     work = _workspace(lib.mlxc_random_walk_workspace_bytes(rowptr.numel() - 1, col.numel(), N, L),
                       device)
+    graph = (_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N)
+    outs = (_ptr(n_out), _ptr(e_out) if return_edges else None, work.data_ptr(), work.numel() * 8,
+            handle)
     with torch.cuda.device(device):
-        rc = lib.mlxc_random_walk(_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(),
-                                  _ptr(start), N, _ptr(rand), L, _ptr(n_out),
-                                  _ptr(e_out) if return_edges else None, work.data_ptr(),
-                                  work.numel() * 8, handle)
+        if rand is None:
+            rc = lib.mlxc_random_walk_seeded(*graph, L, seed, *outs)
+        else:
+            rand = _on(rand, device)
+            rc = lib.mlxc_random_walk(*graph, _ptr(rand), L, *outs)
     _lib.check(rc, "random_walk")
     if check:
         _raise_status(work, stream, "random_walk")

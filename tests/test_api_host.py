@@ -42,6 +42,13 @@ def test_random_walk_validation(kw, exc):
                        args["walk_length"])
 
 
+def test_seed_and_rand_are_exclusive():
+    with pytest.raises(ValueError, match="seed"):
+        mc.random_walk(ROWPTR, COL, START, None, 4)
+    with pytest.raises(ValueError, match="either"):
+        mc.random_walk(ROWPTR, COL, START, RAND, 4, seed=3)
+
+
 @pytest.mark.parametrize("stream", ["cpu", torch.device("cpu")])
 def test_cpu_stream_is_refused(stream):
     with pytest.raises(ValueError, match="GPU only"):

@@ -213,3 +213,25 @@ def test_all_kernel_paths_agree(N, L, cuda):
     outs["unaligned"] = big[1:].view(N, L + 1)
     for name, o in outs.items():
         np.testing.assert_array_equal(o.cpu().numpy(), ref, err_msg=name)
+
+
+@pytest.mark.parametrize("N,L", [(1, 1), (37, 5), (1000, 16), (4096, 23), (30_000, 80)])
+def test_seeded_uniforms_match_rand_tensor(N, L, cuda):
+    """rand=None, seed=s generates in the kernel exactly the stream
+    philox_uniform((N, L), s) holds: every kernel path (edge records, CSR
+    reads, edge output) gives the walks of the explicit tensor, and the oracle's."""
+    rowptr, col = synth.rmat_csr(9, 3000, seed=N, device=cuda)
+    V = rowptr.numel() - 1
+    start = (torch.arange(N, device=cuda) * 17) % V
+    seed = 0xABCDEF0123 + N
+    rand = mc.philox_uniform((N, L), seed, device=cuda)
+    want = mc.random_walk(rowptr, col, start, rand, L)
+    got = mc.random_walk(rowptr, col, start, None, L, seed=seed)
+    assert torch.equal(got, want)
+    got_n, got_e = mc.random_walk(rowptr, col, start, None, L, seed=seed, return_edges=True)
+    want_n, want_e = mc.random_walk(rowptr, col, start, rand, L, return_edges=True)
+    assert torch.equal(got_n, want) and torch.equal(got_e, want_e)
+    ref, _, st, _ = oracle.uniform_walk(rowptr.cpu().numpy(), col.cpu().numpy(),
+                                        start.cpu().numpy(), oracle.philox_uniform(N * L, seed), L)
+    assert st == 0
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
