@@ -10,7 +10,8 @@ Drop-in for the reference package's two functions (re-exported by
 The walks run in hand-written HIP kernels for gfx950 (libmlxc.so, C ABI in
 include/mlxc.h); the package has no CPU fallback.
 """
+from .csr import to_csr
 from .walks import csr_check, philox_uniform, random_walk, rejection_sampling
 
-__all__ = ["random_walk", "rejection_sampling", "csr_check", "philox_uniform"]
+__all__ = ["random_walk", "rejection_sampling", "csr_check", "philox_uniform", "to_csr"]
 __version__ = "0.1.0"

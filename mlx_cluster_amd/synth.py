@@ -17,22 +17,14 @@ from typing import Tuple
 import numpy as np
 import torch
 
+from .csr import to_csr
+
 
 def csr_from_edges(row: torch.Tensor, col: torch.Tensor, num_nodes: int, *,
                    symmetrize: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """Deduplicated CSR (rowptr, col) sorted by (row, col)."""
-    row = row.to(torch.int64)
-    col = col.to(torch.int64)
-    if symmetrize:
-        row, col = torch.cat([row, col]), torch.cat([col, row])
-    key = torch.unique(row * num_nodes + col, sorted=True)
-    r = torch.div(key, num_nodes, rounding_mode="floor")
-    c = key - r * num_nodes
-    del key
-    counts = torch.bincount(r, minlength=num_nodes)
-    rowptr = torch.zeros(num_nodes + 1, dtype=torch.int64, device=row.device)
-    torch.cumsum(counts, 0, out=rowptr[1:])
-    return rowptr, c.contiguous()
+    return to_csr(torch.stack([row.to(torch.int64), col.to(torch.int64)]), num_nodes,
+                  symmetrize=symmetrize, dedup=True)
 
 
 def rmat_edges(scale: int, num_samples: int, a: float = 0.57, b: float = 0.19,
