@@ -135,7 +135,7 @@ enum : int {
 // a new rand block always travels together with a record read and never costs
 // a round trip of its own.  Output stores issued after the wait overlap the
 // next iteration's read.
-template <int W, int RW, bool kGen>
+template <int W, int RW, bool kGen, bool kEdges>
 __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                                                                   const EdgeRecord* __restrict__ recs,
                                                                   const EdgeRecord* __restrict__ init) {
@@ -153,6 +153,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
     bool need_block[W];        // ... if set
     RandWindow<RW> rw[W];
     OutWin<int32_t> ow[W];
+    OutWin<int32_t> ew[W];     // edge ids (kEdges): e_out[n*L + l] is step l's edge
     uint32_t status = 0;
 
 #pragma unroll
@@ -162,6 +163,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
         l[s] = 0;
         e[s] = 0;
         fr[s] = 0;
+        ew[s].count = 0;
         need_block[s] = false;
         rw[s].valid = 0;
         ow[s].count = 0;
@@ -221,27 +223,36 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                 need_block[s] = false;
             }
             const int32_t node = rec[s].x, begin = rec[s].y, deg = rec[s].z;
+            const int64_t e0 = n[s] * L;  // edge output index of the walk's step 0
             bool fill = false, flush = false;
+            if (ph[s] == kSlotStart) {
+                ow[s].count = 0;
+                ew[s].count = 0;
+            }
             if (deg < 0) {
                 // malformed start or graph entry: stop (outputs unspecified)
                 status |= deg == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
-                if (ph[s] == kSlotStart) ow[s].count = 0;
                 ow_fill(ow[s], a.n_out, g, g0 + L, node);
+                // edges of steps 0 .. l are buffered after a pick, none at the start
+                if (kEdges) ow_fill(ew[s], a.e_out, e0 + l[s] + (ph[s] == kSlotWalk ? 1 : 0),
+                                    e0 + L - 1, -1);
                 phase[s] = kSlotIdle;
                 continue;
             }
-            if (ph[s] == kSlotStart) ow[s].count = 0;
             ow_push(ow[s], a.n_out, g, node);
             if (ph[s] == kSlotWalk) l[s] += 1;
             if (l[s] == L) flush = true;
             else if (deg == 0) fill = true;  // absorbing node: the walk stays
             if (fill) {
                 ow_fill(ow[s], a.n_out, g + 1, g0 + L, node);
+                if (kEdges) ow_fill(ew[s], a.e_out, e0 + l[s], e0 + L - 1, -1);
             } else if (flush) {
                 if (ow[s].count) ow_flush(ow[s], a.n_out, g);
+                if (kEdges && ew[s].count) ow_flush(ew[s], a.e_out, e0 + L - 1);
             } else {
                 // step l (0-based) leaves this node with uniform rand[n*L + l]
                 e[s] = static_cast<int32_t>(begin + pick_index(rw[s].w[0], deg));
+                if (kEdges) ow_push(ew[s], a.e_out, e0 + l[s], e[s]);
                 rw_shift1(rw[s]);
                 rw[s].valid -= 1;
                 need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
@@ -261,7 +272,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
 // of the new node.  Start records (walk_init_kernel) give the first row.
 // Requirements as for the record walk except num_edges may be any size the
 // int32 start records hold (num_nodes, num_edges below 2^31).
-template <int W, int RW, bool kGen>
+template <int W, int RW, bool kGen, bool kEdges>
 __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                                                                   const EdgeRecord* __restrict__ init) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4), aligned(8)));
@@ -277,6 +288,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
     bool need_block[W];
     RandWindow<RW> rw[W];
     OutWin<int32_t> ow[W];
+    OutWin<int32_t> ew[W];     // edge ids (kEdges): e_out[n*L + l] is step l's edge
     uint32_t status = 0;
 
 #pragma unroll
@@ -287,6 +299,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
         e[s] = 0;
         v[s] = 0;
         fr[s] = 0;
+        ew[s].count = 0;
         need_block[s] = false;
         rw[s].valid = 0;
         ow[s].count = 0;
@@ -343,12 +356,15 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                 need_block[s] = false;
             }
             const int64_t g0 = n[s] * L1;
+            const int64_t e0 = n[s] * L;  // edge output index of the walk's step 0
             int64_t g = g0 + l[s];  // output index of the last buffered entry
+            int64_t eg = e0 + l[s];  // first edge output index not yet buffered
             int64_t begin = 0, deg = -1;  // row to pick from (deg >= 0: pick)
             bool push = false, fill = false, flush = false;
             uint32_t bad = 0;
             if (ph[s] == kSlotStart) {
                 ow[s].count = 0;
+                ew[s].count = 0;
                 v[s] = row[s].x;
                 push = true;
                 if (row[s].z < 0) {
@@ -360,6 +376,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                     deg = row[s].z;
                 }
             } else if (ph[s] == kSlotCol) {
+                eg += 1;  // step l's edge was buffered at its pick
                 if (!node_ok(cv[s], a.num_nodes)) {
                     bad = MLXC_STATUS_BAD_NODE;
                 } else {
@@ -390,6 +407,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                 fill = true;  // absorbing node: the walk stays
             } else if (deg > 0) {
                 e[s] = static_cast<int32_t>(begin + pick_index(rw[s].w[0], deg));
+                if (kEdges) ow_push(ew[s], a.e_out, eg, e[s]);
                 rw_shift1(rw[s]);
                 rw[s].valid -= 1;
                 need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
@@ -399,8 +417,10 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
             if (push) ow_push(ow[s], a.n_out, g, v[s]);
             if (fill) {
                 ow_fill(ow[s], a.n_out, g + 1, g0 + L, v[s]);
-            } else if (flush && ow[s].count) {
-                ow_flush(ow[s], a.n_out, g);
+                if (kEdges) ow_fill(ew[s], a.e_out, eg, e0 + L - 1, -1);
+            } else if (flush) {
+                if (ow[s].count) ow_flush(ow[s], a.n_out, g);
+                if (kEdges && ew[s].count) ow_flush(ew[s], a.e_out, e0 + L - 1);
             }
             if (fill || flush) phase[s] = kSlotIdle;
         }
@@ -446,8 +466,9 @@ UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes, bool gen) {
     const int64_t rtotal = a.num_walks * a.walk_length;
     const bool rand_ok = gen || (reinterpret_cast<uintptr_t>(a.rand) % 16 == 0 && rtotal % 4 == 0 &&
                                  rtotal >= MLXC_RAND_WINDOW);
-    const bool streams_ok = rand_ok && reinterpret_cast<uintptr_t>(a.n_out) % 16 == 0;
-    if (a.e_out || !streams_ok || !records_fit(a.num_nodes, a.num_edges)) return UniformMode::kPlain;
+    const bool streams_ok = rand_ok && reinterpret_cast<uintptr_t>(a.n_out) % 16 == 0 &&
+                            reinterpret_cast<uintptr_t>(a.e_out) % 16 == 0;  // e_out may be null
+    if (!streams_ok || !records_fit(a.num_nodes, a.num_edges)) return UniformMode::kPlain;
     if (records_pay_off(a.num_edges, a.num_walks, a.walk_length) &&
         workspace_bytes >= record_bytes(a.num_edges, a.num_walks))
         return UniformMode::kRecords;
@@ -479,7 +500,7 @@ size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num
 
 namespace {
 
-template <bool kGen>
+template <bool kGen, bool kEdges>
 int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_bytes,
                         hipStream_t stream) {
     constexpr int RW = MLXC_RAND_WINDOW;
@@ -493,7 +514,8 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, stream))
             return rc;
-        return launch_walk_kernel(uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen>, MLXC_REC_SLOTS, a,
+        return launch_walk_kernel(uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen, kEdges>,
+                                  MLXC_REC_SLOTS, a,
                                   stream,
                                   static_cast<const EdgeRecord*>(recs),
                                   static_cast<const EdgeRecord*>(init));
@@ -503,23 +525,27 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, stream))
             return rc;
-        return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW, kGen>, MLXC_CSR_SLOTS, a,
+        return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW, kGen, kEdges>,
+                                  MLXC_CSR_SLOTS, a,
                                   stream,
                                   static_cast<const EdgeRecord*>(init));
     }
     case UniformMode::kPlain:
         break;
     }
-    if (a.e_out) return launch_walk_kernel(uniform_walk_kernel<2, true, kGen>, 2, a, stream);
-    return launch_walk_kernel(uniform_walk_kernel<2, false, kGen>, 2, a, stream);
+    return launch_walk_kernel(uniform_walk_kernel<2, kEdges, kGen>, 2, a, stream);
 }
 
 }  // namespace
 
 int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes, bool generate,
                    hipStream_t stream) {
-    return generate ? launch_uniform_impl<true>(a, workspace, workspace_bytes, stream)
-                    : launch_uniform_impl<false>(a, workspace, workspace_bytes, stream);
+    const bool edges = a.e_out != nullptr;
+    if (generate)
+        return edges ? launch_uniform_impl<true, true>(a, workspace, workspace_bytes, stream)
+                     : launch_uniform_impl<true, false>(a, workspace, workspace_bytes, stream);
+    return edges ? launch_uniform_impl<false, true>(a, workspace, workspace_bytes, stream)
+                 : launch_uniform_impl<false, false>(a, workspace, workspace_bytes, stream);
 }
 
 }  // namespace mlxc

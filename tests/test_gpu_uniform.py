@@ -192,27 +192,30 @@ def test_all_kernel_paths_agree(N, L, cuda):
     V = rowptr.numel() - 1
     start = (torch.arange(N, device=cuda) * 131) % V
     rand = mc.philox_uniform(N * L + 1, 17, device=cuda)
-    ref, _, st, _ = oracle.uniform_walk(rowptr.cpu().numpy(), col.cpu().numpy(),
-                                        start.cpu().numpy(), rand[:N * L].cpu().numpy(), L)
+    ref, ref_e, st, _ = oracle.uniform_walk(rowptr.cpu().numpy(), col.cpu().numpy(),
+                                            start.cpu().numpy(), rand[:N * L].cpu().numpy(), L,
+                                            with_edges=True)
     assert st == 0
-    outs = {}
-    csr_ws = 256 + 16 * N
-    for name, kw in [("records", {}), ("csr", dict(ws_bytes=csr_ws)), ("plain", dict(ws_bytes=32))]:
-        out = torch.full((N, L + 1), -7, dtype=torch.int64, device=cuda)
-        _abi_walk(rowptr, col, start, rand.data_ptr(), L, out.data_ptr(), **kw)
-        outs[name] = out
-    e = torch.empty((N, L), dtype=torch.int64, device=cuda)
-    out = torch.full((N, L + 1), -7, dtype=torch.int64, device=cuda)
-    _abi_walk(rowptr, col, start, rand.data_ptr(), L, out.data_ptr(), e_out=e)
-    outs["edges"] = out
-    # unaligned rand (4-byte offset) and unaligned n_out (8-byte offset)
+    E = col.numel()
+    workspaces = {"records": 256 + 16 * (E + N), "csr": 256 + 16 * N, "plain": 32}
+    for name, ws in workspaces.items():
+        for edges in (False, True):
+            out = torch.full((N, L + 1), -7, dtype=torch.int64, device=cuda)
+            e = torch.full((N, L), -7, dtype=torch.int64, device=cuda) if edges else None
+            _abi_walk(rowptr, col, start, rand.data_ptr(), L, out.data_ptr(), e_out=e,
+                      ws_bytes=ws)
+            np.testing.assert_array_equal(out.cpu().numpy(), ref, err_msg=f"{name} {edges}")
+            if edges:
+                np.testing.assert_array_equal(e.cpu().numpy(), ref_e, err_msg=f"{name} edges")
+    # unaligned rand (4-byte offset), n_out and e_out (8-byte offsets): unwindowed kernel
     rand_u = mc.philox_uniform(N * L + 1, 0, device=cuda)
     rand_u[1:] = rand[:N * L]
     big = torch.full((N * (L + 1) + 1,), -7, dtype=torch.int64, device=cuda)
-    _abi_walk(rowptr, col, start, rand_u.data_ptr() + 4, L, big.data_ptr() + 8)
-    outs["unaligned"] = big[1:].view(N, L + 1)
-    for name, o in outs.items():
-        np.testing.assert_array_equal(o.cpu().numpy(), ref, err_msg=name)
+    big_e = torch.full((N * L + 1,), -7, dtype=torch.int64, device=cuda)
+    e_view = big_e[1:]
+    _abi_walk(rowptr, col, start, rand_u.data_ptr() + 4, L, big.data_ptr() + 8, e_out=e_view)
+    np.testing.assert_array_equal(big[1:].view(N, L + 1).cpu().numpy(), ref, err_msg="unaligned")
+    np.testing.assert_array_equal(e_view.view(N, L).cpu().numpy(), ref_e, err_msg="unaligned e")
 
 
 @pytest.mark.parametrize("N,L", [(1, 1), (37, 5), (1000, 16), (4096, 23), (30_000, 80)])
