@@ -220,7 +220,7 @@ __device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, double r, bool 
 // waits once.  Sorted rows are searched through the block index (see
 // kSearchBlock); unsorted rows are scanned one entry per iteration, as the
 // reference scans them.
-template <int kRule>
+template <int kRule, bool kEdges>
 __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
     const bool sorted = a.rows == MLXC_ROWS_SORTED ||
@@ -243,7 +243,9 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     int32_t blk = 0, blo = 0, bhi = 0;  // block to read and the row's entries in it
     float r = 0.0f;         // acceptance uniform of the current trial
     OutWin<int32_t> ow;
+    OutWin<int32_t> ew;     // edge ids (kEdges): e_out[n*L + l] is step l's edge
     ow.count = 0;
+    ew.count = 0;
     uint32_t status = 0;
 
     while (true) {
@@ -276,10 +278,12 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
 
         // 3. Consume.
         const int64_t g0 = n * L1;
+        const int64_t e0 = n * L;  // edge output index of the walk's step 0
         bool push = false, fill = false, flush = false, accept = false, next_trial = false;
         int64_t g = g0 + l;  // output index of the last buffered entry
         if (ph == kN2vStart) {
             ow.count = 0;
+            ew.count = 0;
             v = rec.x;
             push = true;
             if (rec.z < 0) {
@@ -395,6 +399,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             }
         }
         if (accept) {
+            if (kEdges) ow_push(ew, a.w.e_out, e0 + l, e);
             push = true;
             g += 1;
             l += 1;
@@ -421,8 +426,10 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
         if (push) ow_push(ow, a.w.n_out, g, v);
         if (fill) {
             ow_fill(ow, a.w.n_out, g + 1, g0 + L, v);
-        } else if (flush && ow.count) {
-            ow_flush(ow, a.w.n_out, g);
+            if (kEdges) ow_fill(ew, a.w.e_out, e0 + l, e0 + L - 1, -1);  // l edges buffered
+        } else if (flush) {
+            if (ow.count) ow_flush(ow, a.w.n_out, g);
+            if (kEdges && ew.count) ow_flush(ew, a.w.e_out, e0 + L - 1);
         }
         if (fill || flush) phase = kN2vIdle;
     }
@@ -452,9 +459,9 @@ int dispatch_n2v(const N2VArgs& a, bool sorted, bool edges, hipStream_t stream) 
                  : launch_n2v<kRule, false, false>(a, stream);
 }
 
-template <int kRule>
+template <int kRule, bool kEdges>
 int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
-    auto kernel = node2vec_rec_kernel<kRule>;
+    auto kernel = node2vec_rec_kernel<kRule, kEdges>;
     int grid = 0;
     if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
@@ -491,7 +498,9 @@ size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t nu
 int launch_node2vec(const WalkArgs& w, const N2VParams& p, void* workspace, size_t workspace_bytes,
                     hipStream_t stream) {
     const N2VLayout lay = n2v_layout(w.num_edges, w.num_walks);
-    if (!w.e_out && records_fit(w.num_nodes, w.num_edges) && workspace_bytes >= lay.total) {
+    const bool aligned = reinterpret_cast<uintptr_t>(w.n_out) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(w.e_out) % 16 == 0;  // e_out may be null
+    if (aligned && records_fit(w.num_nodes, w.num_edges) && workspace_bytes >= lay.total) {
         N2VRecArgs a;
         a.w = w;
         char* base = static_cast<char*>(workspace);
@@ -518,11 +527,16 @@ int launch_node2vec(const WalkArgs& w, const N2VParams& p, void* workspace, size
         a.key0 = p.key0;
         a.key1 = p.key1;
         a.rows = p.rows;
-        return p.rule == MLXC_RULE_REF_CHAIN ? launch_n2v_rec<MLXC_RULE_REF_CHAIN>(a, stream)
-                                             : launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT>(a, stream);
+        const bool edges = w.e_out != nullptr;
+        if (p.rule == MLXC_RULE_REF_CHAIN)
+            return edges ? launch_n2v_rec<MLXC_RULE_REF_CHAIN, true>(a, stream)
+                         : launch_n2v_rec<MLXC_RULE_REF_CHAIN, false>(a, stream);
+        return edges ? launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, true>(a, stream)
+                     : launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, false>(a, stream);
     }
-    // Edge output or graphs beyond int32: the direct CSR kernel, which needs
-    // the row order on the host.
+    // Graphs beyond int32, a workspace too small for the records, or output
+    // buffers not 16-byte aligned: the direct CSR kernel, which needs the row
+    // order on the host.
     bool sorted = p.rows == MLXC_ROWS_SORTED;
     if (p.rows == MLXC_ROWS_DETECT) {
         if (int rc = launch_csr_check(w.rowptr, w.num_nodes, w.col, w.num_edges, w.work, stream))

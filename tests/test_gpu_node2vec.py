@@ -19,16 +19,41 @@ pytestmark = pytest.mark.gpu
 RULE_NAME = {oracle.RULE_REF_CHAIN: "ref_chain", oracle.RULE_NODE2VEC_EXACT: "node2vec"}
 
 
+def _direct_walk(rowptr, col, start, L, p, q, seed, rule, rows):
+    """mlxc_rejection_sampling through the C ABI with the minimal workspace:
+    the direct CSR kernel (no records), with edge output."""
+    from mlx_cluster_amd import _lib
+    lib = _lib.load()
+    N = start.numel()
+    n = torch.empty((N, L + 1), dtype=torch.int64, device=start.device)
+    e = torch.empty((N, L), dtype=torch.int64, device=start.device)
+    ws = torch.zeros(4, dtype=torch.int64, device=start.device)
+    ptr = lambda t: t.data_ptr() if t.numel() else None
+    rc = lib.mlxc_rejection_sampling(ptr(rowptr), rowptr.numel() - 1, ptr(col), col.numel(),
+                                     ptr(start), N, L, p, q, seed, rule, rows, ptr(n), ptr(e),
+                                     ws.data_ptr(), 32, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    assert int(ws[0].item()) == 0
+    return n, e
+
+
 def gpu_walk(rowptr, col, start, L, p, q, seed, rule, cuda, **kw):
-    """Runs both kernels: the record walk (node output only) and the direct
-    CSR walk (taken when edge ids are requested); their node outputs must
-    agree.  Returns (nodes, edges)."""
+    """Runs the record walk without and with edge output and the direct CSR
+    walk (minimal workspace); all node outputs must agree, and both edge
+    outputs.  Returns (nodes, edges)."""
     t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.int64)).to(cuda)
     args = (t(rowptr), t(col), t(start), L, p, q)
     n_rec = mc.rejection_sampling(*args, seed=seed, rule=RULE_NAME[rule], **kw)
     n, e = mc.rejection_sampling(*args, seed=seed, rule=RULE_NAME[rule], return_edges=True, **kw)
     np.testing.assert_array_equal(n_rec.cpu().numpy(), n.cpu().numpy(),
-                                  err_msg="record walk != CSR walk")
+                                  err_msg="record walk: nodes differ with edge output")
+    rows = {None: 2, True: 1, False: 0}[kw.get("rows_sorted")]
+    nd, ed = _direct_walk(*args[:3], L, p, q, seed, rule, rows)
+    np.testing.assert_array_equal(nd.cpu().numpy(), n.cpu().numpy(),
+                                  err_msg="direct CSR walk != record walk")
+    np.testing.assert_array_equal(ed.cpu().numpy(), e.cpu().numpy(),
+                                  err_msg="direct CSR walk edges != record walk edges")
     return n.cpu().numpy(), e.cpu().numpy()
 
 
