@@ -109,6 +109,38 @@ def cpu_baseline_uniform(np, oracle, rowptr_h, col_h, start, rand, L, target_s=1
     return walks * L / dt, walks, dt
 
 
+def host_info():
+    """CPU model and the cores this process may use (its affinity set)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model, len(os.sched_getaffinity(0))
+
+
+def cpu_all_cores_context(np, torch, mc, kind, rowptr_h, col_h, start, rand, L, extra, walks,
+                          threads):
+    """The library's own host evaluation (stream='cpu', all threads) on the
+    same walk sample as the baseline: context for the one-thread baseline."""
+    idx = torch.from_numpy(np.linspace(0, start.shape[0] - 1, walks).astype(np.int64))
+    rp, cl = torch.from_numpy(rowptr_h), torch.from_numpy(col_h)
+    s = torch.from_numpy(start)[idx]
+    t0 = time.perf_counter()
+    if kind == "uniform":
+        mc.random_walk(rp, cl, s, torch.from_numpy(rand)[idx], L, stream="cpu", threads=threads)
+    else:
+        mc.rejection_sampling(rp, cl, s, L, extra["p"], extra["q"], seed=extra["seed"],
+                              rule=extra["rule"], rows_sorted=True, stream="cpu", threads=threads)
+    dt = time.perf_counter() - t0
+    return {"value": walks * L / dt, "unit": "walk-steps/s", "threads": threads,
+            "seconds": dt, "what": "mlx_cluster_amd host twin (stream='cpu'), same sample"}
+
+
 def gather_ceiling(torch, dev):
     """Random-gather ceiling: out[i] = table[idx[i]] with 2^26 independent
     uniform int64 indices (torch.take), for tables from 32 MiB (L2/MALL
@@ -152,7 +184,8 @@ def node2vec_bytes(np, oracle, rowptr_h, col_h, start_h, L, extra, walks=200_000
     S, Z, T = c["moving_steps"] * f, c["sink_walks"] * f, c["trials"] * f
     Q, P = c["member_tests"] * f, c["member_lines"] * f
     b = LINE * (S + Z) + LINE * T + LINE * (Q + P) + 8 * N * (L + 1) + 8 * N
-    return int(b), dict(moving_steps=int(S), sink_walks=int(Z), trials=int(T),
+    useful = 16 * (S + Z) + 8 * T + 8 * P + 8 * N * (L + 1) + 8 * N
+    return int(b), int(useful), dict(moving_steps=int(S), sink_walks=int(Z), trials=int(T),
                         member_tests=int(Q), member_lines=int(P), counts_sample_walks=int(idx.size),
                         bytes_formula="64*(S+Z) + 64*T + 64*(Q+P) + 8*N*(L+1) + 8*N")
 
@@ -262,7 +295,9 @@ def main():
         ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    kernel_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
+    event_ms = [a.elapsed_time(b) for a, b in events]
+    kernel_ms = float(np.mean(event_ms))
+    kernel_ms_median = float(np.median(event_ms))
     ms_per_step = wall / args.steps * 1e3
     steps_per_launch = N * L
     value = steps_per_launch / (ms_per_step / 1e3)
@@ -281,20 +316,25 @@ def main():
         M, Z = uniform_counts(torch, rowptr, out)
         rand_bytes = 0 if seeded else 4 * M  # generated uniforms are not read
         roof_bytes = LINE * (M + Z) + LINE * M + rand_bytes + 8 * N * (L + 1) + 8 * N
+        useful_bytes = 16 * (M + Z) + 8 * M + rand_bytes + 8 * N * (L + 1) + 8 * N
         units = dict(moving_steps=M, sink_walks=Z,
                      bytes_formula=("64*(M+Z) + 64*M + 8*N*(L+1) + 8*N" if seeded else
                                     "64*(M+Z) + 64*M + 4*M + 8*N*(L+1) + 8*N"))
     else:
         # node2vec: the work depends on rejections, so it is counted by the
         # oracle on an evenly strided sample of walks and scaled to N.
-        roof_bytes, units = node2vec_bytes(np, oracle, rowptr_h, col_h, start.cpu().numpy(), L,
+        roof_bytes, useful_bytes, units = node2vec_bytes(np, oracle, rowptr_h, col_h, start.cpu().numpy(), L,
                                            extra)
     achieved = roof_bytes / (kernel_ms / 1e3) / 1e9 if roof_bytes else None
     traffic = traffic_from_profile(f"{kind}_walk_{args.config}")
     roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": (achieved / PEAK_HBM_GBS) if achieved else None, "traffic": traffic,
                 "algorithmic_bytes_per_launch": roof_bytes,
-                "kernel_ms": kernel_ms, "kernel_ms_source": "HIP events around each call on its stream",
+                "kernel_ms": kernel_ms, "kernel_ms_median": kernel_ms_median,
+                "kernel_ms_source": "HIP events around each call on its stream (mean; median beside it)",
+                "useful_gbs": useful_bytes / (kernel_ms / 1e3) / 1e9,
+                "useful_bytes_per_launch": useful_bytes,
+                "hbm_gbs_measured": (traffic / (kernel_ms / 1e3) / 1e9) if traffic else None,
                 **units}
 
     # Sampled bit-exact parity against the oracle, and the CPU baseline.
@@ -315,9 +355,11 @@ def main():
         got = out[s0:s0 + 2000].cpu().numpy()
     parity = bool(st == 0 and np.array_equal(got, ref))
     cpu = None
+    model, cores = host_info()
     if not args.no_cpu_baseline and kind == "uniform":
+        rand_h = rand.cpu().numpy()
         rate, walks, dt = cpu_baseline_uniform(np, oracle, rowptr_h, col_h, start.cpu().numpy(),
-                                               rand.cpu().numpy(), L, args.cpu_seconds)
+                                               rand_h, L, args.cpu_seconds)
         cpu = {"value": rate, "unit": "walk-steps/s", "cores": 1, "kind": "port",
                "sample": f"{walks} of {N} walks (evenly strided) x {L} steps, {dt:.1f} s, "
                          f"oracle/walk_oracle.c uniform walk, 1 thread"}
@@ -329,8 +371,16 @@ def main():
                "sample": f"{walks} of {N} walks (evenly strided) x {L} steps, {dt:.1f} s, "
                          f"oracle/walk_oracle.c node2vec walk with libc rand() and linear "
                          f"is_neighbor scans as in the reference, 1 thread"}
+        rand_h = None
         log(f"cpu baseline {rate:.3e} steps/s over {walks} walks")
 
+    if cpu:
+        cpu["host_cpu"] = model
+        cpu["host_cores_available"] = cores
+        threads = min(cores, 16)  # the GPU box's CPU share
+        ctx = cpu_all_cores_context(np, torch, mc, kind, rowptr_h, col_h, start.cpu().numpy(),
+                                    rand_h, L, extra, walks, threads)
+        log(f"cpu all-cores context {ctx['value']:.3e} steps/s on {threads} threads")
     line = {
         "metric": METRIC, "value": value, "unit": "walk-steps/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
@@ -343,6 +393,7 @@ def main():
     }
     if cpu:
         line["speedup_vs_cpu_baseline"] = value / cpu["value"]
+        line["cpu_all_cores_context"] = ctx
     print(json.dumps(line), flush=True)
 
 

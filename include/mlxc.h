@@ -176,6 +176,40 @@ int mlxc_csr_check(const int64_t* d_rowptr, int64_t num_nodes,
  */
 int mlxc_philox_uniform(float* d_out, int64_t n, uint64_t seed, void* stream);
 
+/*
+ * Host twins of the three walk entry points: the same walks, the same
+ * arguments with host pointers, evaluated on `threads` CPU threads (<= 0:
+ * one per hardware thread) and returning when done.  Outputs are
+ * bit-identical to the device entry points for the same inputs and seed.
+ * *status (may be NULL) receives the MLXC_STATUS_* bits that the device
+ * entry points leave in workspace word 0; no workspace is needed.
+ * Replace: the eval_cpu paths the reference takes for stream=mx.cpu —
+ *   /root/reference/random_walks/RandomWalk.cpp:18-62 and
+ *   /root/reference/random_walks/BiasedRandomWalk.cpp:30-102 (serial loops
+ *   there; the biased one draws from libc rand(), these from the Philox
+ *   stream of mlxc_rejection_sampling).
+ */
+int mlxc_random_walk_cpu(const int64_t* rowptr, int64_t num_nodes,
+                         const int64_t* col, int64_t num_edges,
+                         const int64_t* start, int64_t num_walks,
+                         const float* rand, int32_t walk_length,
+                         int64_t* n_out, int64_t* e_out, int32_t threads, int64_t* status);
+
+int mlxc_random_walk_seeded_cpu(const int64_t* rowptr, int64_t num_nodes,
+                                const int64_t* col, int64_t num_edges,
+                                const int64_t* start, int64_t num_walks,
+                                int32_t walk_length, uint64_t seed,
+                                int64_t* n_out, int64_t* e_out, int32_t threads,
+                                int64_t* status);
+
+int mlxc_rejection_sampling_cpu(const int64_t* rowptr, int64_t num_nodes,
+                                const int64_t* col, int64_t num_edges,
+                                const int64_t* start, int64_t num_walks,
+                                int32_t walk_length, double p, double q,
+                                uint64_t seed, int32_t rule, int32_t rows,
+                                int64_t* n_out, int64_t* e_out, int32_t threads,
+                                int64_t* status);
+
 #ifdef __cplusplus
 }
 #endif

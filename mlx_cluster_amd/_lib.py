@@ -60,6 +60,19 @@ SIGNATURES = {
     ),
     "mlxc_csr_check": (ctypes.c_int, [_ptr, _i64, _ptr, _i64, _ptr, _size, _ptr, _ptr]),
     "mlxc_philox_uniform": (ctypes.c_int, [_ptr, _i64, _u64, _ptr]),
+    "mlxc_random_walk_cpu": (
+        ctypes.c_int,
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _i32, _ptr],
+    ),
+    "mlxc_random_walk_seeded_cpu": (
+        ctypes.c_int,
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _u64, _ptr, _ptr, _i32, _ptr],
+    ),
+    "mlxc_rejection_sampling_cpu": (
+        ctypes.c_int,
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _dbl, _dbl, _u64, _i32, _i32,
+         _ptr, _ptr, _i32, _ptr],
+    ),
 }
 
 _lib = None

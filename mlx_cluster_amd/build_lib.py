@@ -12,7 +12,8 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 SOURCES = [os.path.join(CSRC, f) for f in
-           ("mlxc_api.hip", "prep_kernels.hip", "uniform_walk.hip", "node2vec_walk.hip")]
+           ("mlxc_api.hip", "prep_kernels.hip", "uniform_walk.hip", "node2vec_walk.hip",
+            "host_walk.cpp")]
 OUT = os.path.join(PKG_DIR, "libmlxc.so")
 INCLUDE = os.path.join(REPO_DIR, "include")
 

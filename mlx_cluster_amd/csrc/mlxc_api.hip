@@ -48,14 +48,13 @@ int check_workspace(const void* work, size_t work_bytes) {
     return MLXC_OK;
 }
 
-int check_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col, int64_t num_edges,
-               const int64_t* start, int64_t num_walks, int32_t walk_length, const int64_t* n_out,
-               const void* work, size_t work_bytes) {
+int check_graph(const int64_t* rowptr, int64_t num_nodes, const int64_t* col, int64_t num_edges,
+                const int64_t* start, int64_t num_walks, int32_t walk_length,
+                const int64_t* n_out) {
     if (num_nodes < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_nodes must be >= 0");
     if (num_edges < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_edges must be >= 0");
     if (num_walks < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_walks must be >= 0");
     if (walk_length < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "walk_length must be >= 0");
-    if (int rc = check_workspace(work, work_bytes)) return rc;
     if (num_walks > 0) {
         if (!rowptr || !start || !n_out)
             return fail(MLXC_ERR_INVALID_ARGUMENT, "rowptr, start and n_out must not be NULL");
@@ -64,6 +63,44 @@ int check_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col, int
             return fail(MLXC_ERR_INVALID_ARGUMENT, "num_walks * (walk_length + 1) overflows int64");
     }
     return MLXC_OK;
+}
+
+int check_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col, int64_t num_edges,
+               const int64_t* start, int64_t num_walks, int32_t walk_length, const int64_t* n_out,
+               const void* work, size_t work_bytes) {
+    if (int rc = check_graph(rowptr, num_nodes, col, num_edges, start, num_walks, walk_length,
+                             n_out))
+        return rc;
+    return check_workspace(work, work_bytes);
+}
+
+// Parameters of one node2vec call; the acceptance constants exactly as
+// BiasedRandomWalk.cpp:52-55, in FP64.
+int n2v_params(double p, double q, uint64_t seed, int32_t rule, int32_t rows, N2VParams& prm) {
+    if (!(p > 0.0) || !(q > 0.0) || !std::isfinite(p) || !std::isfinite(q))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "p and q must be finite and > 0");
+    if (rule != MLXC_RULE_REF_CHAIN && rule != MLXC_RULE_NODE2VEC_EXACT)
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "rule must be MLXC_RULE_REF_CHAIN or MLXC_RULE_NODE2VEC_EXACT");
+    if (rows != MLXC_ROWS_UNSORTED && rows != MLXC_ROWS_SORTED && rows != MLXC_ROWS_DETECT)
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "rows must be MLXC_ROWS_UNSORTED, MLXC_ROWS_SORTED or MLXC_ROWS_DETECT");
+    const double max_prob = std::fmax(std::fmax(1. / p, 1.), 1. / q);
+    prm.prob0 = 1. / p / max_prob;
+    prm.prob1 = 1. / max_prob;
+    prm.prob2 = 1. / q / max_prob;
+    prm.key0 = static_cast<uint32_t>(seed);
+    prm.key1 = static_cast<uint32_t>(seed >> 32);
+    prm.rule = rule;
+    prm.rows = rows;
+    return MLXC_OK;
+}
+
+HostWalk host_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
+                   int64_t num_edges, const int64_t* start, int64_t num_walks, const float* rand,
+                   int32_t walk_length, uint64_t seed, int64_t* n_out, int64_t* e_out) {
+    return HostWalk{rowptr, col, start, rand, n_out, e_out, num_nodes, num_edges, num_walks,
+                    walk_length, static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32)};
 }
 
 }  // namespace
@@ -132,28 +169,12 @@ int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const in
     if (int rc = check_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
                             walk_length, d_n_out, d_workspace, workspace_bytes))
         return rc;
-    if (!(p > 0.0) || !(q > 0.0) || !std::isfinite(p) || !std::isfinite(q))
-        return fail(MLXC_ERR_INVALID_ARGUMENT, "p and q must be finite and > 0");
-    if (rule != MLXC_RULE_REF_CHAIN && rule != MLXC_RULE_NODE2VEC_EXACT)
-        return fail(MLXC_ERR_INVALID_ARGUMENT,
-                    "rule must be MLXC_RULE_REF_CHAIN or MLXC_RULE_NODE2VEC_EXACT");
-    if (rows != MLXC_ROWS_UNSORTED && rows != MLXC_ROWS_SORTED && rows != MLXC_ROWS_DETECT)
-        return fail(MLXC_ERR_INVALID_ARGUMENT,
-                    "rows must be MLXC_ROWS_UNSORTED, MLXC_ROWS_SORTED or MLXC_ROWS_DETECT");
+    N2VParams prm;
+    if (int rc = n2v_params(p, q, seed, rule, rows, prm)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     int64_t* d_work = static_cast<int64_t*>(d_workspace);
     if (int rc = launch_zero_work(d_work, s)) return rc;
     if (num_walks == 0) return MLXC_OK;
-    // Acceptance constants exactly as BiasedRandomWalk.cpp:52-55, in FP64.
-    const double max_prob = std::fmax(std::fmax(1. / p, 1.), 1. / q);
-    N2VParams prm;
-    prm.prob0 = 1. / p / max_prob;
-    prm.prob1 = 1. / max_prob;
-    prm.prob2 = 1. / q / max_prob;
-    prm.key0 = static_cast<uint32_t>(seed);
-    prm.key1 = static_cast<uint32_t>(seed >> 32);
-    prm.rule = rule;
-    prm.rows = rows;
     const WalkArgs a{d_rowptr, d_col, d_start, nullptr, d_n_out, d_e_out, d_work,
                      num_nodes, num_edges, num_walks, walk_length, 0u, 0u};
     return launch_node2vec(a, prm, d_workspace, workspace_bytes, s);
@@ -185,6 +206,56 @@ int mlxc_philox_uniform(float* d_out, int64_t n, uint64_t seed, void* stream) {
     if (n == 0) return MLXC_OK;
     if (!d_out) return fail(MLXC_ERR_INVALID_ARGUMENT, "out must not be NULL");
     return launch_philox_fill(d_out, n, seed, static_cast<hipStream_t>(stream));
+}
+
+int mlxc_random_walk_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
+                         int64_t num_edges, const int64_t* start, int64_t num_walks,
+                         const float* rand, int32_t walk_length, int64_t* n_out, int64_t* e_out,
+                         int32_t threads, int64_t* status) {
+    if (int rc = check_graph(rowptr, num_nodes, col, num_edges, start, num_walks, walk_length,
+                             n_out))
+        return rc;
+    if (num_walks > 0 && walk_length > 0 && !rand)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "rand must not be NULL");
+    uint32_t bits = 0;
+    const HostWalk w = host_walk(rowptr, num_nodes, col, num_edges, start, num_walks, rand,
+                                 walk_length, 0, n_out, e_out);
+    const int rc = host_uniform(w, false, threads, bits);
+    if (status) *status = bits;
+    return rc;
+}
+
+int mlxc_random_walk_seeded_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
+                                int64_t num_edges, const int64_t* start, int64_t num_walks,
+                                int32_t walk_length, uint64_t seed, int64_t* n_out,
+                                int64_t* e_out, int32_t threads, int64_t* status) {
+    if (int rc = check_graph(rowptr, num_nodes, col, num_edges, start, num_walks, walk_length,
+                             n_out))
+        return rc;
+    uint32_t bits = 0;
+    const HostWalk w = host_walk(rowptr, num_nodes, col, num_edges, start, num_walks, nullptr,
+                                 walk_length, seed, n_out, e_out);
+    const int rc = host_uniform(w, true, threads, bits);
+    if (status) *status = bits;
+    return rc;
+}
+
+int mlxc_rejection_sampling_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
+                                int64_t num_edges, const int64_t* start, int64_t num_walks,
+                                int32_t walk_length, double p, double q, uint64_t seed,
+                                int32_t rule, int32_t rows, int64_t* n_out, int64_t* e_out,
+                                int32_t threads, int64_t* status) {
+    if (int rc = check_graph(rowptr, num_nodes, col, num_edges, start, num_walks, walk_length,
+                             n_out))
+        return rc;
+    N2VParams prm;
+    if (int rc = n2v_params(p, q, seed, rule, rows, prm)) return rc;
+    uint32_t bits = 0;
+    const HostWalk w = host_walk(rowptr, num_nodes, col, num_edges, start, num_walks, nullptr,
+                                 walk_length, seed, n_out, e_out);
+    const int rc = host_node2vec(w, prm, threads, bits);
+    if (status) *status = bits;
+    return rc;
 }
 
 }  // extern "C"

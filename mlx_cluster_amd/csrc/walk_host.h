@@ -91,4 +91,19 @@ size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t nu
 int launch_node2vec(const WalkArgs& a, const N2VParams& p, void* workspace,
                     size_t workspace_bytes, hipStream_t stream);
 
+// ---- host_walk.cpp (host pointers; the same walks on CPU threads)
+struct HostWalk {
+    const int64_t* rowptr;
+    const int64_t* col;
+    const int64_t* start;
+    const float* rand;  // null when the uniforms are generated
+    int64_t* n_out;
+    int64_t* e_out;     // may be null
+    int64_t num_nodes, num_edges, num_walks, walk_length;
+    uint32_t key0, key1;  // Philox key of generated uniforms
+};
+// threads <= 0: one per hardware thread.  status receives MLXC_STATUS_* bits.
+int host_uniform(const HostWalk& w, bool generate, int32_t threads, uint32_t& status);
+int host_node2vec(const HostWalk& w, const N2VParams& p, int32_t threads, uint32_t& status);
+
 }  // namespace mlxc

@@ -14,7 +14,10 @@ current device).  Both functions return the node sequences, an int64 tensor
 [num_walks, walk_length + 1], as the reference ops do (they discard the edge
 output, RandomWalk.cpp:147); `return_edges=True` also returns the edge ids.
 
-Every walk runs in the HIP library libmlxc.so; there is no CPU path.
+Every walk runs in the library libmlxc.so: on the GPU through its HIP
+kernels, or, for stream='cpu' (the reference's eval_cpu), through its host
+twins on CPU threads, which give bit-identical results.  There is no
+fallback from one to the other.
 """
 from __future__ import annotations
 
@@ -34,6 +37,9 @@ _RULES = {"ref_chain": _lib.MLXC_RULE_REF_CHAIN, "node2vec": _lib.MLXC_RULE_NODE
 # ---------------------------------------------------------------- helpers
 
 def _resolve_device(stream, tensors) -> torch.device:
+    if _on_cpu(stream):
+        raise ValueError("this operation runs on the GPU only; stream='cpu' is for "
+                         "random_walk and rejection_sampling")
     if isinstance(stream, torch.cuda.Stream):
         return stream.device
     for t in tensors:
@@ -47,6 +53,9 @@ def _resolve_device(stream, tensors) -> torch.device:
 def _stream_handle(stream, device: torch.device) -> int:
     """hipStream_t for `stream`: None -> torch's current stream on device."""
     _check_stream_arg(stream)
+    if _on_cpu(stream) or device.type != "cuda":
+        raise ValueError("this operation runs on the GPU only; stream='cpu' is for "
+                         "random_walk and rejection_sampling")
     if stream is None:
         return torch.cuda.current_stream(device).cuda_stream
     if isinstance(stream, torch.cuda.Stream):
@@ -87,12 +96,27 @@ def _graph(rowptr, col, start):
 
 
 def _check_stream_arg(stream) -> None:
-    if isinstance(stream, (str, torch.device)) and torch.device(stream).type == "cpu":
-        raise ValueError(
-            "stream='cpu': this build evaluates walks on the GPU only "
-            "(the reference's CPU evaluation is not part of it)")
     if stream is not None and not isinstance(stream, (str, torch.device, torch.cuda.Stream)):
         raise TypeError(f"stream must be None, a torch.cuda.Stream or a device, got {type(stream)!r}")
+    if isinstance(stream, (str, torch.device)):
+        torch.device(stream)  # raises on an unknown device string
+
+
+def _on_cpu(stream) -> bool:
+    """stream='cpu' (or torch.device('cpu')) selects the host evaluation."""
+    return isinstance(stream, (str, torch.device)) and torch.device(stream).type == "cpu"
+
+
+def _threads(threads) -> int:
+    if threads is None:
+        return 0  # one per hardware thread
+    if isinstance(threads, bool) or not isinstance(threads, numbers.Integral) or threads < 1:
+        raise ValueError("threads must be None or an int >= 1")
+    return min(int(threads), 2**31 - 1)
+
+
+def _host(x: torch.Tensor) -> torch.Tensor:
+    return x.cpu().contiguous()
 
 
 def _walk_length(walk_length) -> int:
@@ -115,7 +139,10 @@ def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 def _raise_status(work: torch.Tensor, stream, what: str) -> None:
     if isinstance(stream, torch.cuda.Stream):
         stream.synchronize()  # the kernel ran there, not on torch's current stream
-    bits = int(work[0].item())
+    _raise_bits(int(work[0].item()), what)
+
+
+def _raise_bits(bits: int, what: str) -> None:
     if bits == 0:
         return
     reasons = []
@@ -130,7 +157,8 @@ def _raise_status(work: torch.Tensor, stream, what: str) -> None:
 
 def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
                 rand: Optional[TensorLike], walk_length: int, *, stream=None,
-                return_edges: bool = False, check: bool = True, seed: Optional[int] = None
+                return_edges: bool = False, check: bool = True, seed: Optional[int] = None,
+                threads: Optional[int] = None
                 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """Uniform random walks over a CSR graph.
 
@@ -148,7 +176,9 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
             seed), without the rand tensor's memory traffic.
         walk_length: steps per walk (>= 0).
         stream: None (torch's current stream), a torch.cuda.Stream or a
-            device.  'cpu' raises: this build has no CPU evaluation.
+            device.  'cpu' evaluates on CPU threads (the reference's
+            eval_cpu) with results bit-identical to the GPU's; inputs are
+            copied to host memory and outputs are CPU tensors.
         return_edges: also return the edge ids [num_walks, walk_length]
             (-1 where the walk stayed in a node of out-degree 0), the
             reference's discarded second output (RandomWalk.cpp:58).
@@ -156,6 +186,8 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
             rowptr entry was out of range (the reference reads out of bounds
             there).  With check=False the call stays asynchronous.
         seed: key of the generated uniforms when rand is None.
+        threads: CPU threads for stream='cpu' (None: one per hardware
+            thread); ignored on the GPU.
 
     Returns:
         int64 [num_walks, walk_length + 1] node sequences (and edge ids).
@@ -175,6 +207,22 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
         if rand.numel() != N * L:
             raise ValueError(f"rand must hold num_walks * walk_length = {N * L} values, "
                              f"got {rand.numel()}")
+    if _on_cpu(stream):
+        rowptr, col, start = (_host(t) for t in (rowptr, col, start))
+        n_out = torch.empty((N, L + 1), dtype=torch.int64)
+        e_out = torch.empty((N, L), dtype=torch.int64) if return_edges else None
+        status = _lib.ctypes.c_int64(0)
+        graph = (_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N)
+        outs = (_ptr(n_out), _ptr(e_out), _threads(threads), _lib.ctypes.addressof(status))
+        if rand is None:
+            rc = _lib.load().mlxc_random_walk_seeded_cpu(*graph, L, seed, *outs)
+        else:
+            rand = _host(rand)
+            rc = _lib.load().mlxc_random_walk_cpu(*graph, _ptr(rand), L, *outs)
+        _lib.check(rc, "random_walk")
+        if check:
+            _raise_bits(int(status.value), "random_walk")
+        return (n_out, e_out) if return_edges else n_out
     device = _resolve_device(stream, (rowptr, col, start, rand))
     handle = _stream_handle(stream, device)
     rowptr, col, start = (_on(t, device) for t in (rowptr, col, start))
@@ -219,7 +267,7 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
                        walk_length: int, p: float, q: float, *, stream=None,
                        seed: Optional[int] = None, rule: str = "ref_chain",
                        rows_sorted: Optional[bool] = None, return_edges: bool = False,
-                       check: bool = True
+                       check: bool = True, threads: Optional[int] = None
                        ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """node2vec random walks by rejection sampling.
 
@@ -244,7 +292,7 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
             lets the call check the rows on the device as part of its
             preparation pass, which also validates the whole graph (a
             malformed graph raises ValueError when check=True).
-        return_edges, check: as in random_walk.
+        return_edges, check, threads: as in random_walk.
     """
     L = _walk_length(walk_length)
     p, q = float(p), float(q)
@@ -254,15 +302,28 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
         raise ValueError(f"rule must be one of {sorted(_RULES)}")
     _check_stream_arg(stream)
     rowptr, col, start = _graph(rowptr, col, start)
-    device = _resolve_device(stream, (rowptr, col, start))
-    handle = _stream_handle(stream, device)
-    rowptr, col, start = (_on(t, device) for t in (rowptr, col, start))
     if seed is None:
         seed = int(torch.randint(0, 2**62, (1,)).item())
     seed = int(seed) & (2**64 - 1)
     rows = (_lib.MLXC_ROWS_DETECT if rows_sorted is None else
             _lib.MLXC_ROWS_SORTED if rows_sorted else _lib.MLXC_ROWS_UNSORTED)
     N = start.numel()
+    if _on_cpu(stream):
+        rowptr, col, start = (_host(t) for t in (rowptr, col, start))
+        n_out = torch.empty((N, L + 1), dtype=torch.int64)
+        e_out = torch.empty((N, L), dtype=torch.int64) if return_edges else None
+        status = _lib.ctypes.c_int64(0)
+        rc = _lib.load().mlxc_rejection_sampling_cpu(
+            _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,
+            p, q, seed, _RULES[rule], rows, _ptr(n_out), _ptr(e_out), _threads(threads),
+            _lib.ctypes.addressof(status))
+        _lib.check(rc, "rejection_sampling")
+        if check:
+            _raise_bits(int(status.value), "rejection_sampling")
+        return (n_out, e_out) if return_edges else n_out
+    device = _resolve_device(stream, (rowptr, col, start))
+    handle = _stream_handle(stream, device)
+    rowptr, col, start = (_on(t, device) for t in (rowptr, col, start))
     n_out = torch.empty((N, L + 1), dtype=torch.int64, device=device)
     e_out = torch.empty((N, L), dtype=torch.int64, device=device) if return_edges else None
     lib = _lib.load()

@@ -49,14 +49,6 @@ def test_seed_and_rand_are_exclusive():
         mc.random_walk(ROWPTR, COL, START, RAND, 4, seed=3)
 
 
-@pytest.mark.parametrize("stream", ["cpu", torch.device("cpu")])
-def test_cpu_stream_is_refused(stream):
-    with pytest.raises(ValueError, match="GPU only"):
-        mc.random_walk(ROWPTR, COL, START, RAND, 4, stream=stream)
-    with pytest.raises(ValueError, match="GPU only"):
-        mc.rejection_sampling(ROWPTR, COL, START, 4, 1.0, 1.0, stream=stream)
-
-
 def test_bad_stream_type():
     with pytest.raises(TypeError):
         mc.random_walk(ROWPTR, COL, START, RAND, 4, stream=3.5)

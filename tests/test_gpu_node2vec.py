@@ -174,3 +174,16 @@ def test_seed_none_follows_torch_manual_seed(c1, cuda):
     torch.manual_seed(3)
     b = mc.rejection_sampling(c1["rowptr"], c1["col"], c1["start"], 5, 1.0, 3.0)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("rule", ["ref_chain", "node2vec"])
+def test_cpu_twin_equals_gpu(rule, cuda):
+    """stream='cpu' (host twin) and the GPU kernels give the same node2vec
+    walks and edges on a hub graph, for sorted and unsorted row handling."""
+    rowptr, col = synth.ba_hub_csr(50_000, 5, 4, 8_000, seed=9)
+    start = torch.arange(100_000) % 50_000
+    for rows_sorted in (None, False):
+        kw = dict(seed=17, rule=rule, rows_sorted=rows_sorted, return_edges=True)
+        g = mc.rejection_sampling(rowptr.to(cuda), col.to(cuda), start.to(cuda), 15, 4.0, 0.25, **kw)
+        c = mc.rejection_sampling(rowptr, col, start, 15, 4.0, 0.25, stream="cpu", **kw)
+        assert torch.equal(g[0].cpu(), c[0]) and torch.equal(g[1].cpu(), c[1])

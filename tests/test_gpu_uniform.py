@@ -238,3 +238,19 @@ def test_seeded_uniforms_match_rand_tensor(N, L, cuda):
                                         start.cpu().numpy(), oracle.philox_uniform(N * L, seed), L)
     assert st == 0
     np.testing.assert_array_equal(got.cpu().numpy(), ref)
+
+
+def test_cpu_twin_equals_gpu(cuda):
+    """stream='cpu' (host twin) and the GPU kernels give the same walks and
+    edges, with a rand tensor and with generated uniforms."""
+    rowptr, col = synth.rmat_csr(16, 600_000, seed=6)
+    V = rowptr.numel() - 1
+    start = torch.arange(4 * V) % V
+    L = 21
+    rand = mc.philox_uniform((start.numel(), L), 5, device=cuda)
+    g = mc.random_walk(rowptr.to(cuda), col.to(cuda), start.to(cuda), rand, L, return_edges=True)
+    c = mc.random_walk(rowptr, col, start, rand.cpu(), L, return_edges=True, stream="cpu")
+    assert torch.equal(g[0].cpu(), c[0]) and torch.equal(g[1].cpu(), c[1])
+    g = mc.random_walk(rowptr.to(cuda), col.to(cuda), start.to(cuda), None, L, seed=5)
+    c = mc.random_walk(rowptr, col, start, None, L, seed=5, stream="cpu")
+    assert torch.equal(g.cpu(), c)

@@ -325,6 +325,38 @@ def test_node2vec_transition_chi_square(p, q, rule):
     assert stats.chisquare(class_counts(n, a, b), expect).pvalue > 0.01
 
 
+@pytest.mark.parametrize("p,q,rule", [
+    (0.5, 2.0, oracle.RULE_NODE2VEC_EXACT), (4.0, 0.25, oracle.RULE_NODE2VEC_EXACT),
+    (1.0, 3.0, oracle.RULE_NODE2VEC_EXACT), (4.0, 0.25, oracle.RULE_REF_CHAIN),
+    (0.5, 2.0, oracle.RULE_REF_CHAIN),
+])
+def test_node2vec_return_probability_on_trees(p, q, rule):
+    """On a tree no neighbour of v other than t is adjacent to t, so from v
+    (reached from t) the walk returns to t with probability
+    w0 / (w0 + (deg(v) - 1) * w2): (1/p) / ((1/p) + (deg(v) - 1)/q) for the
+    analytic rule, max(p0, p2) and p2 for the reference chain.  Checked on a
+    random tree over every step that has a previous node and deg(v) >= 2:
+    the count of returns against the sum of the per-step probabilities."""
+    rng = np.random.default_rng(int(p * 100 + q * 10 + rule))
+    V = 400
+    parent = [int(rng.integers(0, i)) for i in range(1, V)]
+    rowptr, col = undirected(V, [(i + 1, parent[i]) for i in range(V - 1)])
+    deg = np.diff(rowptr)
+    N, L = 20_000, 12
+    n, _, _ = n2v(rowptr, col, rng.integers(0, V, N), L, p, q, 77, rule)
+    p0, p1, p2 = oracle.node2vec_probs(p, q)
+    w0 = p0 if rule == oracle.RULE_NODE2VEC_EXACT else max(p0, p2)
+    prev, cur, nxt = n[:, :-2].ravel(), n[:, 1:-1].ravel(), n[:, 2:].ravel()
+    k = deg[cur]
+    use = k >= 2
+    prob = w0 / (w0 + (k[use] - 1) * p2)
+    returns = np.count_nonzero(nxt[use] == prev[use])
+    z = (returns - prob.sum()) / np.sqrt((prob * (1 - prob)).sum())
+    assert abs(z) < 4.5, (returns, prob.sum())
+    # deg(v) == 1 is forced back to t (BiasedRandomWalk.cpp:76-78)
+    assert np.all(nxt[k == 1] == prev[k == 1])
+
+
 def test_node2vec_libc_stream_chi_square():
     """The libc-rand() restatement (the reference's own draw pattern) gives
     the same transition law as the Philox-driven one."""
