@@ -244,8 +244,10 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     float r = 0.0f;         // acceptance uniform of the current trial
     OutWin<int32_t> ow;
     OutWin<int32_t> ew;     // edge ids (kEdges): e_out[n*L + l] is step l's edge
-    ow.count = 0;
-    ew.count = 0;
+    ow_init(ow);
+    ow_init(ew);
+    __shared__ WaveStage stage[kBlock / kWave];
+    WaveStage& st = stage[threadIdx.x / kWave];
     uint32_t status = 0;
 
     while (true) {
@@ -264,6 +266,9 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
 #pragma unroll
             for (int i = 0; i < kSearchBlock / 4; ++i) blkv[i] = bp[i];
         }
+        // ... and the output blocks the last iteration completed are stored.
+        ow_drain(ow, st);
+        if (kEdges) ow_drain(ew, st);
 
         // 2. Idle slots draw walk ids while the read is in flight.
         const bool need = phase == kN2vIdle;
@@ -274,6 +279,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             phase = id < N ? kN2vStart : kN2vDone;
         }
         if (!__any(phase != kN2vDone)) break;
+        wait_vmem();
+        keep_vgpr(rec.w);
         if (ph == kN2vIdle || ph == kN2vDone) continue;
 
         // 3. Consume.

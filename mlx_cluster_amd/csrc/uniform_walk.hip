@@ -154,6 +154,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
     RandWindow<RW> rw[W];
     OutWin<int32_t> ow[W];
     OutWin<int32_t> ew[W];     // edge ids (kEdges): e_out[n*L + l] is step l's edge
+    __shared__ WaveStage stage[kBlock / kWave];
+    WaveStage& st = stage[threadIdx.x / kWave];
     uint32_t status = 0;
 
 #pragma unroll
@@ -163,10 +165,10 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
         l[s] = 0;
         e[s] = 0;
         fr[s] = 0;
-        ew[s].count = 0;
         need_block[s] = false;
         rw[s].valid = 0;
-        ow[s].count = 0;
+        ow_init(ow[s]);
+        ow_init(ew[s]);
     }
 
     while (true) {
@@ -186,6 +188,12 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
 #pragma unroll
         for (int s = 0; s < W; ++s)
             if (need_block[s]) rw_fetch<RW, kGen>(rw[s], a, fr[s], rtotal);
+        // ... and the output blocks the last iteration completed are stored.
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            ow_drain(ow[s], st);
+            if (kEdges) ow_drain(ew[s], st);
+        }
 
         // 2. While the reads are in flight, idle slots draw walk ids from the
         // wave queue; they issue their start reads next iteration.
@@ -203,6 +211,9 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
             alive |= phase[s] != kSlotDone;
         }
         if (!__any(alive)) break;  // every slot done: nothing was read above
+        wait_vmem();
+#pragma unroll
+        for (int s = 0; s < W; ++s) keep_vgpr(rec[s].w);
 
         // 3. Consume: buffer the node, finish or pick the next edge.
 #pragma unroll
@@ -289,6 +300,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
     RandWindow<RW> rw[W];
     OutWin<int32_t> ow[W];
     OutWin<int32_t> ew[W];     // edge ids (kEdges): e_out[n*L + l] is step l's edge
+    __shared__ WaveStage stage[kBlock / kWave];
+    WaveStage& st = stage[threadIdx.x / kWave];
     uint32_t status = 0;
 
 #pragma unroll
@@ -299,10 +312,10 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
         e[s] = 0;
         v[s] = 0;
         fr[s] = 0;
-        ew[s].count = 0;
         need_block[s] = false;
         rw[s].valid = 0;
-        ow[s].count = 0;
+        ow_init(ow[s]);
+        ow_init(ew[s]);
     }
 
     while (true) {
@@ -324,6 +337,12 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
         for (int s = 0; s < W; ++s)  // a block due after a pick travels with the col read
             if (need_block[s] && ph[s] != kSlotRow)
                 rw_fetch<RW, kGen>(rw[s], a, fr[s], rtotal);
+        // ... and the output blocks the last iteration completed are stored.
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+            ow_drain(ow[s], st);
+            if (kEdges) ow_drain(ew[s], st);
+        }
 
         // 2. Idle slots draw walk ids while the reads are in flight.
         bool alive = false;
@@ -340,6 +359,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
             alive |= phase[s] != kSlotDone;
         }
         if (!__any(alive)) break;
+        wait_vmem();
 
         // 3. Consume.  Each slot ends the iteration with at most one
         // buffered entry, then at most one tail fill or flush.
@@ -430,15 +450,14 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
 
 // ------------------------------------------------------------- launcher
 
-// Walks in flight per lane.  The record walk is bound by the random-read
-// rate and runs best at the higher occupancy of one slot; the CSR walk (two
-// dependent reads per step, often over graphs of several GB) is latency-bound
-// and gains from a second slot.  Measured on MI355X, configurations 2 and 4.
+// Walks in flight per lane.  Both walks run best with one slot at the
+// higher occupancy it allows (measured on MI355X: configuration 4, CSR walk,
+// 6.8 ms with one slot against 8.0 ms with two).
 #ifndef MLXC_REC_SLOTS
 #define MLXC_REC_SLOTS 1
 #endif
 #ifndef MLXC_CSR_SLOTS
-#define MLXC_CSR_SLOTS 2
+#define MLXC_CSR_SLOTS 1
 #endif
 #ifndef MLXC_RAND_WINDOW
 #define MLXC_RAND_WINDOW 16    // uniforms per rand block (4-byte floats)

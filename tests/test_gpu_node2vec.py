@@ -187,3 +187,16 @@ def test_cpu_twin_equals_gpu(rule, cuda):
         g = mc.rejection_sampling(rowptr.to(cuda), col.to(cuda), start.to(cuda), 15, 4.0, 0.25, **kw)
         c = mc.rejection_sampling(rowptr, col, start, 15, 4.0, 0.25, stream="cpu", **kw)
         assert torch.equal(g[0].cpu(), c[0]) and torch.equal(g[1].cpu(), c[1])
+
+
+@pytest.mark.parametrize("L", [8, 300])
+def test_long_walks_with_sinks(L, cuda):
+    """Directed R-MAT graph (many nodes of out-degree 0): sink tails of up to
+    hundreds of 64-byte blocks and walks ending on a block boundary, stored
+    cooperatively by the wavefront; both rules, bit-exact."""
+    rowptr, col = synth.rmat_csr(10, 4000, seed=45)
+    rowptr, col = rowptr.numpy(), col.numpy()
+    start = (np.arange(2000) * 7) % (rowptr.size - 1)
+    for rule in (oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT):
+        _, counts = assert_parity(rowptr, col, start, L, 0.5, 2.0, 71, rule, cuda)
+        assert counts["sink_walks"] > 500

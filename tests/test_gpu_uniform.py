@@ -254,3 +254,31 @@ def test_cpu_twin_equals_gpu(cuda):
     g = mc.random_walk(rowptr.to(cuda), col.to(cuda), start.to(cuda), None, L, seed=5)
     c = mc.random_walk(rowptr, col, start, None, L, seed=5, stream="cpu")
     assert torch.equal(g.cpu(), c)
+
+
+@pytest.mark.parametrize("L", [7, 8, 9, 600])
+def test_long_and_block_sized_walks_with_sinks(L, cuda):
+    """Walk lengths around one 64-byte output block and far beyond it, on a
+    graph with many out-degree-0 nodes: completed blocks of many lanes at once
+    and sink tails of hundreds of blocks, all stored cooperatively by the
+    wavefront.  Nodes and edges bit-exact against the oracle for the record
+    walk (full workspace) and the CSR walk (start records only), and nodes
+    for generated uniforms."""
+    rowptr, col = synth.rmat_csr(10, 4000, seed=44, device=cuda)
+    V, E = rowptr.numel() - 1, col.numel()
+    N = 3000  # N * L >= 4 * E and a multiple of 4: both windowed walks apply
+    assert N * L >= 4 * E and (N * L) % 4 == 0
+    start = (torch.arange(N, device=cuda) * 7) % V
+    rand = mc.philox_uniform((N, L), 8, device=cuda)
+    n_ref, e_ref, st, counts = oracle.uniform_walk(rowptr.cpu().numpy(), col.cpu().numpy(),
+                                                   start.cpu().numpy(), rand.cpu().numpy(), L,
+                                                   with_edges=True)
+    assert st == 0 and counts["sink_walks"] > N // 4
+    for ws_bytes in (256 + 16 * (E + N), 256 + 16 * N):
+        n = torch.empty((N, L + 1), dtype=torch.int64, device=cuda)
+        e = torch.empty((N, L), dtype=torch.int64, device=cuda)
+        _abi_walk(rowptr, col, start, rand.data_ptr(), L, n.data_ptr(), e_out=e, ws_bytes=ws_bytes)
+        np.testing.assert_array_equal(n.cpu().numpy(), n_ref)
+        np.testing.assert_array_equal(e.cpu().numpy(), e_ref)
+    g = mc.random_walk(rowptr, col, start, None, L, seed=8)
+    np.testing.assert_array_equal(g.cpu().numpy(), n_ref)
