@@ -16,7 +16,6 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5
 from __future__ import annotations
 
 import argparse
-import hashlib
 import json
 import os
 import sys
@@ -56,12 +55,10 @@ def log(*a):
 
 
 def kernel_source_hash() -> str:
-    """sha256[:16] over every source file of libmlxc.so."""
-    from mlx_cluster_amd.build_lib import source_files
-    h = hashlib.sha256()
-    for path in source_files():
-        h.update(open(path, "rb").read())
-    return h.hexdigest()[:16]
+    """sha256[:16] over the code (not the comments) of every source file of
+    libmlxc.so."""
+    from mlx_cluster_amd.build_lib import source_hash
+    return source_hash()
 
 
 def traffic_from_profile(name: str):

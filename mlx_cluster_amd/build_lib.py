@@ -4,7 +4,9 @@ Usage: python -m mlx_cluster_amd.build_lib   (or build() from __graft_entry__)
 """
 from __future__ import annotations
 
+import hashlib
 import os
+import re
 import subprocess
 import sys
 
@@ -53,6 +55,24 @@ def source_files() -> list[str]:
     """Every file the library is built from (kernels, headers, C ABI)."""
     return sorted([os.path.join(CSRC, f) for f in os.listdir(CSRC)] +
                   [os.path.join(INCLUDE, "mlxc.h")])
+
+
+def _code_only(text: str) -> str:
+    """C/C++ source without comments, trailing blanks and empty lines."""
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return "\n".join(line.rstrip() for line in text.splitlines() if line.strip())
+
+
+def source_hash() -> str:
+    """sha256[:16] over the code of every source file (comments excluded, so
+    that a profile taken of a build stays matched to it across comment
+    edits)."""
+    h = hashlib.sha256()
+    for path in source_files():
+        h.update(os.path.basename(path).encode())
+        h.update(_code_only(open(path, encoding="utf-8").read()).encode())
+    return h.hexdigest()[:16]
 
 
 if __name__ == "__main__":

@@ -212,8 +212,8 @@ __device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, double r, bool 
     return adjacent ? (r < a.prob1) : (r < a.prob2);
 }
 
-// node2vec walk over edge records (num_nodes, num_edges below 2^31; no edge
-// output).  One walk per lane slot from the wave queue.  Every iteration a
+// node2vec walk over edge records (num_nodes, num_edges below 2^31; n_out and
+// e_out 16-byte aligned).  One walk per lane slot from the wave queue.  Every iteration a
 // live slot issues one dependent read — a start record, the edge record of
 // its candidate (which carries the candidate's row, so the neighbour test
 // needs no rowptr read), or one step of the neighbour search — and the wave

@@ -124,17 +124,18 @@ enum : int {
     kSlotDone = 5,   // the queue is exhausted
 };
 
-// Uniform walk over edge records (requires 16-byte aligned rand and n_out,
-// num_nodes and num_edges below 2^31, num_walks * walk_length a multiple of
-// 4 and at least RW; no edge output).
+// Uniform walk over edge records (requires 16-byte aligned rand, n_out and
+// e_out, num_nodes and num_edges below 2^31, num_walks * walk_length a
+// multiple of 4 and at least RW).
 //
 // Loop invariant: every live slot issues exactly one dependent 16-byte read
 // per iteration (a start record or an edge record), plus at most one
 // independent rand block, and the wave waits once.  The rand value for a step
 // is taken from the window in the iteration before the read it addresses, so
 // a new rand block always travels together with a record read and never costs
-// a round trip of its own.  Output stores issued after the wait overlap the
-// next iteration's read.
+// a round trip of its own.  The whole blocks of output completed in one
+// iteration are stored by the wavefront (ow_drain) right after the next
+// iteration's reads are issued, so they overlap those reads.
 template <int W, int RW, bool kGen, bool kEdges>
 __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                                                                   const EdgeRecord* __restrict__ recs,
