@@ -88,6 +88,20 @@ def uniform_counts(torch, rowptr, walks):
     return M, int(sunk.sum())
 
 
+class one_core:
+    """Pins this process to one core of its affinity set for the block (the
+    single-threaded CPU baseline), restoring the set afterwards."""
+
+    def __enter__(self):
+        self.saved = os.sched_getaffinity(0)
+        self.core = min(self.saved)
+        os.sched_setaffinity(0, {self.core})
+        return self
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.saved)
+
+
 def cpu_baseline_uniform(np, oracle, rowptr_h, col_h, start, rand, L, target_s=12.0):
     """Single-threaded oracle walk on an evenly strided sample of walks."""
     N = start.shape[0]
@@ -300,6 +314,17 @@ def main():
     value = steps_per_launch / (ms_per_step / 1e3)
     log(f"{ms_per_step:.3f} ms/step wall, {kernel_ms:.3f} ms/launch (events)")
 
+    # One end-to-end call with allocation: the caching allocator is emptied
+    # first, so the output and workspace come from fresh device allocations.
+    del out
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    t0 = time.perf_counter()
+    out = step()
+    torch.cuda.synchronize()
+    e2e_alloc_ms = (time.perf_counter() - t0) * 1e3
+    log(f"{e2e_alloc_ms:.3f} ms end to end with fresh allocations")
+
     import oracle
     rowptr_h, col_h = rowptr.cpu().numpy(), col.cpu().numpy()
     g = torch.Generator().manual_seed(1)
@@ -328,6 +353,7 @@ def main():
                 "frac": (achieved / PEAK_HBM_GBS) if achieved else None, "traffic": traffic,
                 "algorithmic_bytes_per_launch": roof_bytes,
                 "kernel_ms": kernel_ms, "kernel_ms_median": kernel_ms_median,
+                "e2e_ms_with_allocation": e2e_alloc_ms,
                 "kernel_ms_source": "HIP events around each call on its stream (mean; median beside it)",
                 "useful_gbs": useful_bytes / (kernel_ms / 1e3) / 1e9,
                 "useful_bytes_per_launch": useful_bytes,
@@ -355,25 +381,30 @@ def main():
     model, cores = host_info()
     if not args.no_cpu_baseline and kind == "uniform":
         rand_h = rand.cpu().numpy()
-        rate, walks, dt = cpu_baseline_uniform(np, oracle, rowptr_h, col_h, start.cpu().numpy(),
-                                               rand_h, L, args.cpu_seconds)
+        with one_core() as pin:
+            rate, walks, dt = cpu_baseline_uniform(np, oracle, rowptr_h, col_h,
+                                                   start.cpu().numpy(), rand_h, L,
+                                                   args.cpu_seconds)
         cpu = {"value": rate, "unit": "walk-steps/s", "cores": 1, "kind": "port",
                "sample": f"{walks} of {N} walks (evenly strided) x {L} steps, {dt:.1f} s, "
-                         f"oracle/walk_oracle.c uniform walk, 1 thread"}
+                         f"oracle/walk_oracle.c uniform walk, 1 thread pinned to one core"}
         log(f"cpu baseline {rate:.3e} steps/s over {walks} walks")
     elif not args.no_cpu_baseline:
-        rate, walks, dt = cpu_baseline_node2vec(np, oracle, rowptr_h, col_h, start.cpu().numpy(),
-                                                L, extra, args.cpu_seconds)
+        with one_core() as pin:
+            rate, walks, dt = cpu_baseline_node2vec(np, oracle, rowptr_h, col_h,
+                                                    start.cpu().numpy(), L, extra,
+                                                    args.cpu_seconds)
         cpu = {"value": rate, "unit": "walk-steps/s", "cores": 1, "kind": "port",
                "sample": f"{walks} of {N} walks (evenly strided) x {L} steps, {dt:.1f} s, "
                          f"oracle/walk_oracle.c node2vec walk with libc rand() and linear "
-                         f"is_neighbor scans as in the reference, 1 thread"}
+                         f"is_neighbor scans as in the reference, 1 thread pinned to one core"}
         rand_h = None
         log(f"cpu baseline {rate:.3e} steps/s over {walks} walks")
 
     if cpu:
         cpu["host_cpu"] = model
         cpu["host_cores_available"] = cores
+        cpu["pinned_core"] = pin.core
         threads = min(cores, 16)  # the GPU box's CPU share
         ctx = cpu_all_cores_context(np, torch, mc, kind, rowptr_h, col_h, start.cpu().numpy(),
                                     rand_h, L, extra, walks, threads)
