@@ -35,6 +35,9 @@ CONFIGS = {
     "c2s": ("R-MAT 2^20 uniform walk, 10 walks/node, L=80, uniforms generated in the kernel "
             "(seed=2, the stream of c2's rand tensor)", "uniform_seeded",
             dict(scale=20, samples=1 << 24, symmetrize=False), 10, 80, {}),
+    "c2i": ("R-MAT 2^20 uniform walk, 10 walks/node, L=80, compact int32 output "
+            "(out_dtype=torch.int32; same walks as c2)", "uniform",
+            dict(scale=20, samples=1 << 24, symmetrize=False), 10, 80, dict(out_dtype="int32")),
     "c3": ("node2vec p=0.5 q=2 on symmetrized R-MAT 2^20, 4 walks/node, L=40", "node2vec",
            dict(scale=20, samples=1 << 24, symmetrize=True), 4, 40,
            dict(p=0.5, q=2.0, seed=3, rule="ref_chain")),
@@ -81,7 +84,7 @@ def uniform_counts(torch, rowptr, walks):
     M = 0
     sunk = torch.zeros(walks.shape[0], dtype=torch.bool, device=walks.device)
     for l in range(L):
-        u = walks[:, l]
+        u = walks[:, l].long()
         deg = rowptr[u + 1] - rowptr[u]
         M += int((deg > 0).sum())
         sunk |= deg == 0
@@ -285,7 +288,8 @@ def main():
         step = lambda: mc.random_walk(rowptr, col, start, None, L, seed=2)
     elif kind == "uniform":
         rand = mc.philox_uniform((N, L), 2, device=dev)
-        step = lambda: mc.random_walk(rowptr, col, start, rand, L)
+        out_dtype = getattr(torch, extra.get("out_dtype", "int64"))
+        step = lambda: mc.random_walk(rowptr, col, start, rand, L, out_dtype=out_dtype)
     else:
         rand = None
         step = lambda: mc.rejection_sampling(rowptr, col, start, L, extra["p"], extra["q"],
@@ -337,11 +341,12 @@ def main():
     if kind == "uniform":
         M, Z = uniform_counts(torch, rowptr, out)
         rand_bytes = 0 if seeded else 4 * M  # generated uniforms are not read
-        roof_bytes = LINE * (M + Z) + LINE * M + rand_bytes + 8 * N * (L + 1) + 8 * N
-        useful_bytes = 16 * (M + Z) + 8 * M + rand_bytes + 8 * N * (L + 1) + 8 * N
+        ob = out.element_size()  # output bytes per entry: 8, or 4 with int32 output
+        roof_bytes = LINE * (M + Z) + LINE * M + rand_bytes + ob * N * (L + 1) + 8 * N
+        useful_bytes = 16 * (M + Z) + 8 * M + rand_bytes + ob * N * (L + 1) + 8 * N
         units = dict(moving_steps=M, sink_walks=Z,
-                     bytes_formula=("64*(M+Z) + 64*M + 8*N*(L+1) + 8*N" if seeded else
-                                    "64*(M+Z) + 64*M + 4*M + 8*N*(L+1) + 8*N"))
+                     bytes_formula=(f"64*(M+Z) + 64*M + {'4*M + ' if not seeded else ''}"
+                                    f"{ob}*N*(L+1) + 8*N"))
     else:
         # node2vec: the work depends on rejections, so it is counted by the
         # oracle on an evenly strided sample of walks and scaled to N.
@@ -412,7 +417,8 @@ def main():
     line = {
         "metric": METRIC, "value": value, "unit": "walk-steps/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int64",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int32" if out.dtype == torch.int32 else "int64",
         "data": "synthetic",
         "config": {"workload": f"{args.config}: {desc}", "num_nodes": V, "num_edges": E,
                    "num_walks": N, "walk_length": L, "walk_steps_per_launch": steps_per_launch,

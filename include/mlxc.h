@@ -60,6 +60,12 @@ extern "C" {
 #define MLXC_CSR_BAD_COL 2      /* a col value outside [0, V) */
 #define MLXC_CSR_UNSORTED 4     /* some row is not sorted ascending */
 
+/* Element type of the walk outputs (out_type argument).  The reference
+ * writes int64 (RandomWalk.cpp:43,57-58); int32 halves the output bytes and
+ * needs num_nodes (and, with edge output, num_edges) below 2^31. */
+#define MLXC_OUT_INT64 0
+#define MLXC_OUT_INT32 1
+
 /* Trial cap of one biased step (the reference loops without bound,
  * BiasedRandomWalk.cpp:80): after this many rejections the last candidate is
  * kept. */
@@ -95,8 +101,9 @@ size_t mlxc_rejection_sampling_workspace_bytes(int64_t num_nodes, int64_t num_ed
  *
  * d_rowptr  int64 [num_nodes + 1]     d_col  int64 [num_edges]
  * d_start   int64 [num_walks]         d_rand float32 [num_walks * walk_length]
- * d_n_out   int64 [num_walks * (walk_length + 1)]  (row-major [N, L+1])
- * d_e_out   int64 [num_walks * walk_length] or NULL (edge ids, -1 = stayed)
+ * d_n_out   [num_walks * (walk_length + 1)]  (row-major [N, L+1])
+ * d_e_out   [num_walks * walk_length] or NULL (edge ids, -1 = stayed)
+ * out_type  MLXC_OUT_INT64 or MLXC_OUT_INT32: element type of both outputs
  * d_workspace, workspace_bytes: device workspace (see above).
  *
  * Step l of walk n at node v: deg = rowptr[v+1] - rowptr[v]; deg == 0 keeps
@@ -107,7 +114,7 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes,
                      const int64_t* d_col, int64_t num_edges,
                      const int64_t* d_start, int64_t num_walks,
                      const float* d_rand, int32_t walk_length,
-                     int64_t* d_n_out, int64_t* d_e_out,
+                     void* d_n_out, void* d_e_out, int32_t out_type,
                      void* d_workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -125,7 +132,7 @@ int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes,
                             const int64_t* d_col, int64_t num_edges,
                             const int64_t* d_start, int64_t num_walks,
                             int32_t walk_length, uint64_t seed,
-                            int64_t* d_n_out, int64_t* d_e_out,
+                            void* d_n_out, void* d_e_out, int32_t out_type,
                             void* d_workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -152,7 +159,7 @@ int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes,
                             const int64_t* d_start, int64_t num_walks,
                             int32_t walk_length, double p, double q,
                             uint64_t seed, int32_t rule, int32_t rows,
-                            int64_t* d_n_out, int64_t* d_e_out,
+                            void* d_n_out, void* d_e_out, int32_t out_type,
                             void* d_workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -193,22 +200,23 @@ int mlxc_random_walk_cpu(const int64_t* rowptr, int64_t num_nodes,
                          const int64_t* col, int64_t num_edges,
                          const int64_t* start, int64_t num_walks,
                          const float* rand, int32_t walk_length,
-                         int64_t* n_out, int64_t* e_out, int32_t threads, int64_t* status);
+                         void* n_out, void* e_out, int32_t out_type,
+                         int32_t threads, int64_t* status);
 
 int mlxc_random_walk_seeded_cpu(const int64_t* rowptr, int64_t num_nodes,
                                 const int64_t* col, int64_t num_edges,
                                 const int64_t* start, int64_t num_walks,
                                 int32_t walk_length, uint64_t seed,
-                                int64_t* n_out, int64_t* e_out, int32_t threads,
-                                int64_t* status);
+                                void* n_out, void* e_out, int32_t out_type,
+                                int32_t threads, int64_t* status);
 
 int mlxc_rejection_sampling_cpu(const int64_t* rowptr, int64_t num_nodes,
                                 const int64_t* col, int64_t num_edges,
                                 const int64_t* start, int64_t num_walks,
                                 int32_t walk_length, double p, double q,
                                 uint64_t seed, int32_t rule, int32_t rows,
-                                int64_t* n_out, int64_t* e_out, int32_t threads,
-                                int64_t* status);
+                                void* n_out, void* e_out, int32_t out_type,
+                                int32_t threads, int64_t* status);
 
 #ifdef __cplusplus
 }

@@ -108,15 +108,15 @@ constexpr int64_t kHostChunk = 1024;  // walks per chunk
 // Uniform walks [first, last): the loop of RandomWalk.cpp:41-60, with the
 // out-of-range handling of uniform_walk_kernel (the walk stops and repeats
 // its node, edge id -1).
-template <bool kGen>
+template <bool kGen, typename OutT>
 uint32_t uniform_range(const HostWalk& w, int64_t first, int64_t last) {
     const int64_t L = w.walk_length;
     uint32_t status = 0;
     for (int64_t n = first; n < last; ++n) {
-        int64_t* out = w.n_out + n * (L + 1);
-        int64_t* eout = w.e_out ? w.e_out + n * L : nullptr;
+        OutT* out = static_cast<OutT*>(w.n_out) + n * (L + 1);
+        OutT* eout = w.e_out ? static_cast<OutT*>(w.e_out) + n * L : nullptr;
         int64_t v = w.start[n];
-        out[0] = v;
+        out[0] = static_cast<OutT>(v);
         int64_t l = 0;
         int64_t block = -1;  // Philox block whose four uniforms are in u[]
         float u[4] = {0.f, 0.f, 0.f, 0.f};
@@ -150,8 +150,8 @@ uint32_t uniform_range(const HostWalk& w, int64_t first, int64_t last) {
                 }
                 const int64_t e = begin + pick_index_host(r, end - begin);
                 const int64_t x = w.col[e];
-                out[l + 1] = x;
-                if (eout) eout[l] = e;
+                out[l + 1] = static_cast<OutT>(x);
+                if (eout) eout[l] = static_cast<OutT>(e);
                 v = x;
                 if (!node_in(x, w.num_nodes)) {
                     status |= MLXC_STATUS_BAD_NODE;
@@ -161,7 +161,7 @@ uint32_t uniform_range(const HostWalk& w, int64_t first, int64_t last) {
             }
         }
         for (int64_t j = l; j < L; ++j) {
-            out[j + 1] = v;
+            out[j + 1] = static_cast<OutT>(v);
             if (eout) eout[j] = -1;
         }
     }
@@ -199,17 +199,17 @@ bool accept_host(const HostWalk& w, const N2VParams& prm, bool sorted, double r,
 
 // node2vec walks [first, last): BiasedRandomWalk.cpp:57-100 on the Philox
 // stream (counter = walk, step, trial), as node2vec_walk_kernel.
-template <int kRule>
+template <int kRule, typename OutT>
 uint32_t node2vec_range(const HostWalk& w, const N2VParams& prm, bool sorted, int64_t first,
                         int64_t last) {
     const int64_t L = w.walk_length;
     const int64_t V = w.num_nodes;
     uint32_t status = 0;
     for (int64_t n = first; n < last; ++n) {
-        int64_t* out = w.n_out + n * (L + 1);
-        int64_t* eout = w.e_out ? w.e_out + n * L : nullptr;
+        OutT* out = static_cast<OutT*>(w.n_out) + n * (L + 1);
+        OutT* eout = w.e_out ? static_cast<OutT*>(w.e_out) + n * L : nullptr;
         int64_t t = w.start[n];
-        out[0] = t;
+        out[0] = static_cast<OutT>(t);
         if (L == 0) {
             if (!node_in(t, V)) status |= MLXC_STATUS_BAD_NODE;
             continue;
@@ -233,8 +233,8 @@ uint32_t node2vec_range(const HostWalk& w, const N2VParams& prm, bool sorted, in
                 v = w.col[e];
             }
         }
-        out[1] = v;
-        if (eout) eout[0] = e;
+        out[1] = static_cast<OutT>(v);
+        if (eout) eout[0] = static_cast<OutT>(e);
         for (int64_t l = 1; l < L; ++l) {
             int64_t x = v;
             e = -1;
@@ -268,8 +268,8 @@ uint32_t node2vec_range(const HostWalk& w, const N2VParams& prm, bool sorted, in
                     }
                 }
             }
-            out[l + 1] = x;
-            if (eout) eout[l] = e;
+            out[l + 1] = static_cast<OutT>(x);
+            if (eout) eout[l] = static_cast<OutT>(e);
             t = v;
             v = x;
         }
@@ -313,15 +313,35 @@ uint32_t host_csr_scan(const HostWalk& w, int threads, bool& sorted) {
     return status;
 }
 
+template <typename OutT>
+int host_uniform_typed(const HostWalk& w, bool generate, int t, uint32_t& status) {
+    if (generate)
+        return run_chunks(w.num_walks, t, kHostChunk,
+                          [&](int64_t a, int64_t b) { return uniform_range<true, OutT>(w, a, b); },
+                          status);
+    return run_chunks(w.num_walks, t, kHostChunk,
+                      [&](int64_t a, int64_t b) { return uniform_range<false, OutT>(w, a, b); },
+                      status);
+}
+
+template <typename OutT>
+int host_node2vec_typed(const HostWalk& w, const N2VParams& prm, bool sorted, int t,
+                        uint32_t& status) {
+    if (prm.rule == MLXC_RULE_REF_CHAIN)
+        return run_chunks(w.num_walks, t, kHostChunk, [&](int64_t a, int64_t b) {
+            return node2vec_range<MLXC_RULE_REF_CHAIN, OutT>(w, prm, sorted, a, b);
+        }, status);
+    return run_chunks(w.num_walks, t, kHostChunk, [&](int64_t a, int64_t b) {
+        return node2vec_range<MLXC_RULE_NODE2VEC_EXACT, OutT>(w, prm, sorted, a, b);
+    }, status);
+}
+
 }  // namespace
 
 int host_uniform(const HostWalk& w, bool generate, int32_t threads, uint32_t& status) {
     const int t = resolve_threads(threads);
-    if (generate)
-        return run_chunks(w.num_walks, t, kHostChunk,
-                          [&](int64_t a, int64_t b) { return uniform_range<true>(w, a, b); }, status);
-    return run_chunks(w.num_walks, t, kHostChunk,
-                      [&](int64_t a, int64_t b) { return uniform_range<false>(w, a, b); }, status);
+    return w.out_type == MLXC_OUT_INT32 ? host_uniform_typed<int32_t>(w, generate, t, status)
+                                        : host_uniform_typed<int64_t>(w, generate, t, status);
 }
 
 int host_node2vec(const HostWalk& w, const N2VParams& prm, int32_t threads, uint32_t& status) {
@@ -329,15 +349,9 @@ int host_node2vec(const HostWalk& w, const N2VParams& prm, int32_t threads, uint
     uint32_t prep = 0;
     bool sorted = prm.rows == MLXC_ROWS_SORTED;
     if (prm.rows == MLXC_ROWS_DETECT && w.num_walks > 0) prep = host_csr_scan(w, t, sorted);
-    int rc;
-    if (prm.rule == MLXC_RULE_REF_CHAIN)
-        rc = run_chunks(w.num_walks, t, kHostChunk, [&](int64_t a, int64_t b) {
-            return node2vec_range<MLXC_RULE_REF_CHAIN>(w, prm, sorted, a, b);
-        }, status);
-    else
-        rc = run_chunks(w.num_walks, t, kHostChunk, [&](int64_t a, int64_t b) {
-            return node2vec_range<MLXC_RULE_NODE2VEC_EXACT>(w, prm, sorted, a, b);
-        }, status);
+    const int rc = w.out_type == MLXC_OUT_INT32
+                       ? host_node2vec_typed<int32_t>(w, prm, sorted, t, status)
+                       : host_node2vec_typed<int64_t>(w, prm, sorted, t, status);
     status |= prep;
     return rc;
 }

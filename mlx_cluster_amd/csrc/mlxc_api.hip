@@ -50,7 +50,7 @@ int check_workspace(const void* work, size_t work_bytes) {
 
 int check_graph(const int64_t* rowptr, int64_t num_nodes, const int64_t* col, int64_t num_edges,
                 const int64_t* start, int64_t num_walks, int32_t walk_length,
-                const int64_t* n_out) {
+                const void* n_out) {
     if (num_nodes < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_nodes must be >= 0");
     if (num_edges < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_edges must be >= 0");
     if (num_walks < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_walks must be >= 0");
@@ -65,12 +65,23 @@ int check_graph(const int64_t* rowptr, int64_t num_nodes, const int64_t* col, in
     return MLXC_OK;
 }
 
+// The output element type, and whether the ids fit it.
+int check_out_type(int32_t out_type, int64_t num_nodes, int64_t num_edges, const void* e_out) {
+    if (out_type != MLXC_OUT_INT64 && out_type != MLXC_OUT_INT32)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "out_type must be MLXC_OUT_INT64 or MLXC_OUT_INT32");
+    if (out_type == MLXC_OUT_INT32 && (num_nodes > INT32_MAX || (e_out && num_edges > INT32_MAX)))
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "MLXC_OUT_INT32 needs num_nodes (and, with edge output, num_edges) below 2^31");
+    return MLXC_OK;
+}
+
 int check_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col, int64_t num_edges,
-               const int64_t* start, int64_t num_walks, int32_t walk_length, const int64_t* n_out,
-               const void* work, size_t work_bytes) {
+               const int64_t* start, int64_t num_walks, int32_t walk_length, const void* n_out,
+               const void* e_out, int32_t out_type, const void* work, size_t work_bytes) {
     if (int rc = check_graph(rowptr, num_nodes, col, num_edges, start, num_walks, walk_length,
                              n_out))
         return rc;
+    if (int rc = check_out_type(out_type, num_nodes, num_edges, e_out)) return rc;
     return check_workspace(work, work_bytes);
 }
 
@@ -93,14 +104,17 @@ int n2v_params(double p, double q, uint64_t seed, int32_t rule, int32_t rows, N2
     prm.key1 = static_cast<uint32_t>(seed >> 32);
     prm.rule = rule;
     prm.rows = rows;
+    prm.out_type = MLXC_OUT_INT64;
     return MLXC_OK;
 }
 
 HostWalk host_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                    int64_t num_edges, const int64_t* start, int64_t num_walks, const float* rand,
-                   int32_t walk_length, uint64_t seed, int64_t* n_out, int64_t* e_out) {
-    return HostWalk{rowptr, col, start, rand, n_out, e_out, num_nodes, num_edges, num_walks,
-                    walk_length, static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32)};
+                   int32_t walk_length, uint64_t seed, void* n_out, void* e_out,
+                   int32_t out_type) {
+    return HostWalk{rowptr, col, start, rand, n_out, e_out, out_type, num_nodes, num_edges,
+                    num_walks, walk_length, static_cast<uint32_t>(seed),
+                    static_cast<uint32_t>(seed >> 32)};
 }
 
 }  // namespace
@@ -110,7 +124,7 @@ using namespace mlxc;
 
 extern "C" {
 
-int mlxc_version(void) { return 100; }
+int mlxc_version(void) { return 200; }
 
 const char* mlxc_last_error(void) { return g_last_error.c_str(); }
 
@@ -126,10 +140,10 @@ size_t mlxc_rejection_sampling_workspace_bytes(int64_t num_nodes, int64_t num_ed
 
 int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
                      int64_t num_edges, const int64_t* d_start, int64_t num_walks,
-                     const float* d_rand, int32_t walk_length, int64_t* d_n_out,
-                     int64_t* d_e_out, void* d_workspace, size_t workspace_bytes, void* stream) {
+                     const float* d_rand, int32_t walk_length, void* d_n_out, void* d_e_out,
+                     int32_t out_type, void* d_workspace, size_t workspace_bytes, void* stream) {
     if (int rc = check_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
-                            walk_length, d_n_out, d_workspace, workspace_bytes))
+                            walk_length, d_n_out, d_e_out, out_type, d_workspace, workspace_bytes))
         return rc;
     if (num_walks > 0 && walk_length > 0 && !d_rand)
         return fail(MLXC_ERR_INVALID_ARGUMENT, "rand must not be NULL");
@@ -139,16 +153,16 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* 
     if (num_walks == 0) return MLXC_OK;
     const WalkArgs a{d_rowptr, d_col, d_start, d_rand, d_n_out, d_e_out, d_work,
                      num_nodes, num_edges, num_walks, walk_length, 0u, 0u};
-    return launch_uniform(a, d_workspace, workspace_bytes, false, s);
+    return launch_uniform(a, d_workspace, workspace_bytes, false, out_type, s);
 }
 
 int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
                             int64_t num_edges, const int64_t* d_start, int64_t num_walks,
-                            int32_t walk_length, uint64_t seed, int64_t* d_n_out,
-                            int64_t* d_e_out, void* d_workspace, size_t workspace_bytes,
+                            int32_t walk_length, uint64_t seed, void* d_n_out, void* d_e_out,
+                            int32_t out_type, void* d_workspace, size_t workspace_bytes,
                             void* stream) {
     if (int rc = check_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
-                            walk_length, d_n_out, d_workspace, workspace_bytes))
+                            walk_length, d_n_out, d_e_out, out_type, d_workspace, workspace_bytes))
         return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     int64_t* d_work = static_cast<int64_t*>(d_workspace);
@@ -157,20 +171,21 @@ int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes, const in
     const WalkArgs a{d_rowptr, d_col, d_start, nullptr, d_n_out, d_e_out, d_work,
                      num_nodes, num_edges, num_walks, walk_length,
                      static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32)};
-    return launch_uniform(a, d_workspace, workspace_bytes, true, s);
+    return launch_uniform(a, d_workspace, workspace_bytes, true, out_type, s);
 }
 
 int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
                             int64_t num_edges, const int64_t* d_start, int64_t num_walks,
                             int32_t walk_length, double p, double q, uint64_t seed,
-                            int32_t rule, int32_t rows, int64_t* d_n_out,
-                            int64_t* d_e_out, void* d_workspace, size_t workspace_bytes,
+                            int32_t rule, int32_t rows, void* d_n_out, void* d_e_out,
+                            int32_t out_type, void* d_workspace, size_t workspace_bytes,
                             void* stream) {
     if (int rc = check_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
-                            walk_length, d_n_out, d_workspace, workspace_bytes))
+                            walk_length, d_n_out, d_e_out, out_type, d_workspace, workspace_bytes))
         return rc;
     N2VParams prm;
     if (int rc = n2v_params(p, q, seed, rule, rows, prm)) return rc;
+    prm.out_type = out_type;
     hipStream_t s = static_cast<hipStream_t>(stream);
     int64_t* d_work = static_cast<int64_t*>(d_workspace);
     if (int rc = launch_zero_work(d_work, s)) return rc;
@@ -210,16 +225,17 @@ int mlxc_philox_uniform(float* d_out, int64_t n, uint64_t seed, void* stream) {
 
 int mlxc_random_walk_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                          int64_t num_edges, const int64_t* start, int64_t num_walks,
-                         const float* rand, int32_t walk_length, int64_t* n_out, int64_t* e_out,
-                         int32_t threads, int64_t* status) {
+                         const float* rand, int32_t walk_length, void* n_out, void* e_out,
+                         int32_t out_type, int32_t threads, int64_t* status) {
     if (int rc = check_graph(rowptr, num_nodes, col, num_edges, start, num_walks, walk_length,
                              n_out))
         return rc;
+    if (int rc = check_out_type(out_type, num_nodes, num_edges, e_out)) return rc;
     if (num_walks > 0 && walk_length > 0 && !rand)
         return fail(MLXC_ERR_INVALID_ARGUMENT, "rand must not be NULL");
     uint32_t bits = 0;
     const HostWalk w = host_walk(rowptr, num_nodes, col, num_edges, start, num_walks, rand,
-                                 walk_length, 0, n_out, e_out);
+                                 walk_length, 0, n_out, e_out, out_type);
     const int rc = host_uniform(w, false, threads, bits);
     if (status) *status = bits;
     return rc;
@@ -227,14 +243,15 @@ int mlxc_random_walk_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t
 
 int mlxc_random_walk_seeded_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                                 int64_t num_edges, const int64_t* start, int64_t num_walks,
-                                int32_t walk_length, uint64_t seed, int64_t* n_out,
-                                int64_t* e_out, int32_t threads, int64_t* status) {
+                                int32_t walk_length, uint64_t seed, void* n_out, void* e_out,
+                                int32_t out_type, int32_t threads, int64_t* status) {
     if (int rc = check_graph(rowptr, num_nodes, col, num_edges, start, num_walks, walk_length,
                              n_out))
         return rc;
+    if (int rc = check_out_type(out_type, num_nodes, num_edges, e_out)) return rc;
     uint32_t bits = 0;
     const HostWalk w = host_walk(rowptr, num_nodes, col, num_edges, start, num_walks, nullptr,
-                                 walk_length, seed, n_out, e_out);
+                                 walk_length, seed, n_out, e_out, out_type);
     const int rc = host_uniform(w, true, threads, bits);
     if (status) *status = bits;
     return rc;
@@ -243,16 +260,18 @@ int mlxc_random_walk_seeded_cpu(const int64_t* rowptr, int64_t num_nodes, const 
 int mlxc_rejection_sampling_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                                 int64_t num_edges, const int64_t* start, int64_t num_walks,
                                 int32_t walk_length, double p, double q, uint64_t seed,
-                                int32_t rule, int32_t rows, int64_t* n_out, int64_t* e_out,
-                                int32_t threads, int64_t* status) {
+                                int32_t rule, int32_t rows, void* n_out, void* e_out,
+                                int32_t out_type, int32_t threads, int64_t* status) {
     if (int rc = check_graph(rowptr, num_nodes, col, num_edges, start, num_walks, walk_length,
                              n_out))
         return rc;
+    if (int rc = check_out_type(out_type, num_nodes, num_edges, e_out)) return rc;
     N2VParams prm;
     if (int rc = n2v_params(p, q, seed, rule, rows, prm)) return rc;
+    prm.out_type = out_type;
     uint32_t bits = 0;
     const HostWalk w = host_walk(rowptr, num_nodes, col, num_edges, start, num_walks, nullptr,
-                                 walk_length, seed, n_out, e_out);
+                                 walk_length, seed, n_out, e_out, out_type);
     const int rc = host_node2vec(w, prm, threads, bits);
     if (status) *status = bits;
     return rc;

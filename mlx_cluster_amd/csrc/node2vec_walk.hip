@@ -60,7 +60,7 @@ __device__ __forceinline__ bool accept(const N2VArgs& a, double r, int64_t x, in
     return is_neighbor<kSorted>(a.w.rowptr, a.w.col, a.w.num_edges, x, t, status) ? lt1 : lt2;
 }
 
-template <int kRule, bool kSorted, bool kEdges>
+template <int kRule, bool kSorted, bool kEdges, typename OutT>
 __global__ __launch_bounds__(kBlock) void node2vec_walk_kernel(N2VArgs a) {
     const int64_t L = a.w.walk_length;
     const int64_t N = a.w.num_walks;
@@ -71,10 +71,10 @@ __global__ __launch_bounds__(kBlock) void node2vec_walk_kernel(N2VArgs a) {
     while (true) {
         const int64_t n = queue_take(q, true, counter);
         if (n >= N) break;  // wave-uniform: every lane asked, ids are consecutive
-        int64_t* out = a.w.n_out + n * (L + 1);
-        int64_t* eout = kEdges ? a.w.e_out + n * L : nullptr;
+        OutT* out = static_cast<OutT*>(a.w.n_out) + n * (L + 1);
+        OutT* eout = kEdges ? static_cast<OutT*>(a.w.e_out) + n * L : nullptr;
         int64_t t = a.w.start[n];
-        out[0] = t;
+        out[0] = static_cast<OutT>(t);
         if (L == 0) {
             if (!node_ok(t, V)) status |= MLXC_STATUS_BAD_NODE;
             continue;
@@ -97,8 +97,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_walk_kernel(N2VArgs a) {
                 v = a.w.col[e];
             }
         }
-        out[1] = v;
-        if (kEdges) eout[0] = e;
+        out[1] = static_cast<OutT>(v);
+        if (kEdges) eout[0] = static_cast<OutT>(e);
         for (int64_t l = 1; l < L; ++l) {
             int64_t x = v;
             e = -1;
@@ -132,8 +132,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_walk_kernel(N2VArgs a) {
                     }
                 }
             }
-            out[l + 1] = x;
-            if (kEdges) eout[l] = e;
+            out[l + 1] = static_cast<OutT>(x);
+            if (kEdges) eout[l] = static_cast<OutT>(e);
             t = v;
             v = x;
         }
@@ -220,9 +220,11 @@ __device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, double r, bool 
 // waits once.  Sorted rows are searched through the block index (see
 // kSearchBlock); unsorted rows are scanned one entry per iteration, as the
 // reference scans them.
-template <int kRule, bool kEdges>
+template <int kRule, bool kEdges, typename OutT>
 __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    OutT* const nout = static_cast<OutT*>(a.w.n_out);
+    OutT* const eout = static_cast<OutT*>(a.w.e_out);
     const bool sorted = a.rows == MLXC_ROWS_SORTED ||
                         (a.rows == MLXC_ROWS_DETECT && a.w.work[2] == a.w.work[3]);
     const int64_t L = a.w.walk_length;
@@ -267,8 +269,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             for (int i = 0; i < kSearchBlock / 4; ++i) blkv[i] = bp[i];
         }
         // ... and the output blocks the last iteration completed are stored.
-        ow_drain(ow, st);
-        if (kEdges) ow_drain(ew, st);
+        ow_drain<OutT>(ow, st);
+        if (kEdges) ow_drain<OutT>(ew, st);
 
         // 2. Idle slots draw walk ids while the read is in flight.
         const bool need = phase == kN2vIdle;
@@ -406,7 +408,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             }
         }
         if (accept) {
-            if (kEdges) ow_push(ew, a.w.e_out, e0 + l, e);
+            if (kEdges) ow_push(ew, eout, e0 + l, e);
             push = true;
             g += 1;
             l += 1;
@@ -430,13 +432,13 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                 phase = kN2vCand;
             }
         }
-        if (push) ow_push(ow, a.w.n_out, g, v);
+        if (push) ow_push(ow, nout, g, v);
         if (fill) {
-            ow_fill(ow, a.w.n_out, g + 1, g0 + L, v);
-            if (kEdges) ow_fill(ew, a.w.e_out, e0 + l, e0 + L - 1, -1);  // l edges buffered
+            ow_fill(ow, nout, g + 1, g0 + L, v);
+            if (kEdges) ow_fill(ew, eout, e0 + l, e0 + L - 1, -1);  // l edges buffered
         } else if (flush) {
-            if (ow.count) ow_flush(ow, a.w.n_out, g);
-            if (kEdges && ew.count) ow_flush(ew, a.w.e_out, e0 + L - 1);
+            if (ow.count) ow_flush(ow, nout, g);
+            if (kEdges && ew.count) ow_flush(ew, eout, e0 + L - 1);
         }
         if (fill || flush) phase = kN2vIdle;
     }
@@ -447,9 +449,9 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
 
 namespace {
 
-template <int kRule, bool kSorted, bool kEdges>
+template <int kRule, bool kSorted, bool kEdges, typename OutT>
 int launch_n2v(const N2VArgs& a, hipStream_t stream) {
-    auto kernel = node2vec_walk_kernel<kRule, kSorted, kEdges>;
+    auto kernel = node2vec_walk_kernel<kRule, kSorted, kEdges, OutT>;
     int grid = 0;
     if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
@@ -457,18 +459,18 @@ int launch_n2v(const N2VArgs& a, hipStream_t stream) {
     return MLXC_OK;
 }
 
-template <int kRule>
+template <int kRule, typename OutT>
 int dispatch_n2v(const N2VArgs& a, bool sorted, bool edges, hipStream_t stream) {
     if (sorted)
-        return edges ? launch_n2v<kRule, true, true>(a, stream)
-                     : launch_n2v<kRule, true, false>(a, stream);
-    return edges ? launch_n2v<kRule, false, true>(a, stream)
-                 : launch_n2v<kRule, false, false>(a, stream);
+        return edges ? launch_n2v<kRule, true, true, OutT>(a, stream)
+                     : launch_n2v<kRule, true, false, OutT>(a, stream);
+    return edges ? launch_n2v<kRule, false, true, OutT>(a, stream)
+                 : launch_n2v<kRule, false, false, OutT>(a, stream);
 }
 
-template <int kRule, bool kEdges>
+template <int kRule, bool kEdges, typename OutT>
 int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
-    auto kernel = node2vec_rec_kernel<kRule, kEdges>;
+    auto kernel = node2vec_rec_kernel<kRule, kEdges, OutT>;
     int grid = 0;
     if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
@@ -502,8 +504,11 @@ size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t nu
     return n2v_layout(num_edges, num_walks).total;
 }
 
-int launch_node2vec(const WalkArgs& w, const N2VParams& p, void* workspace, size_t workspace_bytes,
-                    hipStream_t stream) {
+namespace {
+
+template <typename OutT>
+int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream) {
     const N2VLayout lay = n2v_layout(w.num_edges, w.num_walks);
     const bool aligned = reinterpret_cast<uintptr_t>(w.n_out) % 16 == 0 &&
                          reinterpret_cast<uintptr_t>(w.e_out) % 16 == 0;  // e_out may be null
@@ -536,10 +541,10 @@ int launch_node2vec(const WalkArgs& w, const N2VParams& p, void* workspace, size
         a.rows = p.rows;
         const bool edges = w.e_out != nullptr;
         if (p.rule == MLXC_RULE_REF_CHAIN)
-            return edges ? launch_n2v_rec<MLXC_RULE_REF_CHAIN, true>(a, stream)
-                         : launch_n2v_rec<MLXC_RULE_REF_CHAIN, false>(a, stream);
-        return edges ? launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, true>(a, stream)
-                     : launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, false>(a, stream);
+            return edges ? launch_n2v_rec<MLXC_RULE_REF_CHAIN, true, OutT>(a, stream)
+                         : launch_n2v_rec<MLXC_RULE_REF_CHAIN, false, OutT>(a, stream);
+        return edges ? launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, true, OutT>(a, stream)
+                     : launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, false, OutT>(a, stream);
     }
     // Graphs beyond int32, a workspace too small for the records, or output
     // buffers not 16-byte aligned: the direct CSR kernel, which needs the row
@@ -566,8 +571,17 @@ int launch_node2vec(const WalkArgs& w, const N2VParams& p, void* workspace, size
     a.key1 = p.key1;
     const bool edges = w.e_out != nullptr;
     return p.rule == MLXC_RULE_REF_CHAIN
-               ? dispatch_n2v<MLXC_RULE_REF_CHAIN>(a, sorted, edges, stream)
-               : dispatch_n2v<MLXC_RULE_NODE2VEC_EXACT>(a, sorted, edges, stream);
+               ? dispatch_n2v<MLXC_RULE_REF_CHAIN, OutT>(a, sorted, edges, stream)
+               : dispatch_n2v<MLXC_RULE_NODE2VEC_EXACT, OutT>(a, sorted, edges, stream);
+}
+
+}  // namespace
+
+int launch_node2vec(const WalkArgs& w, const N2VParams& p, void* workspace, size_t workspace_bytes,
+                    hipStream_t stream) {
+    return p.out_type == MLXC_OUT_INT32
+               ? launch_node2vec_typed<int32_t>(w, p, workspace, workspace_bytes, stream)
+               : launch_node2vec_typed<int64_t>(w, p, workspace, workspace_bytes, stream);
 }
 
 }  // namespace mlxc

@@ -15,10 +15,12 @@ namespace mlxc {
 // the wave queue, 8-byte loads and stores.  Serves the cases the windowed
 // kernels do not: the edge-id output and buffers that are not 16-byte
 // aligned.
-template <int W, bool kEdges, bool kGen>
+template <int W, bool kEdges, bool kGen, typename OutT>
 __global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
     const int64_t L = a.walk_length;
     const int64_t N = a.num_walks;
+    OutT* const nout = static_cast<OutT*>(a.n_out);
+    OutT* const eout = static_cast<OutT*>(a.e_out);
     unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.work + 1);
     WaveQueue q{0, 0};
     int64_t n[W], v[W], l[W];
@@ -38,14 +40,14 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
                 n[s] = id;  // id >= N ends the slot for good
                 if (id < N) {
                     const int64_t s0 = a.start[id];
-                    a.n_out[id * (L + 1)] = s0;
+                    nout[id * (L + 1)] = static_cast<OutT>(s0);
                     v[s] = s0;
                     l[s] = 0;
                     if (!node_ok(s0, a.num_nodes)) {
                         status |= MLXC_STATUS_BAD_NODE;
-                        for (int64_t j = 1; j <= L; ++j) a.n_out[id * (L + 1) + j] = s0;
+                        for (int64_t j = 1; j <= L; ++j) nout[id * (L + 1) + j] = static_cast<OutT>(s0);
                         if (kEdges)
-                            for (int64_t j = 0; j < L; ++j) a.e_out[id * L + j] = -1;
+                            for (int64_t j = 0; j < L; ++j) eout[id * L + j] = -1;
                         l[s] = L;
                     }
                 }
@@ -92,11 +94,11 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
         for (int s = 0; s < W; ++s) {
             const bool live = (n[s] < N) && (l[s] < L);
             if (!live) continue;
-            int64_t* out = a.n_out + n[s] * (L + 1);
+            OutT* out = nout + n[s] * (L + 1);
             const bool moved = e[s] >= 0;
             bool stop = !moved;  // deg == 0 (absorbing) or malformed row
-            out[l[s] + 1] = x[s];
-            if (kEdges) a.e_out[n[s] * L + l[s]] = e[s];
+            out[l[s] + 1] = static_cast<OutT>(x[s]);
+            if (kEdges) eout[n[s] * L + l[s]] = static_cast<OutT>(e[s]);
             l[s] += 1;
             if (moved && !node_ok(x[s], a.num_nodes)) {
                 status |= MLXC_STATUS_BAD_NODE;
@@ -104,9 +106,9 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
             }
             v[s] = x[s];
             if (stop) {
-                for (int64_t j = l[s] + 1; j <= L; ++j) out[j] = x[s];
+                for (int64_t j = l[s] + 1; j <= L; ++j) out[j] = static_cast<OutT>(x[s]);
                 if (kEdges)
-                    for (int64_t j = l[s]; j < L; ++j) a.e_out[n[s] * L + j] = -1;
+                    for (int64_t j = l[s]; j < L; ++j) eout[n[s] * L + j] = -1;
                 l[s] = L;
             }
         }
@@ -136,11 +138,13 @@ enum : int {
 // a round trip of its own.  The whole blocks of output completed in one
 // iteration are stored by the wavefront (ow_drain) right after the next
 // iteration's reads are issued, so they overlap those reads.
-template <int W, int RW, bool kGen, bool kEdges>
+template <int W, int RW, bool kGen, bool kEdges, typename OutT>
 __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                                                                   const EdgeRecord* __restrict__ recs,
                                                                   const EdgeRecord* __restrict__ init) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    OutT* const nout = static_cast<OutT*>(a.n_out);
+    OutT* const eout = static_cast<OutT*>(a.e_out);
     const int64_t L = a.walk_length;
     const int64_t L1 = L + 1;
     const int64_t N = a.num_walks;
@@ -192,8 +196,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
         // ... and the output blocks the last iteration completed are stored.
 #pragma unroll
         for (int s = 0; s < W; ++s) {
-            ow_drain(ow[s], st);
-            if (kEdges) ow_drain(ew[s], st);
+            ow_drain<OutT>(ow[s], st);
+            if (kEdges) ow_drain<OutT>(ew[s], st);
         }
 
         // 2. While the reads are in flight, idle slots draw walk ids from the
@@ -244,27 +248,27 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
             if (deg < 0) {
                 // malformed start or graph entry: stop (outputs unspecified)
                 status |= deg == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
-                ow_fill(ow[s], a.n_out, g, g0 + L, node);
+                ow_fill(ow[s], nout, g, g0 + L, node);
                 // edges of steps 0 .. l are buffered after a pick, none at the start
-                if (kEdges) ow_fill(ew[s], a.e_out, e0 + l[s] + (ph[s] == kSlotWalk ? 1 : 0),
+                if (kEdges) ow_fill(ew[s], eout, e0 + l[s] + (ph[s] == kSlotWalk ? 1 : 0),
                                     e0 + L - 1, -1);
                 phase[s] = kSlotIdle;
                 continue;
             }
-            ow_push(ow[s], a.n_out, g, node);
+            ow_push(ow[s], nout, g, node);
             if (ph[s] == kSlotWalk) l[s] += 1;
             if (l[s] == L) flush = true;
             else if (deg == 0) fill = true;  // absorbing node: the walk stays
             if (fill) {
-                ow_fill(ow[s], a.n_out, g + 1, g0 + L, node);
-                if (kEdges) ow_fill(ew[s], a.e_out, e0 + l[s], e0 + L - 1, -1);
+                ow_fill(ow[s], nout, g + 1, g0 + L, node);
+                if (kEdges) ow_fill(ew[s], eout, e0 + l[s], e0 + L - 1, -1);
             } else if (flush) {
-                if (ow[s].count) ow_flush(ow[s], a.n_out, g);
-                if (kEdges && ew[s].count) ow_flush(ew[s], a.e_out, e0 + L - 1);
+                if (ow[s].count) ow_flush(ow[s], nout, g);
+                if (kEdges && ew[s].count) ow_flush(ew[s], eout, e0 + L - 1);
             } else {
                 // step l (0-based) leaves this node with uniform rand[n*L + l]
                 e[s] = static_cast<int32_t>(begin + pick_index(rw[s].w[0], deg));
-                if (kEdges) ow_push(ew[s], a.e_out, e0 + l[s], e[s]);
+                if (kEdges) ow_push(ew[s], eout, e0 + l[s], e[s]);
                 rw_shift1(rw[s]);
                 rw[s].valid -= 1;
                 need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
@@ -284,10 +288,12 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
 // of the new node.  Start records (walk_init_kernel) give the first row.
 // Requirements as for the record walk except num_edges may be any size the
 // int32 start records hold (num_nodes, num_edges below 2^31).
-template <int W, int RW, bool kGen, bool kEdges>
+template <int W, int RW, bool kGen, bool kEdges, typename OutT>
 __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                                                                   const EdgeRecord* __restrict__ init) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4), aligned(8)));
+    OutT* const nout = static_cast<OutT*>(a.n_out);
+    OutT* const eout = static_cast<OutT*>(a.e_out);
     const int64_t L = a.walk_length;
     const int64_t L1 = L + 1;
     const int64_t N = a.num_walks;
@@ -341,8 +347,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
         // ... and the output blocks the last iteration completed are stored.
 #pragma unroll
         for (int s = 0; s < W; ++s) {
-            ow_drain(ow[s], st);
-            if (kEdges) ow_drain(ew[s], st);
+            ow_drain<OutT>(ow[s], st);
+            if (kEdges) ow_drain<OutT>(ew[s], st);
         }
 
         // 2. Idle slots draw walk ids while the reads are in flight.
@@ -428,20 +434,20 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                 fill = true;  // absorbing node: the walk stays
             } else if (deg > 0) {
                 e[s] = static_cast<int32_t>(begin + pick_index(rw[s].w[0], deg));
-                if (kEdges) ow_push(ew[s], a.e_out, eg, e[s]);
+                if (kEdges) ow_push(ew[s], eout, eg, e[s]);
                 rw_shift1(rw[s]);
                 rw[s].valid -= 1;
                 need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
                 fr[s] = n[s] * L + l[s] + 1;
                 phase[s] = kSlotCol;
             }
-            if (push) ow_push(ow[s], a.n_out, g, v[s]);
+            if (push) ow_push(ow[s], nout, g, v[s]);
             if (fill) {
-                ow_fill(ow[s], a.n_out, g + 1, g0 + L, v[s]);
-                if (kEdges) ow_fill(ew[s], a.e_out, eg, e0 + L - 1, -1);
+                ow_fill(ow[s], nout, g + 1, g0 + L, v[s]);
+                if (kEdges) ow_fill(ew[s], eout, eg, e0 + L - 1, -1);
             } else if (flush) {
-                if (ow[s].count) ow_flush(ow[s], a.n_out, g);
-                if (kEdges && ew[s].count) ow_flush(ew[s], a.e_out, e0 + L - 1);
+                if (ow[s].count) ow_flush(ow[s], nout, g);
+                if (kEdges && ew[s].count) ow_flush(ew[s], eout, e0 + L - 1);
             }
             if (fill || flush) phase[s] = kSlotIdle;
         }
@@ -520,7 +526,7 @@ size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num
 
 namespace {
 
-template <bool kGen, bool kEdges>
+template <bool kGen, bool kEdges, typename OutT>
 int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_bytes,
                         hipStream_t stream) {
     constexpr int RW = MLXC_RAND_WINDOW;
@@ -534,7 +540,7 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, stream))
             return rc;
-        return launch_walk_kernel(uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen, kEdges>,
+        return launch_walk_kernel(uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen, kEdges, OutT>,
                                   MLXC_REC_SLOTS, a,
                                   stream,
                                   static_cast<const EdgeRecord*>(recs),
@@ -545,7 +551,7 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, stream))
             return rc;
-        return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW, kGen, kEdges>,
+        return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW, kGen, kEdges, OutT>,
                                   MLXC_CSR_SLOTS, a,
                                   stream,
                                   static_cast<const EdgeRecord*>(init));
@@ -553,19 +559,31 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
     case UniformMode::kPlain:
         break;
     }
-    return launch_walk_kernel(uniform_walk_kernel<2, kEdges, kGen>, 2, a, stream);
+    return launch_walk_kernel(uniform_walk_kernel<2, kEdges, kGen, OutT>, 2, a, stream);
+}
+
+}  // namespace
+
+namespace {
+
+template <typename OutT>
+int launch_uniform_typed(const WalkArgs& a, void* workspace, size_t workspace_bytes,
+                         bool generate, hipStream_t stream) {
+    const bool edges = a.e_out != nullptr;
+    if (generate)
+        return edges ? launch_uniform_impl<true, true, OutT>(a, workspace, workspace_bytes, stream)
+                     : launch_uniform_impl<true, false, OutT>(a, workspace, workspace_bytes, stream);
+    return edges ? launch_uniform_impl<false, true, OutT>(a, workspace, workspace_bytes, stream)
+                 : launch_uniform_impl<false, false, OutT>(a, workspace, workspace_bytes, stream);
 }
 
 }  // namespace
 
 int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes, bool generate,
-                   hipStream_t stream) {
-    const bool edges = a.e_out != nullptr;
-    if (generate)
-        return edges ? launch_uniform_impl<true, true>(a, workspace, workspace_bytes, stream)
-                     : launch_uniform_impl<true, false>(a, workspace, workspace_bytes, stream);
-    return edges ? launch_uniform_impl<false, true>(a, workspace, workspace_bytes, stream)
-                 : launch_uniform_impl<false, false>(a, workspace, workspace_bytes, stream);
+                   int32_t out_type, hipStream_t stream) {
+    return out_type == MLXC_OUT_INT32
+               ? launch_uniform_typed<int32_t>(a, workspace, workspace_bytes, generate, stream)
+               : launch_uniform_typed<int64_t>(a, workspace, workspace_bytes, generate, stream);
 }
 
 }  // namespace mlxc

@@ -146,8 +146,8 @@ struct WalkArgs {
     const int64_t* col;
     const int64_t* start;
     const float* rand;
-    int64_t* n_out;
-    int64_t* e_out;
+    void* n_out;    // OutT [num_walks, walk_length + 1]
+    void* e_out;    // OutT [num_walks, walk_length] or null
     int64_t* work;  // [0] status bits, [1] walk-queue counter
     int64_t num_nodes;
     int64_t num_edges;
@@ -261,25 +261,28 @@ __device__ __forceinline__ void rw_shift_by(RandWindow<RW>& r, int k) {
     }
 }
 
-// Output rows are written in 64-byte blocks (8 int64 entries, aligned in the
-// output).  A lane buffers its walk's entries in an OutWin.  The stores of a
-// completed block, and of the run of whole blocks that a walk absorbed by a
-// sink repeats to the end of its row, are deferred to ow_drain, which the
-// whole wavefront executes together: completed blocks are staged through LDS
-// and stored four lanes per block, one 16-byte non-temporal store each, and
-// runs are stored by the whole wavefront in consecutive 16-byte pieces.  Every
-// store instruction thus covers whole 64-byte blocks and the L2 sends one full
-// write per block; a lane storing its own block in four pieces leaves up to
-// four partial writes of it (measured: 3.6 write requests per block on
-// MI355X, against 1.0 here).  Only the partial blocks at the two ends of a
-// row are stored by the lane itself, entry by entry.
+// Output rows are written in blocks of 8 entries, aligned in the output: 64
+// bytes of int64 entries, or 32 bytes with the compact int32 output.  A lane
+// buffers its walk's entries in an OutWin.  The stores of a completed block,
+// and of the run of whole blocks that a walk absorbed by a sink repeats to
+// the end of its row, are deferred to ow_drain, which the whole wavefront
+// executes together: completed blocks are staged through LDS and stored by
+// several lanes per block, one 16-byte non-temporal store each, and runs are
+// stored by the whole wavefront in consecutive 16-byte pieces.  Every store
+// instruction thus covers whole blocks and the L2 sends one full write per
+// block; a lane storing its own 64-byte block in four pieces leaves up to four
+// partial writes of it (measured: 3.6 write requests per block on MI355X,
+// against 1.0 here).  Only the partial blocks at the two ends of a row are
+// stored by the lane itself, entry by entry.
 //
 // Between a completion and the drain the window is not pushed again: each
 // iteration of the walk loops pushes at most one entry per window, and a run
 // that follows a completed block starts on a block boundary.
 //
-// T is the type the entries are buffered in (int32_t when node ids fit);
-// they are written as int64.
+// T is the type the entries are buffered in (int32_t: the windowed walks'
+// node and edge ids fit in it); OutT is the output element type, int64_t (the
+// reference's layout) or int32_t.
+
 // Cache policy of the two kinds of output store.  Whole blocks stream past
 // the caches (non-temporal).  The partial blocks at the ends of a row are
 // shared with the neighbouring row, which another lane writes at about the
@@ -294,21 +297,60 @@ __device__ __forceinline__ void rw_shift_by(RandWindow<RW>& r, int k) {
 #define MLXC_PARTIAL_NT 0
 #endif
 
-template <typename V, typename P>
-__device__ __forceinline__ void store_block_part(V v, P* p) {
-    if (MLXC_BLOCK_NT) __builtin_nontemporal_store(v, p); else *p = v;
+// 16 bytes of output entries: 2 int64 or 4 int32.
+template <typename OutT>
+struct Vec16;
+template <>
+struct Vec16<int64_t> {
+    typedef int64_t type __attribute__((ext_vector_type(2)));
+    static constexpr int kLanes = 2;
+};
+template <>
+struct Vec16<int32_t> {
+    typedef int32_t type __attribute__((ext_vector_type(4)));
+    static constexpr int kLanes = 4;
+};
+
+template <typename OutT>
+__device__ __forceinline__ void store_block_part(typename Vec16<OutT>::type v, OutT* p) {
+    typedef typename Vec16<OutT>::type V;
+    if (MLXC_BLOCK_NT) __builtin_nontemporal_store(v, reinterpret_cast<V*>(p));
+    else *reinterpret_cast<V*>(p) = v;
 }
 
-__device__ __forceinline__ void store_partial(int64_t v, int64_t* p) {
+template <typename OutT>
+__device__ __forceinline__ void store_partial(OutT v, OutT* p) {
     if (MLXC_PARTIAL_NT) __builtin_nontemporal_store(v, p); else *p = v;
+}
+
+// Entries p[0 .. kLanes-1] (int32) widened to one 16-byte vector of OutT.
+template <typename OutT>
+__device__ __forceinline__ typename Vec16<OutT>::type vec16_from(const int32_t* p);
+template <>
+__device__ __forceinline__ Vec16<int64_t>::type vec16_from<int64_t>(const int32_t* p) {
+    typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+    const i32x2 v = *reinterpret_cast<const i32x2*>(p);
+    return Vec16<int64_t>::type{static_cast<int64_t>(v.x), static_cast<int64_t>(v.y)};
+}
+template <>
+__device__ __forceinline__ Vec16<int32_t>::type vec16_from<int32_t>(const int32_t* p) {
+    return *reinterpret_cast<const Vec16<int32_t>::type*>(p);
+}
+
+template <typename OutT>
+__device__ __forceinline__ typename Vec16<OutT>::type vec16_splat(OutT x) {
+    typename Vec16<OutT>::type v;
+#pragma unroll
+    for (int i = 0; i < Vec16<OutT>::kLanes; ++i) v[i] = x;
+    return v;
 }
 
 template <typename T>
 struct OutWin {
     T w[8];              // w[8-count .. 7] hold the newest entries; w[7] is entry g
     int count;
-    int64_t* blk;        // set: w[0..7] is a completed block, to be stored at blk
-    int64_t* run;        // set: run_blocks whole blocks of run_val, to be stored at run
+    void* blk;           // set: w[0..7] is a completed block, to be stored at blk
+    void* run;           // set: run_blocks whole blocks of run_val, to be stored at run
     int32_t run_blocks;
     T run_val;
 };
@@ -325,41 +367,44 @@ __device__ __forceinline__ void ow_init(OutWin<T>& o) {
 // Per-wavefront LDS staging of ow_drain.
 struct WaveStage {
     int32_t vals[kWave][8];  // completed blocks (entries as int32)
-    int64_t* dst[kWave];
+    void* dst[kWave];
 };
 
 // Writes the buffered entries, the newest of which is output index g: a
 // complete aligned block is left to ow_drain, a partial one is stored here.
-template <typename T>
-__device__ __forceinline__ void ow_flush(OutWin<T>& o, int64_t* __restrict__ out, int64_t g) {
+template <typename T, typename OutT>
+__device__ __forceinline__ void ow_flush(OutWin<T>& o, OutT* __restrict__ out, int64_t g) {
     if (o.count == 8 && ((g + 1) & 7) == 0) {
         o.blk = out + (g - 7);
     } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            if (i >= 8 - o.count) store_partial(static_cast<int64_t>(o.w[i]), out + g - 7 + i);
+            if (i >= 8 - o.count) store_partial(static_cast<OutT>(o.w[i]), out + g - 7 + i);
     }
     o.count = 0;
 }
 
 // Stores a completed block still pending in the window, lane by lane (only
 // reached if a window were pushed again before the drain).
-template <typename T>
-__device__ __forceinline__ void ow_store_pending(OutWin<T>& o) {
-    typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
+template <typename T, typename OutT>
+__device__ __forceinline__ void ow_store_pending(OutWin<T>& o, OutT*) {
+    constexpr int kPer = Vec16<OutT>::kLanes;
+    OutT* p = static_cast<OutT*>(o.blk);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const i64x2 x = {static_cast<int64_t>(o.w[2 * i]), static_cast<int64_t>(o.w[2 * i + 1])};
-        __builtin_nontemporal_store(x, reinterpret_cast<i64x2*>(o.blk + 2 * i));
+    for (int i = 0; i < 8; i += kPer) {
+        typename Vec16<OutT>::type x;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) x[j] = static_cast<OutT>(o.w[i + j]);
+        store_block_part(x, p + i);
     }
     o.blk = nullptr;
 }
 
 // Appends the entry for output index g; completes the window's block when g
-// closes a 64-byte block.
-template <typename T>
-__device__ __forceinline__ void ow_push(OutWin<T>& o, int64_t* __restrict__ out, int64_t g, T x) {
-    if (o.blk) ow_store_pending(o);
+// closes a block.
+template <typename T, typename OutT>
+__device__ __forceinline__ void ow_push(OutWin<T>& o, OutT* __restrict__ out, int64_t g, T x) {
+    if (o.blk) ow_store_pending(o, out);
 #pragma unroll
     for (int i = 0; i < 7; ++i) o.w[i] = o.w[i + 1];
     o.w[7] = x;
@@ -370,8 +415,8 @@ __device__ __forceinline__ void ow_push(OutWin<T>& o, int64_t* __restrict__ out,
 // Output indices g .. g_last (inclusive) all hold x; the window holds the
 // entries before g.  The whole blocks of the run are left to ow_drain; the
 // entries before the first and after the last are stored here.
-template <typename T>
-__device__ __forceinline__ void ow_fill(OutWin<T>& o, int64_t* __restrict__ out, int64_t g,
+template <typename T, typename OutT>
+__device__ __forceinline__ void ow_fill(OutWin<T>& o, OutT* __restrict__ out, int64_t g,
                                         int64_t g_last, T x) {
     while (g <= g_last && (g & 7) != 0) ow_push(o, out, g++, x);
     if (o.count) ow_flush(o, out, g - 1);
@@ -382,7 +427,7 @@ __device__ __forceinline__ void ow_fill(OutWin<T>& o, int64_t* __restrict__ out,
         o.run_val = x;
         g += 8 * blocks;
     }
-    for (; g <= g_last; ++g) store_partial(static_cast<int64_t>(x), out + g);
+    for (; g <= g_last; ++g) store_partial(static_cast<OutT>(x), out + g);
 }
 
 // s_waitcnt vmcnt(0): every vector-memory operation of the wavefront has
@@ -406,24 +451,24 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ int64_t* read_lane_ptr(int64_t* p, int lane) {
+__device__ __forceinline__ void* read_lane_ptr(void* p, int lane) {
     const uint64_t u = reinterpret_cast<uint64_t>(p);
     const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(u), lane);
     const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(u >> 32), lane);
-    return reinterpret_cast<int64_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+    return reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// Stores the deferred blocks and runs of every lane's window.  Must be
-// reached by all lanes of the wavefront together (wave-uniform control
-// flow); st is the wavefront's own staging area.
-template <typename T>
+// Stores the deferred blocks and runs of every lane's window into an output
+// of OutT.  Must be reached by all lanes of the wavefront together
+// (wave-uniform control flow); st is the wavefront's own staging area.
+template <typename OutT, typename T>
 __device__ __forceinline__ void ow_drain(OutWin<T>& o, WaveStage& st) {
-    typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-    typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
     static_assert(sizeof(T) == 4, "staged and broadcast as 32-bit entries");
+    constexpr int kPer = Vec16<OutT>::kLanes;  // entries per 16-byte store
+    constexpr int kParts = 8 / kPer;           // lanes per block: 4 (int64) or 2 (int32)
     const int lane = __lane_id();
-    const int quarter = lane & 3;
+    const int part = lane % kParts;
     const uint64_t blocks = __ballot(o.blk != nullptr);
     if (blocks) {
         if (o.blk) {
@@ -439,13 +484,11 @@ __device__ __forceinline__ void ow_drain(OutWin<T>& o, WaveStage& st) {
         }
         wave_sync();
         const int c = __popcll(blocks);
-        for (int r = 0; r < c; r += kWave / 4) {  // 16 blocks per store instruction
-            const int k = r + (lane >> 2);
-            if (k < c) {
-                const i32x2 v = *reinterpret_cast<const i32x2*>(&st.vals[k][2 * quarter]);
-                const i64x2 x = {static_cast<int64_t>(v.x), static_cast<int64_t>(v.y)};
-                store_block_part(x, reinterpret_cast<i64x2*>(st.dst[k] + 2 * quarter));
-            }
+        for (int r = 0; r < c; r += kWave / kParts) {  // kWave / kParts blocks per store
+            const int k = r + lane / kParts;
+            if (k < c)
+                store_block_part(vec16_from<OutT>(&st.vals[k][kPer * part]),
+                                 static_cast<OutT*>(st.dst[k]) + kPer * part);
         }
         wave_sync();
     }
@@ -453,13 +496,12 @@ __device__ __forceinline__ void ow_drain(OutWin<T>& o, WaveStage& st) {
     while (runs) {  // wave-uniform: one lane's run at a time, the whole wave storing it
         const int src = __builtin_ctzll(runs);
         runs &= runs - 1;
-        int64_t* dst = read_lane_ptr(o.run, src);
-        const int32_t chunks = 4 * __builtin_amdgcn_readlane(o.run_blocks, src);
-        const int64_t x = static_cast<int64_t>(
+        OutT* dst = static_cast<OutT*>(read_lane_ptr(o.run, src));
+        const int32_t chunks = kParts * __builtin_amdgcn_readlane(o.run_blocks, src);
+        const OutT x = static_cast<OutT>(
             static_cast<T>(__builtin_amdgcn_readlane(static_cast<int32_t>(o.run_val), src)));
-        const i64x2 xx = {x, x};
-        for (int c = lane; c < chunks; c += kWave)
-            store_block_part(xx, reinterpret_cast<i64x2*>(dst + 2 * c));
+        const typename Vec16<OutT>::type xx = vec16_splat(x);
+        for (int c = lane; c < chunks; c += kWave) store_block_part(xx, dst + kPer * c);
     }
     o.run = nullptr;
     o.run_blocks = 0;

@@ -75,9 +75,10 @@ int launch_philox_fill(float* out, int64_t n, uint64_t seed, hipStream_t stream)
 size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
                                int32_t walk_length);
 // generate: the kernels compute their uniforms from the Philox key in a
-// (key0, key1) instead of reading a.rand.
+// (key0, key1) instead of reading a.rand.  out_type: MLXC_OUT_* of a.n_out
+// and a.e_out.
 int launch_uniform(const WalkArgs& a, void* workspace, size_t workspace_bytes, bool generate,
-                   hipStream_t stream);
+                   int32_t out_type, hipStream_t stream);
 
 // ---- node2vec_walk.hip
 struct N2VParams {
@@ -85,6 +86,7 @@ struct N2VParams {
     uint32_t key0, key1;         // Philox key (the seed)
     int32_t rule;                // MLXC_RULE_*
     int32_t rows;                // MLXC_ROWS_*
+    int32_t out_type;            // MLXC_OUT_*
 };
 size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
                                 int32_t walk_length);
@@ -97,8 +99,9 @@ struct HostWalk {
     const int64_t* col;
     const int64_t* start;
     const float* rand;  // null when the uniforms are generated
-    int64_t* n_out;
-    int64_t* e_out;     // may be null
+    void* n_out;        // int64 or int32 (out_type)
+    void* e_out;        // may be null
+    int32_t out_type;   // MLXC_OUT_*
     int64_t num_nodes, num_edges, num_walks, walk_length;
     uint32_t key0, key1;  // Philox key of generated uniforms
 };

@@ -12,7 +12,8 @@ Same names, positional order and keyword-only `stream`.  Arrays are torch
 tensors on a ROCm device (numpy arrays and CPU tensors are copied to the
 current device).  Both functions return the node sequences, an int64 tensor
 [num_walks, walk_length + 1], as the reference ops do (they discard the edge
-output, RandomWalk.cpp:147); `return_edges=True` also returns the edge ids.
+output, RandomWalk.cpp:147); `return_edges=True` also returns the edge ids,
+and `out_dtype=torch.int32` gives both as int32, with half the bytes.
 
 Every walk runs in the library libmlxc.so: on the GPU through its HIP
 kernels, or, for stream='cpu' (the reference's eval_cpu), through its host
@@ -119,6 +120,15 @@ def _host(x: torch.Tensor) -> torch.Tensor:
     return x.cpu().contiguous()
 
 
+_OUT_TYPES = {torch.int64: _lib.MLXC_OUT_INT64, torch.int32: _lib.MLXC_OUT_INT32}
+
+
+def _out_type(out_dtype) -> int:
+    if out_dtype not in _OUT_TYPES:
+        raise TypeError(f"out_dtype must be torch.int64 or torch.int32, got {out_dtype!r}")
+    return _OUT_TYPES[out_dtype]
+
+
 def _walk_length(walk_length) -> int:
     if isinstance(walk_length, bool) or not isinstance(walk_length, numbers.Integral):
         raise TypeError("walk_length must be an int")
@@ -158,7 +168,7 @@ def _raise_bits(bits: int, what: str) -> None:
 def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
                 rand: Optional[TensorLike], walk_length: int, *, stream=None,
                 return_edges: bool = False, check: bool = True, seed: Optional[int] = None,
-                threads: Optional[int] = None
+                threads: Optional[int] = None, out_dtype: torch.dtype = torch.int64
                 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """Uniform random walks over a CSR graph.
 
@@ -188,11 +198,15 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
         seed: key of the generated uniforms when rand is None.
         threads: CPU threads for stream='cpu' (None: one per hardware
             thread); ignored on the GPU.
+        out_dtype: torch.int64 (the reference's output) or torch.int32, a
+            compact output with half the bytes (node ids, and edge ids with
+            return_edges, must be below 2^31).
 
     Returns:
-        int64 [num_walks, walk_length + 1] node sequences (and edge ids).
+        [num_walks, walk_length + 1] node sequences (and edge ids) of out_dtype.
     """
     L = _walk_length(walk_length)
+    otype = _out_type(out_dtype)
     _check_stream_arg(stream)
     rowptr, col, start = _graph(rowptr, col, start)
     N = start.numel()
@@ -209,11 +223,12 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
                              f"got {rand.numel()}")
     if _on_cpu(stream):
         rowptr, col, start = (_host(t) for t in (rowptr, col, start))
-        n_out = torch.empty((N, L + 1), dtype=torch.int64)
-        e_out = torch.empty((N, L), dtype=torch.int64) if return_edges else None
+        n_out = torch.empty((N, L + 1), dtype=out_dtype)
+        e_out = torch.empty((N, L), dtype=out_dtype) if return_edges else None
         status = _lib.ctypes.c_int64(0)
         graph = (_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N)
-        outs = (_ptr(n_out), _ptr(e_out), _threads(threads), _lib.ctypes.addressof(status))
+        outs = (_ptr(n_out), _ptr(e_out), otype, _threads(threads),
+                _lib.ctypes.addressof(status))
         if rand is None:
             rc = _lib.load().mlxc_random_walk_seeded_cpu(*graph, L, seed, *outs)
         else:
@@ -226,14 +241,14 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     device = _resolve_device(stream, (rowptr, col, start, rand))
     handle = _stream_handle(stream, device)
     rowptr, col, start = (_on(t, device) for t in (rowptr, col, start))
-    n_out = torch.empty((N, L + 1), dtype=torch.int64, device=device)
-    e_out = torch.empty((N, L), dtype=torch.int64, device=device) if return_edges else None
+    n_out = torch.empty((N, L + 1), dtype=out_dtype, device=device)
+    e_out = torch.empty((N, L), dtype=out_dtype, device=device) if return_edges else None
     lib = _lib.load()
     work = _workspace(lib.mlxc_random_walk_workspace_bytes(rowptr.numel() - 1, col.numel(), N, L),
                       device)
     graph = (_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N)
-    outs = (_ptr(n_out), _ptr(e_out) if return_edges else None, work.data_ptr(), work.numel() * 8,
-            handle)
+    outs = (_ptr(n_out), _ptr(e_out) if return_edges else None, otype, work.data_ptr(),
+            work.numel() * 8, handle)
     with torch.cuda.device(device):
         if rand is None:
             rc = lib.mlxc_random_walk_seeded(*graph, L, seed, *outs)
@@ -267,7 +282,8 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
                        walk_length: int, p: float, q: float, *, stream=None,
                        seed: Optional[int] = None, rule: str = "ref_chain",
                        rows_sorted: Optional[bool] = None, return_edges: bool = False,
-                       check: bool = True, threads: Optional[int] = None
+                       check: bool = True, threads: Optional[int] = None,
+                       out_dtype: torch.dtype = torch.int64
                        ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """node2vec random walks by rejection sampling.
 
@@ -292,9 +308,10 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
             lets the call check the rows on the device as part of its
             preparation pass, which also validates the whole graph (a
             malformed graph raises ValueError when check=True).
-        return_edges, check, threads: as in random_walk.
+        return_edges, check, threads, out_dtype: as in random_walk.
     """
     L = _walk_length(walk_length)
+    otype = _out_type(out_dtype)
     p, q = float(p), float(q)
     if not (np.isfinite(p) and np.isfinite(q) and p > 0 and q > 0):
         raise ValueError("p and q must be finite and > 0")
@@ -310,12 +327,12 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     N = start.numel()
     if _on_cpu(stream):
         rowptr, col, start = (_host(t) for t in (rowptr, col, start))
-        n_out = torch.empty((N, L + 1), dtype=torch.int64)
-        e_out = torch.empty((N, L), dtype=torch.int64) if return_edges else None
+        n_out = torch.empty((N, L + 1), dtype=out_dtype)
+        e_out = torch.empty((N, L), dtype=out_dtype) if return_edges else None
         status = _lib.ctypes.c_int64(0)
         rc = _lib.load().mlxc_rejection_sampling_cpu(
             _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,
-            p, q, seed, _RULES[rule], rows, _ptr(n_out), _ptr(e_out), _threads(threads),
+            p, q, seed, _RULES[rule], rows, _ptr(n_out), _ptr(e_out), otype, _threads(threads),
             _lib.ctypes.addressof(status))
         _lib.check(rc, "rejection_sampling")
         if check:
@@ -324,8 +341,8 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     device = _resolve_device(stream, (rowptr, col, start))
     handle = _stream_handle(stream, device)
     rowptr, col, start = (_on(t, device) for t in (rowptr, col, start))
-    n_out = torch.empty((N, L + 1), dtype=torch.int64, device=device)
-    e_out = torch.empty((N, L), dtype=torch.int64, device=device) if return_edges else None
+    n_out = torch.empty((N, L + 1), dtype=out_dtype, device=device)
+    e_out = torch.empty((N, L), dtype=out_dtype, device=device) if return_edges else None
     lib = _lib.load()
     work = _workspace(lib.mlxc_rejection_sampling_workspace_bytes(rowptr.numel() - 1, col.numel(),
                                                                   N, L), device)
@@ -333,7 +350,8 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
         rc = lib.mlxc_rejection_sampling(
             _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,
             p, q, seed, _RULES[rule], rows, _ptr(n_out),
-            _ptr(e_out) if return_edges else None, work.data_ptr(), work.numel() * 8, handle)
+            _ptr(e_out) if return_edges else None, otype, work.data_ptr(), work.numel() * 8,
+            handle)
     _lib.check(rc, "rejection_sampling")
     if check:
         _raise_status(work, stream, "rejection_sampling")

@@ -47,7 +47,7 @@ def test_header_constants_match_binding():
 
 
 def test_version():
-    assert _lib.load().mlxc_version() == 100
+    assert _lib.load().mlxc_version() == 200
 
 
 FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
@@ -71,8 +71,22 @@ WS = 64  # workspace bytes passed with FAKE
 ])
 def test_random_walk_rejects_bad_arguments(args, msg):
     lib = _lib.load()
+    args = args[:10] + (_lib.MLXC_OUT_INT64,) + args[10:]  # out_type after d_e_out
     assert lib.mlxc_random_walk(*args) == _lib.MLXC_ERR_INVALID_ARGUMENT
     assert msg in _lib.last_error()
+
+
+@pytest.mark.parametrize("num_nodes,num_edges,e_out,out_type,msg", [
+    (1, 0, None, 5, "out_type"),
+    (2**31, 0, None, 1, "MLXC_OUT_INT32"),
+    (1, 2**31, FAKE, 1, "MLXC_OUT_INT32"),
+])
+def test_out_type_is_checked(num_nodes, num_edges, e_out, out_type, msg):
+    lib = _lib.load()
+    for fn in (lib.mlxc_random_walk, lambda *a: lib.mlxc_random_walk_cpu(*a[:11], 1, None)):
+        rc = fn(FAKE, num_nodes, FAKE, num_edges, FAKE, 1, FAKE, 1, FAKE, e_out, out_type, FAKE,
+                WS, None)
+        assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT and msg in _lib.last_error()
 
 
 @pytest.mark.parametrize("p,q,rule,msg", [
@@ -82,7 +96,7 @@ def test_random_walk_rejects_bad_arguments(args, msg):
 def test_rejection_sampling_rejects_bad_arguments(p, q, rule, msg):
     lib = _lib.load()
     rc = lib.mlxc_rejection_sampling(FAKE, 1, FAKE, 0, FAKE, 0, 3, p, q, 1, rule, 1, FAKE, None,
-                                     FAKE, WS, None)
+                                     0, FAKE, WS, None)
     assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT
     assert msg in _lib.last_error()
 
@@ -90,7 +104,7 @@ def test_rejection_sampling_rejects_bad_arguments(p, q, rule, msg):
 def test_rejection_sampling_rejects_bad_row_mode():
     lib = _lib.load()
     rc = lib.mlxc_rejection_sampling(FAKE, 1, FAKE, 0, FAKE, 0, 3, 1.0, 1.0, 1, 0, 3, FAKE, None,
-                                     FAKE, WS, None)
+                                     0, FAKE, WS, None)
     assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT and "rows" in _lib.last_error()
 
 

@@ -31,7 +31,8 @@ def _direct_walk(rowptr, col, start, L, p, q, seed, rule, rows):
     ptr = lambda t: t.data_ptr() if t.numel() else None
     rc = lib.mlxc_rejection_sampling(ptr(rowptr), rowptr.numel() - 1, ptr(col), col.numel(),
                                      ptr(start), N, L, p, q, seed, rule, rows, ptr(n), ptr(e),
-                                     ws.data_ptr(), 32, torch.cuda.current_stream().cuda_stream)
+                                     _lib.MLXC_OUT_INT64, ws.data_ptr(), 32,
+                                     torch.cuda.current_stream().cuda_stream)
     assert rc == 0, _lib.last_error()
     torch.cuda.synchronize()
     assert int(ws[0].item()) == 0
@@ -200,3 +201,20 @@ def test_long_walks_with_sinks(L, cuda):
     for rule in (oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT):
         _, counts = assert_parity(rowptr, col, start, L, 0.5, 2.0, 71, rule, cuda)
         assert counts["sink_walks"] > 500
+
+
+@pytest.mark.parametrize("rule", ["ref_chain", "node2vec"])
+def test_int32_output(rule, cuda):
+    """out_dtype=torch.int32: the record walk (with and without edges) and
+    the direct kernel give the int64 results, narrowed."""
+    rowptr, col = synth.rmat_csr(12, 40_000, seed=13, symmetrize=True)
+    rowptr, col = rowptr.to(cuda), col.to(cuda)
+    start = torch.arange(9000, device=cuda) % (rowptr.numel() - 1)
+    kw = dict(seed=5, rule=rule, return_edges=True)
+    a = mc.rejection_sampling(rowptr, col, start, 21, 0.5, 2.0, **kw)
+    b = mc.rejection_sampling(rowptr, col, start, 21, 0.5, 2.0, out_dtype=torch.int32, **kw)
+    assert b[0].dtype == torch.int32
+    assert torch.equal(a[0], b[0].long()) and torch.equal(a[1], b[1].long())
+    c = mc.rejection_sampling(rowptr, col, start, 21, 0.5, 2.0, out_dtype=torch.int32, seed=5,
+                              rule=rule)
+    assert torch.equal(a[0], c.long())

@@ -162,7 +162,8 @@ def test_c2_full_size_properties(cuda):
     np.testing.assert_array_equal(n[sample].cpu().numpy(), n_ref)
 
 
-def _abi_walk(rowptr, col, start, rand_t, L, n_out_t, *, e_out=None, ws_bytes=None):
+def _abi_walk(rowptr, col, start, rand_t, L, n_out_t, *, e_out=None, ws_bytes=None,
+              out_type=0):
     """Calls mlxc_random_walk directly so each kernel path can be selected:
     edge records (full workspace, many steps per edge), CSR reads with start
     records (workspace for start records only), and the unwindowed kernel
@@ -175,8 +176,8 @@ def _abi_walk(rowptr, col, start, rand_t, L, n_out_t, *, e_out=None, ws_bytes=No
     ws = torch.empty((ws_bytes + 7) // 8, dtype=torch.int64, device=rowptr.device)
     rc = lib.mlxc_random_walk(rowptr.data_ptr(), V, col.data_ptr(), E, start.data_ptr(),
                               start.numel(), rand_t, L, n_out_t,
-                              None if e_out is None else e_out.data_ptr(), ws.data_ptr(),
-                              ws_bytes, torch.cuda.current_stream().cuda_stream)
+                              None if e_out is None else e_out.data_ptr(), out_type,
+                              ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
     assert rc == 0, _lib.last_error()
     torch.cuda.synchronize()
     assert int(ws[0].item()) == 0
@@ -281,4 +282,31 @@ def test_long_and_block_sized_walks_with_sinks(L, cuda):
         np.testing.assert_array_equal(n.cpu().numpy(), n_ref)
         np.testing.assert_array_equal(e.cpu().numpy(), e_ref)
     g = mc.random_walk(rowptr, col, start, None, L, seed=8)
+    np.testing.assert_array_equal(g.cpu().numpy(), n_ref)
+
+
+@pytest.mark.parametrize("L", [7, 9, 80, 600])
+def test_int32_output_all_kernel_paths(L, cuda):
+    """out_type MLXC_OUT_INT32 (8-entry blocks of 32 bytes, two lanes per
+    block in the wavefront stores): nodes and edges equal the int64 output
+    for the record walk, the CSR walk and the unwindowed kernel, and the
+    oracle."""
+    rowptr, col = synth.rmat_csr(10, 4000, seed=46, device=cuda)
+    V, E = rowptr.numel() - 1, col.numel()
+    N = 3000
+    start = (torch.arange(N, device=cuda) * 5) % V
+    rand = mc.philox_uniform((N, L), 9, device=cuda)
+    n_ref, e_ref, st, _ = oracle.uniform_walk(rowptr.cpu().numpy(), col.cpu().numpy(),
+                                              start.cpu().numpy(), rand.cpu().numpy(), L,
+                                              with_edges=True)
+    assert st == 0
+    for ws_bytes in (256 + 16 * (E + N), 256 + 16 * N, 32):
+        n = torch.empty((N, L + 1), dtype=torch.int32, device=cuda)
+        e = torch.empty((N, L), dtype=torch.int32, device=cuda)
+        _abi_walk(rowptr, col, start, rand.data_ptr(), L, n.data_ptr(), e_out=e,
+                  ws_bytes=ws_bytes, out_type=1)
+        np.testing.assert_array_equal(n.cpu().numpy(), n_ref)
+        np.testing.assert_array_equal(e.cpu().numpy(), e_ref)
+    g = mc.random_walk(rowptr, col, start, None, L, seed=9, out_dtype=torch.int32)
+    assert g.dtype == torch.int32
     np.testing.assert_array_equal(g.cpu().numpy(), n_ref)

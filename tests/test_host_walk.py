@@ -175,3 +175,33 @@ def test_gpu_only_helpers_refuse_the_cpu_stream():
         mc.csr_check(rowptr, col, stream="cpu")
     with pytest.raises(ValueError, match="GPU only"):
         mc.philox_uniform(8, 1, stream="cpu")
+
+
+def test_int32_output_equals_int64():
+    rowptr, col = synth.rmat_csr(11, 20000, seed=6)
+    V = rowptr.numel() - 1
+    start = torch.arange(3 * V) % V
+    for seed_kw in (dict(seed=4), None):
+        rand = None if seed_kw else torch.from_numpy(oracle.philox_uniform(start.numel() * 9, 4)
+                                                      .reshape(-1, 9))
+        kw = seed_kw or {}
+        a = mc.random_walk(rowptr, col, start, rand, 9, stream="cpu", return_edges=True, **kw)
+        b = mc.random_walk(rowptr, col, start, rand, 9, stream="cpu", return_edges=True,
+                           out_dtype=torch.int32, **kw)
+        assert b[0].dtype == torch.int32 and b[1].dtype == torch.int32
+        assert torch.equal(a[0], b[0].long()) and torch.equal(a[1], b[1].long())
+    a = mc.rejection_sampling(rowptr, col, start, 7, 0.5, 2.0, seed=3, stream="cpu",
+                              return_edges=True)
+    b = mc.rejection_sampling(rowptr, col, start, 7, 0.5, 2.0, seed=3, stream="cpu",
+                              return_edges=True, out_dtype=torch.int32)
+    assert torch.equal(a[0], b[0].long()) and torch.equal(a[1], b[1].long())
+
+
+def test_out_dtype_validation():
+    rowptr, col = csr(3, [(0, 1), (1, 2), (2, 0)])
+    with pytest.raises(TypeError, match="out_dtype"):
+        mc.random_walk(rowptr, col, np.array([0]), None, 2, seed=1, stream="cpu",
+                       out_dtype=torch.int16)
+    with pytest.raises(TypeError, match="out_dtype"):
+        mc.rejection_sampling(rowptr, col, np.array([0]), 2, 1.0, 1.0, stream="cpu",
+                              out_dtype=torch.float32)
