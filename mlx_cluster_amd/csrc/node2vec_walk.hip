@@ -468,11 +468,17 @@ int dispatch_n2v(const N2VArgs& a, bool sorted, bool edges, hipStream_t stream) 
                  : launch_n2v<kRule, false, false, OutT>(a, stream);
 }
 
+// Resident blocks per compute unit of the node2vec record walk (0: as many
+// as its registers allow, 5; fewer measured slower at configuration 3).
+#ifndef MLXC_N2V_BLOCKS_PER_CU
+#define MLXC_N2V_BLOCKS_PER_CU 0
+#endif
+
 template <int kRule, bool kEdges, typename OutT>
 int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
     auto kernel = node2vec_rec_kernel<kRule, kEdges, OutT>;
     int grid = 0;
-    if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid)) return rc;
+    if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid, MLXC_N2V_BLOCKS_PER_CU)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;

@@ -502,11 +502,24 @@ UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes, bool gen) {
     return UniformMode::kPlain;
 }
 
+// Resident blocks per compute unit of the persistent walks (0: as many as
+// the kernel's registers allow).  The record walk runs best below its
+// register limit of 6: measured on MI355X at configuration 2, 7.68 ms with 4
+// blocks per CU, 7.70 with 3 or 5, 7.80 with 6 and 8.18 with 2 (the same
+// order for the seeded and the int32-output variants).  The CSR walk runs
+// best at its limit (configuration 4: 6.77 ms with 4, 7.35 with 3).
+#ifndef MLXC_REC_BLOCKS_PER_CU
+#define MLXC_REC_BLOCKS_PER_CU 4
+#endif
+#ifndef MLXC_CSR_BLOCKS_PER_CU
+#define MLXC_CSR_BLOCKS_PER_CU 0
+#endif
+
 template <typename Kernel, typename... Extra>
-int launch_walk_kernel(Kernel kernel, int slots, const WalkArgs& a, hipStream_t stream,
-                       Extra... extra) {
+int launch_walk_kernel(Kernel kernel, int slots, int max_per_cu, const WalkArgs& a,
+                       hipStream_t stream, Extra... extra) {
     int grid = 0;
-    if (int rc = persistent_grid(kernel, a.num_walks, slots, grid)) return rc;
+    if (int rc = persistent_grid(kernel, a.num_walks, slots, grid, max_per_cu)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a, extra...);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
@@ -541,7 +554,7 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
                                       init, stream))
             return rc;
         return launch_walk_kernel(uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen, kEdges, OutT>,
-                                  MLXC_REC_SLOTS, a,
+                                  MLXC_REC_SLOTS, MLXC_REC_BLOCKS_PER_CU, a,
                                   stream,
                                   static_cast<const EdgeRecord*>(recs),
                                   static_cast<const EdgeRecord*>(init));
@@ -552,14 +565,14 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
                                       init, stream))
             return rc;
         return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW, kGen, kEdges, OutT>,
-                                  MLXC_CSR_SLOTS, a,
+                                  MLXC_CSR_SLOTS, MLXC_CSR_BLOCKS_PER_CU, a,
                                   stream,
                                   static_cast<const EdgeRecord*>(init));
     }
     case UniformMode::kPlain:
         break;
     }
-    return launch_walk_kernel(uniform_walk_kernel<2, kEdges, kGen, OutT>, 2, a, stream);
+    return launch_walk_kernel(uniform_walk_kernel<2, kEdges, kGen, OutT>, 2, 0, a, stream);
 }
 
 }  // namespace

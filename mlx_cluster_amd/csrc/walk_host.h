@@ -35,14 +35,16 @@ int device_info(DeviceInfo& info);
 // at most blocks_per_cu per compute unit.
 int stream_grid(int64_t items, int blocks_per_cu, int& grid);
 
-// Persistent grid: the blocks that stay resident on the device, but no more
-// than the walks can feed (each block serves slots * kBlock walks at once).
+// Persistent grid: the blocks that stay resident on the device (at most
+// max_per_cu per compute unit when max_per_cu > 0), but no more than the
+// walks can feed (each block serves slots * kBlock walks at once).
 template <typename Kernel>
-int persistent_grid(Kernel kernel, int64_t num_walks, int slots, int& grid) {
+int persistent_grid(Kernel kernel, int64_t num_walks, int slots, int& grid, int max_per_cu = 0) {
     DeviceInfo info;
     if (int rc = device_info(info)) return rc;
     int per_cu = 0;
     MLXC_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kBlock, 0));
+    if (max_per_cu > 0 && per_cu > max_per_cu) per_cu = max_per_cu;
     if (per_cu < 1) per_cu = 1;
     const int64_t resident = static_cast<int64_t>(info.cus) * per_cu;
     const int64_t per_block = static_cast<int64_t>(slots) * kBlock;
