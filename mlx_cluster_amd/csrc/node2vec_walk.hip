@@ -147,11 +147,10 @@ __global__ __launch_bounds__(kBlock) void node2vec_walk_kernel(N2VArgs a) {
 enum : int {
     kN2vIdle = 0,    // wants a walk id
     kN2vStart = 1,   // reads the start record of walk n
-    kN2vCand = 2,     // reads the edge record of the current candidate
-    kN2vSummary = 3,  // sorted rows: bisects the block index of row(x)
-    kN2vBlock = 4,    // sorted rows: reads the 16-entry block that may hold t
-    kN2vScan = 5,     // unsorted rows: reads the next entry of row(x)
-    kN2vDone = 6,     // the queue is exhausted
+    kN2vCand = 2,    // reads the edge record of the current candidate
+    kN2vLevel = 3,   // sorted rows: reads one 16-entry block of a search-index level
+    kN2vScan = 4,    // unsorted rows: reads the next 16 entries of row(x)
+    kN2vDone = 5,    // the queue is exhausted
 };
 
 // The two uniforms of a trial: Philox4x32-10 with key = seed and counter =
@@ -167,20 +166,74 @@ __device__ __forceinline__ void n2v_uniforms(int64_t n, int32_t step, uint32_t t
     u1 = unit_float(c1);
 }
 
-// Neighbour search on sorted rows.  col32 is col as int32 (padded to a
-// multiple of kSearchBlock entries) and index[j] = col32[kSearchBlock * j]:
-// a dense sample of every row, E / 16 entries, that stays in the caches.  A
-// search bisects the index entries inside row(x) and then reads the one
-// aligned 64-byte block of col32 that can hold t — one line from HBM instead
-// of one per bisection step.
-constexpr int kSearchBlock = 16;
+// Neighbour search on sorted rows, through the levels of IndexLevels.  Inside
+// a sorted row the level-k samples are sorted too, so one aligned block of 16
+// level-k entries splits the 16^(k+1) col32 positions it covers into 16
+// segments of 16^k positions: one read narrows the search to one segment,
+// which is exactly one aligned block of level k-1.  A search for t in row
+// [b, e) starts at the finest level at which one block covers the whole row
+// and ends with one 64-byte block of col32: k + 1 dependent reads for a row
+// of up to 16^(k+1) entries, from arrays 16 times smaller per level (the
+// upper levels stay in L2).  Bisection needs about log2(deg / 16) reads of
+// the E/16-entry level instead.
+//
+// lo, hi: the col32 positions that can still hold t.  Returns 1 (found), 0
+// (absent) or -1 (continue with the updated lvl, blk, lo, hi).
+__device__ __forceinline__ int level_step(const int32_t (&v)[kSearchBlock], int32_t t, int& lvl,
+                                          int32_t& blk, int32_t& lo, int32_t& hi) {
+    const int sh = 4 * lvl;  // log2 of the distance S between samples of this level
+    const int64_t base = static_cast<int64_t>(kSearchBlock) * blk << sh;  // sample 0's position
+    // samples i_lo .. i_hi-1 of the block lie in [lo, hi): ceil((lo - base) / S) ..
+    const int64_t s_minus_1 = (int64_t{1} << sh) - 1;
+    const int i_lo = lo > base ? static_cast<int>(min(int64_t{kSearchBlock}, (lo - base + s_minus_1) >> sh)) : 0;
+    const int i_hi = hi > base ? static_cast<int>(min(int64_t{kSearchBlock}, (hi - base + s_minus_1) >> sh)) : 0;
+    int best = -1;       // last sample in [lo, hi) that is <= t
+    bool found = false;  // a sample in [lo, hi) equals t
+#pragma unroll
+    for (int i = 0; i < kSearchBlock; ++i) {
+        const bool inside = i >= i_lo && i < i_hi;
+        if (inside && v[i] <= t) best = i;
+        found |= inside && v[i] == t;
+    }
+    if (found) return 1;
+    if (lvl == 0) return 0;
+    if (best >= 0) {
+        // t is after sample best and before the next one: the segment
+        // [pos, pos + S) is block kSearchBlock * blk + best of level lvl-1
+        const int64_t pos = base + (static_cast<int64_t>(best) << sh);
+        lo = static_cast<int32_t>(pos + 1);
+        hi = static_cast<int32_t>(min(static_cast<int64_t>(hi), pos + s_minus_1 + 1));
+        blk = kSearchBlock * blk + best;
+    } else {
+        // every sample of the row here is > t: t is before the first one
+        hi = static_cast<int32_t>(min(static_cast<int64_t>(hi), base + (static_cast<int64_t>(i_lo) << sh)));
+        blk = static_cast<int32_t>(static_cast<int64_t>(lo) >> sh);
+    }
+    lvl -= 1;
+    return lo < hi ? -1 : 0;
+}
+
+// Linear scan of an unsorted row, 16 entries (one 64-byte block of col32)
+// per read: the entries of block lo / 16 inside [lo, hi).
+__device__ __forceinline__ int scan_step(const int32_t (&v)[kSearchBlock], int32_t t, int32_t& lo,
+                                         int32_t hi) {
+    const int32_t base = lo & ~(kSearchBlock - 1);
+    bool found = false;
+#pragma unroll
+    for (int i = 0; i < kSearchBlock; ++i) {
+        const int32_t pos = base + i;
+        found |= pos >= lo && pos < hi && v[i] == t;
+    }
+    if (found) return 1;
+    lo = base + kSearchBlock;
+    return lo < hi ? -1 : 0;
+}
 
 struct N2VRecArgs {
     WalkArgs w;
     const EdgeRecord* recs;   // [num_edges]
     const EdgeRecord* init;   // [num_walks]
-    const int32_t* col32;     // [num_edges rounded up to kSearchBlock] col as int32
-    const int32_t* index;     // [ceil(num_edges / kSearchBlock)] col32[kSearchBlock * j]
+    IndexLevels index;        // search index (level 0 = col32)
     int32_t rows;             // MLXC_ROWS_*; DETECT reads the prep pass's counts in work[2..3]
     double prob0, prob1, prob2;
     uint32_t key0, key1;
@@ -213,13 +266,14 @@ __device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, double r, bool 
 }
 
 // node2vec walk over edge records (num_nodes, num_edges below 2^31; n_out and
-// e_out 16-byte aligned).  One walk per lane slot from the wave queue.  Every iteration a
-// live slot issues one dependent read — a start record, the edge record of
-// its candidate (which carries the candidate's row, so the neighbour test
-// needs no rowptr read), or one step of the neighbour search — and the wave
-// waits once.  Sorted rows are searched through the block index (see
-// kSearchBlock); unsorted rows are scanned one entry per iteration, as the
-// reference scans them.
+// e_out 16-byte aligned).  One walk per lane slot from the wave queue.  Every
+// iteration a live slot issues one dependent read of one 64-byte block — the
+// block holding its start record or its candidate's edge record (which
+// carries the candidate's row, so the neighbour test needs no rowptr read),
+// or one block of the neighbour search — as four unconditional 16-byte loads
+// (idle slots read the first start records), and the wave waits once.
+// Sorted rows are searched through the index levels (level_step); unsorted
+// rows are scanned 16 entries per read, as the reference scans them.
 template <int kRule, bool kEdges, typename OutT>
 __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -240,9 +294,9 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     int32_t v = 0, bv = 0, dv = 0;   // current node and its row
     int32_t e = 0;          // candidate edge
     int32_t x = 0, bx = 0, dx = 0;   // candidate node and its row (from its record)
-    int32_t lo = 0, hi = 0; // search range: index entries (sorted) or col32 entries (unsorted)
-    int32_t first = 0;      // first index entry inside row(x)
-    int32_t blk = 0, blo = 0, bhi = 0;  // block to read and the row's entries in it
+    int lvl = 0;            // search: index level of the block to read next
+    int32_t blk = 0;        // search: that block (kN2vLevel)
+    int32_t lo = 0, hi = 0; // search: col32 positions that can still hold t
     float r = 0.0f;         // acceptance uniform of the current trial
     OutWin<int32_t> ow;
     OutWin<int32_t> ew;     // edge ids (kEdges): e_out[n*L + l] is step l's edge
@@ -253,21 +307,38 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     uint32_t status = 0;
 
     while (true) {
-        // 1. This iteration's read: a record, an index entry, a block of
-        // col32 or one col32 entry.
+        // 1. This iteration's read: one 64-byte block.  Records are read as
+        // the block of four records holding them (the block may run past
+        // the end of its array into the next workspace array or the slack
+        // after the last one).
         const int ph = phase;
-        const EdgeRecord* p = ph == kN2vStart ? a.init + n : ph == kN2vCand ? a.recs + e : a.init;
-        const i32x4 rec = *reinterpret_cast<const i32x4*>(p);
-        const int32_t mid = lo + ((hi - lo) >> 1);
-        int32_t sv;                       // kN2vSummary / kN2vScan
-        i32x4 blkv[kSearchBlock / 4];    // kN2vBlock
-        if (ph == kN2vSummary) sv = a.index[mid];
-        if (ph == kN2vScan) sv = a.col32[lo];
-        if (ph == kN2vBlock) {
-            const i32x4* bp = reinterpret_cast<const i32x4*>(a.col32 + kSearchBlock * blk);
+        const int32_t* bp;
+        if (ph == kN2vStart) {
+            bp = reinterpret_cast<const int32_t*>(a.init + n);
+        } else if (ph == kN2vCand) {
+            bp = reinterpret_cast<const int32_t*>(a.recs + e);
+        } else if (ph == kN2vLevel) {
+            const int32_t* lp = a.index.level[0];
 #pragma unroll
-            for (int i = 0; i < kSearchBlock / 4; ++i) blkv[i] = bp[i];
+            for (int k = 1; k < kMaxLevels; ++k)
+                if (lvl == k) lp = a.index.level[k];
+            bp = lp + static_cast<int64_t>(kSearchBlock) * blk;
+        } else if (ph == kN2vScan) {
+            bp = a.index.level[0] + (lo & ~(kSearchBlock - 1));
+        } else {
+            bp = reinterpret_cast<const int32_t*>(a.init);
         }
+        i32x4 qb[4];
+        qb[0] = reinterpret_cast<const i32x4*>(bp)[0];
+#ifndef MLXC_N2V_FULL_BLOCKS
+        if (ph == kN2vLevel || ph == kN2vScan) {
+#pragma unroll
+            for (int i = 1; i < 4; ++i) qb[i] = reinterpret_cast<const i32x4*>(bp)[i];
+        }
+#else
+#pragma unroll
+        for (int i = 1; i < 4; ++i) qb[i] = reinterpret_cast<const i32x4*>(bp)[i];
+#endif
         // ... and the output blocks the last iteration completed are stored.
         ow_drain<OutT>(ow, st);
         if (kEdges) ow_drain<OutT>(ew, st);
@@ -282,8 +353,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
         }
         if (!__any(phase != kN2vDone)) break;
         wait_vmem();
-        keep_vgpr(rec.w);
         if (ph == kN2vIdle || ph == kN2vDone) continue;
+        const i32x4 rec = qb[0];
 
         // 3. Consume.
         const int64_t g0 = n * L1;
@@ -330,69 +401,29 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                 } else if (dx == 0) {
                     accept = n2v_resolve<kRule>(a, static_cast<double>(r), false);
                     next_trial = !accept;
-                } else if (!sorted) {
+                } else {
                     lo = bx;
                     hi = bx + dx;
-                    phase = kN2vScan;
-                } else {
-                    // index entries j with bx <= kSearchBlock * j < bx + dx
-                    first = (bx + kSearchBlock - 1) / kSearchBlock;
-                    const int32_t last = (bx + dx - 1) / kSearchBlock;
-                    if (first > last) {  // short row inside one block
-                        blk = bx / kSearchBlock;
-                        blo = bx;
-                        bhi = bx + dx;
-                        phase = kN2vBlock;
+                    if (!sorted) {
+                        phase = kN2vScan;
                     } else {
-                        lo = first;
-                        hi = last + 1;
-                        phase = kN2vSummary;
+                        // finest level whose aligned blocks (16^(lvl+1) positions)
+                        // hold the whole row in one
+                        const uint32_t diff = static_cast<uint32_t>(lo) ^ static_cast<uint32_t>(hi - 1);
+                        lvl = diff ? (31 - __builtin_clz(diff)) >> 2 : 0;
+                        blk = static_cast<int32_t>(static_cast<int64_t>(lo) >> (4 * (lvl + 1)));
+                        phase = kN2vLevel;
                     }
                 }
             }
         } else {  // the neighbour search: is t in row(x)?
-            bool done = false, found = false;
-            if (ph == kN2vSummary) {
-                if (sv == t) {
-                    done = found = true;
-                } else {
-                    if (sv < t) lo = mid + 1;
-                    else hi = mid;
-                    if (lo >= hi) {
-                        // index entries first .. lo-1 are < t, lo .. are > t:
-                        // t can only be in the block after entry lo-1, or
-                        // before the row's first index entry
-                        const int32_t row_end = bx + dx;
-                        if (lo == first) {
-                            blk = first - 1;
-                            blo = bx;
-                            bhi = min(kSearchBlock * first, row_end);
-                        } else {
-                            blk = lo - 1;
-                            blo = kSearchBlock * blk;
-                            bhi = min(blo + kSearchBlock, row_end);
-                        }
-                        phase = kN2vBlock;
-                    }
-                }
-            } else if (ph == kN2vBlock) {
+            int32_t vals[kSearchBlock];
 #pragma unroll
-                for (int i = 0; i < kSearchBlock; ++i) {
-                    const int32_t idx = kSearchBlock * blk + i;
-                    const int32_t cv = blkv[i / 4][i % 4];
-                    found |= idx >= blo && idx < bhi && cv == t;
-                }
-                done = true;
-            } else {  // kN2vScan
-                if (sv == t) {
-                    done = found = true;
-                } else {
-                    lo += 1;
-                    done = lo >= hi;
-                }
-            }
-            if (done) {
-                accept = n2v_resolve<kRule>(a, static_cast<double>(r), found);
+            for (int i = 0; i < kSearchBlock; ++i) vals[i] = qb[i / 4][i % 4];
+            const int res = ph == kN2vLevel ? level_step(vals, t, lvl, blk, lo, hi)
+                                            : scan_step(vals, t, lo, hi);
+            if (res >= 0) {
+                accept = n2v_resolve<kRule>(a, static_cast<double>(r), res == 1);
                 next_trial = !accept;
             }
         }
@@ -469,9 +500,11 @@ int dispatch_n2v(const N2VArgs& a, bool sorted, bool edges, hipStream_t stream) 
 }
 
 // Resident blocks per compute unit of the node2vec record walk (0: as many
-// as its registers allow, 5; fewer measured slower at configuration 3).
+// as its registers allow, 6).  Measured on MI355X: configuration 3 13.57 ms
+// with 4, 13.67 with 5 and 13.65 with 6; configuration 5 10.93, 10.97 and
+// 11.02 ms.
 #ifndef MLXC_N2V_BLOCKS_PER_CU
-#define MLXC_N2V_BLOCKS_PER_CU 0
+#define MLXC_N2V_BLOCKS_PER_CU 4
 #endif
 
 template <int kRule, bool kEdges, typename OutT>
@@ -485,18 +518,28 @@ int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
 }
 
 // Workspace of the record walk: edge records, start records, then (128-byte
-// aligned) col as int32 padded to whole search blocks, then the block index.
+// aligned) the levels of the search index — col as int32, then its samples
+// every 16^k entries — each padded to whole blocks of kSearchBlock entries,
+// then 64 bytes of slack for the block reads of the last start records.
 struct N2VLayout {
-    size_t col32, index, total;
+    size_t level[kMaxLevels];
+    int count;
+    size_t total;
 };
 
 N2VLayout n2v_layout(int64_t num_edges, int64_t num_walks) {
     N2VLayout lay;
-    const size_t blocks = static_cast<size_t>((num_edges + kSearchBlock - 1) / kSearchBlock);
-    lay.col32 = kRecordOffset + static_cast<size_t>(num_edges + num_walks) * sizeof(EdgeRecord);
-    lay.col32 = (lay.col32 + 127) & ~static_cast<size_t>(127);
-    lay.index = lay.col32 + blocks * kSearchBlock * sizeof(int32_t);
-    lay.total = lay.index + blocks * sizeof(int32_t);
+    lay.count = index_levels(num_edges);
+    size_t pos = kRecordOffset + static_cast<size_t>(num_edges + num_walks) * sizeof(EdgeRecord);
+    pos = (pos + 127) & ~static_cast<size_t>(127);
+    int64_t entries = num_edges;  // level k has ceil(num_edges / 16^k) entries
+    for (int k = 0; k < lay.count; ++k) {
+        lay.level[k] = pos;
+        const int64_t blocks = (entries + kSearchBlock - 1) / kSearchBlock;
+        pos += static_cast<size_t>(blocks) * kSearchBlock * sizeof(int32_t);
+        entries = blocks;
+    }
+    lay.total = pos + 64;
     return lay;
 }
 
@@ -524,12 +567,13 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         char* base = static_cast<char*>(workspace);
         EdgeRecord* recs = reinterpret_cast<EdgeRecord*>(base + kRecordOffset);
         EdgeRecord* init = recs + w.num_edges;
-        int32_t* col32 = reinterpret_cast<int32_t*>(base + lay.col32);
-        int32_t* index = reinterpret_cast<int32_t*>(base + lay.index);
-        // one pass builds the search arrays and, for MLXC_ROWS_DETECT, checks
+        IndexLevels index{};
+        index.count = lay.count;
+        for (int k = 0; k < lay.count; ++k)
+            index.level[k] = reinterpret_cast<int32_t*>(base + lay.level[k]);
+        // one pass builds the search index and, for MLXC_ROWS_DETECT, checks
         // the rows (the walk reads the result on the device: no host sync)
-        if (int rc = launch_edge_records(w.rowptr, w.col, w.num_nodes, w.num_edges, recs, col32,
-                                         index, kSearchBlock,
+        if (int rc = launch_edge_records(w.rowptr, w.col, w.num_nodes, w.num_edges, recs, index,
                                          p.rows == MLXC_ROWS_DETECT ? w.work : nullptr, stream))
             return rc;
         if (int rc = launch_walk_init(w.rowptr, w.start, w.num_nodes, w.num_edges, w.num_walks,
@@ -537,7 +581,6 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
             return rc;
         a.recs = recs;
         a.init = init;
-        a.col32 = col32;
         a.index = index;
         a.prob0 = p.prob0;
         a.prob1 = p.prob1;

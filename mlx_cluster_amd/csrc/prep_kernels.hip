@@ -58,19 +58,17 @@ struct CsrCheck {
     }
 };
 
-// Edge records (see EdgeRecord); optionally also col as int32 (col32 may be
-// null) and every index_stride-th entry of it (index), the neighbour-search
-// arrays of the node2vec walk.  With a non-null work pointer the same pass
-// validates the whole CSR (status bits into work[0]) and counts the row
-// descents into work[2] / work[3], from which the node2vec walk decides
-// whether its rows are sorted.
+// Edge records (see EdgeRecord); optionally (index.count > 0) also the
+// levels of the node2vec walk's search index: col as int32 and its samples
+// col32[16^k * i].  With a non-null work pointer the same pass validates the
+// whole CSR (status bits into work[0]) and counts the row descents into
+// work[2] / work[3], from which the node2vec walk decides whether its rows
+// are sorted.
 __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __restrict__ rowptr,
                                                              const int64_t* __restrict__ col,
                                                              int64_t num_nodes, int64_t num_edges,
                                                              EdgeRecord* __restrict__ rec,
-                                                             int32_t* __restrict__ col32,
-                                                             int32_t* __restrict__ index,
-                                                             int index_stride, int64_t* work) {
+                                                             IndexLevels index, int64_t* work) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -89,9 +87,11 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
             }
         }
         *reinterpret_cast<i32x4*>(rec + e) = r;
-        if (col32) {
-            col32[e] = r.x;
-            if (e % index_stride == 0) index[e / index_stride] = r.x;
+        if (index.count > 0) {
+            index.level[0][e] = r.x;
+            // e is a multiple of 16^k for k = 1 .. while its low 4k bits are 0
+            for (int k = 1; k < index.count && (e & ((int64_t{1} << (4 * k)) - 1)) == 0; ++k)
+                index.level[k][e >> (4 * k)] = r.x;
         }
     }
     if (work) {
@@ -184,14 +184,14 @@ int launch_zero_work(int64_t* d_work, hipStream_t stream) {
 }
 
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
-                        int64_t num_edges, EdgeRecord* recs, int32_t* col32, int32_t* index,
-                        int index_stride, int64_t* check_work, hipStream_t stream) {
+                        int64_t num_edges, EdgeRecord* recs, const IndexLevels& index,
+                        int64_t* check_work, hipStream_t stream) {
     if (num_edges == 0 && !check_work) return MLXC_OK;
     int grid = 0;
     const int64_t items = check_work && num_nodes > num_edges ? num_nodes : num_edges;
     if (int rc = stream_grid(items, 16, grid)) return rc;
     hipLaunchKernelGGL(edge_record_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col,
-                       num_nodes, num_edges, recs, col32, index, index_stride, check_work);
+                       num_nodes, num_edges, recs, index, check_work);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

@@ -547,8 +547,8 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
     switch (uniform_mode(a, workspace_bytes, kGen)) {
     case UniformMode::kRecords: {
         EdgeRecord* init = recs + a.num_edges;
-        if (int rc = launch_edge_records(a.rowptr, a.col, a.num_nodes, a.num_edges, recs, nullptr,
-                                         nullptr, 1, nullptr, stream))
+        if (int rc = launch_edge_records(a.rowptr, a.col, a.num_nodes, a.num_edges, recs,
+                                         IndexLevels{}, nullptr, stream))
             return rc;
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, stream))

@@ -275,6 +275,12 @@ __device__ __forceinline__ void rw_shift_by(RandWindow<RW>& r, int k) {
 // against 1.0 here).  Only the partial blocks at the two ends of a row are
 // stored by the lane itself, entry by entry.
 //
+// Every output store is issued by ow_drain, which the walk loops call right
+// after issuing their reads and before their single wait.  No store is then
+// in flight when a loop iteration begins and reuses registers: on gfx9 vmcnt
+// counts stores too, and the compiler makes a register that a pending store
+// reads wait for that store.
+//
 // Between a completion and the drain the window is not pushed again: each
 // iteration of the walk loops pushes at most one entry per window, and a run
 // that follows a completed block starts on a block boundary.
@@ -349,9 +355,12 @@ template <typename T>
 struct OutWin {
     T w[8];              // w[8-count .. 7] hold the newest entries; w[7] is entry g
     int count;
-    void* blk;           // set: w[0..7] is a completed block, to be stored at blk
-    void* run;           // set: run_blocks whole blocks of run_val, to be stored at run
-    int32_t run_blocks;
+    // Deferred stores, written by ow_drain:
+    void* blk;           // set: w[i] belongs at blk + i; the last blk_n entries are
+    int32_t blk_n;       //   stored (8: a complete aligned block, by the wavefront)
+    void* run;           // set: run_blocks whole blocks of run_val, then tail_n more
+    int32_t run_blocks;  //   entries of run_val, from the aligned position run
+    int32_t tail_n;
     T run_val;
 };
 
@@ -359,8 +368,10 @@ template <typename T>
 __device__ __forceinline__ void ow_init(OutWin<T>& o) {
     o.count = 0;
     o.blk = nullptr;
+    o.blk_n = 0;
     o.run = nullptr;
     o.run_blocks = 0;
+    o.tail_n = 0;
     o.run_val = 0;
 }
 
@@ -370,41 +381,22 @@ struct WaveStage {
     void* dst[kWave];
 };
 
-// Writes the buffered entries, the newest of which is output index g: a
-// complete aligned block is left to ow_drain, a partial one is stored here.
+// Writes (defers to ow_drain) the buffered entries, the newest of which is
+// output index g: a complete aligned block, or the partial block at an end
+// of the row.
 template <typename T, typename OutT>
 __device__ __forceinline__ void ow_flush(OutWin<T>& o, OutT* __restrict__ out, int64_t g) {
-    if (o.count == 8 && ((g + 1) & 7) == 0) {
-        o.blk = out + (g - 7);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (i >= 8 - o.count) store_partial(static_cast<OutT>(o.w[i]), out + g - 7 + i);
+    if (o.count > 0) {
+        o.blk = out + (g - 7);  // only blk + 8 - blk_n .. blk + 7 is written
+        o.blk_n = o.count;
     }
     o.count = 0;
-}
-
-// Stores a completed block still pending in the window, lane by lane (only
-// reached if a window were pushed again before the drain).
-template <typename T, typename OutT>
-__device__ __forceinline__ void ow_store_pending(OutWin<T>& o, OutT*) {
-    constexpr int kPer = Vec16<OutT>::kLanes;
-    OutT* p = static_cast<OutT*>(o.blk);
-#pragma unroll
-    for (int i = 0; i < 8; i += kPer) {
-        typename Vec16<OutT>::type x;
-#pragma unroll
-        for (int j = 0; j < kPer; ++j) x[j] = static_cast<OutT>(o.w[i + j]);
-        store_block_part(x, p + i);
-    }
-    o.blk = nullptr;
 }
 
 // Appends the entry for output index g; completes the window's block when g
 // closes a block.
 template <typename T, typename OutT>
 __device__ __forceinline__ void ow_push(OutWin<T>& o, OutT* __restrict__ out, int64_t g, T x) {
-    if (o.blk) ow_store_pending(o, out);
 #pragma unroll
     for (int i = 0; i < 7; ++i) o.w[i] = o.w[i + 1];
     o.w[7] = x;
@@ -413,21 +405,21 @@ __device__ __forceinline__ void ow_push(OutWin<T>& o, OutT* __restrict__ out, in
 }
 
 // Output indices g .. g_last (inclusive) all hold x; the window holds the
-// entries before g.  The whole blocks of the run are left to ow_drain; the
-// entries before the first and after the last are stored here.
+// entries before g.  The entries up to the first block boundary go through
+// the window; the whole blocks and the entries after the last one are left
+// to ow_drain as a run.
 template <typename T, typename OutT>
 __device__ __forceinline__ void ow_fill(OutWin<T>& o, OutT* __restrict__ out, int64_t g,
                                         int64_t g_last, T x) {
     while (g <= g_last && (g & 7) != 0) ow_push(o, out, g++, x);
     if (o.count) ow_flush(o, out, g - 1);
-    const int64_t blocks = (g_last + 1 - g) >> 3;
-    if (blocks > 0) {
+    if (g <= g_last) {
+        const int64_t blocks = (g_last + 1 - g) >> 3;
         o.run = out + g;
         o.run_blocks = static_cast<int32_t>(blocks);
+        o.tail_n = static_cast<int32_t>(g_last + 1 - g - 8 * blocks);
         o.run_val = x;
-        g += 8 * blocks;
     }
-    for (; g <= g_last; ++g) store_partial(static_cast<OutT>(x), out + g);
 }
 
 // s_waitcnt vmcnt(0): every vector-memory operation of the wavefront has
@@ -469,9 +461,10 @@ __device__ __forceinline__ void ow_drain(OutWin<T>& o, WaveStage& st) {
     constexpr int kParts = 8 / kPer;           // lanes per block: 4 (int64) or 2 (int32)
     const int lane = __lane_id();
     const int part = lane % kParts;
-    const uint64_t blocks = __ballot(o.blk != nullptr);
+    const bool full = o.blk != nullptr && o.blk_n == 8;
+    const uint64_t blocks = __ballot(full);
     if (blocks) {
-        if (o.blk) {
+        if (full) {
             const int rank = lane_rank(blocks);
             *reinterpret_cast<i32x4*>(&st.vals[rank][0]) =
                 i32x4{static_cast<int32_t>(o.w[0]), static_cast<int32_t>(o.w[1]),
@@ -480,7 +473,6 @@ __device__ __forceinline__ void ow_drain(OutWin<T>& o, WaveStage& st) {
                 i32x4{static_cast<int32_t>(o.w[4]), static_cast<int32_t>(o.w[5]),
                       static_cast<int32_t>(o.w[6]), static_cast<int32_t>(o.w[7])};
             st.dst[rank] = o.blk;
-            o.blk = nullptr;
         }
         wave_sync();
         const int c = __popcll(blocks);
@@ -491,6 +483,19 @@ __device__ __forceinline__ void ow_drain(OutWin<T>& o, WaveStage& st) {
                                  static_cast<OutT*>(st.dst[k]) + kPer * part);
         }
         wave_sync();
+    }
+    if (o.blk != nullptr && !full) {  // partial block at an end of a row: this lane alone
+        OutT* p = static_cast<OutT*>(o.blk);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (i >= 8 - o.blk_n) store_partial(static_cast<OutT>(o.w[i]), p + i);
+    }
+    o.blk = nullptr;
+    if (o.tail_n > 0) {  // the entries of a run after its last whole block
+        OutT* p = static_cast<OutT*>(o.run) + 8 * static_cast<int64_t>(o.run_blocks);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (j < o.tail_n) store_partial(static_cast<OutT>(o.run_val), p + j);
     }
     uint64_t runs = __ballot(o.run_blocks > 0);
     while (runs) {  // wave-uniform: one lane's run at a time, the whole wave storing it
@@ -505,6 +510,7 @@ __device__ __forceinline__ void ow_drain(OutWin<T>& o, WaveStage& st) {
     }
     o.run = nullptr;
     o.run_blocks = 0;
+    o.tail_n = 0;
 }
 
 // ----------------------------------------------------------- edge records
@@ -522,6 +528,26 @@ struct __attribute__((aligned(16))) EdgeRecord {
     int32_t deg;    // rowptr[col[e] + 1] - rowptr[col[e]]; < 0 marks a malformed entry
     int32_t pad;
 };
+// Search index of the node2vec walk over sorted rows: level 0 is col as
+// int32 (col32); level k >= 1 holds col32[16^k * i] for every i.  Every
+// level is padded to whole blocks of 16 entries (64 bytes).  Built by
+// edge_record_kernel, read by node2vec_rec_kernel.
+constexpr int kSearchBlock = 16;
+constexpr int kMaxLevels = 8;  // 16^8 = 2^32 > any num_edges the records allow
+struct IndexLevels {
+    int32_t* level[kMaxLevels];
+    int32_t count;  // levels in use; 0: no col32 (the uniform walk)
+};
+
+// Levels a graph of num_edges entries needs: the coarsest level k at which a
+// row may have to start its search is msb(num_edges - 1) / 4.
+inline __host__ __device__ int index_levels(int64_t num_edges) {
+    if (num_edges <= 1) return 1;
+    int msb = 0;
+    for (int64_t x = num_edges - 1; x > 1; x >>= 1) ++msb;
+    return msb / 4 + 1;
+}
+
 constexpr int32_t kRecBadNode = -1;  // col[e] outside [0, num_nodes)
 constexpr int32_t kRecBadRow = -2;   // row of col[e] outside [0, num_edges] or decreasing
 constexpr size_t kRecordOffset = 256;  // bytes of workspace before the records

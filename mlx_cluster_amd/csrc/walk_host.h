@@ -61,12 +61,11 @@ inline bool records_fit(int64_t num_nodes, int64_t num_edges) {
 
 // ---- prep_kernels.hip
 int launch_zero_work(int64_t* d_work, hipStream_t stream);
-// col32 / index may be null (the uniform walk needs neither); a non-null
-// check_work also validates the CSR and counts row descents (see
-// edge_record_kernel).
+// index.count == 0: records only (the uniform walk); a non-null check_work
+// also validates the CSR and counts row descents (see edge_record_kernel).
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
-                        int64_t num_edges, EdgeRecord* recs, int32_t* col32, int32_t* index,
-                        int index_stride, int64_t* check_work, hipStream_t stream);
+                        int64_t num_edges, EdgeRecord* recs, const IndexLevels& index,
+                        int64_t* check_work, hipStream_t stream);
 int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
                      int64_t num_edges, int64_t num_walks, EdgeRecord* init, hipStream_t stream);
 int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,

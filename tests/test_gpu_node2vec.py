@@ -218,3 +218,35 @@ def test_int32_output(rule, cuda):
     c = mc.rejection_sampling(rowptr, col, start, 21, 0.5, 2.0, out_dtype=torch.int32, seed=5,
                               rule=rule)
     assert torch.equal(a[0], c.long())
+
+
+def test_c3_full_size_properties(cuda):
+    """Configuration 3 at full size (node2vec p=0.5, q=2 on the symmetrized
+    R-MAT 2^20 graph, 4 walks per node, L=40).  Every one of the 167,772,160
+    steps follows its recorded edge (inside the row of the current node, and
+    col[e] is the next node) or stays, with edge id -1, at a node of
+    out-degree 0; and three blocks of 2,000 walks (start, middle and end of
+    the walk-id range, hence of the Philox counters) are bit-exact against the
+    oracle, nodes and edges."""
+    rowptr, col = synth.rmat_csr(20, 1 << 24, seed=0, device=cuda, symmetrize=True)
+    V, E = rowptr.numel() - 1, col.numel()
+    N, L = 4 * V, 40
+    start = torch.arange(N, device=cuda) % V
+    n, e = mc.rejection_sampling(rowptr, col, start, L, 0.5, 2.0, seed=3, return_edges=True)
+    assert torch.equal(n[:, 0], start)
+    bad = 0
+    for l in range(L):
+        u, v, el = n[:, l], n[:, l + 1], e[:, l]
+        rs, re = rowptr[u], rowptr[u + 1]
+        stay = (el == -1) & (re == rs) & (v == u)
+        move = (el >= rs) & (el < re) & (col[el.clamp(0, E - 1)] == v)
+        bad += int((~(stay | move)).sum())
+    assert bad == 0
+    rp, cl = rowptr.cpu().numpy(), col.cpu().numpy()
+    for s0 in (0, N // 2, N - 2000):
+        ref, ref_e, st, _ = oracle.node2vec_walk(rp, cl, start[s0:s0 + 2000].cpu().numpy(), L,
+                                                 0.5, 2.0, 3, rule=oracle.RULE_REF_CHAIN,
+                                                 rows_sorted=True, with_edges=True, first_walk=s0)
+        assert st == 0
+        np.testing.assert_array_equal(n[s0:s0 + 2000].cpu().numpy(), ref)
+        np.testing.assert_array_equal(e[s0:s0 + 2000].cpu().numpy(), ref_e)
