@@ -11,7 +11,7 @@ random gather: one 64-B line per dependent read, streams at their byte
 count) and a CPU baseline (the oracle's single-threaded restatement of the
 reference's eval_cpu loop, timed on a bounded sample of the same walks).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5|csr2|csr4|...]
 """
 from __future__ import annotations
 
@@ -51,6 +51,19 @@ CONFIGS = {
             dict(p=4.0, q=0.25, seed=5, rule="node2vec")),
 }
 RULE_ID = {"ref_chain": 0, "node2vec": 1}
+
+# CSR construction from an edge list (the step before the walk): name ->
+# (description, R-MAT scale, samples, symmetrize).  Both deduplicate, as the
+# walk configurations' graphs do.
+CSR_CONFIGS = {
+    "csr2": ("CSR build (sort + dedup) of R-MAT 2^20, 2^24 edge samples (the graph of c2)",
+             20, 1 << 24, False),
+    "csr3": ("CSR build (symmetrize + sort + dedup) of R-MAT 2^20, 2^24 edge samples "
+             "(the graph of c3)", 20, 1 << 24, True),
+    "csr4": ("CSR build (sort + dedup) of R-MAT 2^24, 2^28 edge samples (the graph of c4)",
+             24, 1 << 28, False),
+}
+CSR_METRIC = "CSR build: input edges/sec at 1 MI355X + achieved GB/s vs HBM roofline"
 
 
 def log(*a):
@@ -222,12 +235,162 @@ def cpu_baseline_node2vec(np, oracle, rowptr_h, col_h, start, L, extra, target_s
     return walks * L / dt, walks, dt
 
 
+def bench_csr(args, np, torch, mc, synth, dev):
+    """One line for a CSR_CONFIGS entry: mlxc_csr_build on an edge list
+    resident in HBM, preallocated outputs and workspace."""
+    import oracle
+    from mlx_cluster_amd import _lib
+    desc, scale, samples, sym = CSR_CONFIGS[args.config]
+    log(f"config {args.config}: {desc} on {torch.cuda.get_device_name(dev)}")
+    V = 1 << scale
+    row, col = synth.rmat_edges(scale, samples, seed=0, device=dev)
+    ei = torch.stack([row, col])
+    del row, col
+    E = ei.shape[1]
+    flags = _lib.MLXC_CSR_DEDUP | (_lib.MLXC_CSR_SYMMETRIZE if sym else 0)
+    total = 2 * E if sym else E
+    lib = _lib.load()
+    nbytes = lib.mlxc_csr_build_workspace_bytes(V, E, flags)
+    work = torch.empty((nbytes + 7) // 8, dtype=torch.int64, device=dev)
+    rowptr = torch.empty(V + 1, dtype=torch.int64, device=dev)
+    col_out = torch.empty(total, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    args_c = (ei[0].data_ptr(), ei[1].data_ptr(), E, V, flags, rowptr.data_ptr(),
+              col_out.data_ptr(), work.data_ptr(), nbytes, stream.cuda_stream)
+
+    def step():
+        rc = lib.mlxc_csr_build(*args_c)
+        if rc != 0:
+            raise RuntimeError(_lib.last_error())
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for ev0, ev1 in events:
+        ev0.record(stream)
+        step()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    event_ms = [a.elapsed_time(b) for a, b in events]
+    kernel_ms = float(np.mean(event_ms))
+    ms_per_step = wall / args.steps * 1e3
+    value = E / (ms_per_step / 1e3)
+    status, kept = (int(x) for x in work[:2].tolist())
+    assert status == 0
+    log(f"{ms_per_step:.3f} ms/step wall, {kernel_ms:.3f} ms/launch (events); "
+        f"E={E} -> {kept} entries")
+
+    # End to end through to_csr with fresh allocations (it synchronises once).
+    del work
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    t0 = time.perf_counter()
+    rp2, c2 = mc.to_csr(ei, V, symmetrize=sym, dedup=True)
+    torch.cuda.synchronize()
+    e2e_ms = (time.perf_counter() - t0) * 1e3
+    same = bool(torch.equal(rp2, rowptr) and torch.equal(c2, col_out[:kept]))
+    del rp2, c2
+
+    # The sort-based torch path this replaces (torch.unique of row*V+col,
+    # bincount, cumsum), timed as context; its result must be ours.
+    def torch_path():
+        r, c = ei[0], ei[1]
+        if sym:
+            r, c = torch.cat([r, c]), torch.cat([c, r])
+        key = torch.unique(r * V + c, sorted=True)
+        rr = key // V
+        rp = torch.zeros(V + 1, dtype=torch.int64, device=dev)
+        torch.cumsum(torch.bincount(rr, minlength=V), 0, out=rp[1:])
+        return rp, key - rr * V
+    torch_path()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    trp, tcol = torch_path()
+    torch.cuda.synchronize()
+    torch_ms = (time.perf_counter() - t0) * 1e3
+    full_equal = bool(torch.equal(trp, rowptr) and torch.equal(tcol, col_out[:kept]))
+    del trp, tcol
+
+    # Bit-exact parity of a prefix of the list against the oracle.
+    S = min(E, 1 << 22)
+    r_h, c_h = ei[0, :S].cpu().numpy(), ei[1, :S].cpu().numpy()
+    prp, pc = mc.to_csr(ei[:, :S], V, symmetrize=sym, dedup=True)
+    orp, oc = oracle.csr_build(r_h, c_h, V, symmetrize=sym, dedup=True)
+    parity = bool(np.array_equal(prp.cpu().numpy(), orp) and np.array_equal(pc.cpu().numpy(), oc))
+    del prp, pc
+
+    # Bytes: any CSR build reads the two id arrays and writes col and rowptr
+    # once.  The radix passes move more; their stream volume is reported too.
+    algo_bytes = 16 * E + 8 * kept + 8 * (V + 1)
+    cbits = (V - 1).bit_length()
+    k = 8 if 2 * cbits > 32 else 4
+    passes = max(1, -(-2 * cbits // 8))
+    tiles = -(-total // 4096)
+    pass_bytes = (total * (16 + 16 + k) + (passes - 1) * total * 3 * k
+                  + total * 2 * k + 8 * kept + 5 * 8 * (V + 1)
+                  + passes * 3 * 8 * 256 * tiles)
+    achieved = algo_bytes / (kernel_ms / 1e3) / 1e9
+    traffic = traffic_from_profile(f"csr_build_{args.config}")
+    roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
+                "algorithmic_bytes_per_launch": algo_bytes,
+                "bytes_formula": "16*E (row, col) + 8*E_out (col) + 8*(V+1) (rowptr)",
+                "kernel_ms": kernel_ms, "kernel_ms_median": float(np.median(event_ms)),
+                "e2e_ms_with_allocation": e2e_ms,
+                "kernel_ms_source": "HIP events around each call on its stream (mean; median beside it)",
+                "radix_passes": passes, "key_bytes": k,
+                "radix_stream_bytes_per_launch": pass_bytes,
+                "radix_stream_gbs": pass_bytes / (kernel_ms / 1e3) / 1e9,
+                "hbm_gbs_measured": (traffic / (kernel_ms / 1e3) / 1e9) if traffic else None}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        model, cores = host_info()
+        with one_core() as pin:
+            n = min(E, 1 << 20)
+            t0 = time.perf_counter()
+            oracle.csr_build(ei[0, :n].cpu().numpy(), ei[1, :n].cpu().numpy(), V,
+                             symmetrize=sym, dedup=True)
+            rate = n / (time.perf_counter() - t0)
+            n = int(min(E, max(n, args.cpu_seconds * rate)))
+            r_h, c_h = ei[0, :n].cpu().numpy(), ei[1, :n].cpu().numpy()
+            t0 = time.perf_counter()
+            oracle.csr_build(r_h, c_h, V, symmetrize=sym, dedup=True)
+            dt = time.perf_counter() - t0
+        cpu = {"value": n / dt, "unit": "edges/s", "cores": 1, "kind": "port",
+               "sample": f"first {n} of {E} edges, {dt:.1f} s, oracle.csr_build (numpy lexsort, "
+                         f"bincount, cumsum: the reference tests' pipeline), 1 thread pinned "
+                         f"to one core",
+               "host_cpu": model, "host_cores_available": cores, "pinned_core": pin.core}
+        log(f"cpu baseline {n / dt:.3e} edges/s over {n} edges")
+    line = {
+        "metric": CSR_METRIC, "value": value, "unit": "edges/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int64", "data": "synthetic",
+        "config": {"workload": f"{args.config}: {desc}", "num_nodes": V, "num_edges_in": E,
+                   "entries_sorted": total, "entries_out": kept,
+                   "parity_prefix_bit_exact": parity, "prefix_edges": S,
+                   "full_size_equals_torch_sort_path": full_equal,
+                   "to_csr_equals_abi_call": same},
+        "roofline": roofline, "cpu_baseline": cpu,
+        "torch_sort_path_ms": torch_ms,
+    }
+    if cpu:
+        line["speedup_vs_cpu_baseline"] = value / cpu["value"]
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS) + sorted(CSR_CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -262,6 +425,10 @@ def main():
 
     if args.gather_ceiling:
         print(json.dumps(gather_ceiling(torch, dev)), flush=True)
+        return
+
+    if args.config in CSR_CONFIGS:
+        bench_csr(args, np, torch, mc, synth, dev)
         return
 
     desc, kind, gargs, per_node, L, extra = CONFIGS[args.config]

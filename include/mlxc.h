@@ -66,6 +66,10 @@ extern "C" {
 #define MLXC_OUT_INT64 0
 #define MLXC_OUT_INT32 1
 
+/* flags of mlxc_csr_build. */
+#define MLXC_CSR_SYMMETRIZE 1 /* also add every reversed pair (col, row) */
+#define MLXC_CSR_DEDUP 2      /* keep one entry of each repeated (row, col) pair */
+
 /* Trial cap of one biased step (the reference loops without bound,
  * BiasedRandomWalk.cpp:80): after this many rejections the last candidate is
  * kept. */
@@ -182,6 +186,47 @@ int mlxc_csr_check(const int64_t* d_rowptr, int64_t num_nodes,
  * tensor (/root/reference/tests/test_random_walk.py:31).
  */
 int mlxc_philox_uniform(float* d_out, int64_t n, uint64_t seed, void* stream);
+
+/* Workspace bytes mlxc_csr_build needs (at least 16-byte aligned): two key
+ * arrays of 4 bytes per entry (8 when num_nodes > 65536), entries = num_edges,
+ * or 2 * num_edges with MLXC_CSR_SYMMETRIZE, plus 8 bytes per 16 entries of
+ * digit counts.  No reference counterpart. */
+size_t mlxc_csr_build_workspace_bytes(int64_t num_nodes, int64_t num_edges, int32_t flags);
+
+/*
+ * CSR of an edge list, built on the device: rows sorted by (row, col),
+ * rowptr over all num_nodes rows (rows without entries included).
+ * Replaces: the CSR pipeline of the reference tests,
+ *   /root/reference/tests/test_random_walk.py:23-28 (and
+ *   test_rejection_sampling.py:22-27): mlx_graphs 0.0.7 sort_edge_index
+ *   (lexicographic (row, col) order, duplicates kept), then rowptr =
+ *   [0, cumsum(np.unique(row, return_counts=True))], which drops rows
+ *   without entries; here rowptr always has num_nodes + 1 entries.
+ *
+ * d_row, d_col  int64 [num_edges]: entry i is the pair (row[i], col[i])
+ * num_nodes     V, at most 2^32; every id must lie in [0, V)
+ * flags         MLXC_CSR_SYMMETRIZE | MLXC_CSR_DEDUP (or 0)
+ * d_rowptr      int64 [V + 1]
+ * d_col_out     int64 [num_edges] (2 * num_edges with MLXC_CSR_SYMMETRIZE)
+ * d_workspace   mlxc_csr_build_workspace_bytes() bytes, 16-byte aligned.
+ *
+ * Asynchronous on `stream`.  After completion, workspace word 0 holds
+ * MLXC_STATUS_BAD_NODE if some id lay outside [0, V) (the output is then
+ * unspecified but every write stays inside the buffers), and word 1 the
+ * number of entries written to d_col_out (= d_rowptr[V]).
+ */
+int mlxc_csr_build(const int64_t* d_row, const int64_t* d_col, int64_t num_edges,
+                   int64_t num_nodes, int32_t flags, int64_t* d_rowptr, int64_t* d_col_out,
+                   void* d_workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Host twin of mlxc_csr_build: the same CSR from host arrays, on the calling
+ * thread.  *count receives the entries written to col_out, *status (may be
+ * NULL) the MLXC_STATUS_* bits.  No workspace.
+ */
+int mlxc_csr_build_cpu(const int64_t* row, const int64_t* col, int64_t num_edges,
+                       int64_t num_nodes, int32_t flags, int64_t* rowptr, int64_t* col_out,
+                       int64_t* count, int64_t* status);
 
 /*
  * Host twins of the three walk entry points: the same walks, the same

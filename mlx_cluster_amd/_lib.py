@@ -32,6 +32,8 @@ MLXC_CSR_BAD_COL = 2
 MLXC_CSR_UNSORTED = 4
 MLXC_OUT_INT64 = 0
 MLXC_OUT_INT32 = 1
+MLXC_CSR_SYMMETRIZE = 1
+MLXC_CSR_DEDUP = 2
 MLXC_MAX_TRIALS = 65536
 
 _i64 = ctypes.c_int64
@@ -62,6 +64,13 @@ SIGNATURES = {
     ),
     "mlxc_csr_check": (ctypes.c_int, [_ptr, _i64, _ptr, _i64, _ptr, _size, _ptr, _ptr]),
     "mlxc_philox_uniform": (ctypes.c_int, [_ptr, _i64, _u64, _ptr]),
+    "mlxc_csr_build_workspace_bytes": (_size, [_i64, _i64, _i32]),
+    "mlxc_csr_build": (
+        ctypes.c_int, [_ptr, _ptr, _i64, _i64, _i32, _ptr, _ptr, _ptr, _size, _ptr],
+    ),
+    "mlxc_csr_build_cpu": (
+        ctypes.c_int, [_ptr, _ptr, _i64, _i64, _i32, _ptr, _ptr, _ptr, _ptr],
+    ),
     "mlxc_random_walk_cpu": (
         ctypes.c_int,
         [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _i32, _i32, _ptr],

@@ -1,0 +1,549 @@
+// CSR construction on the device: the step before the walk.  The reference
+// tests build their CSR on the host (/root/reference/tests/
+// test_random_walk.py:23-28: mlx_graphs 0.0.7 sort_edge_index, then rowptr
+// from np.unique counts and a cumsum); this does the same on the GPU, with
+// rowptr over all num_nodes rows.
+//
+// Method: an LSD radix sort of packed keys (row << cbits | col), cbits =
+// bits(num_nodes - 1), sorting only the 2 * cbits bits that can be non-zero,
+// 8 bits per pass.  Keys are 32-bit when they fit (num_nodes <= 65536).  Each
+// pass is three launches and needs no inter-block waiting:
+//   radix_hist_kernel     per 4096-key tile, a 256-digit histogram, written
+//                         digit-major (hist[d * tiles + tile]);
+//   scan_*                one exclusive scan of that array, which turns it
+//                         into every (digit, tile)'s first output position;
+//   radix_scatter_kernel  stable rank of each key inside its tile (wavefront
+//                         match of the digit), reorder of the tile in LDS,
+//                         then stores in digit runs.
+// The first pass reads the caller's (row, col) arrays directly (and the
+// reversed pairs, for symmetrize); the last pass's keys go to csr_emit_kernel,
+// which writes col, marks row starts and, with dedup, drops repeated keys.
+// rowptr is filled with the entry count, row starts are written into it, and a
+// reverse inclusive min-scan gives empty rows the start of the next row.
+#include "walk_host.h"
+
+namespace mlxc {
+
+namespace {
+
+constexpr int kRadixBits = 8;
+constexpr int kRadix = 1 << kRadixBits;  // 256 digits, one per thread of a block
+constexpr int kItems = 16;               // keys per thread per tile
+constexpr int kTile = kBlock * kItems;   // 4096 keys per tile (and per scan chunk)
+constexpr int kWaveTile = kWave * kItems;
+constexpr int kWaves = kBlock / kWave;
+
+static_assert(kRadix == kBlock, "one digit per thread");
+
+constexpr int kOpSum = 0;
+constexpr int kOpMin = 1;
+
+struct EdgeSrc {
+    const int64_t* row;
+    const int64_t* col;
+    int64_t num_edges;  // entries of row / col (the list before symmetrizing)
+    int64_t num_nodes;
+    int cbits;          // bits of the col field of a key
+};
+
+// Key of entry i of the (optionally symmetrized) list: i < num_edges is
+// (row[i], col[i]); i >= num_edges the reversed pair of entry i - num_edges.
+// Ids outside [0, num_nodes) set `bad` and become 0, so that every index
+// derived from a key stays in bounds.
+template <typename KeyT>
+__device__ __forceinline__ KeyT src_key(const EdgeSrc& s, int64_t i, bool& bad) {
+    int64_t r, c;
+    if (i < s.num_edges) {
+        r = s.row[i];
+        c = s.col[i];
+    } else {
+        r = s.col[i - s.num_edges];
+        c = s.row[i - s.num_edges];
+    }
+    const bool ok = static_cast<uint64_t>(r) < static_cast<uint64_t>(s.num_nodes) &&
+                    static_cast<uint64_t>(c) < static_cast<uint64_t>(s.num_nodes);
+    if (!ok) {
+        bad = true;
+        r = 0;
+        c = 0;
+    }
+    return (static_cast<KeyT>(r) << s.cbits) | static_cast<KeyT>(c);
+}
+
+template <typename KeyT>
+__device__ __forceinline__ uint32_t digit_of(KeyT k, int shift) {
+    return static_cast<uint32_t>(k >> shift) & (kRadix - 1);
+}
+
+// Lanes of this wavefront that are active and hold the same digit d.
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, bool active) {
+    uint64_t peers = __ballot(active);
+#pragma unroll
+    for (int b = 0; b < kRadixBits; ++b) {
+        const bool bit = (d >> b) & 1u;
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+    }
+    return peers;
+}
+
+__device__ __forceinline__ bool is_leader(uint64_t peers) {
+    return __lane_id() == __ffsll(static_cast<long long>(peers)) - 1;
+}
+
+template <int kOp>
+__device__ __forceinline__ int64_t op_apply(int64_t a, int64_t b) {
+    return kOp == kOpSum ? a + b : (a < b ? a : b);
+}
+
+template <int kOp>
+__device__ __forceinline__ int64_t op_identity() {
+    return kOp == kOpSum ? 0 : INT64_MAX;
+}
+
+// Exclusive scan of one value per thread over the block, in thread order.
+// `wtot` is kWaves words of LDS.  Returns the exclusive prefix; *total (if
+// given) receives the block's reduction.  Contains two __syncthreads.
+template <int kOp>
+__device__ int64_t block_exclusive_scan(int64_t v, int64_t* wtot, int64_t* total = nullptr) {
+    const int lane = __lane_id();
+    const int w = threadIdx.x / kWave;
+    int64_t inc = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int64_t u = __shfl_up(inc, o, kWave);
+        if (lane >= o) inc = op_apply<kOp>(inc, u);
+    }
+    if (lane == kWave - 1) wtot[w] = inc;
+    __syncthreads();
+    int64_t before = op_identity<kOp>();
+    for (int k = 0; k < w; ++k) before = op_apply<kOp>(before, wtot[k]);
+    int64_t all = op_identity<kOp>();
+    for (int k = 0; k < kWaves; ++k) all = op_apply<kOp>(all, wtot[k]);
+    int64_t excl = __shfl_up(inc, 1, kWave);
+    if (lane == 0) excl = op_identity<kOp>();
+    if (total) *total = all;
+    __syncthreads();
+    return op_apply<kOp>(before, excl);
+}
+
+// ------------------------------------------------------------- radix pass
+
+template <typename KeyT, bool kFirst>
+__global__ __launch_bounds__(kBlock) void radix_hist_kernel(EdgeSrc src,
+                                                            const KeyT* __restrict__ keys,
+                                                            int shift, int64_t total,
+                                                            int64_t tiles,
+                                                            int64_t* __restrict__ hist,
+                                                            int64_t* __restrict__ work) {
+    __shared__ int32_t cnt[kWaves][kRadix];
+    const int t = threadIdx.x, w = t / kWave, lane = t % kWave;
+    for (int k = t; k < kWaves * kRadix; k += kBlock) (&cnt[0][0])[k] = 0;
+    __syncthreads();
+    const int64_t tile = blockIdx.x;
+    const int64_t base = tile * kTile + w * kWaveTile + lane;
+    bool bad = false;
+#pragma unroll 4
+    for (int s = 0; s < kItems; ++s) {
+        const int64_t i = base + static_cast<int64_t>(s) * kWave;
+        const bool active = i < total;
+        KeyT k = 0;
+        if (active) k = kFirst ? src_key<KeyT>(src, i, bad) : keys[i];
+        const uint32_t d = digit_of(k, shift);
+        const uint64_t peers = match_digit(d, active);
+        if (active && is_leader(peers)) cnt[w][d] += __popcll(peers);
+    }
+    __syncthreads();
+    hist[static_cast<int64_t>(t) * tiles + tile] = cnt[0][t] + cnt[1][t] + cnt[2][t] + cnt[3][t];
+    if (kFirst && bad)
+        atomicOr(reinterpret_cast<unsigned long long*>(work),
+                 static_cast<unsigned long long>(MLXC_STATUS_BAD_NODE));
+}
+
+template <typename KeyT, bool kFirst>
+__global__ __launch_bounds__(kBlock) void radix_scatter_kernel(EdgeSrc src,
+                                                               const KeyT* __restrict__ keys_in,
+                                                               KeyT* __restrict__ keys_out,
+                                                               int shift, int64_t total,
+                                                               int64_t tiles,
+                                                               const int64_t* __restrict__ offsets) {
+    __shared__ KeyT buf[kTile];
+    __shared__ int32_t cnt[kWaves][kRadix];
+    __shared__ int32_t first[kRadix];
+    __shared__ int64_t goff[kRadix];
+    __shared__ int64_t wtot[kWaves];
+    const int t = threadIdx.x, w = t / kWave, lane = t % kWave;
+    const int64_t tile = blockIdx.x;
+    for (int k = t; k < kWaves * kRadix; k += kBlock) (&cnt[0][0])[k] = 0;
+    goff[t] = offsets[static_cast<int64_t>(t) * tiles + tile];
+    __syncthreads();
+
+    // Rank of every key among the keys of its digit that come before it in
+    // this tile's order (wavefront, then slot, then lane): stable.
+    const int64_t base = tile * kTile + w * kWaveTile + lane;
+    KeyT key[kItems];
+    int32_t pos[kItems];
+    bool bad = false;
+#pragma unroll
+    for (int s = 0; s < kItems; ++s) {
+        const int64_t i = base + static_cast<int64_t>(s) * kWave;
+        const bool active = i < total;
+        KeyT k = 0;
+        if (active) k = kFirst ? src_key<KeyT>(src, i, bad) : keys_in[i];
+        key[s] = k;
+        const uint32_t d = digit_of(k, shift);
+        const uint64_t peers = match_digit(d, active);
+        const int32_t before = cnt[w][d];
+        pos[s] = before + lane_rank(peers);
+        if (active && is_leader(peers)) cnt[w][d] = before + __popcll(peers);
+    }
+    __syncthreads();
+
+    // Thread t owns digit t: its first position in the reordered tile, and
+    // the first position of each wavefront's keys of that digit.
+    const int32_t c0 = cnt[0][t], c1 = cnt[1][t], c2 = cnt[2][t];
+    const int32_t tot = c0 + c1 + c2 + cnt[3][t];
+    const int32_t at = static_cast<int32_t>(block_exclusive_scan<kOpSum>(tot, wtot));
+    first[t] = at;
+    cnt[0][t] = at;
+    cnt[1][t] = at + c0;
+    cnt[2][t] = at + c0 + c1;
+    cnt[3][t] = at + c0 + c1 + c2;
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < kItems; ++s) {
+        const int64_t i = base + static_cast<int64_t>(s) * kWave;
+        if (i < total) buf[cnt[w][digit_of(key[s], shift)] + pos[s]] = key[s];
+    }
+    __syncthreads();
+
+    // Consecutive entries of one digit go to consecutive output positions.
+    const int64_t left = total - tile * kTile;
+    const int n = left < kTile ? static_cast<int>(left) : kTile;
+    for (int j = t; j < n; j += kBlock) {
+        const KeyT k = buf[j];
+        const uint32_t d = digit_of(k, shift);
+        keys_out[goff[d] + (j - first[d])] = k;
+    }
+}
+
+// ------------------------------------------------------------- device scan
+// In place over n int64 values, chunks of kTile per block.  kRev scans from
+// the end (logical element j is data[n - 1 - j]).
+
+template <int kOp, bool kRev>
+__device__ __forceinline__ int64_t scan_load(const int64_t* data, int64_t n, int64_t j) {
+    if (j >= n) return op_identity<kOp>();
+    return data[kRev ? n - 1 - j : j];
+}
+
+template <int kOp, bool kRev>
+__global__ __launch_bounds__(kBlock) void scan_reduce_kernel(const int64_t* __restrict__ data,
+                                                             int64_t n,
+                                                             int64_t* __restrict__ sums) {
+    __shared__ int64_t wtot[kWaves];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+    int64_t acc = op_identity<kOp>();
+    for (int s = 0; s < kItems; ++s)
+        acc = op_apply<kOp>(acc, scan_load<kOp, kRev>(data, n, base + s * kBlock + threadIdx.x));
+    int64_t total;
+    block_exclusive_scan<kOp>(acc, wtot, &total);
+    if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+// One block: sums[b] <- reduction of sums[0..b) (exclusive); *total_out (if
+// given) <- reduction of all nb values.
+template <int kOp>
+__global__ __launch_bounds__(kBlock) void scan_top_kernel(int64_t* __restrict__ sums, int64_t nb,
+                                                          int64_t* __restrict__ total_out) {
+    __shared__ int64_t wtot[kWaves];
+    int64_t carry = op_identity<kOp>();
+    for (int64_t base = 0; base < nb; base += kBlock) {
+        const int64_t j = base + threadIdx.x;
+        const int64_t v = j < nb ? sums[j] : op_identity<kOp>();
+        int64_t total;
+        const int64_t ex = block_exclusive_scan<kOp>(v, wtot, &total);
+        if (j < nb) sums[j] = op_apply<kOp>(carry, ex);
+        carry = op_apply<kOp>(carry, total);
+    }
+    if (total_out && threadIdx.x == 0) *total_out = carry;
+}
+
+template <int kOp, bool kRev, bool kExcl>
+__global__ __launch_bounds__(kBlock) void scan_down_kernel(int64_t* __restrict__ data, int64_t n,
+                                                           const int64_t* __restrict__ sums) {
+    // Padded so that thread t's 16 consecutive values sit in distinct banks.
+    __shared__ int64_t vals[kTile + kTile / kItems];
+    __shared__ int64_t wtot[kWaves];
+    const int t = threadIdx.x;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+    auto slot = [](int j) { return j + j / kItems; };
+    for (int s = 0; s < kItems; ++s) {
+        const int j = s * kBlock + t;
+        vals[slot(j)] = scan_load<kOp, kRev>(data, n, base + j);
+    }
+    __syncthreads();
+    int64_t run = op_identity<kOp>();
+    for (int s = 0; s < kItems; ++s) run = op_apply<kOp>(run, vals[slot(t * kItems + s)]);
+    int64_t acc = op_apply<kOp>(sums[blockIdx.x], block_exclusive_scan<kOp>(run, wtot));
+    for (int s = 0; s < kItems; ++s) {
+        const int j = slot(t * kItems + s);
+        const int64_t v = vals[j];
+        if (kExcl) {
+            vals[j] = acc;
+            acc = op_apply<kOp>(acc, v);
+        } else {
+            acc = op_apply<kOp>(acc, v);
+            vals[j] = acc;
+        }
+    }
+    __syncthreads();
+    for (int s = 0; s < kItems; ++s) {
+        const int64_t j = base + s * kBlock + t;
+        if (j < n) data[kRev ? n - 1 - j : j] = vals[slot(s * kBlock + t)];
+    }
+}
+
+// ------------------------------------------------------------- finish
+
+__global__ void fill_words_kernel(int64_t* __restrict__ out, int64_t n,
+                                  const int64_t* __restrict__ value) {
+    const int64_t v = *value;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        out[i] = v;
+}
+
+__global__ void set_word_kernel(int64_t* __restrict__ word, int64_t v) {
+    if (threadIdx.x == 0) *word = v;
+}
+
+// Entry i of the sorted keys is kept unless dedup is on and it repeats
+// entry i - 1.
+template <typename KeyT, bool kDedup>
+__device__ __forceinline__ bool kept(const KeyT* __restrict__ keys, int64_t i, KeyT k) {
+    return !kDedup || i == 0 || keys[i - 1] != k;
+}
+
+// sums[chunk] <- kept entries of chunk (kTile entries).
+template <typename KeyT>
+__global__ __launch_bounds__(kBlock) void dedup_count_kernel(const KeyT* __restrict__ keys,
+                                                             int64_t total,
+                                                             int64_t* __restrict__ sums) {
+    __shared__ int64_t wtot[kWaves];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+    int64_t c = 0;
+    for (int s = 0; s < kItems; ++s) {
+        const int64_t i = base + s * kBlock + threadIdx.x;
+        if (i < total) c += kept<KeyT, true>(keys, i, keys[i]);
+    }
+    int64_t all;
+    block_exclusive_scan<kOpSum>(c, wtot, &all);
+    if (threadIdx.x == 0) sums[blockIdx.x] = all;
+}
+
+// Writes col[p] for every kept entry (p = its rank among kept entries) and
+// rowptr[row] = p at the first entry of each row present.  kDedup: the
+// chunk's first p comes from sums (exclusive scan of dedup_count_kernel).
+template <typename KeyT, bool kDedup>
+__global__ __launch_bounds__(kBlock) void csr_emit_kernel(const KeyT* __restrict__ keys,
+                                                          int64_t total, int cbits,
+                                                          const int64_t* __restrict__ sums,
+                                                          int64_t* __restrict__ rowptr,
+                                                          int64_t* __restrict__ col_out) {
+    __shared__ int32_t wkept[kItems][kWaves];
+    const int t = threadIdx.x, w = t / kWave;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+    const KeyT cmask = cbits == 0 ? KeyT(0) : (~KeyT(0) >> (8 * sizeof(KeyT) - cbits));
+    KeyT key[kItems];
+    uint32_t keep_bits = 0, start_bits = 0;
+#pragma unroll
+    for (int s = 0; s < kItems; ++s) {
+        const int64_t i = base + s * kBlock + t;
+        const bool valid = i < total;
+        KeyT k = 0, prev = 0;
+        if (valid) {
+            k = keys[i];
+            if (i > 0) prev = keys[i - 1];
+        }
+        key[s] = k;
+        const bool keep = valid && (!kDedup || i == 0 || prev != k);
+        const bool row_start = valid && (i == 0 || (prev >> cbits) != (k >> cbits));
+        keep_bits |= static_cast<uint32_t>(keep) << s;
+        start_bits |= static_cast<uint32_t>(row_start) << s;
+        if (kDedup) {
+            const uint64_t m = __ballot(keep);
+            if (__lane_id() == 0) wkept[s][w] = __popcll(m);
+        }
+    }
+    int64_t p0 = base;
+    if (kDedup) {
+        __syncthreads();
+        p0 = sums[blockIdx.x];
+        // entries before slot 0 of this wavefront: earlier wavefronts of slot 0
+        for (int k = 0; k < w; ++k) p0 += wkept[0][k];
+    }
+#pragma unroll
+    for (int s = 0; s < kItems; ++s) {
+        int64_t p;
+        if (kDedup) {
+            const bool keep = (keep_bits >> s) & 1u;
+            p = p0 + lane_rank(__ballot(keep));
+            // advance p0 to slot s + 1 of this wavefront: the rest of slot s
+            // (this and later wavefronts), then earlier wavefronts of s + 1
+            for (int k = w; k < kWaves; ++k) p0 += wkept[s][k];
+            if (s + 1 < kItems)
+                for (int k = 0; k < w; ++k) p0 += wkept[s + 1][k];
+        } else {
+            p = base + s * kBlock + t;
+        }
+        if ((keep_bits >> s) & 1u) {
+            const KeyT k = key[s];
+            col_out[p] = static_cast<int64_t>(k & cmask);
+            if ((start_bits >> s) & 1u) rowptr[static_cast<int64_t>(k >> cbits)] = p;
+        }
+    }
+}
+
+// ------------------------------------------------------------- host side
+
+int bits_for(int64_t num_nodes) {
+    int b = 0;
+    for (uint64_t x = num_nodes > 1 ? static_cast<uint64_t>(num_nodes - 1) : 0; x; x >>= 1) ++b;
+    return b;
+}
+
+size_t round256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+struct CsrLayout {
+    int64_t total = 0;  // entries to sort
+    int cbits = 0;
+    int passes = 0;
+    bool wide = false;  // 64-bit keys
+    int64_t tiles = 0;
+    size_t keys0 = 0, keys1 = 0, hist = 0, sums = 0, bytes = 0;
+};
+
+CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
+    CsrLayout l;
+    l.total = (flags & MLXC_CSR_SYMMETRIZE) ? 2 * num_edges : num_edges;
+    l.cbits = bits_for(num_nodes);
+    const int key_bits = 2 * l.cbits;
+    l.wide = key_bits > 32;
+    l.passes = key_bits == 0 ? 1 : (key_bits + kRadixBits - 1) / kRadixBits;
+    l.tiles = (l.total + kTile - 1) / kTile;
+    const size_t ksz = l.wide ? 8 : 4;
+    int64_t scan_n = kRadix * l.tiles;
+    if (num_nodes + 1 > scan_n) scan_n = num_nodes + 1;
+    if (l.total > scan_n) scan_n = l.total;
+    const int64_t chunks = (scan_n + kTile - 1) / kTile;
+    size_t at = round256(MLXC_WORK_WORDS * sizeof(int64_t));
+    l.keys0 = at;
+    at += round256(static_cast<size_t>(l.total) * ksz);
+    l.keys1 = at;
+    at += round256(static_cast<size_t>(l.total) * ksz);
+    l.hist = at;
+    at += round256(static_cast<size_t>(kRadix) * l.tiles * sizeof(int64_t));
+    l.sums = at;
+    at += round256(static_cast<size_t>(chunks + 1) * sizeof(int64_t));
+    l.bytes = at;
+    return l;
+}
+
+template <int kOp, bool kRev, bool kExcl>
+int device_scan(int64_t* data, int64_t n, int64_t* sums, int64_t* total_out, hipStream_t s) {
+    if (n <= 0) return MLXC_OK;
+    const int64_t chunks = (n + kTile - 1) / kTile;
+    hipLaunchKernelGGL((scan_reduce_kernel<kOp, kRev>), dim3(chunks), dim3(kBlock), 0, s, data, n,
+                       sums);
+    hipLaunchKernelGGL((scan_top_kernel<kOp>), dim3(1), dim3(kBlock), 0, s, sums, chunks,
+                       total_out);
+    hipLaunchKernelGGL((scan_down_kernel<kOp, kRev, kExcl>), dim3(chunks), dim3(kBlock), 0, s,
+                       data, n, sums);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int fill_words(int64_t* out, int64_t n, const int64_t* value, hipStream_t s) {
+    int grid = 0;
+    if (int rc = stream_grid(n, 8, grid)) return rc;
+    hipLaunchKernelGGL(fill_words_kernel, dim3(grid), dim3(kBlock), 0, s, out, n, value);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+template <typename KeyT>
+int csr_build_typed(const EdgeSrc& src, const CsrLayout& l, int32_t flags, int64_t* rowptr,
+                    int64_t* col_out, char* ws, hipStream_t s) {
+    int64_t* work = reinterpret_cast<int64_t*>(ws);
+    KeyT* buf[2] = {reinterpret_cast<KeyT*>(ws + l.keys0), reinterpret_cast<KeyT*>(ws + l.keys1)};
+    int64_t* hist = reinterpret_cast<int64_t*>(ws + l.hist);
+    int64_t* sums = reinterpret_cast<int64_t*>(ws + l.sums);
+    const KeyT* in = nullptr;
+    for (int p = 0; p < l.passes; ++p) {
+        const int shift = p * kRadixBits;
+        KeyT* out = buf[p & 1];
+        if (p == 0)
+            hipLaunchKernelGGL((radix_hist_kernel<KeyT, true>), dim3(l.tiles), dim3(kBlock), 0, s,
+                               src, in, shift, l.total, l.tiles, hist, work);
+        else
+            hipLaunchKernelGGL((radix_hist_kernel<KeyT, false>), dim3(l.tiles), dim3(kBlock), 0, s,
+                               src, in, shift, l.total, l.tiles, hist, work);
+        MLXC_HIP_TRY(hipGetLastError());
+        if (int rc = device_scan<kOpSum, false, true>(hist, kRadix * l.tiles, sums, nullptr, s))
+            return rc;
+        if (p == 0)
+            hipLaunchKernelGGL((radix_scatter_kernel<KeyT, true>), dim3(l.tiles), dim3(kBlock), 0,
+                               s, src, in, out, shift, l.total, l.tiles, hist);
+        else
+            hipLaunchKernelGGL((radix_scatter_kernel<KeyT, false>), dim3(l.tiles), dim3(kBlock), 0,
+                               s, src, in, out, shift, l.total, l.tiles, hist);
+        MLXC_HIP_TRY(hipGetLastError());
+        in = out;
+    }
+    // work[1] <- entries kept; rowptr <- that count everywhere, then the row
+    // starts, then the reverse min-scan.
+    const int64_t chunks = l.tiles;
+    if (flags & MLXC_CSR_DEDUP) {
+        hipLaunchKernelGGL((dedup_count_kernel<KeyT>), dim3(chunks), dim3(kBlock), 0, s, in,
+                           l.total, sums);
+        hipLaunchKernelGGL((scan_top_kernel<kOpSum>), dim3(1), dim3(kBlock), 0, s, sums, chunks,
+                           work + 1);
+    } else {
+        hipLaunchKernelGGL(set_word_kernel, dim3(1), dim3(kWave), 0, s, work + 1, l.total);
+    }
+    MLXC_HIP_TRY(hipGetLastError());
+    if (int rc = fill_words(rowptr, src.num_nodes + 1, work + 1, s)) return rc;
+    if (flags & MLXC_CSR_DEDUP)
+        hipLaunchKernelGGL((csr_emit_kernel<KeyT, true>), dim3(chunks), dim3(kBlock), 0, s, in,
+                           l.total, l.cbits, sums, rowptr, col_out);
+    else
+        hipLaunchKernelGGL((csr_emit_kernel<KeyT, false>), dim3(chunks), dim3(kBlock), 0, s, in,
+                           l.total, l.cbits, sums, rowptr, col_out);
+    MLXC_HIP_TRY(hipGetLastError());
+    return device_scan<kOpMin, true, false>(rowptr, src.num_nodes + 1, sums, nullptr, s);
+}
+
+}  // namespace
+
+size_t csr_build_workspace_bytes(int64_t num_nodes, int64_t num_edges, int32_t flags) {
+    return csr_layout(num_nodes, num_edges, flags).bytes;
+}
+
+int launch_csr_build(const int64_t* row, const int64_t* col, int64_t num_edges, int64_t num_nodes,
+                     int32_t flags, int64_t* rowptr, int64_t* col_out, void* workspace,
+                     size_t workspace_bytes, hipStream_t stream) {
+    const CsrLayout l = csr_layout(num_nodes, num_edges, flags);
+    if (workspace_bytes < l.bytes)
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "workspace smaller than mlxc_csr_build_workspace_bytes()");
+    char* ws = static_cast<char*>(workspace);
+    int64_t* work = reinterpret_cast<int64_t*>(ws);
+    if (int rc = launch_zero_work(work, stream)) return rc;
+    if (l.total == 0) return fill_words(rowptr, num_nodes + 1, work + 1, stream);
+    const EdgeSrc src{row, col, num_edges, num_nodes, l.cbits};
+    return l.wide ? csr_build_typed<uint64_t>(src, l, flags, rowptr, col_out, ws, stream)
+                  : csr_build_typed<uint32_t>(src, l, flags, rowptr, col_out, ws, stream);
+}
+
+}  // namespace mlxc

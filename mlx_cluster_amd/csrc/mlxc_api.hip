@@ -108,6 +108,23 @@ int n2v_params(double p, double q, uint64_t seed, int32_t rule, int32_t rows, N2
     return MLXC_OK;
 }
 
+// Arguments of mlxc_csr_build and its host twin.
+int check_csr_build(const int64_t* row, const int64_t* col, int64_t num_edges, int64_t num_nodes,
+                    int32_t flags, const int64_t* rowptr, const int64_t* col_out) {
+    if (num_edges < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_edges must be >= 0");
+    if (num_nodes < 0 || num_nodes > (int64_t(1) << 32))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "num_nodes must lie in [0, 2^32]");
+    if (flags & ~(MLXC_CSR_SYMMETRIZE | MLXC_CSR_DEDUP))
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "flags must be a combination of MLXC_CSR_SYMMETRIZE and MLXC_CSR_DEDUP");
+    if (num_edges > (INT64_MAX / 64))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "num_edges too large");
+    if (!rowptr) return fail(MLXC_ERR_INVALID_ARGUMENT, "rowptr must not be NULL");
+    if (num_edges > 0 && (!row || !col || !col_out))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "row, col and col_out must not be NULL");
+    return MLXC_OK;
+}
+
 HostWalk host_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                    int64_t num_edges, const int64_t* start, int64_t num_walks, const float* rand,
                    int32_t walk_length, uint64_t seed, void* n_out, void* e_out,
@@ -221,6 +238,35 @@ int mlxc_philox_uniform(float* d_out, int64_t n, uint64_t seed, void* stream) {
     if (n == 0) return MLXC_OK;
     if (!d_out) return fail(MLXC_ERR_INVALID_ARGUMENT, "out must not be NULL");
     return launch_philox_fill(d_out, n, seed, static_cast<hipStream_t>(stream));
+}
+
+size_t mlxc_csr_build_workspace_bytes(int64_t num_nodes, int64_t num_edges, int32_t flags) {
+    if (num_nodes < 0 || num_edges < 0 || num_edges > INT64_MAX / 64) return 0;
+    return csr_build_workspace_bytes(num_nodes, num_edges, flags);
+}
+
+int mlxc_csr_build(const int64_t* d_row, const int64_t* d_col, int64_t num_edges,
+                   int64_t num_nodes, int32_t flags, int64_t* d_rowptr, int64_t* d_col_out,
+                   void* d_workspace, size_t workspace_bytes, void* stream) {
+    if (int rc = check_csr_build(d_row, d_col, num_edges, num_nodes, flags, d_rowptr, d_col_out))
+        return rc;
+    if (int rc = check_workspace(d_workspace, workspace_bytes)) return rc;
+    return launch_csr_build(d_row, d_col, num_edges, num_nodes, flags, d_rowptr, d_col_out,
+                            d_workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int mlxc_csr_build_cpu(const int64_t* row, const int64_t* col, int64_t num_edges,
+                       int64_t num_nodes, int32_t flags, int64_t* rowptr, int64_t* col_out,
+                       int64_t* count, int64_t* status) {
+    if (int rc = check_csr_build(row, col, num_edges, num_nodes, flags, rowptr, col_out))
+        return rc;
+    if (!count) return fail(MLXC_ERR_INVALID_ARGUMENT, "count must not be NULL");
+    uint32_t bits = 0;
+    int64_t n = 0;
+    const int rc = host_csr_build(row, col, num_edges, num_nodes, flags, rowptr, col_out, n, bits);
+    *count = n;
+    if (status) *status = bits;
+    return rc;
 }
 
 int mlxc_random_walk_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,

@@ -94,6 +94,12 @@ size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t nu
 int launch_node2vec(const WalkArgs& a, const N2VParams& p, void* workspace,
                     size_t workspace_bytes, hipStream_t stream);
 
+// ---- csr_build.hip
+size_t csr_build_workspace_bytes(int64_t num_nodes, int64_t num_edges, int32_t flags);
+int launch_csr_build(const int64_t* row, const int64_t* col, int64_t num_edges, int64_t num_nodes,
+                     int32_t flags, int64_t* rowptr, int64_t* col_out, void* workspace,
+                     size_t workspace_bytes, hipStream_t stream);
+
 // ---- host_walk.cpp (host pointers; the same walks on CPU threads)
 struct HostWalk {
     const int64_t* rowptr;
@@ -109,5 +115,9 @@ struct HostWalk {
 // threads <= 0: one per hardware thread.  status receives MLXC_STATUS_* bits.
 int host_uniform(const HostWalk& w, bool generate, int32_t threads, uint32_t& status);
 int host_node2vec(const HostWalk& w, const N2VParams& p, int32_t threads, uint32_t& status);
+// The CSR of mlxc_csr_build from host arrays.
+int host_csr_build(const int64_t* row, const int64_t* col, int64_t num_edges, int64_t num_nodes,
+                   int32_t flags, int64_t* rowptr, int64_t* col_out, int64_t& count,
+                   uint32_t& status);
 
 }  // namespace mlxc

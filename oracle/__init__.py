@@ -7,6 +7,7 @@ the product (mlx_cluster_amd) never imports it.
 Functions follow the reference's CPU evaluation:
   uniform_walk   -> /root/reference/random_walks/RandomWalk.cpp:41-60
   node2vec_walk  -> /root/reference/random_walks/BiasedRandomWalk.cpp:20-28,52-100
+  csr_build      -> /root/reference/tests/test_random_walk.py:23-28 (numpy)
 """
 from __future__ import annotations
 
@@ -162,3 +163,32 @@ def node2vec_walk_libc(rowptr, col, start, walk_length, p, q, libc_seed, *,
 def csr_flags(rowptr, col) -> int:
     rowptr, col = _i64(rowptr), _i64(col)
     return int(_load().oracle_csr_flags(_p(rowptr), rowptr.size - 1, _p(col), col.size))
+
+
+def csr_build(row, col, num_nodes: int, *, symmetrize: bool = False, dedup: bool = False):
+    """(rowptr, col) of an edge list, restating the reference tests' pipeline.
+
+    /root/reference/tests/test_random_walk.py:23-28 (and
+    test_rejection_sampling.py:22-27) sort the edge index with mlx_graphs
+    0.0.7 ``sort_edge_index`` (a dependency absent here; it orders the pairs
+    lexicographically by (row, col) and keeps duplicates), then take
+    ``rowptr = [0, cumsum(np.unique(row, return_counts=True)[1])]``.  That
+    rowptr has no entry for a node without out-edges (and is then not a CSR
+    of num_nodes rows); here the counts are ``np.bincount(row,
+    minlength=num_nodes)``, which equals the np.unique counts whenever every
+    node has an out-edge.  symmetrize appends the reversed pairs first, dedup
+    keeps one of each repeated pair.
+    """
+    row = np.asarray(row, dtype=np.int64).reshape(-1)
+    col = np.asarray(col, dtype=np.int64).reshape(-1)
+    if symmetrize:
+        row, col = np.concatenate([row, col]), np.concatenate([col, row])
+    order = np.lexsort((col, row))
+    row, col = row[order], col[order]
+    if dedup and row.size:
+        keep = np.ones(row.size, dtype=bool)
+        keep[1:] = (row[1:] != row[:-1]) | (col[1:] != col[:-1])
+        row, col = row[keep], col[keep]
+    rowptr = np.zeros(num_nodes + 1, dtype=np.int64)
+    np.cumsum(np.bincount(row, minlength=num_nodes), out=rowptr[1:])
+    return rowptr, col

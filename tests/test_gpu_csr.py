@@ -1,0 +1,139 @@
+"""Parity of the HIP CSR build (mlxc_csr_build, via to_csr on a GPU) with the
+oracle's restatement of the reference tests' pipeline
+(tests/test_random_walk.py:23-28): bit-exact rowptr and col."""
+import numpy as np
+import pytest
+import torch
+
+import mlx_cluster_amd as mc
+import oracle
+from mlx_cluster_amd import _lib, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def assert_parity(row, col, V, cuda, symmetrize=False, dedup=False):
+    row, col = np.asarray(row, np.int64), np.asarray(col, np.int64)
+    ei = torch.from_numpy(np.stack([row, col])).to(cuda)
+    rowptr, c = mc.to_csr(ei, V, symmetrize=symmetrize, dedup=dedup)
+    assert rowptr.is_cuda and c.is_cuda
+    ref_rowptr, ref_col = oracle.csr_build(row, col, V, symmetrize=symmetrize, dedup=dedup)
+    np.testing.assert_array_equal(rowptr.cpu().numpy(), ref_rowptr)
+    np.testing.assert_array_equal(c.cpu().numpy(), ref_col)
+
+
+def test_hand_case(cuda):
+    row, col = [3, 0, 0, 3, 0], [0, 2, 1, 1, 2]
+    for sym in (False, True):
+        for dedup in (False, True):
+            assert_parity(row, col, 5, cuda, sym, dedup)
+
+
+def test_empty_and_single_node(cuda):
+    for V in (0, 1, 5):
+        rowptr, c = mc.to_csr(torch.zeros((2, 0), dtype=torch.int64, device=cuda), V)
+        assert rowptr.tolist() == [0] * (V + 1) and c.numel() == 0
+    # one node: every key is 0 (no key bits at all)
+    assert_parity([0] * 9000, [0] * 9000, 1, cuda)
+    assert_parity([0] * 9000, [0] * 9000, 1, cuda, symmetrize=True, dedup=True)
+
+
+@pytest.mark.parametrize("E", [1, 63, 4095, 4096, 4097, 3 * 4096 + 5, 100_003])
+@pytest.mark.parametrize("V", [2, 255, 257, 65536, 65537, 3_000_001])
+def test_random_lists(E, V, cuda):
+    """Tile-ragged sizes; 32-bit keys (V <= 65536) and 64-bit keys."""
+    rng = np.random.default_rng(E * 7 + V)
+    row, col = rng.integers(0, V, E), rng.integers(0, V, E)
+    assert_parity(row, col, V, cuda)
+    assert_parity(row, col, V, cuda, symmetrize=True, dedup=True)
+
+
+@pytest.mark.parametrize("sym,dedup", [(False, False), (False, True), (True, False),
+                                       (True, True)])
+def test_skewed_with_duplicates(sym, dedup, cuda):
+    """A hub row holding most entries, long runs of one digit and repeated
+    pairs crossing tile boundaries."""
+    rng = np.random.default_rng(11)
+    V, E = 40_000, 70_000
+    row, col = rng.integers(0, V, E), rng.integers(0, V, E)
+    row[:50_000] = 17
+    col[10_000:30_000] = 3
+    col[30_000:34_000] = rng.integers(0, 4, 4000)
+    assert_parity(row, col, V, cuda, sym, dedup)
+
+
+def test_rmat_2_20(cuda):
+    """The generator of configurations 2 and 3: R-MAT 2^20, 2^24 samples."""
+    row, col = synth.rmat_edges(20, 1 << 24, seed=0, device=cuda)
+    r, c = row.cpu().numpy(), col.cpu().numpy()
+    for sym, dedup in ((False, True), (True, True), (False, False)):
+        rowptr, cc = mc.to_csr(torch.stack([row, col]), 1 << 20, symmetrize=sym, dedup=dedup)
+        ref_rowptr, ref_col = oracle.csr_build(r, c, 1 << 20, symmetrize=sym, dedup=dedup)
+        np.testing.assert_array_equal(rowptr.cpu().numpy(), ref_rowptr)
+        np.testing.assert_array_equal(cc.cpu().numpy(), ref_col)
+
+
+def test_ids_out_of_range_raise(cuda):
+    for row, col in (([0, 5], [1, 1]), ([0, 1], [-1, 1]), ([0, 2**40], [1, 1])):
+        ei = torch.tensor([row, col], dtype=torch.int64, device=cuda)
+        with pytest.raises(ValueError, match="outside"):
+            mc.to_csr(ei, 3)
+        with pytest.raises(ValueError, match="outside"):
+            mc.to_csr(ei, 3, symmetrize=True, dedup=True)
+    # the device stays usable afterwards
+    assert_parity([2, 0, 1], [0, 2, 2], 3, cuda)
+
+
+def test_side_stream_and_host_twin(cuda):
+    rng = np.random.default_rng(5)
+    V, E = 100_000, 250_000
+    ei = torch.from_numpy(rng.integers(0, V, (2, E))).to(cuda)
+    s = torch.cuda.Stream(device=cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(s):
+        rowptr, col = mc.to_csr(ei, V, symmetrize=True, dedup=True, stream=s)
+    s.synchronize()
+    hrowptr, hcol = mc.to_csr(ei.cpu(), V, symmetrize=True, dedup=True)
+    assert torch.equal(rowptr.cpu(), hrowptr) and torch.equal(col.cpu(), hcol)
+
+
+def test_abi_status_words(cuda):
+    """Workspace word 0 = status bits, word 1 = entries written."""
+    lib = _lib.load()
+    row = torch.tensor([1, 1, 0, 1], dtype=torch.int64, device=cuda)
+    col = torch.tensor([0, 0, 1, 0], dtype=torch.int64, device=cuda)
+    rowptr = torch.empty(3, dtype=torch.int64, device=cuda)
+    out = torch.empty(4, dtype=torch.int64, device=cuda)
+    nbytes = lib.mlxc_csr_build_workspace_bytes(2, 4, _lib.MLXC_CSR_DEDUP)
+    work = torch.full(((nbytes + 7) // 8,), -1, dtype=torch.int64, device=cuda)
+    rc = lib.mlxc_csr_build(row.data_ptr(), col.data_ptr(), 4, 2, _lib.MLXC_CSR_DEDUP,
+                            rowptr.data_ptr(), out.data_ptr(), work.data_ptr(), nbytes,
+                            torch.cuda.current_stream(cuda).cuda_stream)
+    assert rc == 0
+    assert work[:2].tolist() == [0, 2]
+    assert rowptr.tolist() == [0, 1, 2] and out[:2].tolist() == [1, 0]
+
+
+def test_c4_full_size_properties(cuda):
+    """Configuration 4's edge list (R-MAT 2^24, 2^28 samples, 64-bit keys,
+    six radix passes) at full size, against an independent device result
+    instead of the oracle: the sorted unique keys row * V + col of the input
+    (torch.unique).  rowptr must equal their cumulative row counts (torch
+    bincount) and the (row, col) sequence must equal them entry for entry,
+    hence sorted and free of repeats."""
+    V = 1 << 24
+    row, col = synth.rmat_edges(24, 1 << 28, seed=0, device=cuda)
+    rowptr, c = mc.to_csr(torch.stack([row, col]), V, dedup=True)
+    del row, col
+    row, col = synth.rmat_edges(24, 1 << 28, seed=0, device=cuda)
+    key = torch.unique(row * V + col)
+    del row, col
+    assert rowptr[-1].item() == c.numel() == key.numel()
+    urow = key // V
+    expect = torch.zeros(V + 1, dtype=torch.int64, device=cuda)
+    torch.cumsum(torch.bincount(urow, minlength=V), 0, out=expect[1:])
+    assert torch.equal(rowptr, expect)
+    out_row = torch.repeat_interleave(torch.arange(V, device=cuda), rowptr.diff())
+    out_key = out_row * V + c
+    assert bool((out_key[1:] > out_key[:-1]).all())
+    assert torch.equal(out_key, key)

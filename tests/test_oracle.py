@@ -402,3 +402,54 @@ def test_csr_flags():
     assert oracle.csr_flags(rowptr, np.array([1, 9, 1])) == 2         # col out of range
     assert oracle.csr_flags(np.array([0, 2, 1, 3, 3]), col) & 1      # decreasing rowptr
     assert oracle.csr_flags(np.array([0, 2, 2, 3, 4]), col) & 1      # rowptr[V] != E
+
+
+# ---------------------------------------------------------------- CSR build
+
+def _brute_csr(row, col, V, symmetrize, dedup):
+    """Pure-Python CSR: sorted() of the (row, col) tuples, per-node loops."""
+    pairs = list(zip(row.tolist(), col.tolist()))
+    if symmetrize:
+        pairs += [(c, r) for r, c in pairs]
+    pairs = sorted(set(pairs)) if dedup else sorted(pairs)
+    rowptr = [0]
+    for v in range(V):
+        rowptr.append(rowptr[-1] + sum(1 for r, _ in pairs if r == v))
+    return rowptr, [c for _, c in pairs]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_csr_build_matches_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    V = int(rng.integers(1, 20))
+    E = int(rng.integers(0, 60))
+    row, col = rng.integers(0, V, E), rng.integers(0, V, E)
+    for symmetrize in (False, True):
+        for dedup in (False, True):
+            rowptr, c = oracle.csr_build(row, col, V, symmetrize=symmetrize, dedup=dedup)
+            ref_rowptr, ref_col = _brute_csr(row, col, V, symmetrize, dedup)
+            assert rowptr.tolist() == ref_rowptr and c.tolist() == ref_col
+
+
+def test_csr_build_equals_reference_pipeline_without_empty_rows():
+    """tests/test_random_walk.py:26-28 takes rowptr from np.unique counts; on a
+    graph where every node has an out-edge that is exactly this rowptr."""
+    rng = np.random.default_rng(3)
+    V = 50
+    row = np.concatenate([np.arange(V), rng.integers(0, V, 300)])
+    col = rng.integers(0, V, row.size)
+    rowptr, c = oracle.csr_build(row, col, V)
+    order = np.lexsort((col, row))
+    _, counts = np.unique(row[order], return_counts=True)
+    assert rowptr.tolist() == np.concatenate([[0], counts.cumsum()]).tolist()
+    assert c.tolist() == col[order].tolist()
+
+
+def test_csr_build_hand_case():
+    row, col = np.array([3, 0, 0, 3, 0]), np.array([0, 2, 1, 1, 2])
+    rowptr, c = oracle.csr_build(row, col, 5)
+    assert rowptr.tolist() == [0, 3, 3, 3, 5, 5] and c.tolist() == [1, 2, 2, 0, 1]
+    rowptr, c = oracle.csr_build(row, col, 5, dedup=True)
+    assert rowptr.tolist() == [0, 2, 2, 2, 4, 4] and c.tolist() == [1, 2, 0, 1]
+    rowptr, c = oracle.csr_build(np.array([0]), np.array([1]), 2, symmetrize=True)
+    assert rowptr.tolist() == [0, 1, 2] and c.tolist() == [1, 0]
