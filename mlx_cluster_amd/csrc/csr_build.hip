@@ -8,7 +8,7 @@
 // bits(num_nodes - 1), sorting only the 2 * cbits bits that can be non-zero,
 // 8 bits per pass.  Keys are 32-bit when they fit (num_nodes <= 65536).  Each
 // pass is three launches and needs no inter-block waiting:
-//   radix_hist_kernel     per 4096-key tile, a 256-digit histogram, written
+//   radix_hist_kernel     per 8192-key tile, a 256-digit histogram, written
 //                         digit-major (hist[d * tiles + tile]);
 //   scan_*                one exclusive scan of that array, which turns it
 //                         into every (digit, tile)'s first output position;
@@ -27,13 +27,23 @@ namespace mlxc {
 namespace {
 
 constexpr int kRadixBits = 8;
-constexpr int kRadix = 1 << kRadixBits;  // 256 digits, one per thread of a block
-constexpr int kItems = 16;               // keys per thread per tile
-constexpr int kTile = kBlock * kItems;   // 4096 keys per tile (and per scan chunk)
-constexpr int kWaveTile = kWave * kItems;
+constexpr int kRadix = 1 << kRadixBits;  // 256 digits
+constexpr int kItems = 16;               // keys (or values) per thread
+constexpr int kChunk = kBlock * kItems;  // 4096 values per block of the scan and finish kernels
 constexpr int kWaves = kBlock / kWave;
 
-static_assert(kRadix == kBlock, "one digit per thread");
+// Radix tiles: 512 threads x 16 keys.  8192 keys per tile give each digit a
+// run of 32 keys (256 bytes of 64-bit keys) on average in the scatter, which
+// keeps its stores in whole lines; two blocks fit a CU's LDS.
+#ifndef MLXC_CSR_SORT_THREADS
+#define MLXC_CSR_SORT_THREADS 512
+#endif
+constexpr int kSortThreads = MLXC_CSR_SORT_THREADS;
+constexpr int kSortWaves = kSortThreads / kWave;
+constexpr int kSortTile = kSortThreads * kItems;
+constexpr int kWaveTile = kWave * kItems;
+
+static_assert(kRadix == kBlock && kSortThreads >= kRadix, "one digit per thread");
 
 constexpr int kOpSum = 0;
 constexpr int kOpMin = 1;
@@ -101,10 +111,11 @@ __device__ __forceinline__ int64_t op_identity() {
     return kOp == kOpSum ? 0 : INT64_MAX;
 }
 
-// Exclusive scan of one value per thread over the block, in thread order.
-// `wtot` is kWaves words of LDS.  Returns the exclusive prefix; *total (if
-// given) receives the block's reduction.  Contains two __syncthreads.
-template <int kOp>
+// Exclusive scan of one value per thread over a block of kThreads threads,
+// in thread order.  `wtot` is kThreads / 64 words of LDS.  Returns the
+// exclusive prefix; *total (if given) receives the block's reduction.
+// Contains two __syncthreads.
+template <int kOp, int kThreads = kBlock>
 __device__ int64_t block_exclusive_scan(int64_t v, int64_t* wtot, int64_t* total = nullptr) {
     const int lane = __lane_id();
     const int w = threadIdx.x / kWave;
@@ -119,7 +130,7 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t* wtot, int64_t* total
     int64_t before = op_identity<kOp>();
     for (int k = 0; k < w; ++k) before = op_apply<kOp>(before, wtot[k]);
     int64_t all = op_identity<kOp>();
-    for (int k = 0; k < kWaves; ++k) all = op_apply<kOp>(all, wtot[k]);
+    for (int k = 0; k < kThreads / kWave; ++k) all = op_apply<kOp>(all, wtot[k]);
     int64_t excl = __shfl_up(inc, 1, kWave);
     if (lane == 0) excl = op_identity<kOp>();
     if (total) *total = all;
@@ -130,57 +141,64 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t* wtot, int64_t* total
 // ------------------------------------------------------------- radix pass
 
 template <typename KeyT, bool kFirst>
-__global__ __launch_bounds__(kBlock) void radix_hist_kernel(EdgeSrc src,
-                                                            const KeyT* __restrict__ keys,
-                                                            int shift, int64_t total,
-                                                            int64_t tiles,
-                                                            int64_t* __restrict__ hist,
-                                                            int64_t* __restrict__ work) {
-    __shared__ int32_t cnt[kWaves][kRadix];
+__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(EdgeSrc src,
+                                                                  const KeyT* __restrict__ keys,
+                                                                  int shift, int64_t total,
+                                                                  int64_t tiles,
+                                                                  int64_t* __restrict__ hist,
+                                                                  int64_t* __restrict__ work) {
+    __shared__ int32_t cnt[kSortWaves][kRadix];
     const int t = threadIdx.x, w = t / kWave, lane = t % kWave;
-    for (int k = t; k < kWaves * kRadix; k += kBlock) (&cnt[0][0])[k] = 0;
-    __syncthreads();
+    for (int k = t; k < kSortWaves * kRadix; k += kSortThreads) (&cnt[0][0])[k] = 0;
     const int64_t tile = blockIdx.x;
-    const int64_t base = tile * kTile + w * kWaveTile + lane;
+    const int64_t base = tile * kSortTile + w * kWaveTile + lane;
     bool bad = false;
-#pragma unroll 4
+    // all loads first, so that the whole tile is in flight at once
+    KeyT key[kItems];
+#pragma unroll
     for (int s = 0; s < kItems; ++s) {
         const int64_t i = base + static_cast<int64_t>(s) * kWave;
-        const bool active = i < total;
-        KeyT k = 0;
-        if (active) k = kFirst ? src_key<KeyT>(src, i, bad) : keys[i];
-        const uint32_t d = digit_of(k, shift);
-        const uint64_t peers = match_digit(d, active);
-        if (active && is_leader(peers)) cnt[w][d] += __popcll(peers);
+        key[s] = 0;
+        if (i < total) key[s] = kFirst ? src_key<KeyT>(src, i, bad) : keys[i];
     }
     __syncthreads();
-    hist[static_cast<int64_t>(t) * tiles + tile] = cnt[0][t] + cnt[1][t] + cnt[2][t] + cnt[3][t];
+    // Counts do not depend on order, so plain LDS atomics do (measured on
+    // MI355X: 0.52 ms per pass at 2^28 keys, against 0.71 ms with the
+    // wavefront match the scatter needs for its stable ranks).
+#pragma unroll
+    for (int s = 0; s < kItems; ++s) {
+        if (base + static_cast<int64_t>(s) * kWave < total)
+            atomicAdd(&cnt[w][digit_of(key[s], shift)], 1);
+    }
+    __syncthreads();
+    if (t < kRadix) {
+        int32_t sum = 0;
+        for (int k = 0; k < kSortWaves; ++k) sum += cnt[k][t];
+        hist[static_cast<int64_t>(t) * tiles + tile] = sum;
+    }
     if (kFirst && bad)
         atomicOr(reinterpret_cast<unsigned long long*>(work),
                  static_cast<unsigned long long>(MLXC_STATUS_BAD_NODE));
 }
 
 template <typename KeyT, bool kFirst>
-__global__ __launch_bounds__(kBlock) void radix_scatter_kernel(EdgeSrc src,
-                                                               const KeyT* __restrict__ keys_in,
-                                                               KeyT* __restrict__ keys_out,
-                                                               int shift, int64_t total,
-                                                               int64_t tiles,
-                                                               const int64_t* __restrict__ offsets) {
-    __shared__ KeyT buf[kTile];
-    __shared__ int32_t cnt[kWaves][kRadix];
+__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
+    EdgeSrc src, const KeyT* __restrict__ keys_in, KeyT* __restrict__ keys_out, int shift,
+    int64_t total, int64_t tiles, const int64_t* __restrict__ offsets) {
+    __shared__ KeyT buf[kSortTile];
+    __shared__ int32_t cnt[kSortWaves][kRadix];
     __shared__ int32_t first[kRadix];
     __shared__ int64_t goff[kRadix];
-    __shared__ int64_t wtot[kWaves];
+    __shared__ int64_t wtot[kSortWaves];
     const int t = threadIdx.x, w = t / kWave, lane = t % kWave;
     const int64_t tile = blockIdx.x;
-    for (int k = t; k < kWaves * kRadix; k += kBlock) (&cnt[0][0])[k] = 0;
-    goff[t] = offsets[static_cast<int64_t>(t) * tiles + tile];
+    for (int k = t; k < kSortWaves * kRadix; k += kSortThreads) (&cnt[0][0])[k] = 0;
+    if (t < kRadix) goff[t] = offsets[static_cast<int64_t>(t) * tiles + tile];
     __syncthreads();
 
     // Rank of every key among the keys of its digit that come before it in
     // this tile's order (wavefront, then slot, then lane): stable.
-    const int64_t base = tile * kTile + w * kWaveTile + lane;
+    const int64_t base = tile * kSortTile + w * kWaveTile + lane;
     KeyT key[kItems];
     int32_t pos[kItems];
     bool bad = false;
@@ -199,16 +217,26 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(EdgeSrc src,
     }
     __syncthreads();
 
-    // Thread t owns digit t: its first position in the reordered tile, and
-    // the first position of each wavefront's keys of that digit.
-    const int32_t c0 = cnt[0][t], c1 = cnt[1][t], c2 = cnt[2][t];
-    const int32_t tot = c0 + c1 + c2 + cnt[3][t];
-    const int32_t at = static_cast<int32_t>(block_exclusive_scan<kOpSum>(tot, wtot));
-    first[t] = at;
-    cnt[0][t] = at;
-    cnt[1][t] = at + c0;
-    cnt[2][t] = at + c0 + c1;
-    cnt[3][t] = at + c0 + c1 + c2;
+    // Thread t < 256 owns digit t: its first position in the reordered tile,
+    // and the first position of each wavefront's keys of that digit.
+    int32_t c[kSortWaves];
+    int32_t tot = 0;
+    if (t < kRadix) {
+#pragma unroll
+        for (int k = 0; k < kSortWaves; ++k) {
+            c[k] = cnt[k][t];
+            tot += c[k];
+        }
+    }
+    int32_t at = static_cast<int32_t>(block_exclusive_scan<kOpSum, kSortThreads>(tot, wtot));
+    if (t < kRadix) {
+        first[t] = at;
+#pragma unroll
+        for (int k = 0; k < kSortWaves; ++k) {
+            cnt[k][t] = at;
+            at += c[k];
+        }
+    }
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < kItems; ++s) {
@@ -218,9 +246,9 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(EdgeSrc src,
     __syncthreads();
 
     // Consecutive entries of one digit go to consecutive output positions.
-    const int64_t left = total - tile * kTile;
-    const int n = left < kTile ? static_cast<int>(left) : kTile;
-    for (int j = t; j < n; j += kBlock) {
+    const int64_t left = total - tile * kSortTile;
+    const int n = left < kSortTile ? static_cast<int>(left) : kSortTile;
+    for (int j = t; j < n; j += kSortThreads) {
         const KeyT k = buf[j];
         const uint32_t d = digit_of(k, shift);
         keys_out[goff[d] + (j - first[d])] = k;
@@ -228,7 +256,7 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(EdgeSrc src,
 }
 
 // ------------------------------------------------------------- device scan
-// In place over n int64 values, chunks of kTile per block.  kRev scans from
+// In place over n int64 values, chunks of kChunk per block.  kRev scans from
 // the end (logical element j is data[n - 1 - j]).
 
 template <int kOp, bool kRev>
@@ -242,7 +270,7 @@ __global__ __launch_bounds__(kBlock) void scan_reduce_kernel(const int64_t* __re
                                                              int64_t n,
                                                              int64_t* __restrict__ sums) {
     __shared__ int64_t wtot[kWaves];
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
     int64_t acc = op_identity<kOp>();
     for (int s = 0; s < kItems; ++s)
         acc = op_apply<kOp>(acc, scan_load<kOp, kRev>(data, n, base + s * kBlock + threadIdx.x));
@@ -273,10 +301,10 @@ template <int kOp, bool kRev, bool kExcl>
 __global__ __launch_bounds__(kBlock) void scan_down_kernel(int64_t* __restrict__ data, int64_t n,
                                                            const int64_t* __restrict__ sums) {
     // Padded so that thread t's 16 consecutive values sit in distinct banks.
-    __shared__ int64_t vals[kTile + kTile / kItems];
+    __shared__ int64_t vals[kChunk + kChunk / kItems];
     __shared__ int64_t wtot[kWaves];
     const int t = threadIdx.x;
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
     auto slot = [](int j) { return j + j / kItems; };
     for (int s = 0; s < kItems; ++s) {
         const int j = s * kBlock + t;
@@ -325,13 +353,13 @@ __device__ __forceinline__ bool kept(const KeyT* __restrict__ keys, int64_t i, K
     return !kDedup || i == 0 || keys[i - 1] != k;
 }
 
-// sums[chunk] <- kept entries of chunk (kTile entries).
+// counts[chunk] <- kept entries of chunk (kChunk entries).
 template <typename KeyT>
 __global__ __launch_bounds__(kBlock) void dedup_count_kernel(const KeyT* __restrict__ keys,
                                                              int64_t total,
-                                                             int64_t* __restrict__ sums) {
+                                                             int64_t* __restrict__ counts) {
     __shared__ int64_t wtot[kWaves];
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
     int64_t c = 0;
     for (int s = 0; s < kItems; ++s) {
         const int64_t i = base + s * kBlock + threadIdx.x;
@@ -339,21 +367,22 @@ __global__ __launch_bounds__(kBlock) void dedup_count_kernel(const KeyT* __restr
     }
     int64_t all;
     block_exclusive_scan<kOpSum>(c, wtot, &all);
-    if (threadIdx.x == 0) sums[blockIdx.x] = all;
+    if (threadIdx.x == 0) counts[blockIdx.x] = all;
 }
 
 // Writes col[p] for every kept entry (p = its rank among kept entries) and
 // rowptr[row] = p at the first entry of each row present.  kDedup: the
-// chunk's first p comes from sums (exclusive scan of dedup_count_kernel).
+// chunk's first p comes from chunk_base (the exclusive scan of
+// dedup_count_kernel's counts).
 template <typename KeyT, bool kDedup>
 __global__ __launch_bounds__(kBlock) void csr_emit_kernel(const KeyT* __restrict__ keys,
                                                           int64_t total, int cbits,
-                                                          const int64_t* __restrict__ sums,
+                                                          const int64_t* __restrict__ chunk_base,
                                                           int64_t* __restrict__ rowptr,
                                                           int64_t* __restrict__ col_out) {
     __shared__ int32_t wkept[kItems][kWaves];
     const int t = threadIdx.x, w = t / kWave;
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
     const KeyT cmask = cbits == 0 ? KeyT(0) : (~KeyT(0) >> (8 * sizeof(KeyT) - cbits));
     KeyT key[kItems];
     uint32_t keep_bits = 0, start_bits = 0;
@@ -379,7 +408,7 @@ __global__ __launch_bounds__(kBlock) void csr_emit_kernel(const KeyT* __restrict
     int64_t p0 = base;
     if (kDedup) {
         __syncthreads();
-        p0 = sums[blockIdx.x];
+        p0 = chunk_base[blockIdx.x];
         // entries before slot 0 of this wavefront: earlier wavefronts of slot 0
         for (int k = 0; k < w; ++k) p0 += wkept[0][k];
     }
@@ -420,7 +449,8 @@ struct CsrLayout {
     int cbits = 0;
     int passes = 0;
     bool wide = false;  // 64-bit keys
-    int64_t tiles = 0;
+    int64_t tiles = 0;   // radix tiles of kSortTile keys
+    int64_t chunks = 0;  // finish chunks of kChunk keys
     size_t keys0 = 0, keys1 = 0, hist = 0, sums = 0, bytes = 0;
 };
 
@@ -431,19 +461,22 @@ CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
     const int key_bits = 2 * l.cbits;
     l.wide = key_bits > 32;
     l.passes = key_bits == 0 ? 1 : (key_bits + kRadixBits - 1) / kRadixBits;
-    l.tiles = (l.total + kTile - 1) / kTile;
+    l.tiles = (l.total + kSortTile - 1) / kSortTile;
+    l.chunks = (l.total + kChunk - 1) / kChunk;
     const size_t ksz = l.wide ? 8 : 4;
-    int64_t scan_n = kRadix * l.tiles;
+    // the digit counts, and after the last pass the finish chunks' counts
+    int64_t hist_n = kRadix * l.tiles;
+    if (l.chunks > hist_n) hist_n = l.chunks;
+    int64_t scan_n = hist_n;
     if (num_nodes + 1 > scan_n) scan_n = num_nodes + 1;
-    if (l.total > scan_n) scan_n = l.total;
-    const int64_t chunks = (scan_n + kTile - 1) / kTile;
+    const int64_t chunks = (scan_n + kChunk - 1) / kChunk;
     size_t at = round256(MLXC_WORK_WORDS * sizeof(int64_t));
     l.keys0 = at;
     at += round256(static_cast<size_t>(l.total) * ksz);
     l.keys1 = at;
     at += round256(static_cast<size_t>(l.total) * ksz);
     l.hist = at;
-    at += round256(static_cast<size_t>(kRadix) * l.tiles * sizeof(int64_t));
+    at += round256(static_cast<size_t>(hist_n) * sizeof(int64_t));
     l.sums = at;
     at += round256(static_cast<size_t>(chunks + 1) * sizeof(int64_t));
     l.bytes = at;
@@ -453,7 +486,7 @@ CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
 template <int kOp, bool kRev, bool kExcl>
 int device_scan(int64_t* data, int64_t n, int64_t* sums, int64_t* total_out, hipStream_t s) {
     if (n <= 0) return MLXC_OK;
-    const int64_t chunks = (n + kTile - 1) / kTile;
+    const int64_t chunks = (n + kChunk - 1) / kChunk;
     hipLaunchKernelGGL((scan_reduce_kernel<kOp, kRev>), dim3(chunks), dim3(kBlock), 0, s, data, n,
                        sums);
     hipLaunchKernelGGL((scan_top_kernel<kOp>), dim3(1), dim3(kBlock), 0, s, sums, chunks,
@@ -484,31 +517,34 @@ int csr_build_typed(const EdgeSrc& src, const CsrLayout& l, int32_t flags, int64
         const int shift = p * kRadixBits;
         KeyT* out = buf[p & 1];
         if (p == 0)
-            hipLaunchKernelGGL((radix_hist_kernel<KeyT, true>), dim3(l.tiles), dim3(kBlock), 0, s,
+            hipLaunchKernelGGL((radix_hist_kernel<KeyT, true>), dim3(l.tiles), dim3(kSortThreads), 0, s,
                                src, in, shift, l.total, l.tiles, hist, work);
         else
-            hipLaunchKernelGGL((radix_hist_kernel<KeyT, false>), dim3(l.tiles), dim3(kBlock), 0, s,
+            hipLaunchKernelGGL((radix_hist_kernel<KeyT, false>), dim3(l.tiles), dim3(kSortThreads), 0, s,
                                src, in, shift, l.total, l.tiles, hist, work);
         MLXC_HIP_TRY(hipGetLastError());
         if (int rc = device_scan<kOpSum, false, true>(hist, kRadix * l.tiles, sums, nullptr, s))
             return rc;
         if (p == 0)
-            hipLaunchKernelGGL((radix_scatter_kernel<KeyT, true>), dim3(l.tiles), dim3(kBlock), 0,
+            hipLaunchKernelGGL((radix_scatter_kernel<KeyT, true>), dim3(l.tiles), dim3(kSortThreads), 0,
                                s, src, in, out, shift, l.total, l.tiles, hist);
         else
-            hipLaunchKernelGGL((radix_scatter_kernel<KeyT, false>), dim3(l.tiles), dim3(kBlock), 0,
+            hipLaunchKernelGGL((radix_scatter_kernel<KeyT, false>), dim3(l.tiles), dim3(kSortThreads), 0,
                                s, src, in, out, shift, l.total, l.tiles, hist);
         MLXC_HIP_TRY(hipGetLastError());
         in = out;
     }
     // work[1] <- entries kept; rowptr <- that count everywhere, then the row
-    // starts, then the reverse min-scan.
-    const int64_t chunks = l.tiles;
+    // starts, then the reverse min-scan.  The digit counts' space holds the
+    // finish chunks' counts.
+    const int64_t chunks = l.chunks;
+    int64_t* chunk_base = hist;
     if (flags & MLXC_CSR_DEDUP) {
         hipLaunchKernelGGL((dedup_count_kernel<KeyT>), dim3(chunks), dim3(kBlock), 0, s, in,
-                           l.total, sums);
-        hipLaunchKernelGGL((scan_top_kernel<kOpSum>), dim3(1), dim3(kBlock), 0, s, sums, chunks,
-                           work + 1);
+                           l.total, chunk_base);
+        MLXC_HIP_TRY(hipGetLastError());
+        if (int rc = device_scan<kOpSum, false, true>(chunk_base, chunks, sums, work + 1, s))
+            return rc;
     } else {
         hipLaunchKernelGGL(set_word_kernel, dim3(1), dim3(kWave), 0, s, work + 1, l.total);
     }
@@ -516,10 +552,10 @@ int csr_build_typed(const EdgeSrc& src, const CsrLayout& l, int32_t flags, int64
     if (int rc = fill_words(rowptr, src.num_nodes + 1, work + 1, s)) return rc;
     if (flags & MLXC_CSR_DEDUP)
         hipLaunchKernelGGL((csr_emit_kernel<KeyT, true>), dim3(chunks), dim3(kBlock), 0, s, in,
-                           l.total, l.cbits, sums, rowptr, col_out);
+                           l.total, l.cbits, chunk_base, rowptr, col_out);
     else
         hipLaunchKernelGGL((csr_emit_kernel<KeyT, false>), dim3(chunks), dim3(kBlock), 0, s, in,
-                           l.total, l.cbits, sums, rowptr, col_out);
+                           l.total, l.cbits, chunk_base, rowptr, col_out);
     MLXC_HIP_TRY(hipGetLastError());
     return device_scan<kOpMin, true, false>(rowptr, src.num_nodes + 1, sums, nullptr, s);
 }
