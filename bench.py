@@ -65,6 +65,16 @@ CSR_CONFIGS = {
 }
 CSR_METRIC = "CSR build: input edges/sec at 1 MI355X + achieved GB/s vs HBM roofline"
 
+# Skip-gram context windows after the walk (torch_geometric Node2Vec.sample's
+# defaults: walk_length 20, context_size 10, walks_per_node 10, one negative
+# walk per positive): name -> (description, R-MAT scale, samples, walks per
+# node, L, C).
+WIN_CONFIGS = {
+    "win2": ("positive + negative context windows (C=10) of 10 uniform walks/node, L=20, "
+             "on R-MAT 2^20 (the graph of c2)", 20, 1 << 24, 10, 20, 10),
+}
+WIN_METRIC = "context windows/sec at 1 MI355X + achieved GB/s vs HBM roofline"
+
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
@@ -385,12 +395,108 @@ def bench_csr(args, np, torch, mc, synth, dev):
     print(json.dumps(line), flush=True)
 
 
+def bench_windows(args, np, torch, mc, synth, dev):
+    """One line for a WIN_CONFIGS entry: a step is the positive windows of the
+    walks plus as many negative windows (mlxc_context_windows +
+    mlxc_negative_windows), walks and starts resident in HBM."""
+    import oracle
+    desc, scale, samples, per_node, L, C = WIN_CONFIGS[args.config]
+    log(f"config {args.config}: {desc} on {torch.cuda.get_device_name(dev)}")
+    rowptr, col = synth.rmat_csr(scale, samples, seed=0, device=dev)
+    V = rowptr.numel() - 1
+    start = torch.arange(per_node * V, device=dev, dtype=torch.int64) % V
+    walks = mc.random_walk(rowptr, col, start, None, L, seed=2)
+    N = walks.shape[0]
+    W = L + 2 - C
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        return mc.context_windows(walks, C), mc.negative_windows(start, L, C, V, seed=7)
+
+    for _ in range(args.warmup):
+        out = step()
+    del out
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for ev0, ev1 in events:
+        ev0.record(stream)
+        pos, neg = step()
+        ev1.record(stream)
+        del pos, neg
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    event_ms = [a.elapsed_time(b) for a, b in events]
+    kernel_ms = float(np.mean(event_ms))
+    ms_per_step = wall / args.steps * 1e3
+    windows = 2 * W * N
+    value = windows / (ms_per_step / 1e3)
+    log(f"{ms_per_step:.3f} ms/step wall, {kernel_ms:.3f} ms/launch (events)")
+
+    pos, neg = step()
+    ref = walks.unfold(1, C, 1).transpose(0, 1).reshape(W * N, C)
+    full_equal = bool(torch.equal(pos, ref))
+    del ref
+    s = torch.arange(0, N, 997, device=dev)
+    rw = oracle.negative_walks(start[s].cpu().numpy(), L, V, 7, walk_ids=s.cpu().numpy())
+    parity = all(np.array_equal(neg[j * N + s].cpu().numpy(), rw[:, j:j + C]) for j in range(W))
+    del pos, neg
+
+    # bytes: the walks read once, the starts once, both window sets written once
+    algo_bytes = 8 * N * (L + 1) + 8 * N + 2 * 8 * W * N * C
+    achieved = algo_bytes / (kernel_ms / 1e3) / 1e9
+    traffic = traffic_from_profile(f"context_windows_{args.config}")
+    roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
+                "algorithmic_bytes_per_launch": algo_bytes,
+                "bytes_formula": "8*N*(L+1) (walks) + 8*N (starts) + 2 * 8*W*N*C (windows)",
+                "kernel_ms": kernel_ms, "kernel_ms_median": float(np.median(event_ms)),
+                "kernel_ms_source": "HIP events around each step on its stream (mean; median beside it)",
+                "hbm_gbs_measured": (traffic / (kernel_ms / 1e3) / 1e9) if traffic else None}
+    cpu = None
+    if not args.no_cpu_baseline:
+        model, cores = host_info()
+        w_h, s_h = walks.cpu().numpy(), start.cpu().numpy()
+        with one_core() as pin:
+            n = min(N, 20_000)
+            t0 = time.perf_counter()
+            oracle.context_windows(w_h[:n], C)
+            oracle.negative_windows(s_h[:n], L, C, V, 7)
+            rate = 2 * W * n / (time.perf_counter() - t0)
+            n = int(min(N, max(n, args.cpu_seconds * rate / (2 * W))))
+            t0 = time.perf_counter()
+            oracle.context_windows(w_h[:n], C)
+            oracle.negative_windows(s_h[:n], L, C, V, 7)
+            dt = time.perf_counter() - t0
+        cpu = {"value": 2 * W * n / dt, "unit": "windows/s", "cores": 1, "kind": "port",
+               "sample": f"first {n} of {N} walks, {dt:.1f} s, oracle.context_windows + "
+                         f"oracle.negative_windows (numpy), 1 thread pinned to one core",
+               "host_cpu": model, "host_cores_available": cores, "pinned_core": pin.core}
+        log(f"cpu baseline {cpu['value']:.3e} windows/s over {n} walks")
+    line = {
+        "metric": WIN_METRIC, "value": value, "unit": "windows/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int64", "data": "synthetic",
+        "config": {"workload": f"{args.config}: {desc}", "num_nodes": V, "num_walks": N,
+                   "walk_length": L, "context_size": C, "windows_per_step": windows,
+                   "positive_equals_torch_unfold": full_equal,
+                   "negative_sample_bit_exact": bool(parity)},
+        "roofline": roofline, "cpu_baseline": cpu,
+    }
+    if cpu:
+        line["speedup_vs_cpu_baseline"] = value / cpu["value"]
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS) + sorted(CSR_CONFIGS))
+    ap.add_argument("--config", default="c2",
+                    choices=sorted(CONFIGS) + sorted(CSR_CONFIGS) + sorted(WIN_CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -429,6 +535,9 @@ def main():
 
     if args.config in CSR_CONFIGS:
         bench_csr(args, np, torch, mc, synth, dev)
+        return
+    if args.config in WIN_CONFIGS:
+        bench_windows(args, np, torch, mc, synth, dev)
         return
 
     desc, kind, gargs, per_node, L, extra = CONFIGS[args.config]

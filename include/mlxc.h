@@ -229,6 +229,46 @@ int mlxc_csr_build_cpu(const int64_t* row, const int64_t* col, int64_t num_edges
                        int64_t* count, int64_t* status);
 
 /*
+ * Skip-gram context windows of walks, the step after the walk in node2vec
+ * training.  No reference counterpart (the reference stops at the walks,
+ * /root/reference/random_walks/BiasedRandomWalk.cpp:96); the layout is that
+ * of torch_geometric's Node2Vec.pos_sample: with W = walk_nodes -
+ * context_size + 1 windows per walk, window-major,
+ *   d_out[(j * N + n) * C + k] = d_walks[n * walk_nodes + j + k]
+ * for j < W, k < C = context_size, n < N = num_walks.
+ *
+ * d_walks    [N, walk_nodes] row-major, element type elem_type (MLXC_OUT_*)
+ * d_out      [W * N, C], the same element type
+ * walk_nodes in [1, 65536 / element size]; context_size in [1, min(32,
+ * walk_nodes)].
+ * Asynchronous on `stream`; no workspace.
+ */
+int mlxc_context_windows(const void* d_walks, int64_t num_walks, int32_t walk_nodes,
+                         int32_t context_size, int32_t elem_type, void* d_out, void* stream);
+
+/*
+ * Negative context windows (torch_geometric Node2Vec.neg_sample layout): the
+ * windows of mlxc_context_windows over the walks
+ *   [start[n], u(n, 1), ..., u(n, walk_length)],
+ * u(n, l) = (x * num_nodes) >> 32 with x = word 0 of Philox4x32-10(key =
+ * seed; counter = (n lo, n hi, l, 0)): nodes drawn uniformly from
+ * [0, num_nodes), num_nodes in [1, 2^32].  start values are copied as given.
+ * out_type MLXC_OUT_INT64 or MLXC_OUT_INT32 (num_nodes and start values
+ * below 2^31).  walk_length + 1 >= context_size, and (walk_length + 1) times
+ * the element size at most 64 KiB.  No reference counterpart.
+ */
+int mlxc_negative_windows(const int64_t* d_start, int64_t num_walks, int32_t walk_length,
+                          int32_t context_size, int64_t num_nodes, uint64_t seed,
+                          int32_t out_type, void* d_out, void* stream);
+
+/* Host twins of the two window entry points (host pointers, same output). */
+int mlxc_context_windows_cpu(const void* walks, int64_t num_walks, int32_t walk_nodes,
+                             int32_t context_size, int32_t elem_type, void* out);
+int mlxc_negative_windows_cpu(const int64_t* start, int64_t num_walks, int32_t walk_length,
+                              int32_t context_size, int64_t num_nodes, uint64_t seed,
+                              int32_t out_type, void* out);
+
+/*
  * Host twins of the three walk entry points: the same walks, the same
  * arguments with host pointers, evaluated on `threads` CPU threads (<= 0:
  * one per hardware thread) and returning when done.  Outputs are

@@ -12,6 +12,8 @@ include/mlxc.h); the package has no CPU fallback.
 """
 from .csr import to_csr
 from .walks import csr_check, philox_uniform, random_walk, rejection_sampling
+from .windows import context_windows, negative_windows
 
-__all__ = ["random_walk", "rejection_sampling", "csr_check", "philox_uniform", "to_csr"]
+__all__ = ["random_walk", "rejection_sampling", "csr_check", "philox_uniform", "to_csr",
+           "context_windows", "negative_windows"]
 __version__ = "0.1.0"

@@ -71,6 +71,12 @@ SIGNATURES = {
     "mlxc_csr_build_cpu": (
         ctypes.c_int, [_ptr, _ptr, _i64, _i64, _i32, _ptr, _ptr, _ptr, _ptr],
     ),
+    "mlxc_context_windows": (ctypes.c_int, [_ptr, _i64, _i32, _i32, _i32, _ptr, _ptr]),
+    "mlxc_negative_windows": (
+        ctypes.c_int, [_ptr, _i64, _i32, _i32, _i64, _u64, _i32, _ptr, _ptr],
+    ),
+    "mlxc_context_windows_cpu": (ctypes.c_int, [_ptr, _i64, _i32, _i32, _i32, _ptr]),
+    "mlxc_negative_windows_cpu": (ctypes.c_int, [_ptr, _i64, _i32, _i32, _i64, _u64, _i32, _ptr]),
     "mlxc_random_walk_cpu": (
         ctypes.c_int,
         [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _i32, _i32, _ptr],

@@ -338,6 +338,60 @@ int host_node2vec_typed(const HostWalk& w, const N2VParams& prm, bool sorted, in
 
 }  // namespace
 
+namespace {
+
+template <typename T>
+void windows_of(const T* walks, int64_t num_walks, int32_t walk_nodes, int32_t ctx, T* out) {
+    const int64_t windows = walk_nodes - ctx + 1;
+    for (int64_t j = 0; j < windows; ++j)
+        for (int64_t n = 0; n < num_walks; ++n)
+            for (int32_t k = 0; k < ctx; ++k)
+                out[(j * num_walks + n) * ctx + k] = walks[n * walk_nodes + j + k];
+}
+
+template <typename T>
+void negative_windows_of(const int64_t* start, int64_t num_walks, int32_t walk_length,
+                         int32_t ctx, int64_t num_nodes, uint64_t seed, T* out) {
+    const int32_t walk_nodes = walk_length + 1;
+    std::vector<T> rw(static_cast<size_t>(num_walks) * walk_nodes);
+    for (int64_t n = 0; n < num_walks; ++n) {
+        rw[n * walk_nodes] = static_cast<T>(start[n]);
+        for (int32_t l = 1; l < walk_nodes; ++l) {
+            uint32_t c0 = static_cast<uint32_t>(n), c1 = static_cast<uint32_t>(
+                                                        static_cast<uint64_t>(n) >> 32),
+                     c2 = static_cast<uint32_t>(l), c3 = 0;
+            philox_host(c0, c1, c2, c3, static_cast<uint32_t>(seed),
+                        static_cast<uint32_t>(seed >> 32));
+            rw[n * walk_nodes + l] = static_cast<T>(
+                (static_cast<uint64_t>(c0) * static_cast<uint64_t>(num_nodes)) >> 32);
+        }
+    }
+    windows_of(rw.data(), num_walks, walk_nodes, ctx, out);
+}
+
+}  // namespace
+
+void host_context_windows(const void* walks, int64_t num_walks, int32_t walk_nodes, int32_t ctx,
+                          int32_t elem_type, void* out) {
+    if (elem_type == MLXC_OUT_INT32)
+        windows_of(static_cast<const int32_t*>(walks), num_walks, walk_nodes, ctx,
+                   static_cast<int32_t*>(out));
+    else
+        windows_of(static_cast<const int64_t*>(walks), num_walks, walk_nodes, ctx,
+                   static_cast<int64_t*>(out));
+}
+
+void host_negative_windows(const int64_t* start, int64_t num_walks, int32_t walk_length,
+                           int32_t ctx, int64_t num_nodes, uint64_t seed, int32_t out_type,
+                           void* out) {
+    if (out_type == MLXC_OUT_INT32)
+        negative_windows_of(start, num_walks, walk_length, ctx, num_nodes, seed,
+                            static_cast<int32_t*>(out));
+    else
+        negative_windows_of(start, num_walks, walk_length, ctx, num_nodes, seed,
+                            static_cast<int64_t*>(out));
+}
+
 int host_uniform(const HostWalk& w, bool generate, int32_t threads, uint32_t& status) {
     const int t = resolve_threads(threads);
     return w.out_type == MLXC_OUT_INT32 ? host_uniform_typed<int32_t>(w, generate, t, status)

@@ -125,6 +125,35 @@ int check_csr_build(const int64_t* row, const int64_t* col, int64_t num_edges, i
     return MLXC_OK;
 }
 
+int check_windows(const void* walks, int64_t num_walks, int32_t walk_nodes, int32_t ctx,
+                  int32_t elem_type, const void* out) {
+    if (num_walks < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_walks must be >= 0");
+    if (elem_type != MLXC_OUT_INT64 && elem_type != MLXC_OUT_INT32)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "element type must be MLXC_OUT_INT64 or MLXC_OUT_INT32");
+    if (walk_nodes < 1 || walk_nodes > windows_max_nodes(elem_type))
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "nodes per walk must lie in [1, 65536 / element size]");
+    if (ctx < 1 || ctx > 32 || ctx > walk_nodes)
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "context_size must lie in [1, min(32, nodes per walk)]");
+    if (num_walks > 0 && (!walks || !out))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "walks and out must not be NULL");
+    if (num_walks > INT64_MAX / 32 / walk_nodes)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "output size overflows int64");
+    return MLXC_OK;
+}
+
+int check_negative(const int64_t* start, int64_t num_walks, int32_t walk_length, int32_t ctx,
+                   int64_t num_nodes, int32_t out_type, const void* out) {
+    if (walk_length < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "walk_length must be >= 0");
+    if (int rc = check_windows(start, num_walks, walk_length + 1, ctx, out_type, out)) return rc;
+    if (num_nodes < 1 || num_nodes > (int64_t(1) << 32))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "num_nodes must lie in [1, 2^32]");
+    if (out_type == MLXC_OUT_INT32 && num_nodes > INT32_MAX)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "MLXC_OUT_INT32 needs num_nodes below 2^31");
+    return MLXC_OK;
+}
+
 HostWalk host_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                    int64_t num_edges, const int64_t* start, int64_t num_walks, const float* rand,
                    int32_t walk_length, uint64_t seed, void* n_out, void* e_out,
@@ -267,6 +296,45 @@ int mlxc_csr_build_cpu(const int64_t* row, const int64_t* col, int64_t num_edges
     *count = n;
     if (status) *status = bits;
     return rc;
+}
+
+int mlxc_context_windows(const void* d_walks, int64_t num_walks, int32_t walk_nodes,
+                         int32_t context_size, int32_t elem_type, void* d_out, void* stream) {
+    if (int rc = check_windows(d_walks, num_walks, walk_nodes, context_size, elem_type, d_out))
+        return rc;
+    if (num_walks == 0) return MLXC_OK;
+    return launch_context_windows(d_walks, num_walks, walk_nodes, context_size, elem_type, d_out,
+                                  static_cast<hipStream_t>(stream));
+}
+
+int mlxc_negative_windows(const int64_t* d_start, int64_t num_walks, int32_t walk_length,
+                          int32_t context_size, int64_t num_nodes, uint64_t seed,
+                          int32_t out_type, void* d_out, void* stream) {
+    if (int rc = check_negative(d_start, num_walks, walk_length, context_size, num_nodes,
+                                out_type, d_out))
+        return rc;
+    if (num_walks == 0) return MLXC_OK;
+    return launch_negative_windows(d_start, num_walks, walk_length, context_size, num_nodes, seed,
+                                   out_type, d_out, static_cast<hipStream_t>(stream));
+}
+
+int mlxc_context_windows_cpu(const void* walks, int64_t num_walks, int32_t walk_nodes,
+                             int32_t context_size, int32_t elem_type, void* out) {
+    if (int rc = check_windows(walks, num_walks, walk_nodes, context_size, elem_type, out))
+        return rc;
+    host_context_windows(walks, num_walks, walk_nodes, context_size, elem_type, out);
+    return MLXC_OK;
+}
+
+int mlxc_negative_windows_cpu(const int64_t* start, int64_t num_walks, int32_t walk_length,
+                              int32_t context_size, int64_t num_nodes, uint64_t seed,
+                              int32_t out_type, void* out) {
+    if (int rc = check_negative(start, num_walks, walk_length, context_size, num_nodes, out_type,
+                                out))
+        return rc;
+    host_negative_windows(start, num_walks, walk_length, context_size, num_nodes, seed, out_type,
+                          out);
+    return MLXC_OK;
 }
 
 int mlxc_random_walk_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,

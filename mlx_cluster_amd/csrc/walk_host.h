@@ -100,6 +100,16 @@ int launch_csr_build(const int64_t* row, const int64_t* col, int64_t num_edges, 
                      int32_t flags, int64_t* rowptr, int64_t* col_out, void* workspace,
                      size_t workspace_bytes, hipStream_t stream);
 
+// ---- windows.hip
+int launch_context_windows(const void* walks, int64_t num_walks, int32_t walk_nodes, int32_t ctx,
+                           int32_t elem_type, void* out, hipStream_t stream);
+int launch_negative_windows(const int64_t* start, int64_t num_walks, int32_t walk_length,
+                            int32_t ctx, int64_t num_nodes, uint64_t seed, int32_t out_type,
+                            void* out, hipStream_t stream);
+// Most nodes per walk the window kernels accept for this element type (a
+// walk row must fit the LDS tile).
+int windows_max_nodes(int32_t elem_type);
+
 // ---- host_walk.cpp (host pointers; the same walks on CPU threads)
 struct HostWalk {
     const int64_t* rowptr;
@@ -115,6 +125,12 @@ struct HostWalk {
 // threads <= 0: one per hardware thread.  status receives MLXC_STATUS_* bits.
 int host_uniform(const HostWalk& w, bool generate, int32_t threads, uint32_t& status);
 int host_node2vec(const HostWalk& w, const N2VParams& p, int32_t threads, uint32_t& status);
+// The windows of mlxc_context_windows / mlxc_negative_windows from host arrays.
+void host_context_windows(const void* walks, int64_t num_walks, int32_t walk_nodes, int32_t ctx,
+                          int32_t elem_type, void* out);
+void host_negative_windows(const int64_t* start, int64_t num_walks, int32_t walk_length,
+                           int32_t ctx, int64_t num_nodes, uint64_t seed, int32_t out_type,
+                           void* out);
 // The CSR of mlxc_csr_build from host arrays.
 int host_csr_build(const int64_t* row, const int64_t* col, int64_t num_edges, int64_t num_nodes,
                    int32_t flags, int64_t* rowptr, int64_t* col_out, int64_t& count,

@@ -8,6 +8,8 @@ Functions follow the reference's CPU evaluation:
   uniform_walk   -> /root/reference/random_walks/RandomWalk.cpp:41-60
   node2vec_walk  -> /root/reference/random_walks/BiasedRandomWalk.cpp:20-28,52-100
   csr_build      -> /root/reference/tests/test_random_walk.py:23-28 (numpy)
+  context_windows, negative_windows -> torch_geometric Node2Vec.pos_sample /
+                    neg_sample (not in the reference; numpy)
 """
 from __future__ import annotations
 
@@ -192,3 +194,49 @@ def csr_build(row, col, num_nodes: int, *, symmetrize: bool = False, dedup: bool
     rowptr = np.zeros(num_nodes + 1, dtype=np.int64)
     np.cumsum(np.bincount(row, minlength=num_nodes), out=rowptr[1:])
     return rowptr, col
+
+
+def philox4x32_10_np(c0, c1, c2, c3, key: int):
+    """Philox4x32-10 vectorised over counters (uint64 arrays holding 32-bit
+    words), the same rounds as oracle_philox4x32_10 in walk_oracle.c."""
+    c0, c1, c2, c3 = (np.asarray(c, dtype=np.uint64) for c in (c0, c1, c2, c3))
+    k0, k1 = np.uint64(key & 0xFFFFFFFF), np.uint64((key >> 32) & 0xFFFFFFFF)
+    m32 = np.uint64(0xFFFFFFFF)
+    for _ in range(10):
+        p0 = np.uint64(0xD2511F53) * c0
+        p1 = np.uint64(0xCD9E8D57) * c2
+        c0, c1, c2, c3 = ((p1 >> np.uint64(32)) ^ c1 ^ k0, p1 & m32,
+                          (p0 >> np.uint64(32)) ^ c3 ^ k1, p0 & m32)
+        k0 = (k0 + np.uint64(0x9E3779B9)) & m32
+        k1 = (k1 + np.uint64(0xBB67AE85)) & m32
+    return c0, c1, c2, c3
+
+
+def context_windows(walks, context_size: int) -> np.ndarray:
+    """torch_geometric Node2Vec.pos_sample's windows: for j in range(W), the
+    columns j .. j + C - 1 of every walk, concatenated window-major."""
+    walks = np.asarray(walks)
+    C = int(context_size)
+    W = walks.shape[1] - C + 1
+    return np.concatenate([walks[:, j:j + C] for j in range(W)], axis=0)
+
+
+def negative_walks(start, walk_length: int, num_nodes: int, seed: int,
+                   walk_ids=None) -> np.ndarray:
+    """Node2Vec.neg_sample's walks [start, u_1..u_L] with u_l = (x * V) >> 32,
+    x = word 0 of Philox4x32-10(key = seed; counter = (n lo, n hi, l, 0)).
+    n is the walk's index, or walk_ids[i] for a sample of walks."""
+    start = np.asarray(start, dtype=np.int64).reshape(-1)
+    N, L = start.size, int(walk_length)
+    ids = np.arange(N) if walk_ids is None else np.asarray(walk_ids).reshape(-1)
+    n = np.repeat(ids.astype(np.uint64), L)
+    l = np.tile(np.arange(1, L + 1, dtype=np.uint64), N)
+    x, _, _, _ = philox4x32_10_np(n & np.uint64(0xFFFFFFFF), n >> np.uint64(32), l,
+                                  np.zeros_like(n), int(seed) & (2**64 - 1))
+    u = ((x * np.uint64(num_nodes)) >> np.uint64(32)).astype(np.int64).reshape(N, L)
+    return np.concatenate([start[:, None], u], axis=1)
+
+
+def negative_windows(start, walk_length: int, context_size: int, num_nodes: int,
+                     seed: int) -> np.ndarray:
+    return context_windows(negative_walks(start, walk_length, num_nodes, seed), context_size)

@@ -453,3 +453,43 @@ def test_csr_build_hand_case():
     assert rowptr.tolist() == [0, 2, 2, 2, 4, 4] and c.tolist() == [1, 2, 0, 1]
     rowptr, c = oracle.csr_build(np.array([0]), np.array([1]), 2, symmetrize=True)
     assert rowptr.tolist() == [0, 1, 2] and c.tolist() == [1, 0]
+
+
+# ---------------------------------------------------------------- context windows
+
+def test_philox_np_matches_c_oracle():
+    rng = np.random.default_rng(9)
+    for _ in range(64):
+        c = rng.integers(0, 2**32, 4)
+        k = int(rng.integers(0, 2**63)) * 2 + int(rng.integers(0, 2))
+        ref = oracle.philox4x32_10(c, [k & 0xFFFFFFFF, k >> 32])
+        got = oracle.philox4x32_10_np(*[np.array([x], dtype=np.uint64) for x in c], k)
+        assert [int(g[0]) for g in got] == [int(x) for x in ref]
+
+
+def test_context_windows_brute_force_and_unfold():
+    """Pure-Python loops, and torch's unfold (an independent library routine)."""
+    import torch
+    rng = np.random.default_rng(4)
+    for N, nodes, C in ((1, 1, 1), (3, 5, 2), (7, 9, 9), (5, 21, 10)):
+        walks = rng.integers(0, 1000, (N, nodes))
+        got = oracle.context_windows(walks, C)
+        W = nodes - C + 1
+        brute = [[int(walks[n][j + k]) for k in range(C)] for j in range(W) for n in range(N)]
+        assert got.tolist() == brute
+        unf = torch.from_numpy(walks).unfold(1, C, 1).transpose(0, 1).reshape(W * N, C)
+        assert got.tolist() == unf.tolist()
+
+
+def test_negative_walks_closed_form():
+    start = np.array([7, 3, 2**40])
+    rw = oracle.negative_walks(start, 4, 1000, seed=5)
+    assert rw.shape == (3, 5) and rw[:, 0].tolist() == start.tolist()
+    for n in range(3):
+        for l in range(1, 5):
+            x = int(oracle.philox4x32_10([n, 0, l, 0], [5, 0])[0])
+            assert rw[n, l] == (x * 1000) >> 32
+    u = oracle.negative_walks(np.zeros(20000, np.int64), 8, 37, seed=11)[:, 1:].reshape(-1)
+    counts = np.bincount(u, minlength=37)
+    assert u.min() >= 0 and u.max() < 37
+    assert stats.chisquare(counts).pvalue > 1e-4
