@@ -157,6 +157,24 @@ def test_hub_graph_parity(cuda):
             assert counts["member_tests"] > 0
 
 
+@pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
+def test_return_dominated_walks(rule, cuda):
+    """Small p: a trial with r >= prob1 and r >= prob2 is accepted only as a
+    return to t.  On a directed graph without back edges no return exists, so
+    with p = 1e-6 nearly every step runs to the trial cap and keeps its last
+    candidate; on an undirected graph returns are frequent."""
+    edges = [(i, (i + 1) % 64) for i in range(64)] + [(i, (i + 2) % 64) for i in range(64)]
+    rowptr, col = csr(64, edges)
+    start = np.arange(16)
+    _, counts = assert_parity(rowptr, col, start, 4, 1e-6, 1.0, 21, rule, cuda)
+    assert counts["trials"] > 16 * 2 * 60_000
+    rowptr, col = synth.rmat_csr(11, 20_000, seed=5, symmetrize=True)
+    rowptr, col = rowptr.numpy(), col.numpy()
+    start = np.arange(rowptr.size - 1)
+    for p, q in ((1e-3, 1.0), (0.5, 2.0), (0.25, 0.5)):
+        assert_parity(rowptr, col, start, 15, p, q, 8, rule, cuda)
+
+
 def test_csr_check_matches_oracle(cuda):
     rowptr, col = csr(4, [(0, 1), (0, 3), (2, 1)])
     cases = [(rowptr, col), (rowptr, np.array([3, 1, 1])), (rowptr, np.array([1, 9, 1])),
