@@ -90,10 +90,19 @@ const char* mlxc_last_error(void);
 size_t mlxc_random_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges,
                                         int64_t num_walks, int32_t walk_length);
 
-/* Workspace bytes for mlxc_rejection_sampling's fastest layout (same
- * conventions).  No reference counterpart. */
+/* Workspace bytes for mlxc_rejection_sampling's fastest layout for these
+ * arguments (same conventions).  Either edge records (16 bytes per edge), or
+ * the CSR mode's layout, which reads each candidate's node id and then, only
+ * when the decision needs it, its rowptr pair.  CSR mode is chosen when
+ * num_walks * walk_length * (1 + 4 w) < 4 * num_edges, w being the share of
+ * acceptance draws r that can need a row search (|prob1 - prob2| for
+ * MLXC_RULE_NODE2VEC_EXACT, max(0, prob1 - prob2) for the chain).  Both
+ * layouts add 16 bytes per walk and about 4.3 bytes per edge of search index.
+ * A workspace that holds the record layout always runs with records.  No
+ * reference counterpart. */
 size_t mlxc_rejection_sampling_workspace_bytes(int64_t num_nodes, int64_t num_edges,
-                                               int64_t num_walks, int32_t walk_length);
+                                               int64_t num_walks, int32_t walk_length,
+                                               double p, double q, int32_t rule);
 
 /*
  * Uniform random walk.

@@ -48,7 +48,7 @@ SIGNATURES = {
     "mlxc_version": (ctypes.c_int, []),
     "mlxc_last_error": (ctypes.c_char_p, []),
     "mlxc_random_walk_workspace_bytes": (_size, [_i64, _i64, _i64, _i32]),
-    "mlxc_rejection_sampling_workspace_bytes": (_size, [_i64, _i64, _i64, _i32]),
+    "mlxc_rejection_sampling_workspace_bytes": (_size, [_i64, _i64, _i64, _i32, _dbl, _dbl, _i32]),
     "mlxc_random_walk": (
         ctypes.c_int,
         [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _i32, _ptr, _size, _ptr],

@@ -180,8 +180,14 @@ size_t mlxc_random_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges, in
 }
 
 size_t mlxc_rejection_sampling_workspace_bytes(int64_t num_nodes, int64_t num_edges,
-                                               int64_t num_walks, int32_t walk_length) {
-    return node2vec_workspace_bytes(num_nodes, num_edges, num_walks, walk_length);
+                                               int64_t num_walks, int32_t walk_length, double p,
+                                               double q, int32_t rule) {
+    N2VParams prm;
+    // invalid parameters: the call will fail; any size will do
+    const double width = n2v_params(p, q, 0, rule, MLXC_ROWS_DETECT, prm) == MLXC_OK
+                             ? n2v_search_width(prm)
+                             : 1.0;
+    return node2vec_workspace_bytes(num_nodes, num_edges, num_walks, walk_length, width);
 }
 
 int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,

@@ -151,6 +151,13 @@ enum : int {
     kN2vLevel = 3,   // sorted rows: reads one 16-entry block of a search-index level
     kN2vScan = 4,    // unsorted rows: reads the next 16 entries of row(x)
     kN2vDone = 5,    // the queue is exhausted
+    kN2vRow = 6,     // CSR mode: reads rowptr[x], rowptr[x + 1] of the candidate
+};
+
+// What a CSR-mode slot does once the candidate's row has been read.
+enum : int {
+    kRowAccept = 0,  // take the step
+    kRowSearch = 1,  // search t in row(x), then decide
 };
 
 // The two uniforms of a trial: Philox4x32-10 with key = seed and counter =
@@ -231,7 +238,7 @@ __device__ __forceinline__ int scan_step(const int32_t (&v)[kSearchBlock], int32
 
 struct N2VRecArgs {
     WalkArgs w;
-    const EdgeRecord* recs;   // [num_edges]
+    const EdgeRecord* recs;   // [num_edges]; null in CSR mode
     const EdgeRecord* init;   // [num_walks]
     IndexLevels index;        // search index (level 0 = col32)
     int32_t rows;             // MLXC_ROWS_*; DETECT reads the prep pass's counts in work[2..3]
@@ -266,7 +273,13 @@ __device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, double r, bool 
 }
 
 // node2vec walk over edge records (num_nodes, num_edges below 2^31; n_out and
-// e_out 16-byte aligned).  One walk per lane slot from the wave queue.  Every
+// e_out 16-byte aligned).
+//
+// kCsr (CSR mode, for calls with few steps per edge, where building a record
+// per edge costs more than it saves): a candidate is read as its col32 entry
+// alone, and its row from rowptr only when the decision needs it — to take
+// the step, or to search it.  A rejected trial costs one read either way; an
+// accepted one two (one when the walk returns to t, whose row it keeps).  One walk per lane slot from the wave queue.  Every
 // iteration a live slot issues one dependent read of one 64-byte block — the
 // block holding its start record or its candidate's edge record (which
 // carries the candidate's row, so the neighbour test needs no rowptr read),
@@ -274,9 +287,10 @@ __device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, double r, bool 
 // (idle slots read the first start records), and the wave waits once.
 // Sorted rows are searched through the index levels (level_step); unsorted
 // rows are scanned 16 entries per read, as the reference scans them.
-template <int kRule, bool kEdges, typename OutT>
+template <int kRule, bool kEdges, bool kCsr, typename OutT>
 __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    typedef int32_t i32x4a8 __attribute__((ext_vector_type(4), aligned(8)));
     OutT* const nout = static_cast<OutT*>(a.w.n_out);
     OutT* const eout = static_cast<OutT*>(a.w.e_out);
     const bool sorted = a.rows == MLXC_ROWS_SORTED ||
@@ -290,8 +304,9 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     int64_t n = 0;
     int32_t l = 0;          // steps done
     uint32_t trial = 0;
-    int32_t t = 0;          // previous node
+    int32_t t = 0, bt = 0, dt = 0;   // previous node and (CSR mode) its row
     int32_t v = 0, bv = 0, dv = 0;   // current node and its row
+    int row_then = kRowAccept;       // CSR mode: what the row read is for
     int32_t e = 0;          // candidate edge
     int32_t x = 0, bx = 0, dx = 0;   // candidate node and its row (from its record)
     int lvl = 0;            // search: index level of the block to read next
@@ -316,7 +331,12 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
         if (ph == kN2vStart) {
             bp = reinterpret_cast<const int32_t*>(a.init + n);
         } else if (ph == kN2vCand) {
-            bp = reinterpret_cast<const int32_t*>(a.recs + e);
+            if (kCsr)
+                bp = a.index.level[0] + (e & ~3);  // the aligned 16 bytes holding col32[e]
+            else
+                bp = reinterpret_cast<const int32_t*>(a.recs + e);
+        } else if (kCsr && ph == kN2vRow) {
+            bp = reinterpret_cast<const int32_t*>(a.w.rowptr + x);  // 8-byte aligned
         } else if (ph == kN2vLevel) {
             const int32_t* lp = a.index.level[0];
 #pragma unroll
@@ -329,7 +349,10 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             bp = reinterpret_cast<const int32_t*>(a.init);
         }
         i32x4 qb[4];
-        qb[0] = reinterpret_cast<const i32x4*>(bp)[0];
+        if (kCsr)
+            qb[0] = *reinterpret_cast<const i32x4a8*>(bp);
+        else
+            qb[0] = reinterpret_cast<const i32x4*>(bp)[0];
 #ifndef MLXC_N2V_FULL_BLOCKS
         if (ph == kN2vLevel || ph == kN2vScan) {
 #pragma unroll
@@ -383,6 +406,50 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                 trial = 0;
                 phase = kN2vCand;
             }
+        } else if (kCsr && ph == kN2vCand) {
+            const int k = e & 3;
+            x = k == 0 ? rec.x : k == 1 ? rec.y : k == 2 ? rec.z : rec.w;
+            int d = 1;  // first step and forced steps accept
+            if (!(l == 0 || dv == 1)) d = n2v_decide<kRule>(a, static_cast<double>(r), x, t);
+            if (static_cast<uint32_t>(x) >= static_cast<uint32_t>(a.w.num_nodes)) {
+                status |= MLXC_STATUS_BAD_NODE;  // (col32 holds -1 for any bad col)
+                fill = true;
+            } else if (d == 0) {
+                next_trial = true;
+            } else if (d == 1 && x == t && l > 0) {
+                accept = true;  // back to t: its row is known
+                bx = bt;
+                dx = dt;
+            } else {
+                row_then = d == 1 ? kRowAccept : kRowSearch;
+                phase = kN2vRow;
+            }
+        } else if (kCsr && ph == kN2vRow) {
+            // rowptr[x] and rowptr[x + 1] as int32 pairs (low, high)
+            const bool ok = rec.y == 0 && rec.w == 0 && rec.x >= 0 && rec.z >= rec.x &&
+                            rec.z <= a.w.num_edges;
+            bx = rec.x;
+            dx = rec.z - rec.x;
+            if (!ok) {
+                status |= MLXC_STATUS_BAD_ROW;
+                fill = true;
+            } else if (row_then == kRowAccept) {
+                accept = true;
+            } else if (dx == 0) {
+                accept = n2v_resolve<kRule>(a, static_cast<double>(r), false);
+                next_trial = !accept;
+            } else {
+                lo = bx;
+                hi = bx + dx;
+                if (!sorted) {
+                    phase = kN2vScan;
+                } else {
+                    const uint32_t diff = static_cast<uint32_t>(lo) ^ static_cast<uint32_t>(hi - 1);
+                    lvl = diff ? (31 - __builtin_clz(diff)) >> 2 : 0;
+                    blk = static_cast<int32_t>(static_cast<int64_t>(lo) >> (4 * (lvl + 1)));
+                    phase = kN2vLevel;
+                }
+            }
         } else if (ph == kN2vCand) {
             x = rec.x;
             bx = rec.y;
@@ -430,7 +497,18 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
         if (next_trial) {
             trial += 1;
             if (trial >= MLXC_MAX_TRIALS) {
-                accept = true;  // trial cap: keep the last candidate
+                // trial cap: keep the last candidate (CSR mode: read its row
+                // first, unless it is t)
+                if (!kCsr) {
+                    accept = true;
+                } else if (x == t) {
+                    accept = true;
+                    bx = bt;
+                    dx = dt;
+                } else {
+                    row_then = kRowAccept;
+                    phase = kN2vRow;
+                }
             } else {
                 float u0;
                 n2v_uniforms(n, l, trial, a.key0, a.key1, u0, r);
@@ -444,6 +522,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             g += 1;
             l += 1;
             t = v;
+            bt = bv;
+            dt = dv;
             v = x;
             bv = bx;
             dv = dx;
@@ -507,9 +587,9 @@ int dispatch_n2v(const N2VArgs& a, bool sorted, bool edges, hipStream_t stream) 
 #define MLXC_N2V_BLOCKS_PER_CU 4
 #endif
 
-template <int kRule, bool kEdges, typename OutT>
+template <int kRule, bool kEdges, bool kCsr, typename OutT>
 int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
-    auto kernel = node2vec_rec_kernel<kRule, kEdges, OutT>;
+    auto kernel = node2vec_rec_kernel<kRule, kEdges, kCsr, OutT>;
     int grid = 0;
     if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid, MLXC_N2V_BLOCKS_PER_CU)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
@@ -517,20 +597,22 @@ int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
     return MLXC_OK;
 }
 
-// Workspace of the record walk: edge records, start records, then (128-byte
-// aligned) the levels of the search index — col as int32, then its samples
-// every 16^k entries — each padded to whole blocks of kSearchBlock entries,
-// then 64 bytes of slack for the block reads of the last start records.
+// Workspace of the record walk: edge records (record mode only), start
+// records, then (128-byte aligned) the levels of the search index — col as
+// int32, then its samples every 16^k entries — each padded to whole blocks of
+// kSearchBlock entries, then 64 bytes of slack for the block reads of the
+// last start records.
 struct N2VLayout {
     size_t level[kMaxLevels];
     int count;
     size_t total;
 };
 
-N2VLayout n2v_layout(int64_t num_edges, int64_t num_walks) {
+N2VLayout n2v_layout(int64_t num_edges, int64_t num_walks, bool records) {
     N2VLayout lay;
     lay.count = index_levels(num_edges);
-    size_t pos = kRecordOffset + static_cast<size_t>(num_edges + num_walks) * sizeof(EdgeRecord);
+    size_t pos = kRecordOffset +
+                 static_cast<size_t>((records ? num_edges : 0) + num_walks) * sizeof(EdgeRecord);
     pos = (pos + 127) & ~static_cast<size_t>(127);
     int64_t entries = num_edges;  // level k has ceil(num_edges / 16^k) entries
     for (int k = 0; k < lay.count; ++k) {
@@ -543,14 +625,35 @@ N2VLayout n2v_layout(int64_t num_edges, int64_t num_walks) {
     return lay;
 }
 
+// Edge records cost one random rowptr read and 16 bytes per edge and save a
+// rowptr read on every step taken and every row searched; CSR mode wins when
+// the call takes few steps per edge and seldom searches.  With w the share
+// of draws that can need a search, records pay off when
+// steps * (1 + 4 w) >= 4 * edges.  Measured on MI355X: configuration 5
+// (1.07 steps per edge, w = 0) 9.0 ms in CSR mode against 11.0 with
+// records; configuration 5x (w = 0.75) 21.0 against 19.5; configuration 3
+// (5.3 steps per edge) 13.6 either way.
+bool n2v_records_pay_off(int64_t num_edges, int64_t num_walks, int32_t walk_length,
+                         double search_width) {
+    const double steps = static_cast<double>(num_walks) * static_cast<double>(walk_length);
+    return steps * (1.0 + 4.0 * search_width) >= 4.0 * static_cast<double>(num_edges);
+}
+
 }  // namespace
 
+double n2v_search_width(const N2VParams& p) {
+    if (p.rule == MLXC_RULE_REF_CHAIN) return p.prob1 > p.prob2 ? p.prob1 - p.prob2 : 0.0;
+    return p.prob1 > p.prob2 ? p.prob1 - p.prob2 : p.prob2 - p.prob1;
+}
+
 size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
-                                int32_t walk_length) {
+                                int32_t walk_length, double search_width) {
     if (num_nodes < 0 || num_edges < 0 || num_walks < 0 || walk_length < 0 ||
         !records_fit(num_nodes, num_edges))
         return MLXC_WORK_WORDS * sizeof(int64_t);
-    return n2v_layout(num_edges, num_walks).total;
+    return n2v_layout(num_edges, num_walks,
+                      n2v_records_pay_off(num_edges, num_walks, walk_length, search_width))
+        .total;
 }
 
 namespace {
@@ -558,15 +661,22 @@ namespace {
 template <typename OutT>
 int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace,
                           size_t workspace_bytes, hipStream_t stream) {
-    const N2VLayout lay = n2v_layout(w.num_edges, w.num_walks);
     const bool aligned = reinterpret_cast<uintptr_t>(w.n_out) % 16 == 0 &&
                          reinterpret_cast<uintptr_t>(w.e_out) % 16 == 0;  // e_out may be null
-    if (aligned && records_fit(w.num_nodes, w.num_edges) && workspace_bytes >= lay.total) {
+    const N2VLayout lay_rec = n2v_layout(w.num_edges, w.num_walks, true);
+    const N2VLayout lay_csr = n2v_layout(w.num_edges, w.num_walks, false);
+    // Records whenever the workspace holds them: node2vec_workspace_bytes
+    // asks for them only when they pay off.
+    const bool records = workspace_bytes >= lay_rec.total;
+    if (aligned && records_fit(w.num_nodes, w.num_edges) &&
+        (records || workspace_bytes >= lay_csr.total)) {
+        const N2VLayout& lay = records ? lay_rec : lay_csr;
         N2VRecArgs a;
         a.w = w;
         char* base = static_cast<char*>(workspace);
-        EdgeRecord* recs = reinterpret_cast<EdgeRecord*>(base + kRecordOffset);
-        EdgeRecord* init = recs + w.num_edges;
+        EdgeRecord* recs = records ? reinterpret_cast<EdgeRecord*>(base + kRecordOffset) : nullptr;
+        EdgeRecord* init = reinterpret_cast<EdgeRecord*>(base + kRecordOffset) +
+                           (records ? w.num_edges : 0);
         IndexLevels index{};
         index.count = lay.count;
         for (int k = 0; k < lay.count; ++k)
@@ -589,11 +699,18 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         a.key1 = p.key1;
         a.rows = p.rows;
         const bool edges = w.e_out != nullptr;
+        if (records) {
+            if (p.rule == MLXC_RULE_REF_CHAIN)
+                return edges ? launch_n2v_rec<MLXC_RULE_REF_CHAIN, true, false, OutT>(a, stream)
+                             : launch_n2v_rec<MLXC_RULE_REF_CHAIN, false, false, OutT>(a, stream);
+            return edges ? launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, true, false, OutT>(a, stream)
+                         : launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, false, false, OutT>(a, stream);
+        }
         if (p.rule == MLXC_RULE_REF_CHAIN)
-            return edges ? launch_n2v_rec<MLXC_RULE_REF_CHAIN, true, OutT>(a, stream)
-                         : launch_n2v_rec<MLXC_RULE_REF_CHAIN, false, OutT>(a, stream);
-        return edges ? launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, true, OutT>(a, stream)
-                     : launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, false, OutT>(a, stream);
+            return edges ? launch_n2v_rec<MLXC_RULE_REF_CHAIN, true, true, OutT>(a, stream)
+                         : launch_n2v_rec<MLXC_RULE_REF_CHAIN, false, true, OutT>(a, stream);
+        return edges ? launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, true, true, OutT>(a, stream)
+                     : launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, false, true, OutT>(a, stream);
     }
     // Graphs beyond int32, a workspace too small for the records, or output
     // buffers not 16-byte aligned: the direct CSR kernel, which needs the row

@@ -60,7 +60,9 @@ struct CsrCheck {
 
 // Edge records (see EdgeRecord); optionally (index.count > 0) also the
 // levels of the node2vec walk's search index: col as int32 and its samples
-// col32[16^k * i].  With a non-null work pointer the same pass validates the
+// col32[16^k * i].  With rec == nullptr (the node2vec walk's CSR mode) only
+// the index is written, with -1 for a col value outside [0, num_nodes), and
+// no rowptr is read.  With a non-null work pointer the same pass validates the
 // whole CSR (status bits into work[0]) and counts the row descents into
 // work[2] / work[3], from which the node2vec walk decides whether its rows
 // are sorted.
@@ -77,16 +79,20 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
         const int64_t c = col[e];
         if (work) check.edge(col, num_nodes, e, c);
         i32x4 r = {static_cast<int32_t>(c), 0, kRecBadNode, 0};
-        if (node_ok(c, num_nodes)) {
-            const RowBounds rb = load_row(rowptr, c);
-            if (row_ok(rb, num_edges)) {
-                r.y = static_cast<int32_t>(rb.begin);
-                r.z = static_cast<int32_t>(rb.end - rb.begin);
-            } else {
-                r.z = kRecBadRow;
+        if (!rec) {
+            if (!node_ok(c, num_nodes)) r.x = -1;
+        } else {
+            if (node_ok(c, num_nodes)) {
+                const RowBounds rb = load_row(rowptr, c);
+                if (row_ok(rb, num_edges)) {
+                    r.y = static_cast<int32_t>(rb.begin);
+                    r.z = static_cast<int32_t>(rb.end - rb.begin);
+                } else {
+                    r.z = kRecBadRow;
+                }
             }
+            *reinterpret_cast<i32x4*>(rec + e) = r;
         }
-        *reinterpret_cast<i32x4*>(rec + e) = r;
         if (index.count > 0) {
             index.level[0][e] = r.x;
             // e is a multiple of 16^k for k = 1 .. while its low 4k bits are 0

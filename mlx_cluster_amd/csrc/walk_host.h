@@ -89,8 +89,10 @@ struct N2VParams {
     int32_t rows;                // MLXC_ROWS_*
     int32_t out_type;            // MLXC_OUT_*
 };
+// Share of acceptance draws r for which a trial may need the row search.
+double n2v_search_width(const N2VParams& p);
 size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
-                                int32_t walk_length);
+                                int32_t walk_length, double search_width);
 int launch_node2vec(const WalkArgs& a, const N2VParams& p, void* workspace,
                     size_t workspace_bytes, hipStream_t stream);
 

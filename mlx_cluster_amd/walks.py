@@ -344,8 +344,8 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     n_out = torch.empty((N, L + 1), dtype=out_dtype, device=device)
     e_out = torch.empty((N, L), dtype=out_dtype, device=device) if return_edges else None
     lib = _lib.load()
-    work = _workspace(lib.mlxc_rejection_sampling_workspace_bytes(rowptr.numel() - 1, col.numel(),
-                                                                  N, L), device)
+    work = _workspace(lib.mlxc_rejection_sampling_workspace_bytes(
+        rowptr.numel() - 1, col.numel(), N, L, float(p), float(q), _RULES[rule]), device)
     with torch.cuda.device(device):
         rc = lib.mlxc_rejection_sampling(
             _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,

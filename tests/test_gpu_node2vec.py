@@ -19,19 +19,27 @@ pytestmark = pytest.mark.gpu
 RULE_NAME = {oracle.RULE_REF_CHAIN: "ref_chain", oracle.RULE_NODE2VEC_EXACT: "node2vec"}
 
 
-def _direct_walk(rowptr, col, start, L, p, q, seed, rule, rows):
-    """mlxc_rejection_sampling through the C ABI with the minimal workspace:
-    the direct CSR kernel (no records), with edge output."""
+def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode):
+    """mlxc_rejection_sampling through the C ABI, with edge output, in the
+    mode the workspace selects: "direct" (minimal workspace: the direct CSR
+    kernel), "csr" (the CSR-mode layout: the record kernel without edge
+    records) or "records" (the edge-record layout)."""
     from mlx_cluster_amd import _lib
     lib = _lib.load()
     N = start.numel()
+    V, E = rowptr.numel() - 1, col.numel()
     n = torch.empty((N, L + 1), dtype=torch.int64, device=start.device)
     e = torch.empty((N, L), dtype=torch.int64, device=start.device)
-    ws = torch.zeros(4, dtype=torch.int64, device=start.device)
+    query = lambda N_, L_: lib.mlxc_rejection_sampling_workspace_bytes(V, E, N_, L_, p, q, rule)
+    # the query sizes records only for calls of many steps per edge
+    nbytes = {"direct": 32, "csr": query(N, 0), "records": query(max(N, 1), 2**31 - 1)}[mode]
+    if mode == "csr" and E > 0:
+        assert nbytes < query(max(N, 1), 2**31 - 1)
+    ws = torch.zeros((nbytes + 7) // 8, dtype=torch.int64, device=start.device)
     ptr = lambda t: t.data_ptr() if t.numel() else None
-    rc = lib.mlxc_rejection_sampling(ptr(rowptr), rowptr.numel() - 1, ptr(col), col.numel(),
+    rc = lib.mlxc_rejection_sampling(ptr(rowptr), V, ptr(col), E,
                                      ptr(start), N, L, p, q, seed, rule, rows, ptr(n), ptr(e),
-                                     _lib.MLXC_OUT_INT64, ws.data_ptr(), 32,
+                                     _lib.MLXC_OUT_INT64, ws.data_ptr(), nbytes,
                                      torch.cuda.current_stream().cuda_stream)
     assert rc == 0, _lib.last_error()
     torch.cuda.synchronize()
@@ -40,9 +48,10 @@ def _direct_walk(rowptr, col, start, L, p, q, seed, rule, rows):
 
 
 def gpu_walk(rowptr, col, start, L, p, q, seed, rule, cuda, **kw):
-    """Runs the record walk without and with edge output and the direct CSR
-    walk (minimal workspace); all node outputs must agree, and both edge
-    outputs.  Returns (nodes, edges)."""
+    """Runs the walk without and with edge output (the mode the workspace
+    query picks) and through the C ABI in each of the three modes (edge
+    records, CSR mode, the direct kernel); all node outputs must agree, and all
+    edge outputs.  Returns (nodes, edges)."""
     t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.int64)).to(cuda)
     args = (t(rowptr), t(col), t(start), L, p, q)
     n_rec = mc.rejection_sampling(*args, seed=seed, rule=RULE_NAME[rule], **kw)
@@ -50,11 +59,12 @@ def gpu_walk(rowptr, col, start, L, p, q, seed, rule, cuda, **kw):
     np.testing.assert_array_equal(n_rec.cpu().numpy(), n.cpu().numpy(),
                                   err_msg="record walk: nodes differ with edge output")
     rows = {None: 2, True: 1, False: 0}[kw.get("rows_sorted")]
-    nd, ed = _direct_walk(*args[:3], L, p, q, seed, rule, rows)
-    np.testing.assert_array_equal(nd.cpu().numpy(), n.cpu().numpy(),
-                                  err_msg="direct CSR walk != record walk")
-    np.testing.assert_array_equal(ed.cpu().numpy(), e.cpu().numpy(),
-                                  err_msg="direct CSR walk edges != record walk edges")
+    for mode in ("direct", "csr", "records"):
+        nm, em = _abi_walk(*args[:3], L, p, q, seed, rule, rows, mode)
+        np.testing.assert_array_equal(nm.cpu().numpy(), n.cpu().numpy(),
+                                      err_msg=f"{mode} walk nodes differ")
+        np.testing.assert_array_equal(em.cpu().numpy(), e.cpu().numpy(),
+                                      err_msg=f"{mode} walk edges differ")
     return n.cpu().numpy(), e.cpu().numpy()
 
 
