@@ -683,8 +683,11 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
             index.level[k] = reinterpret_cast<int32_t*>(base + lay.level[k]);
         // one pass builds the search index and, for MLXC_ROWS_DETECT, checks
         // the rows (the walk reads the result on the device: no host sync)
-        if (int rc = launch_edge_records(w.rowptr, w.col, w.num_nodes, w.num_edges, recs, index,
-                                         p.rows == MLXC_ROWS_DETECT ? w.work : nullptr, stream))
+        int64_t* check = p.rows == MLXC_ROWS_DETECT ? w.work : nullptr;
+        if (int rc = records ? launch_edge_records(w.rowptr, w.col, w.num_nodes, w.num_edges, recs,
+                                                   index, check, stream)
+                             : launch_edge_index(w.rowptr, w.col, w.num_nodes, w.num_edges, index,
+                                                 check, stream))
             return rc;
         if (int rc = launch_walk_init(w.rowptr, w.start, w.num_nodes, w.num_edges, w.num_walks,
                                       init, stream))

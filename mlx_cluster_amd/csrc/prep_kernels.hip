@@ -107,6 +107,56 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
     }
 }
 
+// The search index alone (the node2vec walk's CSR mode: no records, no rowptr
+// read per edge): col32 = col with -1 for a value outside [0, num_nodes),
+// plus its samples col32[16^k * i]; with a non-null work pointer the same
+// pass validates the CSR, as edge_record_kernel does.  Each thread takes four
+// consecutive entries per iteration (two 16-byte loads, one 16-byte store);
+// col must be 16-byte aligned.
+__global__ __launch_bounds__(kBlock) void edge_index_kernel(const int64_t* __restrict__ rowptr,
+                                                            const int64_t* __restrict__ col,
+                                                            int64_t num_nodes, int64_t num_edges,
+                                                            IndexLevels index, int64_t* work) {
+    typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    CsrCheck check;
+    for (int64_t q = gid; 4 * q < num_edges; q += stride) {
+        const int64_t e0 = 4 * q;
+        int64_t c[4];
+        if (e0 + 4 <= num_edges) {
+            const i64x2 a = reinterpret_cast<const i64x2*>(col + e0)[0];
+            const i64x2 b = reinterpret_cast<const i64x2*>(col + e0)[1];
+            c[0] = a.x; c[1] = a.y; c[2] = b.x; c[3] = b.y;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) c[k] = e0 + k < num_edges ? col[e0 + k] : 0;
+        }
+        int32_t v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t e = e0 + k;
+            v[k] = node_ok(c[k], num_nodes) ? static_cast<int32_t>(c[k]) : -1;
+            if (work && e < num_edges) {
+                if (!node_ok(c[k], num_nodes)) check.bad_col = true;
+                if (e >= 1 && c[k] < (k ? c[k - 1] : col[e - 1])) ++check.desc;
+            }
+        }
+        // col32 is padded to whole 16-entry blocks, so the last store fits
+        *reinterpret_cast<i32x4*>(index.level[0] + e0) = i32x4{v[0], v[1], v[2], v[3]};
+        if ((e0 & 15) == 0) {
+            for (int k = 1; k < index.count && (e0 & ((int64_t{1} << (4 * k)) - 1)) == 0; ++k)
+                index.level[k][e0 >> (4 * k)] = v[0];
+        }
+    }
+    if (work) {
+        check.nodes(rowptr, num_nodes, col, num_edges, gid, stride);
+        unsigned long long* w = reinterpret_cast<unsigned long long*>(work);
+        check.flush(w, MLXC_STATUS_BAD_ROW, MLXC_STATUS_BAD_NODE, w + 2, w + 3);
+    }
+}
+
 // Start records: walk n's start node in the edge-record format, so a slot
 // beginning a walk and a slot taking a step both issue the same single 16-byte
 // read.  Written by walk_init_kernel (one coalesced pass over start).
@@ -198,6 +248,23 @@ int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_n
     if (int rc = stream_grid(items, 16, grid)) return rc;
     hipLaunchKernelGGL(edge_record_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col,
                        num_nodes, num_edges, recs, index, check_work);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int launch_edge_index(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
+                      int64_t num_edges, const IndexLevels& index, int64_t* check_work,
+                      hipStream_t stream) {
+    if (num_edges == 0 && !check_work) return MLXC_OK;
+    if (reinterpret_cast<uintptr_t>(col) % 16 != 0)  // the record pass reads any alignment
+        return launch_edge_records(rowptr, col, num_nodes, num_edges, nullptr, index, check_work,
+                                   stream);
+    int grid = 0;
+    const int64_t quads = (num_edges + 3) / 4;
+    const int64_t items = check_work && num_nodes > quads ? num_nodes : quads;
+    if (int rc = stream_grid(items, 16, grid)) return rc;
+    hipLaunchKernelGGL(edge_index_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col,
+                       num_nodes, num_edges, index, check_work);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

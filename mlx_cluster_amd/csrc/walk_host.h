@@ -66,6 +66,11 @@ int launch_zero_work(int64_t* d_work, hipStream_t stream);
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                         int64_t num_edges, EdgeRecord* recs, const IndexLevels& index,
                         int64_t* check_work, hipStream_t stream);
+// The index levels alone, from col (node2vec CSR mode); a 16-byte aligned col
+// uses four entries per thread, any other alignment the record pass.
+int launch_edge_index(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
+                      int64_t num_edges, const IndexLevels& index, int64_t* check_work,
+                      hipStream_t stream);
 int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
                      int64_t num_edges, int64_t num_walks, EdgeRecord* init, hipStream_t stream);
 int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
