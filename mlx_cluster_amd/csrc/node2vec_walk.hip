@@ -273,20 +273,20 @@ __device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, double r, bool 
 }
 
 // node2vec walk over edge records (num_nodes, num_edges below 2^31; n_out and
-// e_out 16-byte aligned).
+// e_out 16-byte aligned).  One walk per lane slot from the wave queue.  Every
+// iteration a live slot issues one dependent read: its start record or its
+// candidate's edge record (16 bytes; the record carries the candidate's row,
+// so the neighbour test needs no rowptr read), or one 64-byte block of the
+// neighbour search; the read is unconditional (idle slots read the first
+// start record) and the wave waits once.  Sorted rows are searched through
+// the index levels (level_step); unsorted rows are scanned 16 entries per
+// read, as the reference scans them.
 //
 // kCsr (CSR mode, for calls with few steps per edge, where building a record
 // per edge costs more than it saves): a candidate is read as its col32 entry
 // alone, and its row from rowptr only when the decision needs it — to take
 // the step, or to search it.  A rejected trial costs one read either way; an
-// accepted one two (one when the walk returns to t, whose row it keeps).  One walk per lane slot from the wave queue.  Every
-// iteration a live slot issues one dependent read of one 64-byte block — the
-// block holding its start record or its candidate's edge record (which
-// carries the candidate's row, so the neighbour test needs no rowptr read),
-// or one block of the neighbour search — as four unconditional 16-byte loads
-// (idle slots read the first start records), and the wave waits once.
-// Sorted rows are searched through the index levels (level_step); unsorted
-// rows are scanned 16 entries per read, as the reference scans them.
+// accepted one two (one when the walk returns to t, whose row it keeps).
 template <int kRule, bool kEdges, bool kCsr, typename OutT>
 __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -322,10 +322,10 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     uint32_t status = 0;
 
     while (true) {
-        // 1. This iteration's read: one 64-byte block.  Records are read as
-        // the block of four records holding them (the block may run past
-        // the end of its array into the next workspace array or the slack
-        // after the last one).
+        // 1. This iteration's read: 16 bytes (a record, the aligned 16 bytes
+        // of col32 holding a candidate, or a rowptr pair), or a whole 64-byte
+        // block of an index level in the search phases (col32 and every
+        // level are padded to whole blocks).
         const int ph = phase;
         const int32_t* bp;
         if (ph == kN2vStart) {
@@ -353,15 +353,12 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             qb[0] = *reinterpret_cast<const i32x4a8*>(bp);
         else
             qb[0] = reinterpret_cast<const i32x4*>(bp)[0];
-#ifndef MLXC_N2V_FULL_BLOCKS
+        // the other 48 bytes of the block only for the search phases (reading
+        // them for every phase costs registers and measured slower at C5)
         if (ph == kN2vLevel || ph == kN2vScan) {
 #pragma unroll
             for (int i = 1; i < 4; ++i) qb[i] = reinterpret_cast<const i32x4*>(bp)[i];
         }
-#else
-#pragma unroll
-        for (int i = 1; i < 4; ++i) qb[i] = reinterpret_cast<const i32x4*>(bp)[i];
-#endif
         // ... and the output blocks the last iteration completed are stored.
         ow_drain<OutT>(ow, st);
         if (kEdges) ow_drain<OutT>(ew, st);
