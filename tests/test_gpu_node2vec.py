@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 RULE_NAME = {oracle.RULE_REF_CHAIN: "ref_chain", oracle.RULE_NODE2VEC_EXACT: "node2vec"}
 
 
-def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode):
+def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode, out_dtype=torch.int64):
     """mlxc_rejection_sampling through the C ABI, with edge output, in the
     mode the workspace selects: "direct" (minimal workspace: the direct CSR
     kernel), "csr" (the CSR-mode layout: the record kernel without edge
@@ -28,8 +28,9 @@ def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode):
     lib = _lib.load()
     N = start.numel()
     V, E = rowptr.numel() - 1, col.numel()
-    n = torch.empty((N, L + 1), dtype=torch.int64, device=start.device)
-    e = torch.empty((N, L), dtype=torch.int64, device=start.device)
+    n = torch.empty((N, L + 1), dtype=out_dtype, device=start.device)
+    e = torch.empty((N, L), dtype=out_dtype, device=start.device)
+    out_type = _lib.MLXC_OUT_INT32 if out_dtype == torch.int32 else _lib.MLXC_OUT_INT64
     query = lambda N_, L_: lib.mlxc_rejection_sampling_workspace_bytes(V, E, N_, L_, p, q, rule)
     # the query sizes records only for calls of many steps per edge
     nbytes = {"direct": 32, "csr": query(N, 0), "records": query(max(N, 1), 2**31 - 1)}[mode]
@@ -39,7 +40,7 @@ def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode):
     ptr = lambda t: t.data_ptr() if t.numel() else None
     rc = lib.mlxc_rejection_sampling(ptr(rowptr), V, ptr(col), E,
                                      ptr(start), N, L, p, q, seed, rule, rows, ptr(n), ptr(e),
-                                     _lib.MLXC_OUT_INT64, ws.data_ptr(), nbytes,
+                                     out_type, ws.data_ptr(), nbytes,
                                      torch.cuda.current_stream().cuda_stream)
     assert rc == 0, _lib.last_error()
     torch.cuda.synchronize()
@@ -233,8 +234,9 @@ def test_long_walks_with_sinks(L, cuda):
 
 @pytest.mark.parametrize("rule", ["ref_chain", "node2vec"])
 def test_int32_output(rule, cuda):
-    """out_dtype=torch.int32: the record walk (with and without edges) and
-    the direct kernel give the int64 results, narrowed."""
+    """out_dtype=torch.int32: the walk with and without edges, and through
+    the C ABI in each mode (edge records, CSR mode, the direct kernel), gives
+    the int64 results, narrowed."""
     rowptr, col = synth.rmat_csr(12, 40_000, seed=13, symmetrize=True)
     rowptr, col = rowptr.to(cuda), col.to(cuda)
     start = torch.arange(9000, device=cuda) % (rowptr.numel() - 1)
@@ -246,6 +248,11 @@ def test_int32_output(rule, cuda):
     c = mc.rejection_sampling(rowptr, col, start, 21, 0.5, 2.0, out_dtype=torch.int32, seed=5,
                               rule=rule)
     assert torch.equal(a[0], c.long())
+    for mode in ("direct", "csr", "records"):
+        n, e = _abi_walk(rowptr, col, start, 21, 0.5, 2.0, 5, rule, 2, mode,
+                         out_dtype=torch.int32)
+        assert n.dtype == torch.int32
+        assert torch.equal(a[0], n.long()) and torch.equal(a[1], e.long()), mode
 
 
 def test_c3_full_size_properties(cuda):
