@@ -249,7 +249,8 @@ def test_int32_output(rule, cuda):
                               rule=rule)
     assert torch.equal(a[0], c.long())
     for mode in ("direct", "csr", "records"):
-        n, e = _abi_walk(rowptr, col, start, 21, 0.5, 2.0, 5, rule, 2, mode,
+        rule_id = {name: k for k, name in RULE_NAME.items()}[rule]
+        n, e = _abi_walk(rowptr, col, start, 21, 0.5, 2.0, 5, rule_id, 2, mode,
                          out_dtype=torch.int32)
         assert n.dtype == torch.int32
         assert torch.equal(a[0], n.long()) and torch.equal(a[1], e.long()), mode
