@@ -162,7 +162,7 @@ int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes,
  * step, trial)): word 0 picks the candidate as in mlxc_random_walk, word 1
  * gives r = (x1 >> 8) * 2^-24 for the acceptance test against the FP64
  * constants of BiasedRandomWalk.cpp:52-55.  `rows` is one of MLXC_ROWS_*:
- * sorted rows are searched through a block index, unsorted rows scanned
+ * sorted rows are searched through a 16-ary index, unsorted rows scanned
  * linearly as the reference does; MLXC_ROWS_DETECT decides on the device in
  * the call's preparation pass, which also validates the whole CSR (status
  * bits as for the walk).
