@@ -98,7 +98,7 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool active) {
 }
 
 __device__ __forceinline__ bool is_leader(uint64_t peers) {
-    return __lane_id() == __ffsll(static_cast<long long>(peers)) - 1;
+    return static_cast<int>(__lane_id()) == __ffsll(static_cast<long long>(peers)) - 1;
 }
 
 template <int kOp>

@@ -130,7 +130,7 @@ __device__ __forceinline__ int64_t queue_take(WaveQueue& q, bool need,
         // same lane's value, whatever the exec mask.
         const uint64_t active = __ballot(true);
         int64_t base = 0;
-        if (__lane_id() == __ffsll(static_cast<long long>(active)) - 1)
+        if (static_cast<int>(__lane_id()) == __ffsll(static_cast<long long>(active)) - 1)
             base = static_cast<int64_t>(atomicAdd(counter, static_cast<unsigned long long>(kQueueChunk)));
         base = wave_bcast(base);
         id = rank < avail ? q.next + rank : base + (rank - avail);
