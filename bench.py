@@ -41,6 +41,10 @@ CONFIGS = {
     "c3": ("node2vec p=0.5 q=2 on symmetrized R-MAT 2^20, 4 walks/node, L=40", "node2vec",
            dict(scale=20, samples=1 << 24, symmetrize=True), 4, 40,
            dict(p=0.5, q=2.0, seed=3, rule="ref_chain")),
+    "c3y": ("node2vec p=0.5 q=2 on symmetrized R-MAT 2^20, 4 walks/node, L=40, with the "
+            "symmetric-graph hint (the neighbour test searches the shorter row; same walks as c3)",
+            "node2vec", dict(scale=20, samples=1 << 24, symmetrize=True), 4, 40,
+            dict(p=0.5, q=2.0, seed=3, rule="ref_chain", symmetric=True)),
     "c4": ("R-MAT 2^24 uniform walk, 1 walk/node, L=20", "uniform",
            dict(scale=24, samples=1 << 28, symmetrize=False), 1, 20, {}),
     "c5": ("node2vec p=4 q=0.25 (reference chain) on BA 4M nodes m=20 + 64 hubs of 500K, "
@@ -49,6 +53,10 @@ CONFIGS = {
     "c5x": ("node2vec p=4 q=0.25 (analytic rule) on BA 4M nodes m=20 + 64 hubs of 500K, "
             "2 walks/node, L=30", "node2vec", dict(ba=(4_000_000, 20, 64, 500_000)), 2, 30,
             dict(p=4.0, q=0.25, seed=5, rule="node2vec")),
+    "c5xy": ("node2vec p=4 q=0.25 (analytic rule) on BA 4M nodes m=20 + 64 hubs of 500K, "
+             "2 walks/node, L=30, with the symmetric-graph hint (same walks as c5x)", "node2vec",
+             dict(ba=(4_000_000, 20, 64, 500_000)), 2, 30,
+             dict(p=4.0, q=0.25, seed=5, rule="node2vec", symmetric=True)),
 }
 RULE_ID = {"ref_chain": 0, "node2vec": 1}
 
@@ -569,7 +577,8 @@ def main():
     else:
         rand = None
         step = lambda: mc.rejection_sampling(rowptr, col, start, L, extra["p"], extra["q"],
-                                             seed=extra["seed"], rule=extra["rule"])
+                                             seed=extra["seed"], rule=extra["rule"],
+                                             symmetric=extra.get("symmetric", False))
 
     for _ in range(args.warmup):
         out = step()

@@ -54,6 +54,12 @@ extern "C" {
 #define MLXC_ROWS_UNSORTED 0  /* scan rows linearly, as the reference's is_neighbor does */
 #define MLXC_ROWS_SORTED 1    /* the caller promises every row is sorted ascending */
 #define MLXC_ROWS_DETECT 2    /* the call checks the rows on the device (and validates the CSR) */
+/* OR-ed into one of the three above: the caller promises the graph is
+ * symmetric (every (u, v) entry has a (v, u) entry), so that "t in row(x)"
+ * equals "x in row(t)" and the neighbour test may search the shorter row.
+ * Results are those of the reference when the promise holds, unspecified
+ * otherwise.  Record kernels only; the other paths ignore it. */
+#define MLXC_ROWS_SYMMETRIC 4
 
 /* Bits written by mlxc_csr_check. */
 #define MLXC_CSR_BAD_ROWPTR 1   /* rowptr[0] != 0, rowptr[V] != E, or decreasing */

@@ -27,6 +27,7 @@ MLXC_RULE_NODE2VEC_EXACT = 1
 MLXC_ROWS_UNSORTED = 0
 MLXC_ROWS_SORTED = 1
 MLXC_ROWS_DETECT = 2
+MLXC_ROWS_SYMMETRIC = 4
 MLXC_CSR_BAD_ROWPTR = 1
 MLXC_CSR_BAD_COL = 2
 MLXC_CSR_UNSORTED = 4

@@ -93,9 +93,11 @@ int n2v_params(double p, double q, uint64_t seed, int32_t rule, int32_t rows, N2
     if (rule != MLXC_RULE_REF_CHAIN && rule != MLXC_RULE_NODE2VEC_EXACT)
         return fail(MLXC_ERR_INVALID_ARGUMENT,
                     "rule must be MLXC_RULE_REF_CHAIN or MLXC_RULE_NODE2VEC_EXACT");
-    if (rows != MLXC_ROWS_UNSORTED && rows != MLXC_ROWS_SORTED && rows != MLXC_ROWS_DETECT)
+    const int32_t order = rows & ~MLXC_ROWS_SYMMETRIC;
+    if (order != MLXC_ROWS_UNSORTED && order != MLXC_ROWS_SORTED && order != MLXC_ROWS_DETECT)
         return fail(MLXC_ERR_INVALID_ARGUMENT,
-                    "rows must be MLXC_ROWS_UNSORTED, MLXC_ROWS_SORTED or MLXC_ROWS_DETECT");
+                    "rows must be MLXC_ROWS_UNSORTED, MLXC_ROWS_SORTED or MLXC_ROWS_DETECT, "
+                    "optionally with MLXC_ROWS_SYMMETRIC");
     const double max_prob = std::fmax(std::fmax(1. / p, 1.), 1. / q);
     prm.prob0 = 1. / p / max_prob;
     prm.prob1 = 1. / max_prob;
@@ -103,7 +105,8 @@ int n2v_params(double p, double q, uint64_t seed, int32_t rule, int32_t rows, N2
     prm.key0 = static_cast<uint32_t>(seed);
     prm.key1 = static_cast<uint32_t>(seed >> 32);
     prm.rule = rule;
-    prm.rows = rows;
+    prm.rows = order;
+    prm.symmetric = (rows & MLXC_ROWS_SYMMETRIC) != 0;
     prm.out_type = MLXC_OUT_INT64;
     return MLXC_OK;
 }

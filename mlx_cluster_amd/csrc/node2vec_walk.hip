@@ -242,6 +242,7 @@ struct N2VRecArgs {
     const EdgeRecord* init;   // [num_walks]
     IndexLevels index;        // search index (level 0 = col32)
     int32_t rows;             // MLXC_ROWS_*; DETECT reads the prep pass's counts in work[2..3]
+    int32_t symmetric;        // the graph is symmetric: search the shorter row
     double prob0, prob1, prob2;
     uint32_t key0, key1;
 };
@@ -263,6 +264,23 @@ __device__ __forceinline__ int n2v_decide(const N2VRecArgs& a, double r, int32_t
     if (lt1 && lt2) return 1;
     if (!lt1 && !lt2) return 0;
     return -1;
+}
+
+// The row the neighbour test searches: t in row(x), as the reference does
+// (BiasedRandomWalk.cpp:20-28); on a graph the caller declared symmetric,
+// x in row(t) when that row is shorter (the same answer there).
+__device__ __forceinline__ void n2v_search_rows(int32_t symmetric, int32_t x, int32_t bx,
+                                                int32_t dx, int32_t t, int32_t bt, int32_t dt,
+                                                int32_t& lo, int32_t& hi, int32_t& tgt) {
+    if (symmetric && dt < dx) {
+        lo = bt;
+        hi = bt + dt;
+        tgt = x;
+    } else {
+        lo = bx;
+        hi = bx + dx;
+        tgt = t;
+    }
 }
 
 // Decision once the search has answered whether t is in row(x).
@@ -311,7 +329,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     int32_t x = 0, bx = 0, dx = 0;   // candidate node and its row (from its record)
     int lvl = 0;            // search: index level of the block to read next
     int32_t blk = 0;        // search: that block (kN2vLevel)
-    int32_t lo = 0, hi = 0; // search: col32 positions that can still hold t
+    int32_t lo = 0, hi = 0; // search: col32 positions that can still hold tgt
+    int32_t tgt = 0;        // search: the node looked for (t in row(x), or x in row(t))
     float r = 0.0f;         // acceptance uniform of the current trial
     OutWin<int32_t> ow;
     OutWin<int32_t> ew;     // edge ids (kEdges): e_out[n*L + l] is step l's edge
@@ -436,8 +455,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                 accept = n2v_resolve<kRule>(a, static_cast<double>(r), false);
                 next_trial = !accept;
             } else {
-                lo = bx;
-                hi = bx + dx;
+                n2v_search_rows(a.symmetric, x, bx, dx, t, bt, dt, lo, hi, tgt);
                 if (!sorted) {
                     phase = kN2vScan;
                 } else {
@@ -466,8 +484,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                     accept = n2v_resolve<kRule>(a, static_cast<double>(r), false);
                     next_trial = !accept;
                 } else {
-                    lo = bx;
-                    hi = bx + dx;
+                    n2v_search_rows(a.symmetric, x, bx, dx, t, bt, dt, lo, hi, tgt);
                     if (!sorted) {
                         phase = kN2vScan;
                     } else {
@@ -484,8 +501,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             int32_t vals[kSearchBlock];
 #pragma unroll
             for (int i = 0; i < kSearchBlock; ++i) vals[i] = qb[i / 4][i % 4];
-            const int res = ph == kN2vLevel ? level_step(vals, t, lvl, blk, lo, hi)
-                                            : scan_step(vals, t, lo, hi);
+            const int res = ph == kN2vLevel ? level_step(vals, tgt, lvl, blk, lo, hi)
+                                            : scan_step(vals, tgt, lo, hi);
             if (res >= 0) {
                 accept = n2v_resolve<kRule>(a, static_cast<double>(r), res == 1);
                 next_trial = !accept;
@@ -698,6 +715,7 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         a.key0 = p.key0;
         a.key1 = p.key1;
         a.rows = p.rows;
+        a.symmetric = p.symmetric;
         const bool edges = w.e_out != nullptr;
         if (records) {
             if (p.rule == MLXC_RULE_REF_CHAIN)

@@ -91,7 +91,8 @@ struct N2VParams {
     double prob0, prob1, prob2;  // acceptance constants, BiasedRandomWalk.cpp:52-55
     uint32_t key0, key1;         // Philox key (the seed)
     int32_t rule;                // MLXC_RULE_*
-    int32_t rows;                // MLXC_ROWS_*
+    int32_t rows;                // MLXC_ROWS_UNSORTED / SORTED / DETECT
+    int32_t symmetric;           // MLXC_ROWS_SYMMETRIC was given
     int32_t out_type;            // MLXC_OUT_*
 };
 // Share of acceptance draws r for which a trial may need the row search.

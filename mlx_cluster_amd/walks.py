@@ -283,7 +283,7 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
                        seed: Optional[int] = None, rule: str = "ref_chain",
                        rows_sorted: Optional[bool] = None, return_edges: bool = False,
                        check: bool = True, threads: Optional[int] = None,
-                       out_dtype: torch.dtype = torch.int64
+                       out_dtype: torch.dtype = torch.int64, symmetric: bool = False
                        ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """node2vec random walks by rejection sampling.
 
@@ -309,6 +309,12 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
             preparation pass, which also validates the whole graph (a
             malformed graph raises ValueError when check=True).
         return_edges, check, threads, out_dtype: as in random_walk.
+        symmetric: the caller promises the graph is symmetric (every (u, v)
+            has its (v, u), as to_csr(symmetrize=True) makes): the neighbour
+            test then searches the shorter of row(x) and row(t), which gives
+            the same answer there.  False (the default) searches row(x), as
+            the reference does; on a graph that is not symmetric True gives
+            unspecified walks.
     """
     L = _walk_length(walk_length)
     otype = _out_type(out_dtype)
@@ -324,6 +330,8 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     seed = int(seed) & (2**64 - 1)
     rows = (_lib.MLXC_ROWS_DETECT if rows_sorted is None else
             _lib.MLXC_ROWS_SORTED if rows_sorted else _lib.MLXC_ROWS_UNSORTED)
+    if symmetric:
+        rows |= _lib.MLXC_ROWS_SYMMETRIC
     N = start.numel()
     if _on_cpu(stream):
         rowptr, col, start = (_host(t) for t in (rowptr, col, start))

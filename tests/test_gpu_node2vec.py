@@ -60,6 +60,8 @@ def gpu_walk(rowptr, col, start, L, p, q, seed, rule, cuda, **kw):
     np.testing.assert_array_equal(n_rec.cpu().numpy(), n.cpu().numpy(),
                                   err_msg="record walk: nodes differ with edge output")
     rows = {None: 2, True: 1, False: 0}[kw.get("rows_sorted")]
+    if kw.get("symmetric"):
+        rows |= 4  # MLXC_ROWS_SYMMETRIC
     for mode in ("direct", "csr", "records"):
         nm, em = _abi_walk(*args[:3], L, p, q, seed, rule, rows, mode)
         np.testing.assert_array_equal(nm.cpu().numpy(), n.cpu().numpy(),
@@ -184,6 +186,29 @@ def test_return_dominated_walks(rule, cuda):
     start = np.arange(rowptr.size - 1)
     for p, q in ((1e-3, 1.0), (0.5, 2.0), (0.25, 0.5)):
         assert_parity(rowptr, col, start, 15, p, q, 8, rule, cuda)
+
+
+@pytest.mark.parametrize("p,q", [(0.5, 2.0), (2.0, 0.5), (1.0, 3.0), (4.0, 0.25)])
+@pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
+def test_symmetric_hint(p, q, rule, cuda):
+    """symmetric=True (MLXC_ROWS_SYMMETRIC) on symmetric graphs: the shorter
+    of row(x) and row(t) is searched, with the oracle's results (which search
+    row(x)), in every mode; sorted and unsorted rows."""
+    rowptr, col = synth.rmat_csr(12, 40_000, seed=17, symmetrize=True)
+    rowptr, col = rowptr.numpy(), col.numpy()
+    V = rowptr.size - 1
+    start = np.arange(2 * V) % V
+    _, counts = assert_parity(rowptr, col, start, 20, p, q, 99, rule, cuda, symmetric=True)
+    if (p, q) == (0.5, 2.0):
+        assert counts["member_tests"] > 1000
+    rng = np.random.default_rng(8)
+    rowptr, col = undirected(300, rng.integers(0, 300, (2500, 2)), sort=False)
+    start = np.arange(600) % 300
+    assert_parity(rowptr, col, start, 8, p, q, 5, rule, cuda, sorted_rows=False,
+                  rows_sorted=False, symmetric=True)
+    rowptr, col = synth.ba_hub_csr(20_000, 5, 4, 5_000, seed=3)
+    rowptr, col = rowptr.numpy(), col.numpy()
+    assert_parity(rowptr, col, np.arange(20_000), 12, p, q, 55, rule, cuda, symmetric=True)
 
 
 def test_csr_check_matches_oracle(cuda):

@@ -109,6 +109,31 @@ def test_node2vec_unsorted_rows_detected():
             np.testing.assert_array_equal(e, e_ref)
 
 
+def test_symmetric_flag_is_accepted_and_checked():
+    """MLXC_ROWS_SYMMETRIC combines with the row orders; the host twin gives
+    the same walks (it always searches row(x)); other bits are rejected."""
+    rowptr, col = synth.rmat_csr(10, 12000, seed=21, symmetrize=True)
+    start = torch.arange(2000) % (rowptr.numel() - 1)
+    a = mc.rejection_sampling(rowptr, col, start, 10, 0.5, 2.0, seed=4, stream="cpu")
+    b = mc.rejection_sampling(rowptr, col, start, 10, 0.5, 2.0, seed=4, stream="cpu",
+                              symmetric=True)
+    assert torch.equal(a, b)
+    from mlx_cluster_amd import _lib
+    lib = _lib.load()
+    out = torch.empty((1, 3), dtype=torch.int64)
+    ptr = lambda t: t.data_ptr()
+    for rows in (3, 7, 8, -1):
+        rc = lib.mlxc_rejection_sampling_cpu(ptr(rowptr), rowptr.numel() - 1, ptr(col), col.numel(),
+                                             ptr(start), 1, 2, 1.0, 1.0, 1, 0, rows, ptr(out), None,
+                                             _lib.MLXC_OUT_INT64, 1, None)
+        assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT, rows
+    for rows in (4, 5, 6):
+        rc = lib.mlxc_rejection_sampling_cpu(ptr(rowptr), rowptr.numel() - 1, ptr(col), col.numel(),
+                                             ptr(start), 1, 2, 1.0, 1.0, 1, 0, rows, ptr(out), None,
+                                             _lib.MLXC_OUT_INT64, 1, None)
+        assert rc == _lib.MLXC_OK, rows
+
+
 def test_trial_cap_matches_oracle():
     rowptr, col = undirected(40, [(i, (i * 7 + 3) % 40) for i in range(40)] +
                              [(i, (i * 11 + 5) % 40) for i in range(40)])
