@@ -30,6 +30,9 @@ LINE = 64  # bytes charged per dependent random read
 
 CONFIGS = {
     # name: (description, kind, graph builder args, walks per node, L, extra)
+    "c1": ("Cora-like graph (2,708 nodes, 10,556 entries), 2,000 uniform walks, L=5: the "
+           "reference tests' workload, bound by launch latency", "uniform", dict(cora=True), 1, 5,
+           dict(num_walks=2000)),
     "c2": ("R-MAT 2^20 uniform walk, 10 walks/node, L=80", "uniform",
            dict(scale=20, samples=1 << 24, symmetrize=False), 10, 80, {}),
     "c2s": ("R-MAT 2^20 uniform walk, 10 walks/node, L=80, uniforms generated in the kernel "
@@ -550,7 +553,9 @@ def main():
 
     desc, kind, gargs, per_node, L, extra = CONFIGS[args.config]
     log(f"config {args.config}: {desc} on {torch.cuda.get_device_name(dev)}")
-    if "ba" in gargs:
+    if "cora" in gargs:
+        rowptr, col = (torch.from_numpy(a).to(dev) for a in synth.cora_like(seed=0))
+    elif "ba" in gargs:
         nodes, m, hubs, hub_degree = gargs["ba"]
         rowptr, col = synth.ba_hub_csr(nodes, m, hubs, hub_degree, seed=0, device=dev)
     else:
@@ -558,7 +563,7 @@ def main():
                                      symmetrize=gargs["symmetrize"])
     V = rowptr.numel() - 1
     E = col.numel()
-    N = per_node * V
+    N = extra.get("num_walks", per_node * V)
     start = torch.arange(N, device=dev, dtype=torch.int64) % V
     torch.cuda.synchronize()
     log(f"graph V={V} E={E}; walks N={N} L={L}")
