@@ -650,7 +650,8 @@ N2VLayout n2v_layout(int64_t num_edges, int64_t num_walks, bool records) {
 bool n2v_records_pay_off(int64_t num_edges, int64_t num_walks, int32_t walk_length,
                          double search_width) {
     const double steps = static_cast<double>(num_walks) * static_cast<double>(walk_length);
-    return steps * (1.0 + 4.0 * search_width) >= 4.0 * static_cast<double>(num_edges);
+    return steps * (1.0 + 4.0 * search_width) >= 4.0 * static_cast<double>(num_edges) ||
+           num_edges <= kSmallGraphEdgesPerStep * walk_length;  // small graphs, as for the uniform walk
 }
 
 }  // namespace

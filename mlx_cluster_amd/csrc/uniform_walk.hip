@@ -475,9 +475,13 @@ namespace {
 enum class UniformMode { kRecords, kCsr, kPlain };
 
 // Edge records cost one random read per edge to build; they pay off when the
-// call takes several steps per edge.
+// call takes several steps per edge, or when the graph is small enough that
+// the build is cheaper than a read per step of one walk's chain.  Measured
+// on MI355X with the Cora-like graph (10,556 entries): 2,000 walks of 5
+// steps 52 us with the CSR walk; 1,280 walks of 20 steps 171 us.
 bool records_pay_off(int64_t num_edges, int64_t num_walks, int32_t walk_length) {
-    return num_walks * static_cast<int64_t>(walk_length) >= 4 * num_edges;
+    return num_walks * static_cast<int64_t>(walk_length) >= 4 * num_edges ||
+           num_edges <= kSmallGraphEdgesPerStep * walk_length;
 }
 
 size_t record_bytes(int64_t num_edges, int64_t num_walks) {

@@ -54,6 +54,12 @@ int persistent_grid(Kernel kernel, int64_t num_walks, int slots, int& grid, int 
     return MLXC_OK;
 }
 
+// Graphs small enough that building their edge records (one parallel pass,
+// about E / 3e10 s) costs less than the dependent read per step it saves on
+// the walk's serial chain (about 1 us per step when few walks run): records
+// then pay off whatever the number of walks.
+constexpr int64_t kSmallGraphEdgesPerStep = 32768;
+
 // Node ids and edge offsets fit the int32 fields of the record layouts.
 inline bool records_fit(int64_t num_nodes, int64_t num_edges) {
     return num_nodes <= INT32_MAX && num_edges <= INT32_MAX;

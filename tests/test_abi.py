@@ -123,8 +123,12 @@ def test_other_entry_points_reject_bad_arguments():
 
 def test_workspace_size_query():
     q = _lib.load().mlxc_random_walk_workspace_bytes
-    assert q(10, 100, 100, 4) == 256 + 16 * 200   # 400 steps >= 4 * 100 edges: records
-    assert q(10, 100, 99, 4) == 256 + 16 * 99     # 396 steps < 400: start records only
+    E = 10**6                                     # above the small-graph size 32768 * 4
+    assert q(10, E, E, 4) == 256 + 16 * 2 * E     # 4E steps >= 4 * E edges: records
+    assert q(10, E, E - 1, 4) == 256 + 16 * (E - 1)  # fewer steps: start records only
+    assert q(10, 32768 * 4, 1, 4) == 256 + 16 * (32768 * 4 + 1)   # small graph: records
+    assert q(10, 32768 * 4 + 1, 1, 4) == 256 + 16 * 1
+    assert q(10, 100, 1, 4) == 256 + 16 * 101
     assert q(10, 0, 0, 0) == 256 + 16 * 0
     assert q(2**31, 5, 1, 1) == 32
     assert q(5, 2**31, 1, 1) == 32
