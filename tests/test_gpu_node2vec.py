@@ -188,6 +188,31 @@ def test_return_dominated_walks(rule, cuda):
         assert_parity(rowptr, col, start, 15, p, q, 8, rule, cuda)
 
 
+@pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
+def test_return_biased_graph_shapes(rule, cuda):
+    """p < 1, where most trials can only accept a return to t: a directed
+    graph (many edges without a reverse), a symmetric graph with self-loops,
+    and a multigraph whose rows hold some nodes twice must all match the
+    oracle, in every mode."""
+    rowptr, col = synth.rmat_csr(11, 20_000, seed=6)
+    rowptr, col = rowptr.numpy(), col.numpy()
+    V = rowptr.size - 1
+    start = np.arange(2 * V) % V
+    _, counts = assert_parity(rowptr, col, start, 12, 0.25, 4.0, 31, rule, cuda)
+    assert counts["trials"] > 2 * counts["moving_steps"]
+    rng = np.random.default_rng(12)
+    pairs = np.unique(np.sort(rng.integers(0, 300, (2500, 2)), axis=1), axis=0)
+    loops = np.stack([np.arange(0, 300, 7)] * 2, axis=1)
+    pairs = pairs[pairs[:, 0] != pairs[:, 1]]
+    rowptr, col = csr(300, np.concatenate([pairs, pairs[:, ::-1], loops]))
+    assert np.all((np.diff(col) != 0) | (np.diff(np.repeat(np.arange(300), np.diff(rowptr)))) != 0)
+    start = np.arange(900) % 300
+    for p, q in ((0.3, 1.0), (0.05, 2.0)):
+        assert_parity(rowptr, col, start, 16, p, q, 4, rule, cuda)
+    rowptr, col = csr(300, np.concatenate([pairs, pairs[:, ::-1], pairs[:5]]))  # 5 duplicates
+    assert_parity(rowptr, col, start, 16, 0.3, 1.0, 4, rule, cuda)
+
+
 @pytest.mark.parametrize("p,q", [(0.5, 2.0), (2.0, 0.5), (1.0, 3.0), (4.0, 0.25)])
 @pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
 def test_symmetric_hint(p, q, rule, cuda):
