@@ -399,6 +399,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
         const int64_t g0 = n * L1;
         const int64_t e0 = n * L;  // edge output index of the walk's step 0
         bool push = false, fill = false, flush = false, accept = false, next_trial = false;
+        bool draw = false;  // draw trial `trial` of step l from v's row (bv, dv)
         int64_t g = g0 + l;  // output index of the last buffered entry
         if (ph == kN2vStart) {
             ow.count = 0;
@@ -416,10 +417,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                 // first step: uniform, no acceptance test (BiasedRandomWalk.cpp:60-66)
                 bv = rec.y;
                 dv = rec.z;
-                float u0;
-                n2v_uniforms(n, 0, 0u, a.key0, a.key1, u0, r);
-                e = bv + static_cast<int32_t>(pick_index(u0, dv));
                 trial = 0;
+                draw = true;
                 phase = kN2vCand;
             }
         } else if (kCsr && ph == kN2vCand) {
@@ -524,9 +523,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                     phase = kN2vRow;
                 }
             } else {
-                float u0;
-                n2v_uniforms(n, l, trial, a.key0, a.key1, u0, r);
-                e = bv + static_cast<int32_t>(pick_index(u0, dv));
+                draw = true;
                 phase = kN2vCand;
             }
         }
@@ -547,15 +544,19 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                 fill = true;
             } else {
                 trial = 0;
-                if (dv == 1) {
+                if (dv == 1)
                     e = bv;  // forced: no draw
-                } else {
-                    float u0;
-                    n2v_uniforms(n, l, 0u, a.key0, a.key1, u0, r);
-                    e = bv + static_cast<int32_t>(pick_index(u0, dv));
-                }
+                else
+                    draw = true;
                 phase = kN2vCand;
             }
+        }
+        // The trial's candidate and r: one Philox call site for the three
+        // places that draw (a wavefront executes each site any lane needs).
+        if (draw) {
+            float u0;
+            n2v_uniforms(n, l, trial, a.key0, a.key1, u0, r);
+            e = bv + static_cast<int32_t>(pick_index(u0, dv));
         }
         if (push) ow_push(ow, nout, g, v);
         if (fill) {
