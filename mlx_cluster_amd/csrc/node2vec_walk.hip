@@ -1,5 +1,8 @@
 // node2vec walk by rejection sampling (BiasedRandomWalk.cpp:52-100) and its
 // launcher.  The reference has no GPU version (BiasedRandomWalk.cpp:150-155).
+#include <cmath>
+#include <limits>
+
 #include "walk_host.h"
 
 namespace mlxc {
@@ -243,9 +246,19 @@ struct N2VRecArgs {
     IndexLevels index;        // search index (level 0 = col32)
     int32_t rows;             // MLXC_ROWS_*; DETECT reads the prep pass's counts in work[2..3]
     int32_t symmetric;        // the graph is symmetric: search the shorter row
-    double prob0, prob1, prob2;
+    // The acceptance probabilities as the smallest floats >= prob0, prob1,
+    // prob2: for a float r, r < prob_k (in double, as the reference compares)
+    // exactly when r < thr_k.
+    float thr0, thr1, thr2;
     uint32_t key0, key1;
 };
+
+// Smallest float >= p (p > 0), the float threshold of N2VRecArgs.
+static float float_at_or_above(double p) {
+    float f = static_cast<float>(p);
+    if (static_cast<double>(f) < p) f = std::nextafter(f, std::numeric_limits<float>::infinity());
+    return f;
+}
 
 // Decision on candidate x for r before any row search: 1 accept, 0 reject,
 // -1 the answer depends on whether t is in row(x).  The reference's chain
@@ -253,14 +266,14 @@ struct N2VRecArgs {
 // has no side effects, so its cheap terms decide first; the analytic rule
 // uses p0 when x == t, else p1 or p2 by adjacency.
 template <int kRule>
-__device__ __forceinline__ int n2v_decide(const N2VRecArgs& a, double r, int32_t x, int32_t t) {
+__device__ __forceinline__ int n2v_decide(const N2VRecArgs& a, float r, int32_t x, int32_t t) {
     if (kRule == MLXC_RULE_REF_CHAIN) {
-        if (r < a.prob2) return 1;
-        if (x == t && r < a.prob0) return 1;
-        return r < a.prob1 ? -1 : 0;
+        if (r < a.thr2) return 1;
+        if (x == t && r < a.thr0) return 1;
+        return r < a.thr1 ? -1 : 0;
     }
-    if (x == t) return r < a.prob0 ? 1 : 0;
-    const bool lt1 = r < a.prob1, lt2 = r < a.prob2;
+    if (x == t) return r < a.thr0 ? 1 : 0;
+    const bool lt1 = r < a.thr1, lt2 = r < a.thr2;
     if (lt1 && lt2) return 1;
     if (!lt1 && !lt2) return 0;
     return -1;
@@ -285,9 +298,9 @@ __device__ __forceinline__ void n2v_search_rows(int32_t symmetric, int32_t x, in
 
 // Decision once the search has answered whether t is in row(x).
 template <int kRule>
-__device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, double r, bool adjacent) {
+__device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, float r, bool adjacent) {
     if (kRule == MLXC_RULE_REF_CHAIN) return adjacent;  // only searched when r < p1 decides
-    return adjacent ? (r < a.prob1) : (r < a.prob2);
+    return adjacent ? (r < a.thr1) : (r < a.thr2);
 }
 
 // node2vec walk over edge records (num_nodes, num_edges below 2^31; n_out and
@@ -314,12 +327,18 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     const bool sorted = a.rows == MLXC_ROWS_SORTED ||
                         (a.rows == MLXC_ROWS_DETECT && a.w.work[2] == a.w.work[3]);
     const int64_t L = a.w.walk_length;
-    const int64_t L1 = L + 1;
     const int64_t N = a.w.num_walks;
+    // the index levels lie after level 0 in one workspace: 32-bit offsets
+    // (in entries) select a lane's level more cheaply than 64-bit pointers
+    uint32_t level_off[kMaxLevels];
+#pragma unroll
+    for (int k = 0; k < kMaxLevels; ++k)
+        level_off[k] = k < a.index.count ? static_cast<uint32_t>(a.index.level[k] - a.index.level[0]) : 0u;
     unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.w.work + 1);
     WaveQueue q{0, 0};
     int phase = kN2vIdle;
     int64_t n = 0;
+    int64_t e0 = 0, g0 = 0; // output index of the walk's edge 0 (n L) and node 0 (n (L + 1))
     int32_t l = 0;          // steps done
     uint32_t trial = 0;
     int32_t t = 0, bt = 0, dt = 0;   // previous node and (CSR mode) its row
@@ -357,11 +376,11 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
         } else if (kCsr && ph == kN2vRow) {
             bp = reinterpret_cast<const int32_t*>(a.w.rowptr + x);  // 8-byte aligned
         } else if (ph == kN2vLevel) {
-            const int32_t* lp = a.index.level[0];
+            uint32_t off = 0;  // level lvl's offset from level 0, in entries
 #pragma unroll
             for (int k = 1; k < kMaxLevels; ++k)
-                if (lvl == k) lp = a.index.level[k];
-            bp = lp + static_cast<int64_t>(kSearchBlock) * blk;
+                if (lvl == k) off = level_off[k];
+            bp = a.index.level[0] + off + static_cast<int64_t>(kSearchBlock) * blk;
         } else if (ph == kN2vScan) {
             bp = a.index.level[0] + (lo & ~(kSearchBlock - 1));
         } else {
@@ -388,6 +407,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
         if (need) {
             n = id;
             l = 0;
+            e0 = n * L;
+            g0 = e0 + n;
             phase = id < N ? kN2vStart : kN2vDone;
         }
         if (!__any(phase != kN2vDone)) break;
@@ -396,8 +417,6 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
         const i32x4 rec = qb[0];
 
         // 3. Consume.
-        const int64_t g0 = n * L1;
-        const int64_t e0 = n * L;  // edge output index of the walk's step 0
         bool push = false, fill = false, flush = false, accept = false, next_trial = false;
         bool draw = false;  // draw trial `trial` of step l from v's row (bv, dv)
         int64_t g = g0 + l;  // output index of the last buffered entry
@@ -425,7 +444,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             const int k = e & 3;
             x = k == 0 ? rec.x : k == 1 ? rec.y : k == 2 ? rec.z : rec.w;
             int d = 1;  // first step and forced steps accept
-            if (!(l == 0 || dv == 1)) d = n2v_decide<kRule>(a, static_cast<double>(r), x, t);
+            if (!(l == 0 || dv == 1)) d = n2v_decide<kRule>(a, r, x, t);
             if (static_cast<uint32_t>(x) >= static_cast<uint32_t>(a.w.num_nodes)) {
                 status |= MLXC_STATUS_BAD_NODE;  // (col32 holds -1 for any bad col)
                 fill = true;
@@ -451,7 +470,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             } else if (row_then == kRowAccept) {
                 accept = true;
             } else if (dx == 0) {
-                accept = n2v_resolve<kRule>(a, static_cast<double>(r), false);
+                accept = n2v_resolve<kRule>(a, r, false);
                 next_trial = !accept;
             } else {
                 n2v_search_rows(a.symmetric, x, bx, dx, t, bt, dt, lo, hi, tgt);
@@ -474,13 +493,13 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             } else if (l == 0 || dv == 1) {
                 accept = true;  // first step, or a forced step (BiasedRandomWalk.cpp:76-78)
             } else {
-                const int d = n2v_decide<kRule>(a, static_cast<double>(r), x, t);
+                const int d = n2v_decide<kRule>(a, r, x, t);
                 if (d == 1) {
                     accept = true;
                 } else if (d == 0) {
                     next_trial = true;
                 } else if (dx == 0) {
-                    accept = n2v_resolve<kRule>(a, static_cast<double>(r), false);
+                    accept = n2v_resolve<kRule>(a, r, false);
                     next_trial = !accept;
                 } else {
                     n2v_search_rows(a.symmetric, x, bx, dx, t, bt, dt, lo, hi, tgt);
@@ -503,7 +522,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             const int res = ph == kN2vLevel ? level_step(vals, tgt, lvl, blk, lo, hi)
                                             : scan_step(vals, tgt, lo, hi);
             if (res >= 0) {
-                accept = n2v_resolve<kRule>(a, static_cast<double>(r), res == 1);
+                accept = n2v_resolve<kRule>(a, r, res == 1);
                 next_trial = !accept;
             }
         }
@@ -711,9 +730,9 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         a.recs = recs;
         a.init = init;
         a.index = index;
-        a.prob0 = p.prob0;
-        a.prob1 = p.prob1;
-        a.prob2 = p.prob2;
+        a.thr0 = float_at_or_above(p.prob0);
+        a.thr1 = float_at_or_above(p.prob1);
+        a.thr2 = float_at_or_above(p.prob2);
         a.key0 = p.key0;
         a.key1 = p.key1;
         a.rows = p.rows;
