@@ -156,7 +156,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
     int32_t l[W], e[W];        // e: record index read this iteration (kSlotWalk)
     int64_t fr[W];             // rand index whose block the next read brings along
     bool need_block[W];        // ... if set
-    RandWindow<RW> rw[W];
+    LdsWindow<RW> rw[W];
+    __shared__ float rand_area[W][RW][kBlock];
     OutWin<int32_t> ow[W];
     OutWin<int32_t> ew[W];     // edge ids (kEdges): e_out[n*L + l] is step l's edge
     __shared__ WaveStage stage[kBlock / kWave];
@@ -171,6 +172,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
         e[s] = 0;
         fr[s] = 0;
         need_block[s] = false;
+        rw[s].pos = 0;
         rw[s].valid = 0;
         ow_init(ow[s]);
         ow_init(ew[s]);
@@ -190,9 +192,10 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                                                        : init;
             rec[s] = *reinterpret_cast<const i32x4*>(p);
         }
+        RandWindow<RW> blk[W];  // due rand blocks, stored to LDS in step 3
 #pragma unroll
         for (int s = 0; s < W; ++s)
-            if (need_block[s]) rw_fetch<RW, kGen>(rw[s], a, fr[s], rtotal);
+            if (need_block[s]) rw_fetch<RW, kGen>(blk[s], a, fr[s], rtotal);
         // ... and the output blocks the last iteration completed are stored.
 #pragma unroll
         for (int s = 0; s < W; ++s) {
@@ -232,10 +235,9 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
             const int64_t g0 = n[s] * L1;  // output index of the walk's start node
             const int64_t g = g0 + l[s] + (ph[s] == kSlotWalk ? 1 : 0);
             if (need_block[s]) {
-                // block holding rand[fr]: shift it so w[0] is that value
+                // the block holding rand[fr]; fr is its entry k
                 const int k = static_cast<int>(fr[s] - rw_base<RW, kGen>(fr[s], rtotal));
-                rw_shift_by(rw[s], k);
-                rw[s].valid = RW - k;
+                lw_store(rand_area[s], rw[s], blk[s], k);
                 need_block[s] = false;
             }
             const int32_t node = rec[s].x, begin = rec[s].y, deg = rec[s].z;
@@ -267,10 +269,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                 if (kEdges && ew[s].count) ow_flush(ew[s], eout, e0 + L - 1);
             } else {
                 // step l (0-based) leaves this node with uniform rand[n*L + l]
-                e[s] = static_cast<int32_t>(begin + pick_index(rw[s].w[0], deg));
+                e[s] = static_cast<int32_t>(begin + pick_index(lw_take(rand_area[s], rw[s]), deg));
                 if (kEdges) ow_push(ew[s], eout, e0 + l[s], e[s]);
-                rw_shift1(rw[s]);
-                rw[s].valid -= 1;
                 need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
                 fr[s] = n[s] * L + l[s] + 1;
                 phase[s] = kSlotWalk;
@@ -304,7 +304,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
     int64_t n[W], fr[W];
     int32_t l[W], e[W], v[W];  // steps, edge and node ids fit in int32 here
     bool need_block[W];
-    RandWindow<RW> rw[W];
+    LdsWindow<RW> rw[W];
+    __shared__ float rand_area[W][RW][kBlock];
     OutWin<int32_t> ow[W];
     OutWin<int32_t> ew[W];     // edge ids (kEdges): e_out[n*L + l] is step l's edge
     __shared__ WaveStage stage[kBlock / kWave];
@@ -320,6 +321,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
         v[s] = 0;
         fr[s] = 0;
         need_block[s] = false;
+        rw[s].pos = 0;
         rw[s].valid = 0;
         ow_init(ow[s]);
         ow_init(ew[s]);
@@ -340,10 +342,11 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
             row[s] = *p;
             if (ph[s] == kSlotCol) cv[s] = a.col[e[s]];
         }
+        RandWindow<RW> blk[W];  // due rand blocks, stored to LDS in step 3
 #pragma unroll
         for (int s = 0; s < W; ++s)  // a block due after a pick travels with the col read
             if (need_block[s] && ph[s] != kSlotRow)
-                rw_fetch<RW, kGen>(rw[s], a, fr[s], rtotal);
+                rw_fetch<RW, kGen>(blk[s], a, fr[s], rtotal);
         // ... and the output blocks the last iteration completed are stored.
 #pragma unroll
         for (int s = 0; s < W; ++s) {
@@ -376,10 +379,9 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                 need_block[s] = phase[s] == kSlotStart && L > 0;
                 continue;
             }
-            if (need_block[s] && ph[s] != kSlotCol) {
+            if (need_block[s] && ph[s] != kSlotRow) {  // the block fetched above
                 const int k = static_cast<int>(fr[s] - rw_base<RW, kGen>(fr[s], rtotal));
-                rw_shift_by(rw[s], k);
-                rw[s].valid = RW - k;
+                lw_store(rand_area[s], rw[s], blk[s], k);
                 need_block[s] = false;
             }
             const int64_t g0 = n[s] * L1;
@@ -433,10 +435,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
             } else if (deg == 0) {
                 fill = true;  // absorbing node: the walk stays
             } else if (deg > 0) {
-                e[s] = static_cast<int32_t>(begin + pick_index(rw[s].w[0], deg));
+                e[s] = static_cast<int32_t>(begin + pick_index(lw_take(rand_area[s], rw[s]), deg));
                 if (kEdges) ow_push(ew[s], eout, eg, e[s]);
-                rw_shift1(rw[s]);
-                rw[s].valid -= 1;
                 need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
                 fr[s] = n[s] * L + l[s] + 1;
                 phase[s] = kSlotCol;

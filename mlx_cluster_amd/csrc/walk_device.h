@@ -164,8 +164,8 @@ struct WalkArgs {
 // through its own row 4 bytes at a time while its 63 neighbours do the same
 // 4*L bytes apart.  Read one float at a time, nearly every step misses L2 and
 // costs a 128-byte line.  Instead each slot keeps the next RW floats of its
-// row in registers, loaded as one aligned RW*4-byte block, so the stream
-// costs one line per RW steps.
+// row at hand (in LDS, LdsWindow below), loaded as one aligned RW*4-byte
+// block, so the stream costs one line per RW steps.
 //
 // The output: walk n writes n_out[n*(L+1) + j] for j = 0..L, one 8-byte entry
 // per step.  Scattered 8-byte stores reach memory as partial 32-byte writes.
@@ -174,17 +174,11 @@ struct WalkArgs {
 // the constant tails of walks that sink in a node of out-degree 0, as whole
 // 64-byte blocks.  The stores are non-temporal: the output is never read
 // back, and streaming it past the caches keeps them for the graph.
+// One block of RW uniforms as read or generated, before it is stored.
 template <int RW>
 struct RandWindow {
     float w[RW];
-    int valid;  // w[0 .. valid-1] are the next uniforms of the walk
 };
-
-template <int RW>
-__device__ __forceinline__ void rw_shift1(RandWindow<RW>& r) {
-#pragma unroll
-    for (int i = 0; i + 1 < RW; ++i) r.w[i] = r.w[i + 1];
-}
 
 // First index of the rand block that serves rand[f]: the aligned block, or for
 // the array's last partial block the last RW values (total must be a multiple
@@ -250,15 +244,37 @@ __device__ __forceinline__ void rw_fetch(RandWindow<RW>& r, const WalkArgs& a, i
     else rw_load_at(r, a.rand, rw_base<RW, kGen>(f, total));
 }
 
+// The walk loops keep each slot's rand window in LDS rather than in
+// registers: a register window must be shifted on every pick and is copied on
+// every control path that changes it, which made the loops VALU-bound.  The
+// area is uniform-major ([position][thread]), so the lanes of a wavefront
+// reading the same position, or any positions, hit distinct banks.  A block
+// arrives in registers (rw_fetch) and is stored once; each pick reads one
+// float.
 template <int RW>
-__device__ __forceinline__ void rw_shift_by(RandWindow<RW>& r, int k) {
+struct LdsWindow {
+    int32_t pos;    // position of the next uniform
+    int32_t valid;  // uniforms left from pos
+};
+
+// Stores a fetched block whose first k entries precede the walk's next uniform.
+template <int RW>
+__device__ __forceinline__ void lw_store(float (&area)[RW][kBlock], LdsWindow<RW>& lw,
+                                         const RandWindow<RW>& blk, int k) {
 #pragma unroll
-    for (int bit = RW / 2; bit >= 1; bit >>= 1) {
-        if (k & bit) {
-#pragma unroll
-            for (int i = 0; i < RW; ++i) r.w[i] = (i + bit < RW) ? r.w[i + bit] : 0.0f;
-        }
-    }
+    for (int i = 0; i < RW; ++i) area[i][threadIdx.x] = blk.w[i];
+    lw.pos = k;
+    lw.valid = RW - k;
+}
+
+// The next uniform of the window (valid > 0).
+template <int RW>
+__device__ __forceinline__ float lw_take(float (&area)[RW][kBlock], LdsWindow<RW>& lw) {
+    static_assert((RW & (RW - 1)) == 0, "RW is a power of two");
+    const float r = area[lw.pos & (RW - 1)][threadIdx.x];
+    lw.pos += 1;
+    lw.valid -= 1;
+    return r;
 }
 
 // Output rows are written in blocks of 8 entries, aligned in the output: 64
