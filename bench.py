@@ -221,8 +221,10 @@ def gather_ceiling(torch, dev):
 
 
 def node2vec_bytes(np, oracle, rowptr_h, col_h, start_h, L, extra, walks=200_000):
-    """SURVEY 8(d) node2vec bytes, 64*(S_move+Z) + 64*T + 64*(Q+P) + 8*N*(L+1) + 8*N, with
-    the counts from the oracle over an evenly strided sample of walks scaled to N."""
+    """Roofline bytes of a node2vec call, 64*(S_move+Z) + 64*T + 64*(Q+P) + 8*N*(L+1) + 8*N
+    (each dependent random read of the reference loop charged one 64-byte line, streams
+    their bytes), with the counts from the oracle over an evenly strided sample of walks
+    scaled to N."""
     N = start_h.shape[0]
     idx = np.linspace(0, N - 1, min(N, walks)).astype(np.int64)
     _, _, st, c = oracle.node2vec_walk(rowptr_h, col_h, start_h[idx], L, extra["p"], extra["q"],
@@ -516,9 +518,9 @@ def main():
                     help="measure independent random 8-byte gathers over tables of several sizes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: the walks need no cross-GPU exchange and this build "
-              "runs on a single MI355X (see DESIGN.md for how the path shards). Use --gpus 1.",
-              file=sys.stderr)
+        print("bench.py measures one GPU: the walks need no cross-GPU exchange, so k GPUs would "
+              "each take N/k of the walks over a replicated CSR, and this build runs on a single "
+              "MI355X. Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
