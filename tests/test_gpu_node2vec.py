@@ -336,3 +336,38 @@ def test_c3_full_size_properties(cuda):
         assert st == 0
         np.testing.assert_array_equal(n[s0:s0 + 2000].cpu().numpy(), ref)
         np.testing.assert_array_equal(e[s0:s0 + 2000].cpu().numpy(), ref_e)
+
+
+@pytest.mark.parametrize("rule", ["ref_chain", "node2vec"])
+def test_c5_full_size_properties(rule, cuda):
+    """Configuration 5 at full size (BA graph of 4,000,000 nodes, m = 20, plus
+    64 hubs of 500,000 neighbours; p = 4, q = 0.25, 2 walks per node, L = 30),
+    with the reference chain (CSR mode: every draw accepts) and the analytic
+    rule (edge records, frequent searches of hub rows).  Every step follows
+    its recorded edge or stays at a node of out-degree 0, and three blocks of
+    1,000 walks spread over the walk-id range are bit-exact against the
+    oracle."""
+    rowptr, col = synth.ba_hub_csr(4_000_000, 20, 64, 500_000, seed=0, device=cuda)
+    V, E = rowptr.numel() - 1, col.numel()
+    N, L = 2 * V, 30
+    start = torch.arange(N, device=cuda) % V
+    n, e = mc.rejection_sampling(rowptr, col, start, L, 4.0, 0.25, seed=5, rule=rule,
+                                 return_edges=True)
+    assert torch.equal(n[:, 0], start)
+    bad = 0
+    for l in range(L):
+        u, v, el = n[:, l], n[:, l + 1], e[:, l]
+        rs, re = rowptr[u], rowptr[u + 1]
+        stay = (el == -1) & (re == rs) & (v == u)
+        move = (el >= rs) & (el < re) & (col[el.clamp(0, E - 1)] == v)
+        bad += int((~(stay | move)).sum())
+    assert bad == 0
+    rp, cl = rowptr.cpu().numpy(), col.cpu().numpy()
+    rule_id = {name: k for k, name in RULE_NAME.items()}[rule]
+    for s0 in (0, N // 2, N - 1000):
+        ref, ref_e, st, _ = oracle.node2vec_walk(rp, cl, start[s0:s0 + 1000].cpu().numpy(), L,
+                                                 4.0, 0.25, 5, rule=rule_id, rows_sorted=True,
+                                                 with_edges=True, first_walk=s0)
+        assert st == 0
+        np.testing.assert_array_equal(n[s0:s0 + 1000].cpu().numpy(), ref)
+        np.testing.assert_array_equal(e[s0:s0 + 1000].cpu().numpy(), ref_e)
