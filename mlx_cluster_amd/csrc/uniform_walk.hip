@@ -469,6 +469,13 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
 #ifndef MLXC_RAND_WINDOW
 #define MLXC_RAND_WINDOW 16    // uniforms per rand block (4-byte floats)
 #endif
+// Uniforms per generated block (seed=): one Philox call.  Generating costs no
+// memory traffic but VALU work, and a wavefront runs the generation whenever
+// any of its lanes needs a block, which with 16-uniform blocks (four calls)
+// was nearly every iteration.
+#ifndef MLXC_GEN_WINDOW
+#define MLXC_GEN_WINDOW 4
+#endif
 
 namespace {
 
@@ -546,7 +553,7 @@ namespace {
 template <bool kGen, bool kEdges, typename OutT>
 int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_bytes,
                         hipStream_t stream) {
-    constexpr int RW = MLXC_RAND_WINDOW;
+    constexpr int RW = kGen ? MLXC_GEN_WINDOW : MLXC_RAND_WINDOW;
     EdgeRecord* recs = reinterpret_cast<EdgeRecord*>(static_cast<char*>(workspace) + kRecordOffset);
     switch (uniform_mode(a, workspace_bytes, kGen)) {
     case UniformMode::kRecords: {
