@@ -204,8 +204,7 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* 
         return fail(MLXC_ERR_INVALID_ARGUMENT, "rand must not be NULL");
     hipStream_t s = static_cast<hipStream_t>(stream);
     int64_t* d_work = static_cast<int64_t*>(d_workspace);
-    if (int rc = launch_zero_work(d_work, s)) return rc;
-    if (num_walks == 0) return MLXC_OK;
+    if (num_walks == 0) return launch_zero_work(d_work, s);  // (else the walk's launches zero it)
     const WalkArgs a{d_rowptr, d_col, d_start, d_rand, d_n_out, d_e_out, d_work,
                      num_nodes, num_edges, num_walks, walk_length, 0u, 0u};
     return launch_uniform(a, d_workspace, workspace_bytes, false, out_type, s);
@@ -221,8 +220,7 @@ int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes, const in
         return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     int64_t* d_work = static_cast<int64_t*>(d_workspace);
-    if (int rc = launch_zero_work(d_work, s)) return rc;
-    if (num_walks == 0) return MLXC_OK;
+    if (num_walks == 0) return launch_zero_work(d_work, s);  // (else the walk's launches zero it)
     const WalkArgs a{d_rowptr, d_col, d_start, nullptr, d_n_out, d_e_out, d_work,
                      num_nodes, num_edges, num_walks, walk_length,
                      static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32)};

@@ -58,6 +58,24 @@ struct CsrCheck {
     }
 };
 
+// Record of node v as the walks read it: {v, row begin, degree, 0}, with
+// degree kRecBadNode for an id outside [0, num_nodes) and kRecBadRow for a
+// row outside [0, num_edges] or decreasing.
+__device__ __forceinline__ int4 node_record(const int64_t* __restrict__ rowptr, int64_t v,
+                                            int64_t num_nodes, int64_t num_edges) {
+    int4 r = make_int4(static_cast<int32_t>(v), 0, kRecBadNode, 0);
+    if (node_ok(v, num_nodes)) {
+        const RowBounds rb = load_row(rowptr, v);
+        if (row_ok(rb, num_edges)) {
+            r.y = static_cast<int32_t>(rb.begin);
+            r.z = static_cast<int32_t>(rb.end - rb.begin);
+        } else {
+            r.z = kRecBadRow;
+        }
+    }
+    return r;
+}
+
 // Edge records (see EdgeRecord); optionally (index.count > 0) also the
 // levels of the node2vec walk's search index: col as int32 and its samples
 // col32[16^k * i].  With rec == nullptr (the node2vec walk's CSR mode) only
@@ -157,6 +175,29 @@ __global__ __launch_bounds__(kBlock) void edge_index_kernel(const int64_t* __res
     }
 }
 
+// The uniform record walk's whole preparation in one launch (a small call
+// is bound by launch latency): the call's status words zeroed, the edge
+// record of every CSR entry, then the start record of every walk.
+__global__ __launch_bounds__(kBlock) void record_prep_kernel(const int64_t* __restrict__ rowptr,
+                                                             const int64_t* __restrict__ col,
+                                                             const int64_t* __restrict__ start,
+                                                             int64_t num_nodes, int64_t num_edges,
+                                                             int64_t num_walks,
+                                                             EdgeRecord* __restrict__ recs,
+                                                             EdgeRecord* __restrict__ init,
+                                                             int64_t* __restrict__ work) {
+    if (blockIdx.x == 0 && threadIdx.x < MLXC_WORK_WORDS) work[threadIdx.x] = 0;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+         i < num_edges + num_walks; i += stride) {
+        if (i < num_edges)
+            *reinterpret_cast<int4*>(recs + i) = node_record(rowptr, col[i], num_nodes, num_edges);
+        else
+            *reinterpret_cast<int4*>(init + (i - num_edges)) =
+                node_record(rowptr, start[i - num_edges], num_nodes, num_edges);
+    }
+}
+
 // Start records: walk n's start node in the edge-record format, so a slot
 // beginning a walk and a slot taking a step both issue the same single 16-byte
 // read.  Written by walk_init_kernel (one coalesced pass over start).
@@ -165,23 +206,10 @@ __global__ __launch_bounds__(kBlock) void walk_init_kernel(const int64_t* __rest
                                                            int64_t num_nodes, int64_t num_edges,
                                                            int64_t num_walks,
                                                            EdgeRecord* __restrict__ init) {
-    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t n = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; n < num_walks;
-         n += stride) {
-        const int64_t v = start[n];
-        i32x4 r = {static_cast<int32_t>(v), 0, kRecBadNode, 0};
-        if (node_ok(v, num_nodes)) {
-            const RowBounds rb = load_row(rowptr, v);
-            if (row_ok(rb, num_edges)) {
-                r.y = static_cast<int32_t>(rb.begin);
-                r.z = static_cast<int32_t>(rb.end - rb.begin);
-            } else {
-                r.z = kRecBadRow;
-            }
-        }
-        *reinterpret_cast<i32x4*>(init + n) = r;
-    }
+         n += stride)
+        *reinterpret_cast<int4*>(init + n) = node_record(rowptr, start[n], num_nodes, num_edges);
 }
 
 // work[0] |= MLXC_CSR_BAD_ROWPTR / MLXC_CSR_BAD_COL bits; work[1] counts
@@ -276,6 +304,17 @@ int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_no
     if (int rc = stream_grid(num_walks, 16, grid)) return rc;
     hipLaunchKernelGGL(walk_init_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, start,
                        num_nodes, num_edges, num_walks, init);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int launch_record_prep(const int64_t* rowptr, const int64_t* col, const int64_t* start,
+                       int64_t num_nodes, int64_t num_edges, int64_t num_walks, EdgeRecord* recs,
+                       EdgeRecord* init, int64_t* work, hipStream_t stream) {
+    int grid = 0;
+    if (int rc = stream_grid(num_edges + num_walks, 16, grid)) return rc;
+    hipLaunchKernelGGL(record_prep_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col, start,
+                       num_nodes, num_edges, num_walks, recs, init, work);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

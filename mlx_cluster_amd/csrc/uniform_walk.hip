@@ -558,11 +558,8 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
     switch (uniform_mode(a, workspace_bytes, kGen)) {
     case UniformMode::kRecords: {
         EdgeRecord* init = recs + a.num_edges;
-        if (int rc = launch_edge_records(a.rowptr, a.col, a.num_nodes, a.num_edges, recs,
-                                         IndexLevels{}, nullptr, stream))
-            return rc;
-        if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
-                                      init, stream))
+        if (int rc = launch_record_prep(a.rowptr, a.col, a.start, a.num_nodes, a.num_edges,
+                                        a.num_walks, recs, init, a.work, stream))
             return rc;
         return launch_walk_kernel(uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen, kEdges, OutT>,
                                   MLXC_REC_SLOTS, MLXC_REC_BLOCKS_PER_CU, a,
@@ -572,6 +569,7 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
     }
     case UniformMode::kCsr: {
         EdgeRecord* init = recs;
+        if (int rc = launch_zero_work(a.work, stream)) return rc;
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, stream))
             return rc;
@@ -583,6 +581,7 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
     case UniformMode::kPlain:
         break;
     }
+    if (int rc = launch_zero_work(a.work, stream)) return rc;
     return launch_walk_kernel(uniform_walk_kernel<2, kEdges, kGen, OutT>, 2, 0, a, stream);
 }
 

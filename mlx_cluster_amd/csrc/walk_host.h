@@ -67,6 +67,11 @@ inline bool records_fit(int64_t num_nodes, int64_t num_edges) {
 
 // ---- prep_kernels.hip
 int launch_zero_work(int64_t* d_work, hipStream_t stream);
+// The uniform record walk's preparation in one launch: zeroes the status
+// words, writes the edge records and the start records.
+int launch_record_prep(const int64_t* rowptr, const int64_t* col, const int64_t* start,
+                       int64_t num_nodes, int64_t num_edges, int64_t num_walks, EdgeRecord* recs,
+                       EdgeRecord* init, int64_t* work, hipStream_t stream);
 // index.count == 0: records only (the uniform walk); a non-null check_work
 // also validates the CSR and counts row descents (see edge_record_kernel).
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
