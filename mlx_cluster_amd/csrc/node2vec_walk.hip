@@ -716,16 +716,15 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         index.count = lay.count;
         for (int k = 0; k < lay.count; ++k)
             index.level[k] = reinterpret_cast<int32_t*>(base + lay.level[k]);
-        // one pass builds the search index and, for MLXC_ROWS_DETECT, checks
-        // the rows (the walk reads the result on the device: no host sync)
+        // one pass builds the search index and the start records and, for
+        // MLXC_ROWS_DETECT, checks the rows (the walk reads the result on the
+        // device: no host sync)
         int64_t* check = p.rows == MLXC_ROWS_DETECT ? w.work : nullptr;
+        const StartRecords starts{w.start, w.num_walks, init};
         if (int rc = records ? launch_edge_records(w.rowptr, w.col, w.num_nodes, w.num_edges, recs,
-                                                   index, check, stream)
+                                                   index, starts, check, stream)
                              : launch_edge_index(w.rowptr, w.col, w.num_nodes, w.num_edges, index,
-                                                 check, stream))
-            return rc;
-        if (int rc = launch_walk_init(w.rowptr, w.start, w.num_nodes, w.num_edges, w.num_walks,
-                                      init, stream))
+                                                 starts, check, stream))
             return rc;
         a.recs = recs;
         a.init = init;

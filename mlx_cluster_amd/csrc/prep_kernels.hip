@@ -88,7 +88,8 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
                                                              const int64_t* __restrict__ col,
                                                              int64_t num_nodes, int64_t num_edges,
                                                              EdgeRecord* __restrict__ rec,
-                                                             IndexLevels index, int64_t* work) {
+                                                             IndexLevels index, StartRecords starts,
+                                                             int64_t* work) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -118,6 +119,9 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
                 index.level[k][e >> (4 * k)] = r.x;
         }
     }
+    for (int64_t n = gid; n < starts.num_walks; n += stride)
+        *reinterpret_cast<int4*>(starts.init + n) =
+            node_record(rowptr, starts.start[n], num_nodes, num_edges);
     if (work) {
         check.nodes(rowptr, num_nodes, col, num_edges, gid, stride);
         unsigned long long* w = reinterpret_cast<unsigned long long*>(work);
@@ -134,7 +138,8 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
 __global__ __launch_bounds__(kBlock) void edge_index_kernel(const int64_t* __restrict__ rowptr,
                                                             const int64_t* __restrict__ col,
                                                             int64_t num_nodes, int64_t num_edges,
-                                                            IndexLevels index, int64_t* work) {
+                                                            IndexLevels index, StartRecords starts,
+                                                            int64_t* work) {
     typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
@@ -168,6 +173,9 @@ __global__ __launch_bounds__(kBlock) void edge_index_kernel(const int64_t* __res
                 index.level[k][e0 >> (4 * k)] = v[0];
         }
     }
+    for (int64_t n = gid; n < starts.num_walks; n += stride)
+        *reinterpret_cast<int4*>(starts.init + n) =
+            node_record(rowptr, starts.start[n], num_nodes, num_edges);
     if (work) {
         check.nodes(rowptr, num_nodes, col, num_edges, gid, stride);
         unsigned long long* w = reinterpret_cast<unsigned long long*>(work);
@@ -269,30 +277,32 @@ int launch_zero_work(int64_t* d_work, hipStream_t stream) {
 
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                         int64_t num_edges, EdgeRecord* recs, const IndexLevels& index,
-                        int64_t* check_work, hipStream_t stream) {
-    if (num_edges == 0 && !check_work) return MLXC_OK;
+                        const StartRecords& starts, int64_t* check_work, hipStream_t stream) {
+    if (num_edges == 0 && !check_work && starts.num_walks == 0) return MLXC_OK;
     int grid = 0;
-    const int64_t items = check_work && num_nodes > num_edges ? num_nodes : num_edges;
+    int64_t items = check_work && num_nodes > num_edges ? num_nodes : num_edges;
+    if (starts.num_walks > items) items = starts.num_walks;
     if (int rc = stream_grid(items, 16, grid)) return rc;
     hipLaunchKernelGGL(edge_record_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col,
-                       num_nodes, num_edges, recs, index, check_work);
+                       num_nodes, num_edges, recs, index, starts, check_work);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }
 
 int launch_edge_index(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
-                      int64_t num_edges, const IndexLevels& index, int64_t* check_work,
-                      hipStream_t stream) {
-    if (num_edges == 0 && !check_work) return MLXC_OK;
+                      int64_t num_edges, const IndexLevels& index, const StartRecords& starts,
+                      int64_t* check_work, hipStream_t stream) {
+    if (num_edges == 0 && !check_work && starts.num_walks == 0) return MLXC_OK;
     if (reinterpret_cast<uintptr_t>(col) % 16 != 0)  // the record pass reads any alignment
-        return launch_edge_records(rowptr, col, num_nodes, num_edges, nullptr, index, check_work,
-                                   stream);
+        return launch_edge_records(rowptr, col, num_nodes, num_edges, nullptr, index, starts,
+                                   check_work, stream);
     int grid = 0;
     const int64_t quads = (num_edges + 3) / 4;
-    const int64_t items = check_work && num_nodes > quads ? num_nodes : quads;
+    int64_t items = check_work && num_nodes > quads ? num_nodes : quads;
+    if (starts.num_walks > items) items = starts.num_walks;
     if (int rc = stream_grid(items, 16, grid)) return rc;
     hipLaunchKernelGGL(edge_index_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col,
-                       num_nodes, num_edges, index, check_work);
+                       num_nodes, num_edges, index, starts, check_work);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

@@ -564,6 +564,14 @@ inline __host__ __device__ int index_levels(int64_t num_edges) {
     return msb / 4 + 1;
 }
 
+// Start records a preparation pass writes besides its edge pass: walk n's
+// start node in the record format, into init[n].
+struct StartRecords {
+    const int64_t* start;
+    int64_t num_walks;
+    EdgeRecord* init;
+};
+
 constexpr int32_t kRecBadNode = -1;  // col[e] outside [0, num_nodes)
 constexpr int32_t kRecBadRow = -2;   // row of col[e] outside [0, num_edges] or decreasing
 constexpr size_t kRecordOffset = 256;  // bytes of workspace before the records

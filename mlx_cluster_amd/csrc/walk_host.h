@@ -72,16 +72,19 @@ int launch_zero_work(int64_t* d_work, hipStream_t stream);
 int launch_record_prep(const int64_t* rowptr, const int64_t* col, const int64_t* start,
                        int64_t num_nodes, int64_t num_edges, int64_t num_walks, EdgeRecord* recs,
                        EdgeRecord* init, int64_t* work, hipStream_t stream);
-// index.count == 0: records only (the uniform walk); a non-null check_work
-// also validates the CSR and counts row descents (see edge_record_kernel).
+// Edge records and the search index levels (index.count > 0) of the node2vec
+// walk, and in the same pass the start records of `starts` (num_walks 0:
+// none); a non-null check_work also validates the CSR and counts row
+// descents (see edge_record_kernel).
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                         int64_t num_edges, EdgeRecord* recs, const IndexLevels& index,
-                        int64_t* check_work, hipStream_t stream);
-// The index levels alone, from col (node2vec CSR mode); a 16-byte aligned col
-// uses four entries per thread, any other alignment the record pass.
+                        const StartRecords& starts, int64_t* check_work, hipStream_t stream);
+// The index levels alone, from col (node2vec CSR mode), and the start records;
+// a 16-byte aligned col uses four entries per thread, any other alignment the
+// record pass.
 int launch_edge_index(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
-                      int64_t num_edges, const IndexLevels& index, int64_t* check_work,
-                      hipStream_t stream);
+                      int64_t num_edges, const IndexLevels& index, const StartRecords& starts,
+                      int64_t* check_work, hipStream_t stream);
 int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
                      int64_t num_edges, int64_t num_walks, EdgeRecord* init, hipStream_t stream);
 int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
