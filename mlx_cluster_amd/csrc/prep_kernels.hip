@@ -213,7 +213,9 @@ __global__ __launch_bounds__(kBlock) void walk_init_kernel(const int64_t* __rest
                                                            const int64_t* __restrict__ start,
                                                            int64_t num_nodes, int64_t num_edges,
                                                            int64_t num_walks,
-                                                           EdgeRecord* __restrict__ init) {
+                                                           EdgeRecord* __restrict__ init,
+                                                           int64_t* __restrict__ work) {
+    if (blockIdx.x == 0 && threadIdx.x < MLXC_WORK_WORDS) work[threadIdx.x] = 0;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t n = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; n < num_walks;
          n += stride)
@@ -308,12 +310,12 @@ int launch_edge_index(const int64_t* rowptr, const int64_t* col, int64_t num_nod
 }
 
 int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
-                     int64_t num_edges, int64_t num_walks, EdgeRecord* init, hipStream_t stream) {
-    if (num_walks == 0) return MLXC_OK;
+                     int64_t num_edges, int64_t num_walks, EdgeRecord* init, int64_t* work,
+                     hipStream_t stream) {
     int grid = 0;
     if (int rc = stream_grid(num_walks, 16, grid)) return rc;
     hipLaunchKernelGGL(walk_init_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, start,
-                       num_nodes, num_edges, num_walks, init);
+                       num_nodes, num_edges, num_walks, init, work);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

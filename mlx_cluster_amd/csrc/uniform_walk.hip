@@ -569,9 +569,8 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
     }
     case UniformMode::kCsr: {
         EdgeRecord* init = recs;
-        if (int rc = launch_zero_work(a.work, stream)) return rc;
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
-                                      init, stream))
+                                      init, a.work, stream))
             return rc;
         return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW, kGen, kEdges, OutT>,
                                   MLXC_CSR_SLOTS, MLXC_CSR_BLOCKS_PER_CU, a,

@@ -85,8 +85,11 @@ int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_n
 int launch_edge_index(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                       int64_t num_edges, const IndexLevels& index, const StartRecords& starts,
                       int64_t* check_work, hipStream_t stream);
+// Start records of the uniform CSR walk; the same launch zeroes the call's
+// status words.
 int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
-                     int64_t num_edges, int64_t num_walks, EdgeRecord* init, hipStream_t stream);
+                     int64_t num_edges, int64_t num_walks, EdgeRecord* init, int64_t* work,
+                     hipStream_t stream);
 int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                      int64_t num_edges, int64_t* d_work, hipStream_t stream);
 int launch_philox_fill(float* out, int64_t n, uint64_t seed, hipStream_t stream);
