@@ -514,13 +514,13 @@ UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes, bool gen) {
 }
 
 // Resident blocks per compute unit of the persistent walks (0: as many as
-// the kernel's registers allow).  The record walk runs best below its
-// register limit of 6: measured on MI355X at configuration 2, 7.68 ms with 4
-// blocks per CU, 7.70 with 3 or 5, 7.80 with 6 and 8.18 with 2 (the same
+// the kernel's registers allow).  The record walk runs best well below its
+// register limit: measured on MI355X at configuration 2, 7.55 ms with 3
+// blocks per CU, 7.61 with 2 or 4, 7.68 with 5 and 7.73 with 6 (the same
 // order for the seeded and the int32-output variants).  The CSR walk runs
-// best at its limit (configuration 4: 6.77 ms with 4, 7.35 with 3).
+// best at its limit (configuration 4: 6.31 ms at the limit or with 4).
 #ifndef MLXC_REC_BLOCKS_PER_CU
-#define MLXC_REC_BLOCKS_PER_CU 4
+#define MLXC_REC_BLOCKS_PER_CU 3
 #endif
 #ifndef MLXC_CSR_BLOCKS_PER_CU
 #define MLXC_CSR_BLOCKS_PER_CU 0
