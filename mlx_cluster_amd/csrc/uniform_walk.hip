@@ -11,10 +11,11 @@
 
 namespace mlxc {
 
-// Uniform walk without register windows: W walk slots per lane, walks from
-// the wave queue, 8-byte loads and stores.  Serves the cases the windowed
-// kernels do not: the edge-id output and buffers that are not 16-byte
-// aligned.
+// Uniform walk without stream windows: W walk slots per lane, walks from the
+// wave queue, 8-byte loads and stores.  Serves the cases the windowed
+// kernels do not: buffers that are not 16-byte aligned, a rand tensor whose
+// size is not a multiple of 4, graphs beyond int32 ids, and a workspace too
+// small for the start records.
 template <int W, bool kEdges, bool kGen, typename OutT>
 __global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
     const int64_t L = a.walk_length;

@@ -158,7 +158,8 @@ struct WalkArgs {
 
 // ------------------------------------------------- stream windows
 
-// Per-lane register windows for the two streams of the uniform walk.
+// Per-lane windows for the two streams of the uniform walk (rand: LdsWindow
+// below, in LDS; output: OutWin, in registers).
 //
 // The rand stream: walk n reads rand[n*L + l] at step l, so a lane walks
 // through its own row 4 bytes at a time while its 63 neighbours do the same
