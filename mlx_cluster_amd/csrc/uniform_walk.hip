@@ -456,6 +456,87 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
     if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
 }
 
+// Uniform walk on a graph small enough for LDS, for calls bound by launch
+// latency (the reference tests' Cora-sized workload): every block copies
+// rowptr and col, as int32, into its LDS, then runs one walk per thread with
+// no global random read at all.  Uniforms are read 8 at a time (one round
+// trip per 8 steps); outputs are stored entry by entry, which only small
+// calls can afford.  Out-of-range entries are marked -1 on the copy and flag
+// the call when a walk meets them, as in the other kernels.
+constexpr int kLdsGraphEntries = 14336;        // rowptr + col entries (56 KB of LDS)
+constexpr int64_t kLdsWalkSteps = int64_t{1} << 20;  // calls of up to this many steps
+
+static bool lds_walk_fits(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
+                          int32_t walk_length) {
+    return num_nodes + 1 + num_edges <= kLdsGraphEntries && num_walks <= kLdsWalkSteps &&
+           num_walks * static_cast<int64_t>(walk_length) <= kLdsWalkSteps;
+}
+
+template <bool kGen, bool kEdges, typename OutT>
+__global__ __launch_bounds__(kBlock) void uniform_walk_lds_kernel(WalkArgs a) {
+    __shared__ int32_t graph[kLdsGraphEntries];
+    const int64_t V = a.num_nodes, E = a.num_edges, N = a.num_walks, L = a.walk_length;
+    int32_t* const rp = graph;          // rowptr, -1 for an entry outside [0, E]
+    int32_t* const cl = graph + V + 1;  // col, -1 for a value outside [0, V)
+    for (int64_t i = threadIdx.x; i <= V; i += kBlock) {
+        const int64_t r = a.rowptr[i];
+        rp[i] = r >= 0 && r <= E ? static_cast<int32_t>(r) : -1;
+    }
+    for (int64_t i = threadIdx.x; i < E; i += kBlock) {
+        const int64_t c = a.col[i];
+        cl[i] = node_ok(c, V) ? static_cast<int32_t>(c) : -1;
+    }
+    __syncthreads();
+    OutT* const nout = static_cast<OutT*>(a.n_out);
+    OutT* const eout = static_cast<OutT*>(a.e_out);
+    uint32_t status = 0;
+    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; n < N;
+         n += static_cast<int64_t>(gridDim.x) * kBlock) {
+        const int64_t s = a.start[n];
+        OutT* const row = nout + n * (L + 1);
+        OutT* const erow = kEdges ? eout + n * L : nullptr;
+        row[0] = static_cast<OutT>(s);
+        int64_t l = 0;                    // steps taken
+        int32_t v = static_cast<int32_t>(s);
+        bool stop = !node_ok(s, V);       // a sink or an error ends the walk
+        if (stop) status |= MLXC_STATUS_BAD_NODE;
+        while (l < L && !stop) {
+            float r[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (l + j < L)
+                    r[j] = kGen ? philox_uniform_at(n * L + l + j, a.key0, a.key1) : a.rand[n * L + l + j];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (stop || l >= L) break;
+                const int32_t b = rp[v], end = rp[v + 1];
+                if (b < 0 || end < b) {
+                    status |= MLXC_STATUS_BAD_ROW;
+                    stop = true;
+                } else if (end == b) {
+                    stop = true;  // absorbing node: the walk stays
+                } else {
+                    const int32_t e = b + static_cast<int32_t>(pick_index(r[j], end - b));
+                    const int32_t x = cl[e];
+                    if (x < 0) {
+                        status |= MLXC_STATUS_BAD_NODE;
+                        stop = true;
+                    } else {
+                        row[l + 1] = static_cast<OutT>(x);
+                        if (kEdges) erow[l] = static_cast<OutT>(e);
+                        v = x;
+                        l += 1;
+                    }
+                }
+            }
+        }
+        for (int64_t j = l + 1; j <= L; ++j) row[j] = static_cast<OutT>(v);  // the walk stays
+        if (kEdges)
+            for (int64_t j = l; j < L; ++j) erow[j] = static_cast<OutT>(-1);
+    }
+    if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
+}
+
 // ------------------------------------------------------------- launcher
 
 // Walks in flight per lane.  Both walks run best with one slot at the
@@ -480,7 +561,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
 
 namespace {
 
-enum class UniformMode { kRecords, kCsr, kPlain };
+enum class UniformMode { kRecords, kCsr, kLds, kPlain };
 
 // Edge records cost one random read per edge to build; they pay off when the
 // call takes several steps per edge, or when the graph is small enough that
@@ -511,6 +592,7 @@ UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes, bool gen) {
         workspace_bytes >= record_bytes(a.num_edges, a.num_walks))
         return UniformMode::kRecords;
     if (workspace_bytes >= init_bytes(a.num_walks)) return UniformMode::kCsr;
+    if (lds_walk_fits(a.num_nodes, a.num_edges, a.num_walks, a.walk_length)) return UniformMode::kLds;
     return UniformMode::kPlain;
 }
 
@@ -543,7 +625,8 @@ size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num
                                int32_t walk_length) {
     const size_t minimum = MLXC_WORK_WORDS * sizeof(int64_t);
     if (num_nodes < 0 || num_edges < 0 || num_walks < 0 || walk_length < 0 ||
-        !records_fit(num_nodes, num_edges))
+        !records_fit(num_nodes, num_edges) ||
+        lds_walk_fits(num_nodes, num_edges, num_walks, walk_length))  // the LDS walk
         return minimum;
     return records_pay_off(num_edges, num_walks, walk_length) ? record_bytes(num_edges, num_walks)
                                                               : init_bytes(num_walks);
@@ -577,6 +660,14 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
                                   MLXC_CSR_SLOTS, MLXC_CSR_BLOCKS_PER_CU, a,
                                   stream,
                                   static_cast<const EdgeRecord*>(init));
+    }
+    case UniformMode::kLds: {
+        if (int rc = launch_zero_work(a.work, stream)) return rc;
+        const int64_t blocks = (a.num_walks + kBlock - 1) / kBlock;  // at most 4096
+        hipLaunchKernelGGL((uniform_walk_lds_kernel<kGen, kEdges, OutT>), dim3(static_cast<int>(blocks)),
+                           dim3(kBlock), 0, stream, a);
+        MLXC_HIP_TRY(hipGetLastError());
+        return MLXC_OK;
     }
     case UniformMode::kPlain:
         break;

@@ -310,3 +310,71 @@ def test_int32_output_all_kernel_paths(L, cuda):
     g = mc.random_walk(rowptr, col, start, None, L, seed=9, out_dtype=torch.int32)
     assert g.dtype == torch.int32
     np.testing.assert_array_equal(g.cpu().numpy(), n_ref)
+
+
+@pytest.mark.parametrize("V,E_target", [(50, 300), (2708, 10556), (3000, 14336 - 3001)])
+def test_lds_walk(V, E_target, cuda):
+    """Graphs whose rowptr and col fit in LDS (V + 1 + E <= 14,336 entries) on
+    calls of up to 2^20 steps take the LDS walk (the workspace query asks for
+    the status words only).  Nodes and edges bit-exact against the oracle
+    with a rand tensor and generated uniforms, int64 and int32 output, sinks
+    included; a graph one entry over the limit takes the record walk with
+    the same results."""
+    from mlx_cluster_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(V)
+    pairs = rng.integers(0, V, (E_target, 2))
+    pairs[: V // 5, 0] = np.arange(V // 5) * 5 % V  # a spread of rows
+    rowptr, col = csr(V, pairs)
+    keep = np.ones(V, bool)
+    keep[rng.integers(0, V, V // 10)] = False  # some sinks: drop their rows' entries
+    row_of = np.repeat(np.arange(V), np.diff(rowptr))
+    rowptr, col = csr(V, np.stack([row_of[keep[row_of]], col[keep[row_of]]], 1))
+    E = col.size
+    assert V + 1 + E <= 14336
+    for N, L in ((1, 1), (300, 7), (2000, 5), (4000, 80)):
+        assert lib.mlxc_random_walk_workspace_bytes(V, E, N, L) == 32
+        start = (np.arange(N) * 7) % V
+        rand = mc.philox_uniform((N, L), N + L, device=cuda)
+        n_ref, e_ref, st, counts = oracle.uniform_walk(rowptr, col, start, rand.cpu().numpy(), L,
+                                                       with_edges=True)
+        assert st == 0
+        t = lambda a: torch.as_tensor(a).to(cuda)
+        n, e = mc.random_walk(t(rowptr), t(col), t(start), rand, L, return_edges=True)
+        np.testing.assert_array_equal(n.cpu().numpy(), n_ref)
+        np.testing.assert_array_equal(e.cpu().numpy(), e_ref)
+        n32 = mc.random_walk(t(rowptr), t(col), t(start), rand, L, out_dtype=torch.int32)
+        np.testing.assert_array_equal(n32.cpu().numpy(), n_ref)
+        g = mc.random_walk(t(rowptr), t(col), t(start), None, L, seed=N + L)
+        np.testing.assert_array_equal(g.cpu().numpy(), n_ref)
+    # exactly at the limit (the LDS walk) and one entry over it (the record walk)
+    base = np.stack([np.repeat(np.arange(V), np.diff(rowptr)), col], 1)
+    for total, lds in ((14336, True), (14337, False)):
+        rp2, cl2 = csr(V, np.concatenate([base, np.tile([[0, 1]], (total - (V + 1 + E), 1))]))
+        assert V + 1 + cl2.size == total
+        N, L = 2000, 5
+        assert (lib.mlxc_random_walk_workspace_bytes(V, cl2.size, N, L) == 32) == lds
+        start = (np.arange(N) * 3) % V
+        rand = mc.philox_uniform((N, L), 77, device=cuda)
+        n_ref, _, st, _ = oracle.uniform_walk(rp2, cl2, start, rand.cpu().numpy(), L)
+        assert st == 0
+        n = mc.random_walk(torch.as_tensor(rp2).to(cuda), torch.as_tensor(cl2).to(cuda),
+                           torch.as_tensor(start).to(cuda), rand, L)
+        np.testing.assert_array_equal(n.cpu().numpy(), n_ref)
+
+
+def test_lds_walk_flags_bad_input(cuda):
+    """Out-of-range starts, col entries and rowptr entries met by an LDS walk
+    raise ValueError, as on the other paths."""
+    rowptr, col = csr(4, [(0, 1), (1, 2), (2, 3), (3, 0)])
+    t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.int64)).to(cuda)
+    rand = torch.full((2, 3), 0.5, device=cuda)
+    with pytest.raises(ValueError):
+        mc.random_walk(t(rowptr), t(col), t([0, 9]), rand, 3)
+    with pytest.raises(ValueError):
+        mc.random_walk(t(rowptr), t([1, 2, 7, 0]), t([0, 1]), rand, 3)
+    with pytest.raises(ValueError):
+        mc.random_walk(t([0, 1, 2, 9, 4]), t(col), t([2, 2]), rand, 3)
+    # the same graph, well formed: no error
+    n = mc.random_walk(t(rowptr), t(col), t([0, 1]), rand, 3)
+    np.testing.assert_array_equal(n.cpu().numpy(), [[0, 1, 2, 3], [1, 2, 3, 0]])
