@@ -590,6 +590,112 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.w.work), static_cast<unsigned long long>(status));
 }
 
+// node2vec walk on a graph small enough for LDS (lds_walk_fits), for calls
+// bound by launch latency (the reference tests' Cora-sized workload): every
+// block copies rowptr and col, as int32, into its LDS; one walk per thread,
+// the same draws and decisions as the record walk, the neighbour test by
+// bisection (sorted rows) or a linear scan (unsorted rows) in LDS.  With
+// MLXC_ROWS_DETECT each block checks the row order of its copy.
+template <int kRule, bool kEdges, typename OutT>
+__global__ __launch_bounds__(kBlock) void node2vec_lds_kernel(N2VRecArgs a) {
+    __shared__ int32_t graph[kLdsGraphEntries];
+    const int64_t V = a.w.num_nodes, E = a.w.num_edges, N = a.w.num_walks, L = a.w.walk_length;
+    int32_t* const rp = graph;          // rowptr, -1 for an entry outside [0, E]
+    int32_t* const cl = graph + V + 1;  // col, -1 for a value outside [0, V)
+    for (int64_t i = threadIdx.x; i <= V; i += kBlock) {
+        const int64_t r = a.w.rowptr[i];
+        rp[i] = r >= 0 && r <= E ? static_cast<int32_t>(r) : -1;
+    }
+    for (int64_t i = threadIdx.x; i < E; i += kBlock) {
+        const int64_t c = a.w.col[i];
+        cl[i] = node_ok(c, V) ? static_cast<int32_t>(c) : -1;
+    }
+    __syncthreads();
+    bool sorted = a.rows == MLXC_ROWS_SORTED;
+    if (a.rows == MLXC_ROWS_DETECT) {
+        bool descent = false;  // inside some well-formed row
+        for (int64_t u = threadIdx.x; u < V; u += kBlock) {
+            const int32_t b = rp[u], end = rp[u + 1];
+            if (b < 0 || end < b) continue;
+            for (int32_t i = b + 1; i < end; ++i) descent |= cl[i] < cl[i - 1];
+        }
+        sorted = !__syncthreads_or(descent);
+    }
+    OutT* const nout = static_cast<OutT*>(a.w.n_out);
+    OutT* const eout = static_cast<OutT*>(a.w.e_out);
+    uint32_t status = 0;
+    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; n < N;
+         n += static_cast<int64_t>(gridDim.x) * kBlock) {
+        const int64_t s = a.w.start[n];
+        OutT* const row = nout + n * (L + 1);
+        OutT* const erow = kEdges ? eout + n * L : nullptr;
+        row[0] = static_cast<OutT>(s);
+        int64_t l = 0;                    // steps taken
+        int32_t v = static_cast<int32_t>(s), t = v;
+        bool stop = !node_ok(s, V);       // a sink or an error ends the walk
+        if (stop) status |= MLXC_STATUS_BAD_NODE;
+        while (l < L && !stop) {
+            const int32_t b = rp[v], end = rp[v + 1];
+            if (b < 0 || end < b) {
+                status |= MLXC_STATUS_BAD_ROW;
+                break;
+            }
+            const int32_t deg = end - b;
+            if (deg == 0) break;  // absorbing node: the walk stays
+            int32_t e = b, x = 0;
+            for (uint32_t trial = 0;; ++trial) {
+                // the first step and forced steps accept (BiasedRandomWalk.cpp:60-66, 76-78)
+                const bool test = l > 0 && deg > 1;
+                float r = 0.0f;
+                if (l == 0 || deg > 1) {
+                    float u0;
+                    n2v_uniforms(n, static_cast<int32_t>(l), trial, a.key0, a.key1, u0, r);
+                    e = b + static_cast<int32_t>(pick_index(u0, deg));
+                }
+                x = cl[e];
+                const int32_t bx = x >= 0 ? rp[x] : -1, ex = x >= 0 ? rp[x + 1] : -1;
+                if (x < 0 || bx < 0 || ex < bx) {
+                    status |= x < 0 ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
+                    stop = true;
+                    break;
+                }
+                if (!test) break;
+                int d = n2v_decide<kRule>(a, r, x, t);
+                if (d < 0) {  // is t in row(x)?
+                    bool adjacent = false;
+                    if (sorted) {
+                        int32_t lo = bx, count = ex - bx;
+                        while (count > 0) {  // lower_bound
+                            const int32_t half = count >> 1;
+                            if (cl[lo + half] < t) {
+                                lo += half + 1;
+                                count -= half + 1;
+                            } else {
+                                count = half;
+                            }
+                        }
+                        adjacent = lo < ex && cl[lo] == t;
+                    } else {
+                        for (int32_t i = bx; i < ex && !adjacent; ++i) adjacent = cl[i] == t;
+                    }
+                    d = n2v_resolve<kRule>(a, r, adjacent) ? 1 : 0;
+                }
+                if (d == 1 || trial + 1 >= MLXC_MAX_TRIALS) break;  // (the cap keeps the last candidate)
+            }
+            if (stop) break;
+            row[l + 1] = static_cast<OutT>(x);
+            if (kEdges) erow[l] = static_cast<OutT>(e);
+            t = v;
+            v = x;
+            l += 1;
+        }
+        for (int64_t j = l + 1; j <= L; ++j) row[j] = static_cast<OutT>(v);  // the walk stays
+        if (kEdges)
+            for (int64_t j = l; j < L; ++j) erow[j] = static_cast<OutT>(-1);
+    }
+    if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.w.work), static_cast<unsigned long long>(status));
+}
+
 // ------------------------------------------------------------- launcher
 
 namespace {
@@ -686,6 +792,8 @@ size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t nu
     if (num_nodes < 0 || num_edges < 0 || num_walks < 0 || walk_length < 0 ||
         !records_fit(num_nodes, num_edges))
         return MLXC_WORK_WORDS * sizeof(int64_t);
+    if (lds_walk_fits(num_nodes, num_edges, num_walks, walk_length))
+        return kRecordOffset;  // the LDS walk: its size selects it
     return n2v_layout(num_edges, num_walks,
                       n2v_records_pay_off(num_edges, num_walks, walk_length, search_width))
         .total;
@@ -749,6 +857,31 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
                          : launch_n2v_rec<MLXC_RULE_REF_CHAIN, false, true, OutT>(a, stream);
         return edges ? launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, true, true, OutT>(a, stream)
                      : launch_n2v_rec<MLXC_RULE_NODE2VEC_EXACT, false, true, OutT>(a, stream);
+    }
+    // Small graphs with the header-sized workspace the query asks for them:
+    // the LDS walk.
+    if (aligned && workspace_bytes >= kRecordOffset &&
+        lds_walk_fits(w.num_nodes, w.num_edges, w.num_walks, w.walk_length)) {
+        if (int rc = launch_zero_work(w.work, stream)) return rc;
+        N2VRecArgs a{};
+        a.w = w;
+        a.rows = p.rows;
+        a.thr0 = float_at_or_above(p.prob0);
+        a.thr1 = float_at_or_above(p.prob1);
+        a.thr2 = float_at_or_above(p.prob2);
+        a.key0 = p.key0;
+        a.key1 = p.key1;
+        const dim3 grid(static_cast<unsigned>((w.num_walks + kBlock - 1) / kBlock));  // <= 4096
+        const bool edges = w.e_out != nullptr;
+        if (p.rule == MLXC_RULE_REF_CHAIN) {
+            if (edges) hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, true, OutT>), grid, dim3(kBlock), 0, stream, a);
+            else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, false, OutT>), grid, dim3(kBlock), 0, stream, a);
+        } else {
+            if (edges) hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_NODE2VEC_EXACT, true, OutT>), grid, dim3(kBlock), 0, stream, a);
+            else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_NODE2VEC_EXACT, false, OutT>), grid, dim3(kBlock), 0, stream, a);
+        }
+        MLXC_HIP_TRY(hipGetLastError());
+        return MLXC_OK;
     }
     // Graphs beyond int32, a workspace too small for the records, or output
     // buffers not 16-byte aligned: the direct CSR kernel, which needs the row

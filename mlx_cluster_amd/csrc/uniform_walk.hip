@@ -463,14 +463,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
 // trip per 8 steps); outputs are stored entry by entry, which only small
 // calls can afford.  Out-of-range entries are marked -1 on the copy and flag
 // the call when a walk meets them, as in the other kernels.
-constexpr int kLdsGraphEntries = 14336;        // rowptr + col entries (56 KB of LDS)
-constexpr int64_t kLdsWalkSteps = int64_t{1} << 20;  // calls of up to this many steps
 
-static bool lds_walk_fits(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
-                          int32_t walk_length) {
-    return num_nodes + 1 + num_edges <= kLdsGraphEntries && num_walks <= kLdsWalkSteps &&
-           num_walks * static_cast<int64_t>(walk_length) <= kLdsWalkSteps;
-}
 
 template <bool kGen, bool kEdges, typename OutT>
 __global__ __launch_bounds__(kBlock) void uniform_walk_lds_kernel(WalkArgs a) {
@@ -592,7 +585,9 @@ UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes, bool gen) {
         workspace_bytes >= record_bytes(a.num_edges, a.num_walks))
         return UniformMode::kRecords;
     if (workspace_bytes >= init_bytes(a.num_walks)) return UniformMode::kCsr;
-    if (lds_walk_fits(a.num_nodes, a.num_edges, a.num_walks, a.walk_length)) return UniformMode::kLds;
+    if (workspace_bytes >= kRecordOffset &&
+        lds_walk_fits(a.num_nodes, a.num_edges, a.num_walks, a.walk_length))
+        return UniformMode::kLds;
     return UniformMode::kPlain;
 }
 
@@ -625,9 +620,10 @@ size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num
                                int32_t walk_length) {
     const size_t minimum = MLXC_WORK_WORDS * sizeof(int64_t);
     if (num_nodes < 0 || num_edges < 0 || num_walks < 0 || walk_length < 0 ||
-        !records_fit(num_nodes, num_edges) ||
-        lds_walk_fits(num_nodes, num_edges, num_walks, walk_length))  // the LDS walk
+        !records_fit(num_nodes, num_edges))
         return minimum;
+    if (lds_walk_fits(num_nodes, num_edges, num_walks, walk_length))
+        return kRecordOffset;  // the LDS walk: its size selects it
     return records_pay_off(num_edges, num_walks, walk_length) ? record_bytes(num_edges, num_walks)
                                                               : init_bytes(num_walks);
 }

@@ -577,4 +577,16 @@ constexpr int32_t kRecBadNode = -1;  // col[e] outside [0, num_nodes)
 constexpr int32_t kRecBadRow = -2;   // row of col[e] outside [0, num_edges] or decreasing
 constexpr size_t kRecordOffset = 256;  // bytes of workspace before the records
 
+// Walks on graphs small enough for LDS (uniform_walk_lds_kernel,
+// node2vec_lds_kernel): rowptr and col as int32 in each block's LDS, for
+// calls bound by launch latency.  A workspace of kRecordOffset bytes (less
+// than any record or start-record layout) selects them.
+constexpr int kLdsGraphEntries = 14336;              // rowptr + col entries (56 KB)
+constexpr int64_t kLdsWalkSteps = int64_t{1} << 20;  // calls of 1 .. 2^20 steps
+__host__ __device__ inline bool lds_walk_fits(int64_t num_nodes, int64_t num_edges,
+                                              int64_t num_walks, int64_t walk_length) {
+    return num_nodes + 1 + num_edges <= kLdsGraphEntries && walk_length >= 1 &&
+           num_walks <= kLdsWalkSteps && num_walks * walk_length <= kLdsWalkSteps;
+}
+
 }  // namespace mlxc

@@ -129,13 +129,14 @@ def test_workspace_size_query():
     assert q(10, 32768 * 4, 1, 4) == 256 + 16 * (32768 * 4 + 1)   # small graph: records
     assert q(10, 32768 * 4 + 1, 1, 4) == 256 + 16 * 1
     # graphs whose rowptr and col fit in LDS (V + 1 + E <= 14336 entries), on
-    # calls of up to 2^20 steps: the LDS walk, status words only
-    assert q(10, 100, 1, 4) == 32
-    assert q(10, 14336 - 11, 2000, 5) == 32
+    # calls of 1 to 2^20 steps: the LDS walk, selected by a 256-byte workspace
+    assert q(10, 100, 1, 4) == 256
+    assert q(10, 14336 - 11, 2000, 5) == 256
     assert q(10, 14336 - 10, 2000, 5) == 256 + 16 * (14336 - 10 + 2000)   # one entry more
-    assert q(10, 100, 2**18, 4) == 32
+    assert q(10, 100, 2**18, 4) == 256
     assert q(10, 100, 2**18 + 1, 4) == 256 + 16 * (100 + 2**18 + 1)      # > 2^20 steps
-    assert q(10, 0, 0, 0) == 32                    # nothing to walk: status words only
+    assert q(10, 100, 5, 0) == 256 + 16 * 5              # no step: start records only
+    assert q(10, 0, 0, 0) == 256 + 16 * 0
     assert q(2**31, 5, 1, 1) == 32
     assert q(5, 2**31, 1, 1) == 32
     assert q(-1, 5, 1, 1) == 32

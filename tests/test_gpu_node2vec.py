@@ -371,3 +371,65 @@ def test_c5_full_size_properties(rule, cuda):
         assert st == 0
         np.testing.assert_array_equal(n[s0:s0 + 1000].cpu().numpy(), ref)
         np.testing.assert_array_equal(e[s0:s0 + 1000].cpu().numpy(), ref_e)
+
+
+@pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
+def test_lds_walk(rule, cuda):
+    """Graphs whose rowptr and col fit in LDS (V + 1 + E <= 14,336 entries) on
+    calls of 1 to 2^20 steps take the LDS walk: the workspace query asks for
+    the 256-byte header.  Bit-exact nodes and edges against the oracle for
+    sorted, detected and unsorted rows, p < 1 and p > 1, int32 output, at the
+    size limit; one entry over it, the record walk gives the same walks;
+    malformed input raises ValueError."""
+    from mlx_cluster_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(rule + 3)
+    V = 1500
+    pairs = rng.integers(0, V, (5000, 2))
+    rowptr, col = undirected(V, pairs)
+    urowptr, ucol = undirected(V, pairs, sort=False)  # the same rows, unsorted
+    assert np.array_equal(urowptr, rowptr) and oracle.csr_flags(urowptr, ucol) & 4
+    t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.int64)).to(cuda)
+    for N, L, p, q in ((1, 1, 0.5, 2.0), (700, 9, 0.25, 4.0), (3000, 30, 2.0, 0.5)):
+        assert lib.mlxc_rejection_sampling_workspace_bytes(V, col.size, N, L, p, q, rule) == 256
+        start = (np.arange(N) * 11) % V
+        for rp, cl, rows_sorted in ((rowptr, col, None), (rowptr, col, True)):
+            n_ref, e_ref, st, _ = oracle.node2vec_walk(rp, cl, start, L, p, q, 9, rule=rule,
+                                                       rows_sorted=True, with_edges=True)
+            assert st == 0
+            n, e = mc.rejection_sampling(t(rp), t(cl), t(start), L, p, q, seed=9,
+                                         rule=RULE_NAME[rule], rows_sorted=rows_sorted,
+                                         return_edges=True)
+            np.testing.assert_array_equal(n.cpu().numpy(), n_ref)
+            np.testing.assert_array_equal(e.cpu().numpy(), e_ref)
+            n32 = mc.rejection_sampling(t(rp), t(cl), t(start), L, p, q, seed=9,
+                                        rule=RULE_NAME[rule], out_dtype=torch.int32)
+            np.testing.assert_array_equal(n32.cpu().numpy(), n_ref)
+        # unsorted rows: detected, and stated
+        n_ref, _, st, _ = oracle.node2vec_walk(urowptr, ucol, start, L, p, q, 9, rule=rule,
+                                               rows_sorted=False, with_edges=True)
+        assert st == 0
+        for rows_sorted in (None, False):
+            n = mc.rejection_sampling(t(urowptr), t(ucol), t(start), L, p, q, seed=9,
+                                      rule=RULE_NAME[rule], rows_sorted=rows_sorted)
+            np.testing.assert_array_equal(n.cpu().numpy(), n_ref)
+    # at the limit and one entry over it
+    base = np.stack([np.repeat(np.arange(V), np.diff(rowptr)), col], 1)
+    for total, lds in ((14336, True), (14337, False)):
+        rp2, cl2 = csr(V, np.concatenate([base, np.tile([[0, 1]], (total - (V + 1 + col.size), 1))]))
+        N, L = 2000, 6
+        assert (lib.mlxc_rejection_sampling_workspace_bytes(V, cl2.size, N, L, 0.5, 2.0, rule)
+                == 256) == lds
+        start = (np.arange(N) * 3) % V
+        n_ref, _, st, _ = oracle.node2vec_walk(rp2, cl2, start, L, 0.5, 2.0, 4, rule=rule,
+                                               rows_sorted=True, with_edges=True)
+        n = mc.rejection_sampling(t(rp2), t(cl2), t(start), L, 0.5, 2.0, seed=4,
+                                  rule=RULE_NAME[rule])
+        np.testing.assert_array_equal(n.cpu().numpy(), n_ref)
+    # malformed input
+    rp3, cl3 = csr(4, [(0, 1), (1, 2), (1, 3), (2, 3), (3, 0), (3, 1)])
+    with pytest.raises(ValueError):
+        mc.rejection_sampling(t(rp3), t(cl3), t([0, 9]), 3, 0.5, 2.0, seed=1, rule=RULE_NAME[rule])
+    with pytest.raises(ValueError):
+        mc.rejection_sampling(t(rp3), t([1, 2, 3, 7, 0, 1]), t([0, 1, 2, 3]), 4, 0.5, 2.0,
+                              seed=1, rule=RULE_NAME[rule])

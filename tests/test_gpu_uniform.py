@@ -315,8 +315,8 @@ def test_int32_output_all_kernel_paths(L, cuda):
 @pytest.mark.parametrize("V,E_target", [(50, 300), (2708, 10556), (3000, 14336 - 3001)])
 def test_lds_walk(V, E_target, cuda):
     """Graphs whose rowptr and col fit in LDS (V + 1 + E <= 14,336 entries) on
-    calls of up to 2^20 steps take the LDS walk (the workspace query asks for
-    the status words only).  Nodes and edges bit-exact against the oracle
+    calls of 1 to 2^20 steps take the LDS walk (the workspace query asks for
+    the 256-byte header only).  Nodes and edges bit-exact against the oracle
     with a rand tensor and generated uniforms, int64 and int32 output, sinks
     included; a graph one entry over the limit takes the record walk with
     the same results."""
@@ -333,7 +333,7 @@ def test_lds_walk(V, E_target, cuda):
     E = col.size
     assert V + 1 + E <= 14336
     for N, L in ((1, 1), (300, 7), (2000, 5), (4000, 80)):
-        assert lib.mlxc_random_walk_workspace_bytes(V, E, N, L) == 32
+        assert lib.mlxc_random_walk_workspace_bytes(V, E, N, L) == 256
         start = (np.arange(N) * 7) % V
         rand = mc.philox_uniform((N, L), N + L, device=cuda)
         n_ref, e_ref, st, counts = oracle.uniform_walk(rowptr, col, start, rand.cpu().numpy(), L,
@@ -353,7 +353,7 @@ def test_lds_walk(V, E_target, cuda):
         rp2, cl2 = csr(V, np.concatenate([base, np.tile([[0, 1]], (total - (V + 1 + E), 1))]))
         assert V + 1 + cl2.size == total
         N, L = 2000, 5
-        assert (lib.mlxc_random_walk_workspace_bytes(V, cl2.size, N, L) == 32) == lds
+        assert (lib.mlxc_random_walk_workspace_bytes(V, cl2.size, N, L) == 256) == lds
         start = (np.arange(N) * 3) % V
         rand = mc.philox_uniform((N, L), 77, device=cuda)
         n_ref, _, st, _ = oracle.uniform_walk(rp2, cl2, start, rand.cpu().numpy(), L)
