@@ -35,8 +35,9 @@ extern "C" {
  * workspace of the size the *_workspace_bytes queries return also holds
  * per-call layouts of the graph and the starts (16-byte records: node, row
  * begin, row degree) that cut the dependent reads per step; with a smaller
- * workspace the kernels read the CSR arrays directly.  Same results either
- * way. */
+ * workspace the kernels read the CSR arrays directly.  For graphs small
+ * enough (see the queries), a workspace of exactly the 256-byte header runs
+ * the walk with the whole CSR in on-chip memory.  Same results every way. */
 #define MLXC_WORK_WORDS 4
 
 /* Bits a walk kernel ORs into workspace word 0 when the graph or the starts
@@ -88,11 +89,16 @@ int mlxc_version(void);
 const char* mlxc_last_error(void);
 
 /* Workspace bytes that let mlxc_random_walk use its fastest layout for this
- * call: 256 + 16 * (num_edges + num_walks) when the call takes at least
- * 4 * num_edges steps (per-call edge records), else 256 + 16 * num_walks
- * (start records only); MLXC_WORK_WORDS * 8 when num_nodes or num_edges is
- * 2^31 or more.  No reference counterpart (the reference allocates inside
- * eval, RandomWalk.cpp:28-29). */
+ * call:
+ *   256 when num_nodes + 1 + num_edges <= 14336 and the call takes 1 to 2^20
+ *     steps (num_walks <= 2^20): the walk runs with rowptr and col in LDS;
+ *   256 + 16 * (num_edges + num_walks) when the call takes at least
+ *     4 * num_edges steps, or num_edges <= 32768 * walk_length (per-call edge
+ *     records);
+ *   else 256 + 16 * num_walks (start records only);
+ *   MLXC_WORK_WORDS * 8 when num_nodes or num_edges is 2^31 or more.
+ * No reference counterpart (the reference allocates inside eval,
+ * RandomWalk.cpp:28-29). */
 size_t mlxc_random_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges,
                                         int64_t num_walks, int32_t walk_length);
 
@@ -104,6 +110,8 @@ size_t mlxc_random_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges,
  * acceptance draws r that can need a row search (|prob1 - prob2| for
  * MLXC_RULE_NODE2VEC_EXACT, max(0, prob1 - prob2) for the chain).  Both
  * layouts add 16 bytes per walk and about 4.3 bytes per edge of search index.
+ * Records are also chosen when num_edges <= 32768 * walk_length, and 256
+ * bytes (the LDS walk) under the same conditions as for mlxc_random_walk.
  * A workspace that holds the record layout always runs with records.  No
  * reference counterpart. */
 size_t mlxc_rejection_sampling_workspace_bytes(int64_t num_nodes, int64_t num_edges,
