@@ -433,3 +433,41 @@ def test_lds_walk(rule, cuda):
     with pytest.raises(ValueError):
         mc.rejection_sampling(t(rp3), t([1, 2, 3, 7, 0, 1]), t([0, 1, 2, 3]), 4, 0.5, 2.0,
                               seed=1, rule=RULE_NAME[rule])
+
+
+def test_lds_walks_random_sweep(cuda):
+    """Random small graphs (directed and undirected, duplicates and
+    self-loops kept) under the LDS limit, random walk counts and lengths:
+    the uniform and node2vec LDS walks (the Python API's default for these
+    sizes) are bit-exact against the oracle for both rules and several
+    (p, q)."""
+    rng = np.random.default_rng(2024)
+    t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.int64)).to(cuda)
+    for case in range(12):
+        V = int(rng.integers(2, 2000))
+        E_pairs = int(rng.integers(1, 6000))
+        pairs = rng.integers(0, V, (E_pairs, 2))
+        rowptr, col = (undirected(V, pairs) if case % 2 else csr(V, pairs))
+        if V + 1 + col.size > 14336:
+            continue
+        N = int(rng.integers(1, 3000))
+        L = int(rng.integers(1, 50))
+        start = rng.integers(0, V, N)
+        rand = mc.philox_uniform((N, L), case, device=cuda)
+        n_ref, e_ref, st, _ = oracle.uniform_walk(rowptr, col, start, rand.cpu().numpy(), L,
+                                                  with_edges=True)
+        assert st == 0
+        n, e = mc.random_walk(t(rowptr), t(col), t(start), rand, L, return_edges=True)
+        np.testing.assert_array_equal(n.cpu().numpy(), n_ref, err_msg=f"uniform case {case}")
+        np.testing.assert_array_equal(e.cpu().numpy(), e_ref, err_msg=f"uniform edges {case}")
+        for p, q in ((1.0, 1.0), (0.3, 3.0), (4.0, 0.25)):
+            for rule in (oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT):
+                n_ref, e_ref, st, _ = oracle.node2vec_walk(rowptr, col, start, L, p, q, case,
+                                                           rule=rule, rows_sorted=True,
+                                                           with_edges=True)
+                assert st == 0
+                n, e = mc.rejection_sampling(t(rowptr), t(col), t(start), L, p, q, seed=case,
+                                             rule=RULE_NAME[rule], return_edges=True)
+                np.testing.assert_array_equal(n.cpu().numpy(), n_ref,
+                                              err_msg=f"node2vec case {case} {p} {q} {rule}")
+                np.testing.assert_array_equal(e.cpu().numpy(), e_ref)
