@@ -43,7 +43,16 @@ extern "C" {
 /* Bits a walk kernel ORs into workspace word 0 when the graph or the starts
  * are malformed (the reference reads out of bounds in these cases; these
  * kernels never do — the affected walk stops and its remaining output
- * entries are unspecified). */
+ * entries are unspecified).  Which entries are checked does not depend on
+ * the kernel path the workspace selects, nor on the uniforms drawn:
+ *   mlxc_random_walk (and _seeded) reports the entries its walks read, which
+ *     are those the reference's loop reads (RandomWalk.cpp:45-54): a start
+ *     outside [0, num_nodes), the rowptr pair of a node a walk leaves, and
+ *     a chosen col entry.  The row of the node a walk ends at is not read.
+ *   mlxc_rejection_sampling validates the whole CSR on every call
+ *     (rowptr[0] == 0, rowptr[num_nodes] == num_edges, non-decreasing; every
+ *     col entry in [0, num_nodes)) and every start.
+ * The host twins report the same bits. */
 #define MLXC_STATUS_BAD_NODE 1 /* a start or col value outside [0, num_nodes) */
 #define MLXC_STATUS_BAD_ROW 2  /* rowptr[v] / rowptr[v+1] outside [0, num_edges] or decreasing */
 
@@ -178,8 +187,9 @@ int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes,
  * constants of BiasedRandomWalk.cpp:52-55.  `rows` is one of MLXC_ROWS_*:
  * sorted rows are searched through a 16-ary index, unsorted rows scanned
  * linearly as the reference does; MLXC_ROWS_DETECT decides on the device in
- * the call's preparation pass, which also validates the whole CSR (status
- * bits as for the walk).
+ * the call's preparation pass, the pass that also validates the whole CSR
+ * (status bits as above, for every MLXC_ROWS_* value).  No host
+ * synchronisation on any path.
  */
 int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes,
                             const int64_t* d_col, int64_t num_edges,

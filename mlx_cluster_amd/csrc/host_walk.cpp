@@ -400,9 +400,14 @@ int host_uniform(const HostWalk& w, bool generate, int32_t threads, uint32_t& st
 
 int host_node2vec(const HostWalk& w, const N2VParams& prm, int32_t threads, uint32_t& status) {
     const int t = resolve_threads(threads);
+    // the whole CSR is validated on every call, as the device layouts do
     uint32_t prep = 0;
     bool sorted = prm.rows == MLXC_ROWS_SORTED;
-    if (prm.rows == MLXC_ROWS_DETECT && w.num_walks > 0) prep = host_csr_scan(w, t, sorted);
+    if (w.num_walks > 0) {
+        bool detected = false;
+        prep = host_csr_scan(w, t, detected);
+        if (prm.rows == MLXC_ROWS_DETECT) sorted = detected;
+    }
     const int rc = w.out_type == MLXC_OUT_INT32
                        ? host_node2vec_typed<int32_t>(w, prm, sorted, t, status)
                        : host_node2vec_typed<int64_t>(w, prm, sorted, t, status);

@@ -11,20 +11,20 @@ struct N2VArgs {
     WalkArgs w;
     double prob0, prob1, prob2;
     uint32_t key0, key1;
+    int32_t rows;  // MLXC_ROWS_*; DETECT: work[2] != 0 when the rows are sorted
 };
 
 // Is t in row(x)?  BiasedRandomWalk.cpp:20-28 scans the row linearly; on a
 // sorted row lower_bound gives the same answer in log2(deg) probes.
-template <bool kSorted>
 __device__ __forceinline__ bool is_neighbor(const int64_t* __restrict__ rowptr,
                                             const int64_t* __restrict__ col, int64_t num_edges,
-                                            int64_t x, int64_t t, uint32_t& status) {
+                                            bool sorted, int64_t x, int64_t t, uint32_t& status) {
     const RowBounds rb = load_row(rowptr, x);
     if (!row_ok(rb, num_edges)) {
         status |= MLXC_STATUS_BAD_ROW;
         return false;
     }
-    if (!kSorted) {
+    if (!sorted) {
         for (int64_t i = rb.begin; i < rb.end; ++i)
             if (col[i] == t) return true;
         return false;
@@ -46,28 +46,33 @@ __device__ __forceinline__ bool is_neighbor(const int64_t* __restrict__ rowptr,
 // Acceptance of candidate x after previous node t (see accept rules in
 // mlxc.h).  The reference's chain (BiasedRandomWalk.cpp:86-91) has no side
 // effects, so the row search runs only when its answer decides the result.
-template <int kRule, bool kSorted>
-__device__ __forceinline__ bool accept(const N2VArgs& a, double r, int64_t x, int64_t t,
-                                       uint32_t& status) {
+template <int kRule>
+__device__ __forceinline__ bool accept(const N2VArgs& a, bool sorted, double r, int64_t x,
+                                       int64_t t, uint32_t& status) {
     if (kRule == MLXC_RULE_REF_CHAIN) {
         if (r < a.prob2) return true;
         if (x == t && r < a.prob0) return true;
         if (r < a.prob1)
-            return is_neighbor<kSorted>(a.w.rowptr, a.w.col, a.w.num_edges, x, t, status);
+            return is_neighbor(a.w.rowptr, a.w.col, a.w.num_edges, sorted, x, t, status);
         return false;
     }
     if (x == t) return r < a.prob0;
     const bool lt1 = r < a.prob1, lt2 = r < a.prob2;
     if (lt1 && lt2) return true;
     if (!lt1 && !lt2) return false;
-    return is_neighbor<kSorted>(a.w.rowptr, a.w.col, a.w.num_edges, x, t, status) ? lt1 : lt2;
+    return is_neighbor(a.w.rowptr, a.w.col, a.w.num_edges, sorted, x, t, status) ? lt1 : lt2;
 }
 
-template <int kRule, bool kSorted, bool kEdges, typename OutT>
+// node2vec walk on the CSR arrays (the fallback of the record walk).  The row
+// order comes from the device: csr_status_kernel leaves work[2] = 1 when the
+// CSR check found every row sorted, so the call needs no host round trip.
+template <int kRule, bool kEdges, typename OutT>
 __global__ __launch_bounds__(kBlock) void node2vec_walk_kernel(N2VArgs a) {
     const int64_t L = a.w.walk_length;
     const int64_t N = a.w.num_walks;
     const int64_t V = a.w.num_nodes;
+    const bool sorted = a.rows == MLXC_ROWS_SORTED ||
+                        (a.rows == MLXC_ROWS_DETECT && a.w.work[2] != 0);
     unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.w.work + 1);
     WaveQueue q{0, 0};
     uint32_t status = 0;
@@ -130,7 +135,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_walk_kernel(N2VArgs a) {
                             bad = true;
                             break;
                         }
-                        if (accept<kRule, kSorted>(a, r, x, t, status)) break;
+                        if (accept<kRule>(a, sorted, r, x, t, status)) break;
                         if (trial + 1 >= MLXC_MAX_TRIALS) break;
                     }
                 }
@@ -594,23 +599,34 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
 // bound by launch latency (the reference tests' Cora-sized workload): every
 // block copies rowptr and col, as int32, into its LDS; one walk per thread,
 // the same draws and decisions as the record walk, the neighbour test by
-// bisection (sorted rows) or a linear scan (unsorted rows) in LDS.  With
-// MLXC_ROWS_DETECT each block checks the row order of its copy.
+// bisection (sorted rows) or a linear scan (unsorted rows) in LDS.  Every
+// block validates its copy of the whole CSR, as the preparation passes of the
+// other layouts do (block 0 reports it); with MLXC_ROWS_DETECT each block
+// also checks the row order of its copy.
 template <int kRule, bool kEdges, typename OutT>
 __global__ __launch_bounds__(kBlock) void node2vec_lds_kernel(N2VRecArgs a) {
     __shared__ int32_t graph[kLdsGraphEntries];
     const int64_t V = a.w.num_nodes, E = a.w.num_edges, N = a.w.num_walks, L = a.w.walk_length;
     int32_t* const rp = graph;          // rowptr, -1 for an entry outside [0, E]
     int32_t* const cl = graph + V + 1;  // col, -1 for a value outside [0, V)
+    bool bad_row = false, bad_col = false;
     for (int64_t i = threadIdx.x; i <= V; i += kBlock) {
         const int64_t r = a.w.rowptr[i];
-        rp[i] = r >= 0 && r <= E ? static_cast<int32_t>(r) : -1;
+        const bool ok = r >= 0 && r <= E;
+        rp[i] = ok ? static_cast<int32_t>(r) : -1;
+        bad_row |= !ok || (i == 0 && r != 0) || (i == V && r != E);
     }
     for (int64_t i = threadIdx.x; i < E; i += kBlock) {
         const int64_t c = a.w.col[i];
-        cl[i] = node_ok(c, V) ? static_cast<int32_t>(c) : -1;
+        const bool ok = node_ok(c, V);
+        cl[i] = ok ? static_cast<int32_t>(c) : -1;
+        bad_col |= !ok;
     }
     __syncthreads();
+    for (int64_t u = threadIdx.x; u < V; u += kBlock) bad_row |= rp[u + 1] < rp[u];
+    // (both reductions are block-wide barriers every thread reaches)
+    const bool any_bad_row = __syncthreads_or(bad_row);
+    const bool any_bad_col = __syncthreads_or(bad_col);
     bool sorted = a.rows == MLXC_ROWS_SORTED;
     if (a.rows == MLXC_ROWS_DETECT) {
         bool descent = false;  // inside some well-formed row
@@ -624,6 +640,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_lds_kernel(N2VRecArgs a) {
     OutT* const nout = static_cast<OutT*>(a.w.n_out);
     OutT* const eout = static_cast<OutT*>(a.w.e_out);
     uint32_t status = 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        status = (any_bad_row ? MLXC_STATUS_BAD_ROW : 0u) | (any_bad_col ? MLXC_STATUS_BAD_NODE : 0u);
     for (int64_t n = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; n < N;
          n += static_cast<int64_t>(gridDim.x) * kBlock) {
         const int64_t s = a.w.start[n];
@@ -700,9 +718,9 @@ __global__ __launch_bounds__(kBlock) void node2vec_lds_kernel(N2VRecArgs a) {
 
 namespace {
 
-template <int kRule, bool kSorted, bool kEdges, typename OutT>
+template <int kRule, bool kEdges, typename OutT>
 int launch_n2v(const N2VArgs& a, hipStream_t stream) {
-    auto kernel = node2vec_walk_kernel<kRule, kSorted, kEdges, OutT>;
+    auto kernel = node2vec_walk_kernel<kRule, kEdges, OutT>;
     int grid = 0;
     if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
@@ -711,12 +729,8 @@ int launch_n2v(const N2VArgs& a, hipStream_t stream) {
 }
 
 template <int kRule, typename OutT>
-int dispatch_n2v(const N2VArgs& a, bool sorted, bool edges, hipStream_t stream) {
-    if (sorted)
-        return edges ? launch_n2v<kRule, true, true, OutT>(a, stream)
-                     : launch_n2v<kRule, true, false, OutT>(a, stream);
-    return edges ? launch_n2v<kRule, false, true, OutT>(a, stream)
-                 : launch_n2v<kRule, false, false, OutT>(a, stream);
+int dispatch_n2v(const N2VArgs& a, bool edges, hipStream_t stream) {
+    return edges ? launch_n2v<kRule, true, OutT>(a, stream) : launch_n2v<kRule, false, OutT>(a, stream);
 }
 
 // Resident blocks per compute unit of the node2vec record walk (0: as many
@@ -824,10 +838,10 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         index.count = lay.count;
         for (int k = 0; k < lay.count; ++k)
             index.level[k] = reinterpret_cast<int32_t*>(base + lay.level[k]);
-        // one pass builds the search index and the start records and, for
-        // MLXC_ROWS_DETECT, checks the rows (the walk reads the result on the
-        // device: no host sync)
-        int64_t* check = p.rows == MLXC_ROWS_DETECT ? w.work : nullptr;
+        // one pass builds the search index and the start records, validates
+        // the whole CSR and counts the row descents (MLXC_ROWS_DETECT: the walk
+        // reads the result on the device, no host sync)
+        int64_t* check = w.work;
         const StartRecords starts{w.start, w.num_walks, init};
         if (int rc = records ? launch_edge_records(w.rowptr, w.col, w.num_nodes, w.num_edges, recs,
                                                    index, starts, check, stream)
@@ -860,7 +874,8 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
     }
     // Small graphs with the header-sized workspace the query asks for them:
     // the LDS walk.
-    if (aligned && workspace_bytes >= kRecordOffset &&
+    // (it stores single elements: no alignment needed)
+    if (workspace_bytes >= kRecordOffset &&
         lds_walk_fits(w.num_nodes, w.num_edges, w.num_walks, w.walk_length)) {
         if (int rc = launch_zero_work(w.work, stream)) return rc;
         N2VRecArgs a{};
@@ -884,21 +899,13 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         return MLXC_OK;
     }
     // Graphs beyond int32, a workspace too small for the records, or output
-    // buffers not 16-byte aligned: the direct CSR kernel, which needs the row
-    // order on the host.
-    bool sorted = p.rows == MLXC_ROWS_SORTED;
-    if (p.rows == MLXC_ROWS_DETECT) {
-        if (int rc = launch_csr_check(w.rowptr, w.num_nodes, w.col, w.num_edges, w.work, stream))
-            return rc;
-        int64_t host[3] = {0, 0, 0};
-        MLXC_HIP_TRY(hipMemcpyAsync(host, w.work, sizeof(host), hipMemcpyDeviceToHost, stream));
-        MLXC_HIP_TRY(hipStreamSynchronize(stream));
-        if (host[0] & MLXC_CSR_BAD_ROWPTR) return fail(MLXC_ERR_INVALID_ARGUMENT, "rowptr is malformed");
-        if (host[0] & MLXC_CSR_BAD_COL)
-            return fail(MLXC_ERR_INVALID_ARGUMENT, "a col entry is outside [0, num_nodes)");
-        sorted = host[1] == host[2];
-        if (int rc = launch_zero_work(w.work, stream)) return rc;
-    }
+    // buffers not 16-byte aligned: the direct CSR kernel.  The CSR check
+    // validates the whole graph as the other layouts do; csr_status_kernel
+    // turns its words into the call's status bits and the row order, on the
+    // device.
+    if (int rc = launch_csr_check(w.rowptr, w.num_nodes, w.col, w.num_edges, w.work, stream))
+        return rc;
+    if (int rc = launch_csr_status(w.work, stream)) return rc;
     N2VArgs a;
     a.w = w;
     a.prob0 = p.prob0;
@@ -906,10 +913,11 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
     a.prob2 = p.prob2;
     a.key0 = p.key0;
     a.key1 = p.key1;
+    a.rows = p.rows;
     const bool edges = w.e_out != nullptr;
     return p.rule == MLXC_RULE_REF_CHAIN
-               ? dispatch_n2v<MLXC_RULE_REF_CHAIN, OutT>(a, sorted, edges, stream)
-               : dispatch_n2v<MLXC_RULE_NODE2VEC_EXACT, OutT>(a, sorted, edges, stream);
+               ? dispatch_n2v<MLXC_RULE_REF_CHAIN, OutT>(a, edges, stream)
+               : dispatch_n2v<MLXC_RULE_NODE2VEC_EXACT, OutT>(a, edges, stream);
 }
 
 }  // namespace

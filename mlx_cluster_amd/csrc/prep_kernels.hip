@@ -238,6 +238,19 @@ __global__ __launch_bounds__(kBlock) void csr_check_kernel(const int64_t* __rest
     check.flush(w, MLXC_CSR_BAD_ROWPTR, MLXC_CSR_BAD_COL, w + 1, w + 2);
 }
 
+// The words csr_check_kernel left, turned into a walk's: work[0] = the
+// MLXC_STATUS_* bits of the whole-graph check, work[1] = 0 (the walk queue),
+// work[2] = 1 when every row is sorted (else 0), work[3] = 0.
+__global__ void csr_status_kernel(int64_t* work) {
+    if (threadIdx.x != 0) return;
+    const int64_t bits = work[0], desc = work[1], start_desc = work[2];
+    work[0] = ((bits & MLXC_CSR_BAD_ROWPTR) ? MLXC_STATUS_BAD_ROW : 0) |
+              ((bits & MLXC_CSR_BAD_COL) ? MLXC_STATUS_BAD_NODE : 0);
+    work[1] = 0;
+    work[2] = desc == start_desc ? 1 : 0;
+    work[3] = 0;
+}
+
 __global__ __launch_bounds__(kBlock) void philox_fill_kernel(float* __restrict__ out, int64_t n,
                                                              uint32_t k0, uint32_t k1) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
@@ -337,6 +350,12 @@ int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* co
     if (int rc = stream_grid(num_nodes > num_edges ? num_nodes : num_edges, 8, grid)) return rc;
     hipLaunchKernelGGL(csr_check_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, num_nodes,
                        col, num_edges, d_work);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int launch_csr_status(int64_t* d_work, hipStream_t stream) {
+    hipLaunchKernelGGL(csr_status_kernel, dim3(1), dim3(kWave), 0, stream, d_work);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

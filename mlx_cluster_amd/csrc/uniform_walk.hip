@@ -248,8 +248,10 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                 ow[s].count = 0;
                 ew[s].count = 0;
             }
-            if (deg < 0) {
-                // malformed start or graph entry: stop (outputs unspecified)
+            // a malformed start or col entry, or the malformed row of a node
+            // the walk is to leave: stop (outputs unspecified).  The row of the
+            // node a walk ends at is not read by the reference, nor checked.
+            if (deg == kRecBadNode || (deg < 0 && l[s] + (ph[s] == kSlotWalk ? 1 : 0) < L)) {
                 status |= deg == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
                 ow_fill(ow[s], nout, g, g0 + L, node);
                 // edges of steps 0 .. l are buffered after a pick, none at the start
@@ -397,10 +399,12 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                 ew[s].count = 0;
                 v[s] = row[s].x;
                 push = true;
-                if (row[s].z < 0) {
-                    bad = row[s].z == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
+                if (row[s].z == kRecBadNode) {
+                    bad = MLXC_STATUS_BAD_NODE;
                 } else if (L == 0) {
-                    flush = true;
+                    flush = true;  // (the start's row is not read)
+                } else if (row[s].z < 0) {
+                    bad = MLXC_STATUS_BAD_ROW;
                 } else {
                     begin = row[s].y;
                     deg = row[s].z;
@@ -580,11 +584,14 @@ UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes, bool gen) {
                                  rtotal >= MLXC_RAND_WINDOW);
     const bool streams_ok = rand_ok && reinterpret_cast<uintptr_t>(a.n_out) % 16 == 0 &&
                             reinterpret_cast<uintptr_t>(a.e_out) % 16 == 0;  // e_out may be null
-    if (!streams_ok || !records_fit(a.num_nodes, a.num_edges)) return UniformMode::kPlain;
-    if (records_pay_off(a.num_edges, a.num_walks, a.walk_length) &&
-        workspace_bytes >= record_bytes(a.num_edges, a.num_walks))
-        return UniformMode::kRecords;
-    if (workspace_bytes >= init_bytes(a.num_walks)) return UniformMode::kCsr;
+    if (streams_ok && records_fit(a.num_nodes, a.num_edges)) {
+        if (records_pay_off(a.num_edges, a.num_walks, a.walk_length) &&
+            workspace_bytes >= record_bytes(a.num_edges, a.num_walks))
+            return UniformMode::kRecords;
+        if (workspace_bytes >= init_bytes(a.num_walks)) return UniformMode::kCsr;
+    }
+    // the LDS walk reads rand and stores its outputs one element at a time:
+    // any alignment and length will do
     if (workspace_bytes >= kRecordOffset &&
         lds_walk_fits(a.num_nodes, a.num_edges, a.num_walks, a.walk_length))
         return UniformMode::kLds;

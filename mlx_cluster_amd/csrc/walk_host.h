@@ -90,8 +90,13 @@ int launch_edge_index(const int64_t* rowptr, const int64_t* col, int64_t num_nod
 int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
                      int64_t num_edges, int64_t num_walks, EdgeRecord* init, int64_t* work,
                      hipStream_t stream);
+// work[0] |= MLXC_CSR_* bits, work[1] / work[2] += row descents (all
+// descents / those at a row start); the words must start at zero.
 int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                      int64_t num_edges, int64_t* d_work, hipStream_t stream);
+// Turns the words of launch_csr_check into a walk's: status bits in work[0],
+// work[1] = 0, work[2] = 1 if every row is sorted, work[3] = 0.
+int launch_csr_status(int64_t* d_work, hipStream_t stream);
 int launch_philox_fill(float* out, int64_t n, uint64_t seed, hipStream_t stream);
 
 // ---- uniform_walk.hip

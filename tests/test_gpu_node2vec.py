@@ -19,11 +19,14 @@ pytestmark = pytest.mark.gpu
 RULE_NAME = {oracle.RULE_REF_CHAIN: "ref_chain", oracle.RULE_NODE2VEC_EXACT: "node2vec"}
 
 
-def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode, out_dtype=torch.int64):
+def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode, out_dtype=torch.int64,
+              expect_status=0):
     """mlxc_rejection_sampling through the C ABI, with edge output, in the
     mode the workspace selects: "direct" (minimal workspace: the direct CSR
     kernel), "csr" (the CSR-mode layout: the record kernel without edge
-    records) or "records" (the edge-record layout)."""
+    records), "records" (the edge-record layout) or "lds" (the 256-byte
+    header: the LDS walk, for graphs and calls small enough).  Asserts the
+    call's status word equals expect_status."""
     from mlx_cluster_amd import _lib
     lib = _lib.load()
     N = start.numel()
@@ -33,7 +36,8 @@ def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode, out_dtype=tor
     out_type = _lib.MLXC_OUT_INT32 if out_dtype == torch.int32 else _lib.MLXC_OUT_INT64
     query = lambda N_, L_: lib.mlxc_rejection_sampling_workspace_bytes(V, E, N_, L_, p, q, rule)
     # the query sizes records only for calls of many steps per edge
-    nbytes = {"direct": 32, "csr": query(N, 0), "records": query(max(N, 1), 2**31 - 1)}[mode]
+    nbytes = {"direct": 32, "csr": query(N, 0), "records": query(max(N, 1), 2**31 - 1),
+              "lds": 256}[mode]
     if mode == "csr" and E > 0:
         assert nbytes < query(max(N, 1), 2**31 - 1)
     ws = torch.zeros((nbytes + 7) // 8, dtype=torch.int64, device=start.device)
@@ -44,7 +48,7 @@ def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode, out_dtype=tor
                                      torch.cuda.current_stream().cuda_stream)
     assert rc == 0, _lib.last_error()
     torch.cuda.synchronize()
-    assert int(ws[0].item()) == 0
+    assert int(ws[0].item()) == expect_status, f"{mode}: status {int(ws[0].item())}"
     return n, e
 
 
@@ -237,15 +241,28 @@ def test_symmetric_hint(p, q, rule, cuda):
 
 
 def test_csr_check_matches_oracle(cuda):
+    """csr_check equals the oracle's flags, and a malformed graph raises on
+    every call whether or not a walk meets the bad entry: seed 0 takes
+    candidate 0 of row(0) at walk 0's first step and never reads col[1] = 9,
+    seed 1 takes candidate 1 (both checked on the oracle's stream here)."""
     rowptr, col = csr(4, [(0, 1), (0, 3), (2, 1)])
     cases = [(rowptr, col), (rowptr, np.array([3, 1, 1])), (rowptr, np.array([1, 9, 1])),
              (np.array([0, 2, 1, 3, 3]), col), (np.array([0, 2, 2, 3, 4]), col)]
     for rp, cl in cases:
         assert mc.csr_check(rp, cl) == oracle.csr_flags(rp, cl)
-    with pytest.raises(ValueError, match="outside"):
-        mc.rejection_sampling(rowptr, np.array([1, 9, 1]), np.array([0]), 3, 1.0, 1.0)
-    with pytest.raises(ValueError, match="rowptr"):
-        mc.rejection_sampling(np.array([0, 2, 1, 3, 3]), col, np.array([0]), 3, 1.0, 1.0)
+    u0 = {s: float(oracle.node2vec_trial0_u0(1, 1, s)[0, 0]) for s in (0, 1)}
+    assert oracle.pick_index(u0[0], 2) == 0 and oracle.pick_index(u0[1], 2) == 1
+    for seed in (0, 1):
+        for stream in (None, "cpu"):
+            with pytest.raises(ValueError, match="outside"):
+                mc.rejection_sampling(rowptr, np.array([1, 9, 1]), np.array([0]), 3, 1.0, 1.0,
+                                      seed=seed, stream=stream)
+            with pytest.raises(ValueError, match="rowptr"):
+                mc.rejection_sampling(np.array([0, 2, 1, 3, 3]), col, np.array([0]), 3, 1.0, 1.0,
+                                      seed=seed, stream=stream)
+            with pytest.raises(ValueError, match="rowptr"):  # rowptr[V] != E, every row valid
+                mc.rejection_sampling(np.array([0, 1, 1, 2, 2]), col, np.array([0]), 3, 1.0, 1.0,
+                                      seed=seed, stream=stream)
 
 
 def test_seed_none_follows_torch_manual_seed(c1, cuda):
@@ -441,6 +458,8 @@ def test_lds_walks_random_sweep(cuda):
     the uniform and node2vec LDS walks (the Python API's default for these
     sizes) are bit-exact against the oracle for both rules and several
     (p, q)."""
+    from mlx_cluster_amd import _lib
+    lib = _lib.load()
     rng = np.random.default_rng(2024)
     t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.int64)).to(cuda)
     for case in range(12):
@@ -453,6 +472,9 @@ def test_lds_walks_random_sweep(cuda):
         N = int(rng.integers(1, 3000))
         L = int(rng.integers(1, 50))
         start = rng.integers(0, V, N)
+        # the Python API takes the LDS walks here, whatever N * L is
+        assert lib.mlxc_random_walk_workspace_bytes(V, col.size, N, L) == 256
+        assert lib.mlxc_rejection_sampling_workspace_bytes(V, col.size, N, L, 1.0, 1.0, 0) == 256
         rand = mc.philox_uniform((N, L), case, device=cuda)
         n_ref, e_ref, st, _ = oracle.uniform_walk(rowptr, col, start, rand.cpu().numpy(), L,
                                                   with_edges=True)

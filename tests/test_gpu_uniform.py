@@ -162,6 +162,45 @@ def test_c2_full_size_properties(cuda):
     np.testing.assert_array_equal(n[sample].cpu().numpy(), n_ref)
 
 
+def test_c4_full_size_properties(cuda):
+    """Configuration 4 at full size (R-MAT 2^24 with 2^28 samples, one walk
+    per node, L=20), which the workspace query sends to the CSR walk (fewer
+    than 4 steps per edge): every one of the 335,544,320 steps and its edge id
+    is checked against torch float32 arithmetic on the device, and 4,000
+    sampled walks bit-exactly against the oracle, nodes and edges."""
+    rowptr, col = synth.rmat_csr(24, 1 << 28, seed=0, device=cuda)
+    V, E = rowptr.numel() - 1, col.numel()
+    N, L = V, 20
+    assert N * L < 4 * E  # the CSR walk, not edge records
+    from mlx_cluster_amd import _lib
+    assert _lib.load().mlxc_random_walk_workspace_bytes(V, E, N, L) == 256 + 16 * N
+    start = torch.arange(N, device=cuda)
+    rand = mc.philox_uniform((N, L), 4, device=cuda)
+    n, e = mc.random_walk(rowptr, col, start, rand, L, return_edges=True)
+    assert torch.equal(n[:, 0], start)
+    bad = 0
+    for l in range(L):
+        u, v = n[:, l], n[:, l + 1]
+        rs = rowptr[u]
+        deg = rowptr[u + 1] - rs
+        prod = rand[:, l] * deg.to(torch.float32)
+        idx = torch.minimum(prod.to(torch.int64), (deg - 1).clamp_min(0))
+        moving = deg > 0
+        edge = torch.where(moving, rs + idx, -1)
+        expect = torch.where(moving, col[edge.clamp_min(0)], u)
+        bad += int((expect != v).sum()) + int((edge != e[:, l]).sum())
+        del u, v, rs, deg, prod, idx, moving, edge, expect
+    assert bad == 0
+    g = torch.Generator().manual_seed(4)
+    sample = torch.randint(0, N, (4000,), generator=g).to(cuda)
+    rp, cl = rowptr.cpu().numpy(), col.cpu().numpy()
+    n_ref, e_ref, st, _ = oracle.uniform_walk(rp, cl, start[sample].cpu().numpy(),
+                                              rand[sample].cpu().numpy(), L, with_edges=True)
+    assert st == 0
+    np.testing.assert_array_equal(n[sample].cpu().numpy(), n_ref)
+    np.testing.assert_array_equal(e[sample].cpu().numpy(), e_ref)
+
+
 def _abi_walk(rowptr, col, start, rand_t, L, n_out_t, *, e_out=None, ws_bytes=None,
               out_type=0):
     """Calls mlxc_random_walk directly so each kernel path can be selected:

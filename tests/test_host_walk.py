@@ -11,6 +11,7 @@ import torch
 import mlx_cluster_amd as mc
 import oracle
 from mlx_cluster_amd import synth
+from tests import status_cases
 from tests.graphs import csr, undirected, uniform_transitions_ok
 
 RULE_NAME = {oracle.RULE_REF_CHAIN: "ref_chain", oracle.RULE_NODE2VEC_EXACT: "node2vec"}
@@ -230,3 +231,28 @@ def test_out_dtype_validation():
     with pytest.raises(TypeError, match="out_dtype"):
         mc.rejection_sampling(rowptr, col, np.array([0]), 2, 1.0, 1.0, stream="cpu",
                               out_dtype=torch.float32)
+
+
+@pytest.mark.parametrize("case", status_cases.N2V_CASES, ids=[c[0] for c in status_cases.N2V_CASES])
+def test_node2vec_status_bits(case):
+    """The host twin validates the whole CSR on every call: the hand-derived
+    bits for every row mode and both seeds (one of which never meets the bad
+    col entry of the 'bad col' case)."""
+    from mlx_cluster_amd import _lib
+    name, rowptr, col, start, want = case
+    for seed in (0, 1):
+        for rows in (0, 1, 2):
+            got = status_cases.host_node2vec_status(_lib.load(), rowptr, col, start, 3, 0.5, 2.0,
+                                                    seed, 0, rows)
+            assert got == want, (name, seed, rows, got)
+
+
+@pytest.mark.parametrize("case", status_cases.UNI_CASES, ids=[c[0] for c in status_cases.UNI_CASES])
+def test_uniform_status_bits(case):
+    """The host twin reports what the walks read (a start, the row of a node
+    a walk leaves, a chosen col entry): the hand-derived bits."""
+    from mlx_cluster_amd import _lib
+    name, rowptr, col, start, L, want = case
+    for seed in (None, 5):
+        got = status_cases.host_uniform_status(_lib.load(), rowptr, col, start, L, seed=seed)
+        assert got == want, (name, seed, got)
