@@ -153,6 +153,33 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes,
                      void* d_n_out, void* d_e_out, int32_t out_type,
                      void* d_workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of the device scratch array that mlxc_random_walk_noalloc uses in
+ * place of a workspace (one array per GPU, held until the process ends). */
+#define MLXC_NOALLOC_SCRATCH_BYTES (64 * 1024 * 1024)
+
+/*
+ * mlxc_random_walk without a workspace argument: allocates nothing.
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory around the call (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  The kernels, layouts and results are
+ * those of mlxc_random_walk with a workspace of
+ * mlxc_random_walk_workspace_bytes(num_nodes, num_edges, num_walks,
+ * walk_length) bytes; that workspace lives in a file-scope device array of
+ * MLXC_NOALLOC_SCRATCH_BYTES per GPU instead.  A call whose workspace would
+ * be larger fails with MLXC_ERR_INVALID_ARGUMENT (use mlxc_random_walk).
+ * d_status (device pointer to one int64, or NULL) receives the call's
+ * MLXC_STATUS_* bits on `stream`.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (different streams, or host threads
+ * without ordering) race and must not be issued.  The first call on each GPU
+ * looks up the array's device address (hipGetSymbolAddress) once.
+ */
+int mlxc_random_walk_noalloc(const int64_t* d_rowptr, int64_t num_nodes,
+                             const int64_t* d_col, int64_t num_edges,
+                             const int64_t* d_start, int64_t num_walks,
+                             const float* d_rand, int32_t walk_length,
+                             void* d_n_out, void* d_e_out, int32_t out_type,
+                             int64_t* d_status, void* stream);
+
 /*
  * Uniform random walk that generates its uniforms instead of reading a rand
  * tensor: the same walk as mlxc_random_walk with

@@ -36,6 +36,7 @@ MLXC_OUT_INT32 = 1
 MLXC_CSR_SYMMETRIZE = 1
 MLXC_CSR_DEDUP = 2
 MLXC_MAX_TRIALS = 65536
+MLXC_NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -53,6 +54,10 @@ SIGNATURES = {
     "mlxc_random_walk": (
         ctypes.c_int,
         [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _i32, _ptr, _size, _ptr],
+    ),
+    "mlxc_random_walk_noalloc": (
+        ctypes.c_int,
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _i32, _ptr, _ptr],
     ),
     "mlxc_random_walk_seeded": (
         ctypes.c_int,

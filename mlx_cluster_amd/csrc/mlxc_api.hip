@@ -9,6 +9,11 @@
 
 #include "walk_host.h"
 
+// Workspace of mlxc_random_walk_noalloc, one per GPU.  In host code this
+// name is only a stand-in for the symbol: kernels get its device address,
+// looked up once per device by noalloc_scratch().
+static __device__ __align__(256) unsigned char scratch[MLXC_NOALLOC_SCRATCH_BYTES];
+
 namespace mlxc {
 
 namespace {
@@ -157,6 +162,25 @@ int check_negative(const int64_t* start, int64_t num_walks, int32_t walk_length,
     return MLXC_OK;
 }
 
+// Device address of the current device's scratch array, looked up with
+// that device current on the first call there and kept per device.
+int noalloc_scratch(void** out) {
+    static std::mutex mu;
+    static void* addr[64] = {};
+    int dev = 0;
+    MLXC_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return fail(MLXC_ERR_HIP, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        MLXC_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(MLXC_ERR_HIP, "hipGetSymbolAddress returned NULL for the scratch array");
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return MLXC_OK;
+}
+
 HostWalk host_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                    int64_t num_edges, const int64_t* start, int64_t num_walks, const float* rand,
                    int32_t walk_length, uint64_t seed, void* n_out, void* e_out,
@@ -208,6 +232,37 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* 
     const WalkArgs a{d_rowptr, d_col, d_start, d_rand, d_n_out, d_e_out, d_work,
                      num_nodes, num_edges, num_walks, walk_length, 0u, 0u};
     return launch_uniform(a, d_workspace, workspace_bytes, false, out_type, s);
+}
+
+int mlxc_random_walk_noalloc(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
+                             int64_t num_edges, const int64_t* d_start, int64_t num_walks,
+                             const float* d_rand, int32_t walk_length, void* d_n_out,
+                             void* d_e_out, int32_t out_type, int64_t* d_status, void* stream) {
+    if (int rc = check_graph(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
+                             walk_length, d_n_out))
+        return rc;
+    if (int rc = check_out_type(out_type, num_nodes, num_edges, d_e_out)) return rc;
+    if (num_walks > 0 && walk_length > 0 && !d_rand)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "rand must not be NULL");
+    const size_t need = uniform_workspace_bytes(num_nodes, num_edges, num_walks, walk_length);
+    if (need > static_cast<size_t>(MLXC_NOALLOC_SCRATCH_BYTES))
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "this call needs " + std::to_string(need) +
+                        " bytes of workspace, more than the MLXC_NOALLOC_SCRATCH_BYTES (" +
+                        std::to_string(MLXC_NOALLOC_SCRATCH_BYTES) +
+                        ") of mlxc_random_walk_noalloc; call mlxc_random_walk with a workspace");
+    void* ws = nullptr;
+    if (int rc = noalloc_scratch(&ws)) return rc;
+    // the same call as mlxc_random_walk with a workspace of the queried size;
+    // its launches clear the status words first, so stale contents of the
+    // shared array do not matter
+    if (int rc = mlxc_random_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
+                                  d_rand, walk_length, d_n_out, d_e_out, out_type, ws, need,
+                                  stream))
+        return rc;
+    if (!d_status) return MLXC_OK;
+    return launch_copy_word(static_cast<const int64_t*>(ws), d_status,
+                            static_cast<hipStream_t>(stream));
 }
 
 int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,

@@ -9,6 +9,10 @@ __global__ void zero_words_kernel(int64_t* p, int n) {
     if (i < n) p[i] = 0;
 }
 
+__global__ void copy_word_kernel(const int64_t* src, int64_t* dst) {
+    if (threadIdx.x == 0) *dst = *src;
+}
+
 __device__ __forceinline__ int64_t wave_sum(int64_t x) {
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
@@ -350,6 +354,12 @@ int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* co
     if (int rc = stream_grid(num_nodes > num_edges ? num_nodes : num_edges, 8, grid)) return rc;
     hipLaunchKernelGGL(csr_check_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, num_nodes,
                        col, num_edges, d_work);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int launch_copy_word(const int64_t* d_src, int64_t* d_dst, hipStream_t stream) {
+    hipLaunchKernelGGL(copy_word_kernel, dim3(1), dim3(kWave), 0, stream, d_src, d_dst);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

@@ -97,6 +97,8 @@ int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* co
 // Turns the words of launch_csr_check into a walk's: status bits in work[0],
 // work[1] = 0, work[2] = 1 if every row is sorted, work[3] = 0.
 int launch_csr_status(int64_t* d_work, hipStream_t stream);
+// *d_dst = *d_src on the stream (a kernel, so the call can be captured).
+int launch_copy_word(const int64_t* d_src, int64_t* d_dst, hipStream_t stream);
 int launch_philox_fill(float* out, int64_t n, uint64_t seed, hipStream_t stream);
 
 // ---- uniform_walk.hip
