@@ -98,6 +98,13 @@ def kernel_source_hash() -> str:
     return source_hash()
 
 
+# What roofline.traffic counts: rocprofv3 FETCH_SIZE + WRITE_SIZE, the bytes
+# between the L2 and the data fabric.  Reads served by the Infinity Cache
+# (MALL) are included, so this is an upper bound on DRAM traffic.
+TRAFFIC_KIND = ("L2-to-fabric bytes per launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated); "
+                "Infinity Cache hits included")
+
+
 def traffic_from_profile(name: str):
     """HBM bytes per launch from a committed rocprofv3 --pmc summary of the
     same kernel source (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-
@@ -140,18 +147,20 @@ class one_core:
 
 
 def cpu_baseline_uniform(np, oracle, rowptr_h, col_h, start, rand, L, target_s=12.0):
-    """Single-threaded oracle walk on an evenly strided sample of walks."""
+    """Single-threaded oracle walk on an evenly strided sample of walks, with
+    the edge-id store of RandomWalk.cpp:58 (the reference's loop writes both
+    outputs, whichever the op returns)."""
     N = start.shape[0]
     probe = min(N, 20_000)
     idx = np.linspace(0, N - 1, probe).astype(np.int64)
     t0 = time.perf_counter()
-    oracle.uniform_walk(rowptr_h, col_h, start[idx], rand[idx], L)
+    oracle.uniform_walk(rowptr_h, col_h, start[idx], rand[idx], L, with_edges=True)
     rate = probe * L / (time.perf_counter() - t0)
     walks = int(min(N, max(probe, target_s * rate / L)))
     idx = np.linspace(0, N - 1, walks).astype(np.int64)
     s, r = start[idx], rand[idx]
     t0 = time.perf_counter()
-    _, _, st, _ = oracle.uniform_walk(rowptr_h, col_h, s, r, L)
+    _, _, st, _ = oracle.uniform_walk(rowptr_h, col_h, s, r, L, with_edges=True)
     dt = time.perf_counter() - t0
     assert st == 0
     return walks * L / dt, walks, dt
@@ -180,7 +189,8 @@ def cpu_all_cores_context(np, torch, mc, kind, rowptr_h, col_h, start, rand, L, 
     s = torch.from_numpy(start)[idx]
     t0 = time.perf_counter()
     if kind == "uniform":
-        mc.random_walk(rp, cl, s, torch.from_numpy(rand)[idx], L, stream="cpu", threads=threads)
+        mc.random_walk(rp, cl, s, torch.from_numpy(rand)[idx], L, stream="cpu", threads=threads,
+                       return_edges=True)
     else:
         mc.rejection_sampling(rp, cl, s, L, extra["p"], extra["q"], seed=extra["seed"],
                               rule=extra["rule"], rows_sorted=True, stream="cpu", threads=threads)
@@ -368,7 +378,8 @@ def bench_csr(args, np, torch, mc, synth, dev):
                 "radix_passes": passes, "key_bytes": k,
                 "radix_stream_bytes_per_launch": pass_bytes,
                 "radix_stream_gbs": pass_bytes / (kernel_ms / 1e3) / 1e9,
-                "hbm_gbs_measured": (traffic / (kernel_ms / 1e3) / 1e9) if traffic else None}
+                "fabric_gbs_measured": (traffic / (kernel_ms / 1e3) / 1e9) if traffic else None,
+                "traffic_kind": TRAFFIC_KIND}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -466,7 +477,8 @@ def bench_windows(args, np, torch, mc, synth, dev):
                 "bytes_formula": "8*N*(L+1) (walks) + 8*N (starts) + 2 * 8*W*N*C (windows)",
                 "kernel_ms": kernel_ms, "kernel_ms_median": float(np.median(event_ms)),
                 "kernel_ms_source": "HIP events around each step on its stream (mean; median beside it)",
-                "hbm_gbs_measured": (traffic / (kernel_ms / 1e3) / 1e9) if traffic else None}
+                "fabric_gbs_measured": (traffic / (kernel_ms / 1e3) / 1e9) if traffic else None,
+                "traffic_kind": TRAFFIC_KIND}
     cpu = None
     if not args.no_cpu_baseline:
         model, cores = host_info()
@@ -654,7 +666,8 @@ def main():
                 "kernel_ms_source": "HIP events around each call on its stream (mean; median beside it)",
                 "useful_gbs": useful_bytes / (kernel_ms / 1e3) / 1e9,
                 "useful_bytes_per_launch": useful_bytes,
-                "hbm_gbs_measured": (traffic / (kernel_ms / 1e3) / 1e9) if traffic else None,
+                "fabric_gbs_measured": (traffic / (kernel_ms / 1e3) / 1e9) if traffic else None,
+                "traffic_kind": TRAFFIC_KIND,
                 **units}
 
     # Sampled bit-exact parity against the oracle, and the CPU baseline.
@@ -684,7 +697,9 @@ def main():
                                                    args.cpu_seconds)
         cpu = {"value": rate, "unit": "walk-steps/s", "cores": 1, "kind": "port",
                "sample": f"{walks} of {N} walks (evenly strided) x {L} steps, {dt:.1f} s, "
-                         f"oracle/walk_oracle.c uniform walk, 1 thread pinned to one core"}
+                         f"oracle/walk_oracle.c uniform walk writing nodes and edge ids "
+                         f"(RandomWalk.cpp:57-58), 1 thread pinned to one core",
+               "sample_fraction": walks / N}
         log(f"cpu baseline {rate:.3e} steps/s over {walks} walks")
     elif not args.no_cpu_baseline:
         with one_core() as pin:
@@ -694,7 +709,8 @@ def main():
         cpu = {"value": rate, "unit": "walk-steps/s", "cores": 1, "kind": "port",
                "sample": f"{walks} of {N} walks (evenly strided) x {L} steps, {dt:.1f} s, "
                          f"oracle/walk_oracle.c node2vec walk with libc rand() and linear "
-                         f"is_neighbor scans as in the reference, 1 thread pinned to one core"}
+                         f"is_neighbor scans as in the reference, 1 thread pinned to one core",
+               "sample_fraction": walks / N}
         rand_h = None
         log(f"cpu baseline {rate:.3e} steps/s over {walks} walks")
 
@@ -716,6 +732,9 @@ def main():
                    "num_walks": N, "walk_length": L, "walk_steps_per_launch": steps_per_launch,
                    "parity_sample_bit_exact": parity},
         "roofline": roofline, "cpu_baseline": cpu,
+        # steps that leave a node of out-degree > 0, per second of wall time
+        # (the rest are the stationary steps of walks absorbed by a sink)
+        "moving_steps_per_s": units["moving_steps"] / (ms_per_step / 1e3),
     }
     if cpu:
         line["speedup_vs_cpu_baseline"] = value / cpu["value"]
