@@ -181,6 +181,23 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(EdgeSrc src,
                  static_cast<unsigned long long>(MLXC_STATUS_BAD_NODE));
 }
 
+// Tile of scatter block b.  Workgroups are dispatched to the 8 XCDs round
+// robin, and each XCD has its own L2.  Tile t's run of digit d ends where tile
+// t + 1's run of d begins, in the same 128-byte line; giving each XCD a
+// contiguous range of tiles puts both partial writes of that line into one L2,
+// which merges them.
+#ifndef MLXC_CSR_XCD_REMAP
+#define MLXC_CSR_XCD_REMAP 1
+#endif
+constexpr int kXcds = 8;
+__device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t tiles) {
+    if (!MLXC_CSR_XCD_REMAP) return b;
+    const int64_t q = tiles / kXcds, r = tiles % kXcds;
+    const int64_t x = b % kXcds, i = b / kXcds;  // XCD x runs its i-th block
+    // XCDs 0 .. r-1 take q + 1 tiles, the others q: a bijection of [0, tiles)
+    return x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+}
+
 template <typename KeyT, bool kFirst>
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     EdgeSrc src, const KeyT* __restrict__ keys_in, KeyT* __restrict__ keys_out, int shift,
@@ -191,7 +208,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     __shared__ int64_t goff[kRadix];
     __shared__ int64_t wtot[kSortWaves];
     const int t = threadIdx.x, w = t / kWave, lane = t % kWave;
-    const int64_t tile = blockIdx.x;
+    const int64_t tile = xcd_tile(blockIdx.x, tiles);
     for (int k = t; k < kSortWaves * kRadix; k += kSortThreads) (&cnt[0][0])[k] = 0;
     if (t < kRadix) goff[t] = offsets[static_cast<int64_t>(t) * tiles + tile];
     __syncthreads();
