@@ -160,6 +160,7 @@ enum : int {
     kN2vScan = 4,    // unsorted rows: reads the next 16 entries of row(x)
     kN2vDone = 5,    // the queue is exhausted
     kN2vRow = 6,     // CSR mode: reads rowptr[x], rowptr[x + 1] of the candidate
+    kN2vBit = 7,     // reads the word of a hub bitmap that answers the neighbour test
 };
 
 // What a CSR-mode slot does once the candidate's row has been read.
@@ -256,6 +257,10 @@ struct N2VRecArgs {
     // exactly when r < thr_k.
     float thr0, thr1, thr2;
     uint32_t key0, key1;
+    // Hub bitmaps (record mode; null: none): bitmap s is hub_words words from
+    // hub_bits + s * hub_words, and the records carry each node's slot.
+    const uint32_t* hub_bits;
+    int64_t hub_words;
 };
 
 // Smallest float >= p (p > 0), the float threshold of N2VRecArgs.
@@ -355,6 +360,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     int32_t blk = 0;        // search: that block (kN2vLevel)
     int32_t lo = 0, hi = 0; // search: col32 positions that can still hold tgt
     int32_t tgt = 0;        // search: the node looked for (t in row(x), or x in row(t))
+    int32_t sx = -1, sv = -1, s_t = -1;  // hub bitmap slots of x, v and t (-1: none)
     float r = 0.0f;         // acceptance uniform of the current trial
     OutWin<int32_t> ow;
     OutWin<int32_t> ew;     // edge ids (kEdges): e_out[n*L + l] is step l's edge
@@ -388,6 +394,10 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             bp = a.index.level[0] + off + static_cast<int64_t>(kSearchBlock) * blk;
         } else if (ph == kN2vScan) {
             bp = a.index.level[0] + (lo & ~(kSearchBlock - 1));
+        } else if (!kCsr && ph == kN2vBit) {
+            // the aligned 16 bytes holding word tgt / 32 of bitmap blk
+            bp = reinterpret_cast<const int32_t*>(a.hub_bits + blk * a.hub_words +
+                                                  ((tgt >> 5) & ~3));
         } else {
             bp = reinterpret_cast<const int32_t*>(a.init);
         }
@@ -429,6 +439,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             ow.count = 0;
             ew.count = 0;
             v = rec.x;
+            sv = kCsr ? -1 : rec.w;
             push = true;
             if (rec.z < 0) {
                 status |= rec.z == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
@@ -492,6 +503,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             x = rec.x;
             bx = rec.y;
             dx = rec.z;
+            sx = rec.w;
             if (dx < 0) {
                 status |= dx == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
                 fill = true;
@@ -508,7 +520,18 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                     next_trial = !accept;
                 } else {
                     n2v_search_rows(a.symmetric, x, bx, dx, t, bt, dt, lo, hi, tgt);
-                    if (!sorted) {
+                    // a row inside one aligned 16-entry block takes one read
+                    // either way; longer ones take the bitmap's single read
+                    const bool one_block = ((lo ^ (hi - 1)) >> 4) == 0;
+                    if (!one_block && sx >= 0) {
+                        blk = sx;  // bit t of row(x)'s bitmap
+                        tgt = t;
+                        phase = kN2vBit;
+                    } else if (!one_block && a.symmetric && s_t >= 0) {
+                        blk = s_t;  // bit x of row(t)'s bitmap: the same answer on a symmetric graph
+                        tgt = x;
+                        phase = kN2vBit;
+                    } else if (!sorted) {
                         phase = kN2vScan;
                     } else {
                         // finest level whose aligned blocks (16^(lvl+1) positions)
@@ -520,6 +543,10 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                     }
                 }
             }
+        } else if (!kCsr && ph == kN2vBit) {
+            const uint32_t word = static_cast<uint32_t>(rec[(tgt >> 5) & 3]);
+            accept = n2v_resolve<kRule>(a, r, ((word >> (tgt & 31)) & 1u) != 0);
+            next_trial = !accept;
         } else {  // the neighbour search: is t in row(x)?
             int32_t vals[kSearchBlock];
 #pragma unroll
@@ -559,9 +586,11 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             t = v;
             bt = bv;
             dt = dv;
+            s_t = sv;
             v = x;
             bv = bx;
             dv = dx;
+            sv = sx;
             if (l == L) {
                 flush = true;
             } else if (dv == 0) {
@@ -755,19 +784,33 @@ int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
 // records, then (128-byte aligned) the levels of the search index — col as
 // int32, then its samples every 16^k entries — each padded to whole blocks of
 // kSearchBlock entries, then 64 bytes of slack for the block reads of the
-// last start records.
+// last start records.  Record mode then adds the hub bitmaps: the info words,
+// slot_of [V], node_of [max] and the bitmaps [max][words], up to
+// kHubBudgetBytes of bitmaps and at most one slot per kHubMinDegree entries.
 struct N2VLayout {
     size_t level[kMaxLevels];
     int count;
+    size_t total_no_hubs;  // the layout without hub bitmaps
+    size_t hub_info, hub_slot_of, hub_node_of, hub_bits;
+    int32_t hub_max;
+    int64_t hub_words;
     size_t total;
 };
 
-N2VLayout n2v_layout(int64_t num_edges, int64_t num_walks, bool records) {
+// Bytes of hub bitmaps a record layout reserves at most (0: no bitmaps).
+#ifndef MLXC_HUB_BUDGET_BYTES
+#define MLXC_HUB_BUDGET_BYTES (int64_t{1} << 30)
+#endif
+constexpr int64_t kHubBudgetBytes = MLXC_HUB_BUDGET_BYTES;
+
+size_t align128(size_t x) { return (x + 127) & ~static_cast<size_t>(127); }
+
+N2VLayout n2v_layout(int64_t num_nodes, int64_t num_edges, int64_t num_walks, bool records) {
     N2VLayout lay;
     lay.count = index_levels(num_edges);
     size_t pos = kRecordOffset +
                  static_cast<size_t>((records ? num_edges : 0) + num_walks) * sizeof(EdgeRecord);
-    pos = (pos + 127) & ~static_cast<size_t>(127);
+    pos = align128(pos);
     int64_t entries = num_edges;  // level k has ceil(num_edges / 16^k) entries
     for (int k = 0; k < lay.count; ++k) {
         lay.level[k] = pos;
@@ -775,7 +818,21 @@ N2VLayout n2v_layout(int64_t num_edges, int64_t num_walks, bool records) {
         pos += static_cast<size_t>(blocks) * kSearchBlock * sizeof(int32_t);
         entries = blocks;
     }
-    lay.total = pos + 64;
+    lay.total_no_hubs = pos + 64;
+    lay.hub_words = ((num_nodes + 31) / 32 + 3) / 4 * 4;
+    const int64_t bitmap_bytes = lay.hub_words * 4;
+    int64_t max = records && num_nodes > 0 && kHubBudgetBytes > 0 ? num_edges / kHubMinDegree : 0;
+    if (bitmap_bytes > 0 && max > kHubBudgetBytes / bitmap_bytes) max = kHubBudgetBytes / bitmap_bytes;
+    lay.hub_max = static_cast<int32_t>(max);
+    lay.total = lay.total_no_hubs;
+    lay.hub_info = lay.hub_slot_of = lay.hub_node_of = lay.hub_bits = 0;
+    if (lay.hub_max > 0) {
+        lay.hub_info = align128(lay.total_no_hubs);
+        lay.hub_slot_of = align128(lay.hub_info + kHubInfoWords * sizeof(int64_t));
+        lay.hub_node_of = align128(lay.hub_slot_of + static_cast<size_t>(num_nodes) * sizeof(int32_t));
+        lay.hub_bits = align128(lay.hub_node_of + static_cast<size_t>(max) * sizeof(int32_t));
+        lay.total = lay.hub_bits + static_cast<size_t>(max) * static_cast<size_t>(bitmap_bytes);
+    }
     return lay;
 }
 
@@ -808,29 +865,64 @@ size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t nu
         return MLXC_WORK_WORDS * sizeof(int64_t);
     if (lds_walk_fits(num_nodes, num_edges, num_walks, walk_length))
         return kRecordOffset;  // the LDS walk: its size selects it
-    return n2v_layout(num_edges, num_walks,
+    return n2v_layout(num_nodes, num_edges, num_walks,
                       n2v_records_pay_off(num_edges, num_walks, walk_length, search_width))
         .total;
 }
 
 namespace {
 
+// Smallest row degree worth a hub bitmap in this call.  A bitmap costs
+// num_nodes / 8 bytes of streamed writes per call and saves about two
+// dependent reads on each of the call's searches of its row, about
+// deg * rho of them (rho: searches per CSR entry, at least steps * w / E for
+// a search share w of the draws).  Counting a dependent read as 4 streamed
+// lines of 128 bytes, the bitmap pays off from deg ~ num_nodes / (4096 rho).
+// INT64_MAX: the call makes no searches, so no bitmaps.
+int64_t n2v_hub_min_degree(const WalkArgs& w, const N2VParams& p) {
+    const double width = n2v_search_width(p);
+    const double rho = static_cast<double>(w.num_walks) * w.walk_length * width /
+                       static_cast<double>(w.num_edges > 0 ? w.num_edges : 1);
+    if (!(rho > 0.0)) return INT64_MAX;
+    const double d = static_cast<double>(w.num_nodes) / (4096.0 * rho);
+    if (d >= 1e18) return INT64_MAX;
+    return d > static_cast<double>(kHubMinDegree) ? static_cast<int64_t>(std::ceil(d))
+                                                  : kHubMinDegree;
+}
+
 template <typename OutT>
 int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace,
                           size_t workspace_bytes, hipStream_t stream) {
     const bool aligned = reinterpret_cast<uintptr_t>(w.n_out) % 16 == 0 &&
                          reinterpret_cast<uintptr_t>(w.e_out) % 16 == 0;  // e_out may be null
-    const N2VLayout lay_rec = n2v_layout(w.num_edges, w.num_walks, true);
-    const N2VLayout lay_csr = n2v_layout(w.num_edges, w.num_walks, false);
+    const N2VLayout lay_rec = n2v_layout(w.num_nodes, w.num_edges, w.num_walks, true);
+    const N2VLayout lay_csr = n2v_layout(w.num_nodes, w.num_edges, w.num_walks, false);
     // Records whenever the workspace holds them: node2vec_workspace_bytes
-    // asks for them only when they pay off.
-    const bool records = workspace_bytes >= lay_rec.total;
+    // asks for them only when they pay off; hub bitmaps too when it holds them.
+    const bool records = workspace_bytes >= lay_rec.total_no_hubs;
+    const int64_t hub_min_degree = n2v_hub_min_degree(w, p);
+    const bool hub_bitmaps = records && lay_rec.hub_max > 0 && workspace_bytes >= lay_rec.total &&
+                             hub_min_degree < INT64_MAX;
     if (aligned && records_fit(w.num_nodes, w.num_edges) &&
         (records || workspace_bytes >= lay_csr.total)) {
         const N2VLayout& lay = records ? lay_rec : lay_csr;
         N2VRecArgs a;
         a.w = w;
         char* base = static_cast<char*>(workspace);
+        HubBitmaps hubs{};
+        if (hub_bitmaps) {
+            hubs.slot_of = reinterpret_cast<int32_t*>(base + lay.hub_slot_of);
+            hubs.node_of = reinterpret_cast<int32_t*>(base + lay.hub_node_of);
+            hubs.bits = reinterpret_cast<uint32_t*>(base + lay.hub_bits);
+            hubs.info = reinterpret_cast<int64_t*>(base + lay.hub_info);
+            hubs.words = lay.hub_words;
+            hubs.max = lay.hub_max;
+            if (int rc = launch_hub_bitmaps(w.rowptr, w.col, w.num_nodes, w.num_edges, hubs,
+                                            hub_min_degree, stream))
+                return rc;
+        }
+        a.hub_bits = hub_bitmaps ? hubs.bits : nullptr;
+        a.hub_words = hubs.words;
         EdgeRecord* recs = records ? reinterpret_cast<EdgeRecord*>(base + kRecordOffset) : nullptr;
         EdgeRecord* init = reinterpret_cast<EdgeRecord*>(base + kRecordOffset) +
                            (records ? w.num_edges : 0);
@@ -844,10 +936,13 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         int64_t* check = w.work;
         const StartRecords starts{w.start, w.num_walks, init};
         if (int rc = records ? launch_edge_records(w.rowptr, w.col, w.num_nodes, w.num_edges, recs,
-                                                   index, starts, check, stream)
+                                                   index, starts, check, stream, hubs)
                              : launch_edge_index(w.rowptr, w.col, w.num_nodes, w.num_edges, index,
                                                  starts, check, stream))
             return rc;
+        if (hub_bitmaps)
+            if (int rc = launch_hub_build(w.rowptr, w.col, w.num_nodes, hubs, p.rows, w.work, stream))
+                return rc;
         a.recs = recs;
         a.init = init;
         a.index = index;

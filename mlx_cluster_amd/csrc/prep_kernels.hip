@@ -80,6 +80,13 @@ __device__ __forceinline__ int4 node_record(const int64_t* __restrict__ rowptr, 
     return r;
 }
 
+// Hub slot of a node record for the node2vec record walk: the slot of its
+// bitmap when its row has one (degree at or above the threshold h), else -1.
+__device__ __forceinline__ int4 with_slot(int4 r, const HubBitmaps& hubs, int64_t h) {
+    r.w = r.z >= 0 && r.z >= h ? hubs.slot_of[r.x] : -1;
+    return r;
+}
+
 // Edge records (see EdgeRecord); optionally (index.count > 0) also the
 // levels of the node2vec walk's search index: col as int32 and its samples
 // col32[16^k * i].  With rec == nullptr (the node2vec walk's CSR mode) only
@@ -87,16 +94,18 @@ __device__ __forceinline__ int4 node_record(const int64_t* __restrict__ rowptr, 
 // no rowptr is read.  With a non-null work pointer the same pass validates the
 // whole CSR (status bits into work[0]) and counts the row descents into
 // work[2] / work[3], from which the node2vec walk decides whether its rows
-// are sorted.
+// are sorted.  With hubs.max > 0 every record's pad word holds its node's
+// hub slot (hub_assign_kernel ran before), else -1.
 __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __restrict__ rowptr,
                                                              const int64_t* __restrict__ col,
                                                              int64_t num_nodes, int64_t num_edges,
                                                              EdgeRecord* __restrict__ rec,
                                                              IndexLevels index, StartRecords starts,
-                                                             int64_t* work) {
+                                                             int64_t* work, HubBitmaps hubs) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const int64_t h = hubs.max > 0 ? hubs.info[0] : INT64_MAX;
     CsrCheck check;
     for (int64_t e = gid; e < num_edges; e += stride) {
         const int64_t c = col[e];
@@ -110,10 +119,12 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
                 if (row_ok(rb, num_edges)) {
                     r.y = static_cast<int32_t>(rb.begin);
                     r.z = static_cast<int32_t>(rb.end - rb.begin);
+                    if (r.z >= h) r.w = hubs.slot_of[c];
                 } else {
                     r.z = kRecBadRow;
                 }
             }
+            if (r.z < h) r.w = -1;  // (no hub slot)
             *reinterpret_cast<i32x4*>(rec + e) = r;
         }
         if (index.count > 0) {
@@ -125,11 +136,139 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
     }
     for (int64_t n = gid; n < starts.num_walks; n += stride)
         *reinterpret_cast<int4*>(starts.init + n) =
-            node_record(rowptr, starts.start[n], num_nodes, num_edges);
+            with_slot(node_record(rowptr, starts.start[n], num_nodes, num_edges), hubs, h);
     if (work) {
         check.nodes(rowptr, num_nodes, col, num_edges, gid, stride);
         unsigned long long* w = reinterpret_cast<unsigned long long*>(work);
         check.flush(w, MLXC_STATUS_BAD_ROW, MLXC_STATUS_BAD_NODE, w + 2, w + 3);
+    }
+}
+
+// Rows per degree class into info[2 + k] (k = floor(log2(deg)) - kHubMinLog,
+// the last class holding every larger degree): per-block counts in LDS, one
+// atomic per class per block.  info must start at zero.
+__global__ __launch_bounds__(kBlock) void hub_count_kernel(const int64_t* __restrict__ rowptr,
+                                                           int64_t num_nodes, int64_t num_edges,
+                                                           int64_t* info) {
+    __shared__ int32_t cnt[kHubDegreeClasses];
+    if (threadIdx.x < kHubDegreeClasses) cnt[threadIdx.x] = 0;
+    __syncthreads();
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t u = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; u < num_nodes;
+         u += stride) {
+        const RowBounds rb = load_row(rowptr, u);
+        const int64_t d = rb.end - rb.begin;
+        if (!row_ok(rb, num_edges) || d < kHubMinDegree) continue;
+        const int k = min(63 - __clzll(static_cast<unsigned long long>(d)) - kHubMinLog,
+                          kHubDegreeClasses - 1);
+        atomicAdd(&cnt[k], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x < kHubDegreeClasses && cnt[threadIdx.x] > 0)
+        atomicAdd(reinterpret_cast<unsigned long long*>(info + 2 + threadIdx.x),
+                  static_cast<unsigned long long>(cnt[threadIdx.x]));
+}
+
+// The smallest degree threshold 2^(kHubMinLog + k), at least min_degree,
+// whose rows fit max slots (INT64_MAX when none does).
+__device__ __forceinline__ int64_t hub_threshold(const int64_t* info, int32_t max,
+                                                 int64_t min_degree) {
+    int64_t above = 0, h = INT64_MAX;
+    for (int k = kHubDegreeClasses - 1; k >= 0; --k) {
+        const int64_t hk = int64_t{1} << (kHubMinLog + k);
+        above += info[2 + k];
+        if (above > max || hk < min_degree) break;
+        h = hk;
+    }
+    return h;
+}
+
+// info[0] = the threshold; every row at or above it gets the next slot
+// (info[1] counts them; the order of slots is immaterial).
+__global__ __launch_bounds__(kBlock) void hub_assign_kernel(const int64_t* __restrict__ rowptr,
+                                                            int64_t num_nodes, int64_t num_edges,
+                                                            HubBitmaps hubs, int64_t min_degree) {
+    const int64_t h = hub_threshold(hubs.info, hubs.max, min_degree);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hubs.info[0] = h;
+    if (h == INT64_MAX) return;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t u = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; u < num_nodes;
+         u += stride) {
+        const RowBounds rb = load_row(rowptr, u);
+        if (!row_ok(rb, num_edges) || rb.end - rb.begin < h) continue;
+        const int64_t slot = static_cast<int64_t>(
+            atomicAdd(reinterpret_cast<unsigned long long*>(hubs.info + 1), 1ull));
+        hubs.slot_of[u] = static_cast<int32_t>(slot);  // slot < max: the threshold ensures it
+        hubs.node_of[slot] = static_cast<int32_t>(u);
+    }
+}
+
+// Builds the bitmaps of the assigned slots, each in chunks of
+// kHubChunkWords words: a block clears its chunk in LDS, sets the bits of the
+// row's entries that fall in it (LDS atomics), then stores the chunk whole,
+// so no separate clearing pass and no global atomics are needed.  On sorted
+// rows (rows == MLXC_ROWS_SORTED, or DETECT with work[2] == work[3] from the
+// preparation pass, which must have run) each chunk binary-searches the
+// range of entries it holds; otherwise it scans the whole row.  Entries
+// outside [0, num_nodes) are left out (the preparation pass reports them).
+constexpr int kHubChunkWords = 8192;  // 32 KB of LDS: 2^18 nodes per chunk
+constexpr int64_t kHubScanEntries = 16 * kBlock;  // rows up to this are scanned by every chunk
+
+// lower_bound of v in the sorted a[lo, hi), by the whole block: each round
+// every thread compares one of kBlock evenly spaced samples, and the count of
+// samples below v (a block-wide reduction) narrows the range kBlock-fold, so
+// a row of d entries takes about log256(d) + 1 dependent reads instead of
+// log2(d).  Every thread of the block must call it; all get the same result.
+__device__ int64_t block_lower_bound(const int64_t* __restrict__ a, int64_t lo, int64_t hi,
+                                     int64_t v) {
+    while (hi - lo > kBlock) {
+        const int64_t step = (hi - lo + kBlock - 1) / kBlock;
+        const int64_t k = threadIdx.x;  // sample k sits at lo + k * step
+        const int64_t at = lo + k * step;
+        const int c = __syncthreads_count(at < hi && a[at] < v);
+        // samples 0 .. c-1 are below v and sample c (if any) is not
+        const int64_t new_lo = c == 0 ? lo : lo + (c - 1) * step + 1;
+        const int64_t new_hi = lo + c * step < hi ? lo + c * step : hi;
+        lo = new_lo;
+        hi = new_hi;
+    }
+    const int64_t at = lo + threadIdx.x;
+    return lo + __syncthreads_count(at < hi && a[at] < v);
+}
+
+__global__ __launch_bounds__(kBlock) void hub_build_kernel(const int64_t* __restrict__ rowptr,
+                                                           const int64_t* __restrict__ col,
+                                                           int64_t num_nodes, HubBitmaps hubs,
+                                                           int32_t rows, const int64_t* work) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    __shared__ uint32_t lw[kHubChunkWords];
+    const bool sorted = rows == MLXC_ROWS_SORTED || (rows == MLXC_ROWS_DETECT && work[2] == work[3]);
+    const int64_t chunks = (hubs.words + kHubChunkWords - 1) / kHubChunkWords;
+    const int64_t units = hubs.info[1] * chunks;
+    for (int64_t unit = blockIdx.x; unit < units; unit += gridDim.x) {
+        const int64_t slot = unit / chunks, chunk = unit % chunks;
+        const int64_t w0 = chunk * kHubChunkWords;  // first word of the chunk
+        const int64_t nw = min(static_cast<int64_t>(kHubChunkWords), hubs.words - w0);
+        for (int i = threadIdx.x; i < nw; i += kBlock) lw[i] = 0u;
+        __syncthreads();
+        const RowBounds rb = load_row(rowptr, hubs.node_of[slot]);  // a valid row (assigned)
+        int64_t first = rb.begin, last = rb.end;
+        if (sorted && chunks > 1 && rb.end - rb.begin > kHubScanEntries) {
+            // the entries in [32 w0, 32 (w0 + nw)); shorter rows are scanned whole
+            first = block_lower_bound(col, rb.begin, rb.end, 32 * w0);
+            last = block_lower_bound(col, first, rb.end, 32 * (w0 + nw));
+        }
+        for (int64_t i = first + threadIdx.x; i < last; i += kBlock) {
+            const int64_t c = col[i];
+            const int64_t wi = (c >> 5) - w0;
+            if (node_ok(c, num_nodes) && wi >= 0 && wi < nw)
+                atomicOr(&lw[wi], 1u << (c & 31));
+        }
+        __syncthreads();
+        u32x4* out = reinterpret_cast<u32x4*>(hubs.bits + slot * hubs.words + w0);
+        for (int64_t q = threadIdx.x; 4 * q < nw; q += kBlock)  // nw is a multiple of 4
+            out[q] = u32x4{lw[4 * q], lw[4 * q + 1], lw[4 * q + 2], lw[4 * q + 3]};
+        __syncthreads();
     }
 }
 
@@ -296,14 +435,44 @@ int launch_zero_work(int64_t* d_work, hipStream_t stream) {
 
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                         int64_t num_edges, EdgeRecord* recs, const IndexLevels& index,
-                        const StartRecords& starts, int64_t* check_work, hipStream_t stream) {
+                        const StartRecords& starts, int64_t* check_work, hipStream_t stream,
+                        const HubBitmaps& hubs) {
     if (num_edges == 0 && !check_work && starts.num_walks == 0) return MLXC_OK;
     int grid = 0;
     int64_t items = check_work && num_nodes > num_edges ? num_nodes : num_edges;
     if (starts.num_walks > items) items = starts.num_walks;
     if (int rc = stream_grid(items, 16, grid)) return rc;
     hipLaunchKernelGGL(edge_record_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col,
-                       num_nodes, num_edges, recs, index, starts, check_work);
+                       num_nodes, num_edges, recs, index, starts, check_work, hubs);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int launch_hub_bitmaps(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
+                       int64_t num_edges, const HubBitmaps& hubs, int64_t min_degree,
+                       hipStream_t stream) {
+    if (hubs.max <= 0) return MLXC_OK;
+    static_assert(kHubInfoWords <= kWave, "one zeroing thread per info word");
+    hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(kWave), 0, stream, hubs.info, kHubInfoWords);
+    int grid = 0;
+    if (int rc = stream_grid(num_nodes, 8, grid)) return rc;
+    hipLaunchKernelGGL(hub_count_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, num_nodes,
+                       num_edges, hubs.info);
+    hipLaunchKernelGGL(hub_assign_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, num_nodes,
+                       num_edges, hubs, min_degree);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int launch_hub_build(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
+                     const HubBitmaps& hubs, int32_t rows, const int64_t* work,
+                     hipStream_t stream) {
+    if (hubs.max <= 0) return MLXC_OK;
+    const int64_t chunks = (hubs.words + kHubChunkWords - 1) / kHubChunkWords;
+    int grid = 0;  // four 32 KB blocks per CU
+    if (int rc = stream_grid(static_cast<int64_t>(hubs.max) * chunks * kBlock, 4, grid)) return rc;
+    hipLaunchKernelGGL(hub_build_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col,
+                       num_nodes, hubs, rows, work);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }
@@ -314,7 +483,7 @@ int launch_edge_index(const int64_t* rowptr, const int64_t* col, int64_t num_nod
     if (num_edges == 0 && !check_work && starts.num_walks == 0) return MLXC_OK;
     if (reinterpret_cast<uintptr_t>(col) % 16 != 0)  // the record pass reads any alignment
         return launch_edge_records(rowptr, col, num_nodes, num_edges, nullptr, index, starts,
-                                   check_work, stream);
+                                   check_work, stream, HubBitmaps{});
     int grid = 0;
     const int64_t quads = (num_edges + 3) / 4;
     int64_t items = check_work && num_nodes > quads ? num_nodes : quads;

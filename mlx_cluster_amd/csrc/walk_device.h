@@ -565,6 +565,30 @@ inline __host__ __device__ int index_levels(int64_t num_edges) {
     return msb / 4 + 1;
 }
 
+// Dense adjacency bitmaps of the node2vec record walk's hub rows: bit c of
+// bitmap s is set when node c is in row(node_of[s]).  A membership test on a
+// hub row then costs one read instead of a descent through the index levels
+// (about log16(deg) + 1 reads).  The rows that get one are those of degree at
+// least a threshold, the smallest power of two >= kHubMinDegree for which the
+// rows that reach it fit the reserved slots; it is chosen on the device per
+// call (hub_count_kernel, hub_assign_kernel).  The edge and start records
+// carry the slot of their node in their pad word (-1: none).
+constexpr int64_t kHubMinDegree = 256;
+constexpr int kHubMinLog = 8;        // log2(kHubMinDegree)
+constexpr int kHubDegreeClasses = 24;  // rows counted by floor(log2(deg)) - 8, capped
+// info words: [0] the degree threshold (INT64_MAX: no bitmaps), [1] slots
+// assigned, [2 + k] rows with floor(log2(deg)) - kHubMinLog == k (the last
+// class also holds every larger degree)
+constexpr int kHubInfoWords = 2 + kHubDegreeClasses;
+struct HubBitmaps {
+    int32_t* slot_of;  // [num_nodes]; written only for rows at or above the threshold
+    int32_t* node_of;  // [max]
+    uint32_t* bits;    // [max][words]
+    int64_t* info;     // [kHubInfoWords]
+    int64_t words;     // 32-bit words per bitmap: ceil(num_nodes / 32), rounded up to 4
+    int32_t max;       // slots reserved; 0: no bitmaps
+};
+
 // Start records a preparation pass writes besides its edge pass: walk n's
 // start node in the record format, into init[n].
 struct StartRecords {

@@ -78,7 +78,20 @@ int launch_record_prep(const int64_t* rowptr, const int64_t* col, const int64_t*
 // descents (see edge_record_kernel).
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                         int64_t num_edges, EdgeRecord* recs, const IndexLevels& index,
-                        const StartRecords& starts, int64_t* check_work, hipStream_t stream);
+                        const StartRecords& starts, int64_t* check_work, hipStream_t stream,
+                        const HubBitmaps& hubs);
+// The hub bitmaps (see HubBitmaps), in two launches around
+// launch_edge_records: launch_hub_bitmaps chooses the degree threshold (at
+// least min_degree) and assigns the slots, which the records then carry;
+// launch_hub_build, after the records (whose pass counts the row descents
+// that tell it whether rows are sorted), fills the bitmaps.  Nothing when
+// hubs.max == 0.
+int launch_hub_bitmaps(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
+                       int64_t num_edges, const HubBitmaps& hubs, int64_t min_degree,
+                       hipStream_t stream);
+int launch_hub_build(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
+                     const HubBitmaps& hubs, int32_t rows, const int64_t* work,
+                     hipStream_t stream);
 // The index levels alone, from col (node2vec CSR mode), and the start records;
 // a 16-byte aligned col uses four entries per thread, any other alignment the
 // record pass.

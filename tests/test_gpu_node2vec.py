@@ -24,9 +24,11 @@ def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode, out_dtype=tor
     """mlxc_rejection_sampling through the C ABI, with edge output, in the
     mode the workspace selects: "direct" (minimal workspace: the direct CSR
     kernel), "csr" (the CSR-mode layout: the record kernel without edge
-    records), "records" (the edge-record layout) or "lds" (the 256-byte
-    header: the LDS walk, for graphs and calls small enough).  Asserts the
-    call's status word equals expect_status."""
+    records), "records" (the edge-record layout with its hub bitmaps),
+    "records_nohub" (one byte less: the edge records without the bitmaps,
+    when the layout has any) or "lds" (the 256-byte header: the LDS walk, for
+    graphs and calls small enough).  Asserts the call's status word equals
+    expect_status."""
     from mlx_cluster_amd import _lib
     lib = _lib.load()
     N = start.numel()
@@ -36,7 +38,8 @@ def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode, out_dtype=tor
     out_type = _lib.MLXC_OUT_INT32 if out_dtype == torch.int32 else _lib.MLXC_OUT_INT64
     query = lambda N_, L_: lib.mlxc_rejection_sampling_workspace_bytes(V, E, N_, L_, p, q, rule)
     # the query sizes records only for calls of many steps per edge
-    nbytes = {"direct": 32, "csr": query(N, 0), "records": query(max(N, 1), 2**31 - 1),
+    full = query(max(N, 1), 2**31 - 1)
+    nbytes = {"direct": 32, "csr": query(N, 0), "records": full, "records_nohub": full - 1,
               "lds": 256}[mode]
     if mode == "csr" and E > 0:
         assert nbytes < query(max(N, 1), 2**31 - 1)
@@ -66,7 +69,7 @@ def gpu_walk(rowptr, col, start, L, p, q, seed, rule, cuda, **kw):
     rows = {None: 2, True: 1, False: 0}[kw.get("rows_sorted")]
     if kw.get("symmetric"):
         rows |= 4  # MLXC_ROWS_SYMMETRIC
-    for mode in ("direct", "csr", "records"):
+    for mode in ("direct", "csr", "records", "records_nohub"):
         nm, em = _abi_walk(*args[:3], L, p, q, seed, rule, rows, mode)
         np.testing.assert_array_equal(nm.cpu().numpy(), n.cpu().numpy(),
                                       err_msg=f"{mode} walk nodes differ")
@@ -172,6 +175,31 @@ def test_hub_graph_parity(cuda):
         _, counts = assert_parity(rowptr, col, start, 12, 4.0, 0.25, 55, rule, cuda)
         if rule == oracle.RULE_NODE2VEC_EXACT:
             assert counts["member_tests"] > 0
+
+
+@pytest.mark.parametrize("rule,p,q", [(oracle.RULE_REF_CHAIN, 0.5, 2.0),
+                                      (oracle.RULE_NODE2VEC_EXACT, 4.0, 0.25)])
+def test_hub_bitmaps_parity(rule, p, q, cuda):
+    """Hub rows answered by their bitmaps: 600,000 nodes (bitmaps of three
+    LDS chunks), 8 hubs of 20,000 entries (the chunks' block-wide bound
+    search) and tens of rows of some hundreds, with (p, q) for which a
+    quarter (chain) or three quarters (analytic rule) of the draws can need a
+    neighbour test.  Every mode (edge records with and without bitmaps, CSR
+    mode, direct kernel) against the oracle, for sorted rows, rows shuffled
+    inside (each chunk scans its row) and the symmetric hint."""
+    rowptr, col = synth.ba_hub_csr(600_000, 3, 8, 20_000, seed=5)
+    rowptr, col = rowptr.numpy(), col.numpy()
+    deg = np.diff(rowptr)
+    assert deg.max() >= 20_000 and (deg >= 512).sum() >= 20
+    start = (np.arange(200_000) * 3) % 600_000
+    _, counts = assert_parity(rowptr, col, start, 10, p, q, 77, rule, cuda)
+    assert counts["member_tests"] > 50_000
+    assert_parity(rowptr, col, start, 10, p, q, 78, rule, cuda, symmetric=True)
+    rng = np.random.default_rng(6)
+    shuffled = col.copy()
+    for u in np.flatnonzero(deg >= 512):
+        shuffled[rowptr[u]:rowptr[u + 1]] = rng.permutation(shuffled[rowptr[u]:rowptr[u + 1]])
+    assert_parity(rowptr, shuffled, start, 10, p, q, 79, rule, cuda, sorted_rows=False)
 
 
 @pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
