@@ -75,6 +75,10 @@ extern "C" {
 #define MLXC_CSR_BAD_ROWPTR 1   /* rowptr[0] != 0, rowptr[V] != E, or decreasing */
 #define MLXC_CSR_BAD_COL 2      /* a col value outside [0, V) */
 #define MLXC_CSR_UNSORTED 4     /* some row is not sorted ascending */
+/* some entry (u, v) has no entry (v, u): the graph breaks the promise of
+ * MLXC_ROWS_SYMMETRIC.  Checked (one search per entry) only on a graph with
+ * none of the three bits above set; otherwise left clear. */
+#define MLXC_CSR_ASYMMETRIC 8
 
 /* Element type of the walk outputs (out_type argument).  The reference
  * writes int64 (RandomWalk.cpp:43,57-58); int32 halves the output bytes and
@@ -121,8 +125,12 @@ size_t mlxc_random_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges,
  * layouts add 16 bytes per walk and about 4.3 bytes per edge of search index.
  * Records are also chosen when num_edges <= 32768 * walk_length, and 256
  * bytes (the LDS walk) under the same conditions as for mlxc_random_walk.
- * A workspace that holds the record layout always runs with records.  No
- * reference counterpart. */
+ * The record layout ends with room for dense neighbour bitmaps of the rows
+ * of highest degree (ceil(num_nodes / 32) words each, at most 1 GiB and one
+ * per 256 entries, plus 4 * num_nodes bytes of slot map): membership tests
+ * on those rows then take one read.  A workspace that holds the record
+ * layout without that room runs with records and no bitmaps; one that holds
+ * all of it always runs with records.  No reference counterpart. */
 size_t mlxc_rejection_sampling_workspace_bytes(int64_t num_nodes, int64_t num_edges,
                                                int64_t num_walks, int32_t walk_length,
                                                double p, double q, int32_t rule);

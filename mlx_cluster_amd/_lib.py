@@ -31,6 +31,7 @@ MLXC_ROWS_SYMMETRIC = 4
 MLXC_CSR_BAD_ROWPTR = 1
 MLXC_CSR_BAD_COL = 2
 MLXC_CSR_UNSORTED = 4
+MLXC_CSR_ASYMMETRIC = 8
 MLXC_OUT_INT64 = 0
 MLXC_OUT_INT32 = 1
 MLXC_CSR_SYMMETRIZE = 1

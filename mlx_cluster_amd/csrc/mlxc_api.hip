@@ -315,11 +315,13 @@ int mlxc_csr_check(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_
     int64_t* d_work = static_cast<int64_t*>(d_workspace);
     if (int rc = launch_zero_work(d_work, s)) return rc;
     if (int rc = launch_csr_check(d_rowptr, num_nodes, d_col, num_edges, d_work, s)) return rc;
-    int64_t host[3] = {0, 0, 0};
+    if (int rc = launch_csr_symmetry(d_rowptr, num_nodes, d_col, num_edges, d_work, s)) return rc;
+    int64_t host[4] = {0, 0, 0, 0};
     MLXC_HIP_TRY(hipMemcpyAsync(host, d_work, sizeof(host), hipMemcpyDeviceToHost, s));
     MLXC_HIP_TRY(hipStreamSynchronize(s));
     int32_t flags = static_cast<int32_t>(host[0]);
     if (!(flags & MLXC_CSR_BAD_ROWPTR) && host[1] != host[2]) flags |= MLXC_CSR_UNSORTED;
+    if (host[3]) flags |= MLXC_CSR_ASYMMETRIC;
     *h_flags = flags;
     return MLXC_OK;
 }

@@ -381,6 +381,48 @@ __global__ __launch_bounds__(kBlock) void csr_check_kernel(const int64_t* __rest
     check.flush(w, MLXC_CSR_BAD_ROWPTR, MLXC_CSR_BAD_COL, w + 1, w + 2);
 }
 
+// After csr_check_kernel, on a well-formed graph whose rows are all sorted:
+// work[3] = 1 if some entry (u, v) has no entry (v, u).  Each thread takes
+// runs of 16 consecutive entries; the run's row comes from a binary search of
+// rowptr, then each entry's reverse from a binary search of row(v).
+__global__ __launch_bounds__(kBlock) void csr_symmetry_kernel(const int64_t* __restrict__ rowptr,
+                                                              int64_t V,
+                                                              const int64_t* __restrict__ col,
+                                                              int64_t E, int64_t* work) {
+    constexpr int kRun = 16;
+    if ((work[0] & (MLXC_CSR_BAD_ROWPTR | MLXC_CSR_BAD_COL)) || work[1] != work[2]) return;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    bool asym = false;
+    for (int64_t e0 = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * kRun; e0 < E;
+         e0 += stride * kRun) {
+        int64_t lo = 0, hi = V - 1;  // the last row u with rowptr[u] <= e0
+        while (lo < hi) {
+            const int64_t mid = hi - (hi - lo) / 2;
+            if (rowptr[mid] <= e0) lo = mid;
+            else hi = mid - 1;
+        }
+        int64_t u = lo;
+        const int64_t e1 = e0 + kRun < E ? e0 + kRun : E;
+        for (int64_t e = e0; e < e1; ++e) {
+            while (rowptr[u + 1] <= e) ++u;  // (rowptr[V] = E > e ends it)
+            const int64_t v = col[e];
+            int64_t b = rowptr[v], n = rowptr[v + 1] - b;
+            while (n > 0) {  // lower_bound of u in row(v)
+                const int64_t half = n >> 1;
+                if (col[b + half] < u) {
+                    b += half + 1;
+                    n -= half + 1;
+                } else {
+                    n = half;
+                }
+            }
+            asym |= !(b < rowptr[v + 1] && col[b] == u);
+        }
+    }
+    if (__any(asym) && __lane_id() == 0)
+        atomicOr(reinterpret_cast<unsigned long long*>(work + 3), 1ull);
+}
+
 // The words csr_check_kernel left, turned into a walk's: work[0] = the
 // MLXC_STATUS_* bits of the whole-graph check, work[1] = 0 (the walk queue),
 // work[2] = 1 when every row is sorted (else 0), work[3] = 0.
@@ -529,6 +571,17 @@ int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* co
 
 int launch_copy_word(const int64_t* d_src, int64_t* d_dst, hipStream_t stream) {
     hipLaunchKernelGGL(copy_word_kernel, dim3(1), dim3(kWave), 0, stream, d_src, d_dst);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
+int launch_csr_symmetry(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
+                        int64_t num_edges, int64_t* d_work, hipStream_t stream) {
+    if (num_edges == 0 || num_nodes == 0) return MLXC_OK;
+    int grid = 0;
+    if (int rc = stream_grid((num_edges + 15) / 16, 16, grid)) return rc;
+    hipLaunchKernelGGL(csr_symmetry_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, num_nodes,
+                       col, num_edges, d_work);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

@@ -107,6 +107,10 @@ int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_no
 // descents / those at a row start); the words must start at zero.
 int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                      int64_t num_edges, int64_t* d_work, hipStream_t stream);
+// After launch_csr_check, on a well-formed graph with sorted rows: work[3] = 1
+// when some entry (u, v) has no reverse (v, u).
+int launch_csr_symmetry(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
+                        int64_t num_edges, int64_t* d_work, hipStream_t stream);
 // Turns the words of launch_csr_check into a walk's: status bits in work[0],
 // work[1] = 0, work[2] = 1 if every row is sorted, work[3] = 0.
 int launch_csr_status(int64_t* d_work, hipStream_t stream);

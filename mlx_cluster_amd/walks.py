@@ -262,7 +262,10 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
 
 
 def csr_check(rowptr: TensorLike, col: TensorLike, *, stream=None) -> int:
-    """MLXC_CSR_* bits of a CSR graph, computed on the device (synchronous)."""
+    """MLXC_CSR_* bits of a CSR graph, computed on the device (synchronous):
+    1 malformed rowptr, 2 a col entry outside [0, num_nodes), 4 some row not
+    sorted, 8 (checked on well-formed graphs with sorted rows) some entry
+    (u, v) without its reverse (v, u), i.e. symmetric=True would not hold."""
     _check_stream_arg(stream)
     rowptr, col, _ = _graph(rowptr, col, torch.empty(0, dtype=torch.int64))
     device = _resolve_device(stream, (rowptr, col))
@@ -314,7 +317,8 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
             test then searches the shorter of row(x) and row(t), which gives
             the same answer there.  False (the default) searches row(x), as
             the reference does; on a graph that is not symmetric True gives
-            unspecified walks.
+            unspecified walks.  csr_check(rowptr, col) & MLXC_CSR_ASYMMETRIC
+            (8) tells whether the promise holds (for sorted rows).
     """
     L = _walk_length(walk_length)
     otype = _out_type(out_dtype)

@@ -361,5 +361,14 @@ int32_t oracle_csr_flags(const int64_t* rowptr, int64_t num_nodes,
             for (int64_t i = rowptr[v] + 1; i < rowptr[v + 1]; ++i)
                 if (col[i] < col[i - 1]) f |= 4;
     }
+    if (f == 0) {  /* symmetry, by a linear scan of row(v) for each entry (u, v) */
+        for (int64_t u = 0; u < num_nodes && !(f & 8); ++u)
+            for (int64_t i = rowptr[u]; i < rowptr[u + 1] && !(f & 8); ++i) {
+                const int64_t v = col[i];
+                int found = 0;
+                for (int64_t j = rowptr[v]; j < rowptr[v + 1] && !found; ++j) found = col[j] == u;
+                if (!found) f |= 8;
+            }
+    }
     return f;
 }

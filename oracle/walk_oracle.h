@@ -98,7 +98,8 @@ int oracle_node2vec_walk_libc(const int64_t* rowptr, int64_t num_nodes,
                               int64_t* n_out, int64_t* e_out);
 
 /* CSR checks used by the tests: bit0 rowptr malformed, bit1 col out of range,
- * bit2 some row not sorted ascending. */
+ * bit2 some row not sorted ascending, bit3 (only when bits 0-2 are clear)
+ * some entry (u, v) without an entry (v, u). */
 int32_t oracle_csr_flags(const int64_t* rowptr, int64_t num_nodes,
                          const int64_t* col, int64_t num_edges);
 

@@ -279,6 +279,7 @@ def test_csr_check_matches_oracle(cuda):
     for rp, cl in cases:
         assert mc.csr_check(rp, cl) == oracle.csr_flags(rp, cl)
     u0 = {s: float(oracle.node2vec_trial0_u0(1, 1, s)[0, 0]) for s in (0, 1)}
+    assert mc.csr_check(rowptr, col) == 8  # directed
     assert oracle.pick_index(u0[0], 2) == 0 and oracle.pick_index(u0[1], 2) == 1
     for seed in (0, 1):
         for stream in (None, "cpu"):
@@ -291,6 +292,30 @@ def test_csr_check_matches_oracle(cuda):
             with pytest.raises(ValueError, match="rowptr"):  # rowptr[V] != E, every row valid
                 mc.rejection_sampling(np.array([0, 1, 1, 2, 2]), col, np.array([0]), 3, 1.0, 1.0,
                                       seed=seed, stream=stream)
+
+
+def test_csr_check_asymmetry(cuda):
+    """MLXC_CSR_ASYMMETRIC tells a caller whether the promise behind
+    symmetric=True holds: set on directed graphs, clear on symmetrized ones
+    (with duplicates and self-loops), equal to the oracle's brute force; left
+    clear on unsorted or malformed graphs."""
+    for seed, sym in ((1, False), (2, True), (3, False), (4, True)):
+        rowptr, col = synth.rmat_csr(11, 20_000, seed=seed, symmetrize=sym)
+        rowptr, col = rowptr.numpy(), col.numpy()
+        want = oracle.csr_flags(rowptr, col)
+        assert want == (0 if sym else 8)
+        assert mc.csr_check(rowptr, col) == want
+    rp, cl = undirected(300, np.random.default_rng(5).integers(0, 300, (3000, 2)))
+    assert mc.csr_check(rp, cl) == oracle.csr_flags(rp, cl) == 0
+    cl2 = cl.copy()
+    cl2[17] = (cl2[17] + 1) % 300  # one entry changed: its reverse is missing
+    assert mc.csr_check(rp, cl2) == oracle.csr_flags(rp, cl2)
+    # symmetric=True on a directed graph: caught by the check before the walk
+    rowptr, col = synth.rmat_csr(11, 20_000, seed=1)
+    assert mc.csr_check(rowptr, col) & 8
+    # unsorted rows: bit 2 only
+    rp3, cl3 = undirected(300, np.random.default_rng(6).integers(0, 300, (3000, 2)), sort=False)
+    assert mc.csr_check(rp3, cl3) == oracle.csr_flags(rp3, cl3) == 4
 
 
 def test_seed_none_follows_torch_manual_seed(c1, cuda):

@@ -397,11 +397,43 @@ def test_node2vec_walks_follow_edges(c1):
 
 def test_csr_flags():
     rowptr, col = csr(4, [(0, 1), (0, 3), (2, 1)])
-    assert oracle.csr_flags(rowptr, col) == 0
+    assert oracle.csr_flags(rowptr, col) == 8                         # directed: no (1, 0)
+    srp, scol = undirected(4, [(0, 1), (0, 3), (2, 1)])
+    assert oracle.csr_flags(srp, scol) == 0
     assert oracle.csr_flags(rowptr, np.array([3, 1, 1])) == 4         # row 0 unsorted
     assert oracle.csr_flags(rowptr, np.array([1, 9, 1])) == 2         # col out of range
     assert oracle.csr_flags(np.array([0, 2, 1, 3, 3]), col) & 1      # decreasing rowptr
     assert oracle.csr_flags(np.array([0, 2, 2, 3, 4]), col) & 1      # rowptr[V] != E
+
+
+def test_csr_asymmetry_flag_brute_force():
+    """Bit 3 against a set of pairs: random graphs with duplicates and
+    self-loops, symmetrized (clear) and with one reverse entry removed or one
+    directed entry added (set)."""
+    rng = np.random.default_rng(31)
+    for case in range(40):
+        V = int(rng.integers(1, 60))
+        pairs = rng.integers(0, V, (int(rng.integers(0, 200)), 2))
+        rowptr, col = undirected(V, pairs)
+        pairs_set = set()
+        for u in range(V):
+            pairs_set.update((u, int(v)) for v in col[rowptr[u]:rowptr[u + 1]])
+        assert all((v, u) in pairs_set for u, v in pairs_set)
+        assert oracle.csr_flags(rowptr, col) == 0
+        if len(pairs) == 0:
+            continue
+        # drop every copy of one entry (u, v) with u != v: (v, u) loses its reverse
+        u, v = (int(x) for x in pairs[int(rng.integers(0, len(pairs)))])
+        edges = [(a, int(b)) for a in range(V) for b in col[rowptr[a]:rowptr[a + 1]]]
+        kept = [e for e in edges if e != (u, v)]
+        rp2, cl2 = csr(V, kept) if kept else (np.zeros(V + 1, np.int64), np.zeros(0, np.int64))
+        want = any((b, a) not in set(kept) for a, b in kept)
+        assert bool(oracle.csr_flags(rp2, cl2) & 8) == want, case
+        assert want == (u != v)
+        # one extra directed entry
+        a, b = (int(x) for x in rng.integers(0, V, 2))
+        rp3, cl3 = csr(V, edges + [(a, b)])
+        assert bool(oracle.csr_flags(rp3, cl3) & 8) == ((b, a) not in set(edges) and a != b), case
 
 
 # ---------------------------------------------------------------- CSR build
