@@ -91,11 +91,11 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def kernel_source_hash() -> str:
-    """sha256[:16] over the code (not the comments) of every source file of
-    libmlxc.so."""
+def kernel_source_hash(kind: str) -> str:
+    """sha256[:16] over the code (not the comments) of the source files of
+    libmlxc.so that one kernel family is built from."""
     from mlx_cluster_amd.build_lib import source_hash
-    return source_hash()
+    return source_hash(kind)
 
 
 # What roofline.traffic counts: rocprofv3 FETCH_SIZE + WRITE_SIZE, the bytes
@@ -109,11 +109,14 @@ def traffic_from_profile(name: str):
     """HBM bytes per launch from a committed rocprofv3 --pmc summary of the
     same kernel source (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-
     kernel calibration), or None when no summary for this source exists."""
+    from mlx_cluster_amd.build_lib import KERNEL_SOURCES
+    family = next((k for k in KERNEL_SOURCES if name.startswith(k + "_")), None)
     path = os.path.join(REPO, "profiles", f"{name}_traffic.json")
-    if not os.path.exists(path):
+    if family is None or not os.path.exists(path):
         return None
     d = json.load(open(path))
-    if d.get("kernel_source_sha256_16") != kernel_source_hash():
+    if (d.get("kernel_family") != family or
+            d.get("kernel_source_sha256_16") != kernel_source_hash(family)):
         return None
     return d.get("hbm_bytes_per_launch")
 

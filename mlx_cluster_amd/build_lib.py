@@ -64,12 +64,28 @@ def _code_only(text: str) -> str:
     return "\n".join(line.rstrip() for line in text.splitlines() if line.strip())
 
 
-def source_hash() -> str:
-    """sha256[:16] over the code of every source file (comments excluded, so
-    that a profile taken of a build stays matched to it across comment
-    edits)."""
+# The sources each profiled kernel family is built from: a profile stays
+# matched to a build as long as these files' code is unchanged.
+_COMMON = ["walk_device.h", "walk_host.h", "mlxc_api.hip", "prep_kernels.hip"]
+KERNEL_SOURCES = {
+    "uniform_walk": _COMMON + ["uniform_walk.hip"],
+    "node2vec_walk": _COMMON + ["node2vec_walk.hip"],
+    "csr_build": _COMMON + ["csr_build.hip"],
+    "context_windows": _COMMON + ["windows.hip"],
+}
+
+
+def source_hash(kind: str | None = None) -> str:
+    """sha256[:16] over the code of the source files of one kernel family
+    (KERNEL_SOURCES; every source file when kind is None) and the C ABI
+    header, comments excluded, so that a profile taken of a build stays
+    matched to it across comment edits and changes to unrelated kernels."""
+    files = source_files()
+    if kind is not None:
+        wanted = set(KERNEL_SOURCES[kind]) | {"mlxc.h"}
+        files = [f for f in files if os.path.basename(f) in wanted]
     h = hashlib.sha256()
-    for path in source_files():
+    for path in files:
         h.update(os.path.basename(path).encode())
         h.update(_code_only(open(path, encoding="utf-8").read()).encode())
     return h.hexdigest()[:16]
