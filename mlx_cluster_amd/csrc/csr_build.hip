@@ -58,8 +58,14 @@ struct EdgeSrc {
 
 // Key of entry i of the (optionally symmetrized) list: i < num_edges is
 // (row[i], col[i]); i >= num_edges the reversed pair of entry i - num_edges.
-// Ids outside [0, num_nodes) set `bad` and become 0, so that every index
-// derived from a key stays in bounds.
+// An id outside [0, num_nodes) sets `bad` and becomes 0 (each id on its own),
+// so that every index derived from a key stays in bounds.
+__device__ __forceinline__ int64_t clamp_id(int64_t v, int64_t num_nodes, bool& bad) {
+    const bool ok = static_cast<uint64_t>(v) < static_cast<uint64_t>(num_nodes);
+    bad |= !ok;
+    return ok ? v : 0;
+}
+
 template <typename KeyT>
 __device__ __forceinline__ KeyT src_key(const EdgeSrc& s, int64_t i, bool& bad) {
     int64_t r, c;
@@ -70,14 +76,17 @@ __device__ __forceinline__ KeyT src_key(const EdgeSrc& s, int64_t i, bool& bad) 
         r = s.col[i - s.num_edges];
         c = s.row[i - s.num_edges];
     }
-    const bool ok = static_cast<uint64_t>(r) < static_cast<uint64_t>(s.num_nodes) &&
-                    static_cast<uint64_t>(c) < static_cast<uint64_t>(s.num_nodes);
-    if (!ok) {
-        bad = true;
-        r = 0;
-        c = 0;
-    }
+    r = clamp_id(r, s.num_nodes, bad);
+    c = clamp_id(c, s.num_nodes, bad);
     return (static_cast<KeyT>(r) << s.cbits) | static_cast<KeyT>(c);
+}
+
+// The col field of entry i's key alone (one array read): enough for the
+// digits of a pass that lies inside the col field.
+template <typename KeyT>
+__device__ __forceinline__ KeyT src_col(const EdgeSrc& s, int64_t i, bool& bad) {
+    const int64_t c = i < s.num_edges ? s.col[i] : s.row[i - s.num_edges];
+    return static_cast<KeyT>(clamp_id(c, s.num_nodes, bad));
 }
 
 template <typename KeyT>
@@ -85,16 +94,22 @@ __device__ __forceinline__ uint32_t digit_of(KeyT k, int shift) {
     return static_cast<uint32_t>(k >> shift) & (kRadix - 1);
 }
 
-// Lanes of this wavefront that are active and hold the same digit d.
+// Lanes of this wavefront that are active and hold the same digit d.  For
+// each bit, the lanes whose bit differs from this lane's are m ^ e, with m
+// the wavefront's ballot of the bit and e = 0 or ~0 this lane's bit: OR-ing
+// those over the bits (one XOR and one OR per 32-bit half) leaves the peers
+// as the lanes never marked.
 __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool active) {
-    uint64_t peers = __ballot(active);
+    uint32_t differ_lo = 0, differ_hi = 0;
 #pragma unroll
     for (int b = 0; b < kRadixBits; ++b) {
-        const bool bit = (d >> b) & 1u;
-        const uint64_t m = __ballot(bit);
-        peers &= bit ? m : ~m;
+        const uint32_t e = 0u - ((d >> b) & 1u);
+        const uint64_t m = __ballot(e != 0);
+        differ_lo |= static_cast<uint32_t>(m) ^ e;
+        differ_hi |= static_cast<uint32_t>(m >> 32) ^ e;
     }
-    return peers;
+    const uint64_t act = __ballot(active);
+    return act & ~((static_cast<uint64_t>(differ_hi) << 32) | differ_lo);
 }
 
 __device__ __forceinline__ bool is_leader(uint64_t peers) {
@@ -153,13 +168,18 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(EdgeSrc src,
     const int64_t tile = blockIdx.x;
     const int64_t base = tile * kSortTile + w * kWaveTile + lane;
     bool bad = false;
+    // the first pass's digits lie in the col field (bits 0..7) when it is 8
+    // bits wide or more: only that array is read (bad rows are reported by
+    // the first scatter pass, which reads both)
+    const bool col_only = kFirst && shift + kRadixBits <= src.cbits;
     // all loads first, so that the whole tile is in flight at once
     KeyT key[kItems];
 #pragma unroll
     for (int s = 0; s < kItems; ++s) {
         const int64_t i = base + static_cast<int64_t>(s) * kWave;
         key[s] = 0;
-        if (i < total) key[s] = kFirst ? src_key<KeyT>(src, i, bad) : keys[i];
+        if (i < total)
+            key[s] = !kFirst ? keys[i] : col_only ? src_col<KeyT>(src, i, bad) : src_key<KeyT>(src, i, bad);
     }
     __syncthreads();
     // Counts do not depend on order, so plain LDS atomics do (measured on
@@ -201,10 +221,9 @@ __device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t tiles) {
 template <typename KeyT, bool kFirst>
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     EdgeSrc src, const KeyT* __restrict__ keys_in, KeyT* __restrict__ keys_out, int shift,
-    int64_t total, int64_t tiles, const int64_t* __restrict__ offsets) {
+    int64_t total, int64_t tiles, const int64_t* __restrict__ offsets, int64_t* __restrict__ work) {
     __shared__ KeyT buf[kSortTile];
     __shared__ int32_t cnt[kSortWaves][kRadix];
-    __shared__ int32_t first[kRadix];
     __shared__ int64_t goff[kRadix];
     __shared__ int64_t wtot[kSortWaves];
     const int t = threadIdx.x, w = t / kWave, lane = t % kWave;
@@ -247,7 +266,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     }
     int32_t at = static_cast<int32_t>(block_exclusive_scan<kOpSum, kSortThreads>(tot, wtot));
     if (t < kRadix) {
-        first[t] = at;
+        goff[t] -= at;  // output position of tile entry j of digit t: goff[t] + j
 #pragma unroll
         for (int k = 0; k < kSortWaves; ++k) {
             cnt[k][t] = at;
@@ -267,9 +286,11 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const int n = left < kSortTile ? static_cast<int>(left) : kSortTile;
     for (int j = t; j < n; j += kSortThreads) {
         const KeyT k = buf[j];
-        const uint32_t d = digit_of(k, shift);
-        keys_out[goff[d] + (j - first[d])] = k;
+        keys_out[goff[digit_of(k, shift)] + j] = k;
     }
+    if (kFirst && bad)
+        atomicOr(reinterpret_cast<unsigned long long*>(work),
+                 static_cast<unsigned long long>(MLXC_STATUS_BAD_NODE));
 }
 
 // ------------------------------------------------------------- device scan
@@ -544,10 +565,10 @@ int csr_build_typed(const EdgeSrc& src, const CsrLayout& l, int32_t flags, int64
             return rc;
         if (p == 0)
             hipLaunchKernelGGL((radix_scatter_kernel<KeyT, true>), dim3(l.tiles), dim3(kSortThreads), 0,
-                               s, src, in, out, shift, l.total, l.tiles, hist);
+                               s, src, in, out, shift, l.total, l.tiles, hist, work);
         else
             hipLaunchKernelGGL((radix_scatter_kernel<KeyT, false>), dim3(l.tiles), dim3(kSortThreads), 0,
-                               s, src, in, out, shift, l.total, l.tiles, hist);
+                               s, src, in, out, shift, l.total, l.tiles, hist, work);
         MLXC_HIP_TRY(hipGetLastError());
         in = out;
     }

@@ -25,10 +25,13 @@ int host_csr_build(const int64_t* row, const int64_t* col, int64_t num_edges, in
             r = col[i - num_edges];
             c = row[i - num_edges];
         }
-        if (static_cast<uint64_t>(r) >= static_cast<uint64_t>(num_nodes) ||
-            static_cast<uint64_t>(c) >= static_cast<uint64_t>(num_nodes)) {
+        // an id outside [0, num_nodes) becomes 0, each on its own
+        if (static_cast<uint64_t>(r) >= static_cast<uint64_t>(num_nodes)) {
             status |= MLXC_STATUS_BAD_NODE;
             r = 0;
+        }
+        if (static_cast<uint64_t>(c) >= static_cast<uint64_t>(num_nodes)) {
+            status |= MLXC_STATUS_BAD_NODE;
             c = 0;
         }
         keys[i] = (static_cast<uint64_t>(r) << cbits) | static_cast<uint64_t>(c);
