@@ -122,7 +122,9 @@ size_t mlxc_random_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges,
  * num_walks * walk_length * (1 + 4 w) < 4 * num_edges, w being the share of
  * acceptance draws r that can need a row search (|prob1 - prob2| for
  * MLXC_RULE_NODE2VEC_EXACT, max(0, prob1 - prob2) for the chain).  Both
- * layouts add 16 bytes per walk and about 4.3 bytes per edge of search index.
+ * layouts add 16 bytes per walk, about 4.3 bytes per edge of search index and
+ * 4 bytes per node of int32 row starts (the rows the preparation pass and the
+ * CSR mode read).
  * Records are also chosen when num_edges <= 32768 * walk_length, and 256
  * bytes (the LDS walk) under the same conditions as for mlxc_random_walk.
  * The record layout ends with room for dense neighbour bitmaps of the rows

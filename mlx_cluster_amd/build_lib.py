@@ -64,14 +64,15 @@ def _code_only(text: str) -> str:
     return "\n".join(line.rstrip() for line in text.splitlines() if line.strip())
 
 
-# The sources each profiled kernel family is built from: a profile stays
-# matched to a build as long as these files' code is unchanged.
-_COMMON = ["walk_device.h", "walk_host.h", "mlxc_api.hip", "prep_kernels.hip"]
+# The device code each profiled kernel family is built from (its kernels and
+# launchers, the preparation kernels the walks run first, the shared device
+# helpers): a profile stays matched to a build as long as these files' code
+# is unchanged.
 KERNEL_SOURCES = {
-    "uniform_walk": _COMMON + ["uniform_walk.hip"],
-    "node2vec_walk": _COMMON + ["node2vec_walk.hip"],
-    "csr_build": _COMMON + ["csr_build.hip"],
-    "context_windows": _COMMON + ["windows.hip"],
+    "uniform_walk": ["walk_device.h", "prep_kernels.hip", "uniform_walk.hip"],
+    "node2vec_walk": ["walk_device.h", "prep_kernels.hip", "node2vec_walk.hip"],
+    "csr_build": ["walk_device.h", "csr_build.hip"],
+    "context_windows": ["walk_device.h", "windows.hip"],
 }
 
 

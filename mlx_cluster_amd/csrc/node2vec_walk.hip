@@ -261,6 +261,7 @@ struct N2VRecArgs {
     // hub_bits + s * hub_words, and the records carry each node's slot.
     const uint32_t* hub_bits;
     int64_t hub_words;
+    const int32_t* row32;  // int32 row starts (row32_kernel): the CSR mode's row reads
 };
 
 // Smallest float >= p (p > 0), the float threshold of N2VRecArgs.
@@ -331,7 +332,7 @@ __device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, float r, bool a
 template <int kRule, bool kEdges, bool kCsr, typename OutT>
 __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-    typedef int32_t i32x4a8 __attribute__((ext_vector_type(4), aligned(8)));
+    typedef int32_t i32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
     OutT* const nout = static_cast<OutT*>(a.w.n_out);
     OutT* const eout = static_cast<OutT*>(a.w.e_out);
     const bool sorted = a.rows == MLXC_ROWS_SORTED ||
@@ -385,7 +386,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             else
                 bp = reinterpret_cast<const int32_t*>(a.recs + e);
         } else if (kCsr && ph == kN2vRow) {
-            bp = reinterpret_cast<const int32_t*>(a.w.rowptr + x);  // 8-byte aligned
+            bp = a.row32 + x;  // row32[x], row32[x + 1] (4-byte aligned)
         } else if (ph == kN2vLevel) {
             uint32_t off = 0;  // level lvl's offset from level 0, in entries
 #pragma unroll
@@ -403,7 +404,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
         }
         i32x4 qb[4];
         if (kCsr)
-            qb[0] = *reinterpret_cast<const i32x4a8*>(bp);
+            qb[0] = *reinterpret_cast<const i32x4a4*>(bp);
         else
             qb[0] = reinterpret_cast<const i32x4*>(bp)[0];
         // the other 48 bytes of the block only for the search phases (reading
@@ -475,11 +476,10 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                 phase = kN2vRow;
             }
         } else if (kCsr && ph == kN2vRow) {
-            // rowptr[x] and rowptr[x + 1] as int32 pairs (low, high)
-            const bool ok = rec.y == 0 && rec.w == 0 && rec.x >= 0 && rec.z >= rec.x &&
-                            rec.z <= a.w.num_edges;
+            // row32[x] and row32[x + 1] (-1 marks an entry outside [0, num_edges])
+            const bool ok = rec.x >= 0 && rec.y >= rec.x;
             bx = rec.x;
-            dx = rec.z - rec.x;
+            dx = rec.y - rec.x;
             if (!ok) {
                 status |= MLXC_STATUS_BAD_ROW;
                 fill = true;
@@ -790,6 +790,7 @@ int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
 struct N2VLayout {
     size_t level[kMaxLevels];
     int count;
+    size_t row32;          // the int32 row starts (row32_kernel), num_nodes + 3 entries
     size_t total_no_hubs;  // the layout without hub bitmaps
     size_t hub_info, hub_slot_of, hub_node_of, hub_bits;
     int32_t hub_max;
@@ -818,7 +819,11 @@ N2VLayout n2v_layout(int64_t num_nodes, int64_t num_edges, int64_t num_walks, bo
         pos += static_cast<size_t>(blocks) * kSearchBlock * sizeof(int32_t);
         entries = blocks;
     }
-    lay.total_no_hubs = pos + 64;
+    pos += 64;
+    // the int32 row starts, two entries of slack for the CSR walk's 16-byte reads
+    lay.row32 = align128(pos);
+    pos = lay.row32 + static_cast<size_t>(num_nodes + 3) * sizeof(int32_t);
+    lay.total_no_hubs = pos;
     lay.hub_words = ((num_nodes + 31) / 32 + 3) / 4 * 4;
     const int64_t bitmap_bytes = lay.hub_words * 4;
     int64_t max = records && num_nodes > 0 && kHubBudgetBytes > 0 ? num_edges / kHubMinDegree : 0;
@@ -935,11 +940,13 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         // reads the result on the device, no host sync)
         int64_t* check = w.work;
         const StartRecords starts{w.start, w.num_walks, init};
+        int32_t* row32 = reinterpret_cast<int32_t*>(base + lay.row32);
         if (int rc = records ? launch_edge_records(w.rowptr, w.col, w.num_nodes, w.num_edges, recs,
-                                                   index, starts, check, stream, hubs)
+                                                   index, starts, check, stream, hubs, row32)
                              : launch_edge_index(w.rowptr, w.col, w.num_nodes, w.num_edges, index,
-                                                 starts, check, stream))
+                                                 starts, check, stream, row32))
             return rc;
+        a.row32 = row32;
         if (hub_bitmaps)
             if (int rc = launch_hub_build(w.rowptr, w.col, w.num_nodes, hubs, p.rows, w.work, stream))
                 return rc;

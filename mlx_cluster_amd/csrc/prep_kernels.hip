@@ -80,6 +80,40 @@ __device__ __forceinline__ int4 node_record(const int64_t* __restrict__ rowptr, 
     return r;
 }
 
+// The same record from the int32 row starts row32 (row32[v] = rowptr[v], or
+// -1 for an entry outside [0, num_edges]; see row32_kernel): the row is
+// valid iff row32[v] >= 0 and row32[v + 1] >= row32[v], as row_ok decides on
+// rowptr.  The table is half the size of rowptr, so twice as much of it stays
+// in each XCD's L2 while a preparation pass gathers rows for every entry.
+__device__ __forceinline__ int4 node_record32(const int32_t* __restrict__ row32, int64_t v,
+                                              int64_t num_nodes) {
+    typedef int32_t i32x2 __attribute__((ext_vector_type(2), aligned(4)));
+    int4 r = make_int4(static_cast<int32_t>(v), 0, kRecBadNode, 0);
+    if (node_ok(v, num_nodes)) {
+        const i32x2 b = *reinterpret_cast<const i32x2*>(row32 + v);
+        if (b.x >= 0 && b.y >= b.x) {
+            r.y = b.x;
+            r.z = b.y - b.x;
+        } else {
+            r.z = kRecBadRow;
+        }
+    }
+    return r;
+}
+
+// row32[v] = rowptr[v] as int32 for v in [0, num_nodes], -1 for an entry
+// outside [0, num_edges] (num_edges < 2^31).
+__global__ __launch_bounds__(kBlock) void row32_kernel(const int64_t* __restrict__ rowptr,
+                                                       int64_t num_nodes, int64_t num_edges,
+                                                       int32_t* __restrict__ row32) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t v = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; v <= num_nodes;
+         v += stride) {
+        const int64_t x = rowptr[v];
+        row32[v] = x >= 0 && x <= num_edges ? static_cast<int32_t>(x) : -1;
+    }
+}
+
 // Hub slot of a node record for the node2vec record walk: the slot of its
 // bitmap when its row has one (degree at or above the threshold h), else -1.
 __device__ __forceinline__ int4 with_slot(int4 r, const HubBitmaps& hubs, int64_t h) {
@@ -95,13 +129,15 @@ __device__ __forceinline__ int4 with_slot(int4 r, const HubBitmaps& hubs, int64_
 // whole CSR (status bits into work[0]) and counts the row descents into
 // work[2] / work[3], from which the node2vec walk decides whether its rows
 // are sorted.  With hubs.max > 0 every record's pad word holds its node's
-// hub slot (hub_assign_kernel ran before), else -1.
+// hub slot (hub_assign_kernel ran before), else -1.  With a non-null row32
+// (row32_kernel ran before) the rows are gathered from it instead of rowptr.
 __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __restrict__ rowptr,
                                                              const int64_t* __restrict__ col,
                                                              int64_t num_nodes, int64_t num_edges,
                                                              EdgeRecord* __restrict__ rec,
                                                              IndexLevels index, StartRecords starts,
-                                                             int64_t* work, HubBitmaps hubs) {
+                                                             int64_t* work, HubBitmaps hubs,
+                                                             const int32_t* __restrict__ row32) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -114,17 +150,20 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
         if (!rec) {
             if (!node_ok(c, num_nodes)) r.x = -1;
         } else {
-            if (node_ok(c, num_nodes)) {
+            if (row32) {
+                const int4 n4 = node_record32(row32, c, num_nodes);
+                r.y = n4.y;
+                r.z = n4.z;
+            } else if (node_ok(c, num_nodes)) {
                 const RowBounds rb = load_row(rowptr, c);
                 if (row_ok(rb, num_edges)) {
                     r.y = static_cast<int32_t>(rb.begin);
                     r.z = static_cast<int32_t>(rb.end - rb.begin);
-                    if (r.z >= h) r.w = hubs.slot_of[c];
                 } else {
                     r.z = kRecBadRow;
                 }
             }
-            if (r.z < h) r.w = -1;  // (no hub slot)
+            r.w = r.z >= 0 && r.z >= h ? hubs.slot_of[c] : -1;
             *reinterpret_cast<i32x4*>(rec + e) = r;
         }
         if (index.count > 0) {
@@ -136,7 +175,9 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
     }
     for (int64_t n = gid; n < starts.num_walks; n += stride)
         *reinterpret_cast<int4*>(starts.init + n) =
-            with_slot(node_record(rowptr, starts.start[n], num_nodes, num_edges), hubs, h);
+            with_slot(row32 ? node_record32(row32, starts.start[n], num_nodes)
+                            : node_record(rowptr, starts.start[n], num_nodes, num_edges),
+                      hubs, h);
     if (work) {
         check.nodes(rowptr, num_nodes, col, num_edges, gid, stride);
         unsigned long long* w = reinterpret_cast<unsigned long long*>(work);
@@ -478,14 +519,20 @@ int launch_zero_work(int64_t* d_work, hipStream_t stream) {
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                         int64_t num_edges, EdgeRecord* recs, const IndexLevels& index,
                         const StartRecords& starts, int64_t* check_work, hipStream_t stream,
-                        const HubBitmaps& hubs) {
-    if (num_edges == 0 && !check_work && starts.num_walks == 0) return MLXC_OK;
+                        const HubBitmaps& hubs, int32_t* row32) {
     int grid = 0;
+    if (row32) {
+        if (int rc = stream_grid(num_nodes + 1, 8, grid)) return rc;
+        hipLaunchKernelGGL(row32_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, num_nodes,
+                           num_edges, row32);
+    }
+    if (num_edges == 0 && !check_work && starts.num_walks == 0) return MLXC_OK;
     int64_t items = check_work && num_nodes > num_edges ? num_nodes : num_edges;
     if (starts.num_walks > items) items = starts.num_walks;
     if (int rc = stream_grid(items, 16, grid)) return rc;
     hipLaunchKernelGGL(edge_record_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col,
-                       num_nodes, num_edges, recs, index, starts, check_work, hubs);
+                       num_nodes, num_edges, recs, index, starts, check_work, hubs,
+                       static_cast<const int32_t*>(row32));
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }
@@ -521,12 +568,17 @@ int launch_hub_build(const int64_t* rowptr, const int64_t* col, int64_t num_node
 
 int launch_edge_index(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                       int64_t num_edges, const IndexLevels& index, const StartRecords& starts,
-                      int64_t* check_work, hipStream_t stream) {
-    if (num_edges == 0 && !check_work && starts.num_walks == 0) return MLXC_OK;
+                      int64_t* check_work, hipStream_t stream, int32_t* row32) {
     if (reinterpret_cast<uintptr_t>(col) % 16 != 0)  // the record pass reads any alignment
         return launch_edge_records(rowptr, col, num_nodes, num_edges, nullptr, index, starts,
-                                   check_work, stream, HubBitmaps{});
+                                   check_work, stream, HubBitmaps{}, row32);
     int grid = 0;
+    if (row32) {
+        if (int rc = stream_grid(num_nodes + 1, 8, grid)) return rc;
+        hipLaunchKernelGGL(row32_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, num_nodes,
+                           num_edges, row32);
+    }
+    if (num_edges == 0 && !check_work && starts.num_walks == 0) return MLXC_OK;
     const int64_t quads = (num_edges + 3) / 4;
     int64_t items = check_work && num_nodes > quads ? num_nodes : quads;
     if (starts.num_walks > items) items = starts.num_walks;

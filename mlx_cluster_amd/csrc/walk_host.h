@@ -76,10 +76,12 @@ int launch_record_prep(const int64_t* rowptr, const int64_t* col, const int64_t*
 // walk, and in the same pass the start records of `starts` (num_walks 0:
 // none); a non-null check_work also validates the CSR and counts row
 // descents (see edge_record_kernel).
+// A non-null row32 (num_nodes + 1 int32 of workspace) makes the pass first
+// convert rowptr to int32 row starts and gather the rows from them.
 int launch_edge_records(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                         int64_t num_edges, EdgeRecord* recs, const IndexLevels& index,
                         const StartRecords& starts, int64_t* check_work, hipStream_t stream,
-                        const HubBitmaps& hubs);
+                        const HubBitmaps& hubs, int32_t* row32);
 // The hub bitmaps (see HubBitmaps), in two launches around
 // launch_edge_records: launch_hub_bitmaps chooses the degree threshold (at
 // least min_degree) and assigns the slots, which the records then carry;
@@ -97,7 +99,7 @@ int launch_hub_build(const int64_t* rowptr, const int64_t* col, int64_t num_node
 // record pass.
 int launch_edge_index(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                       int64_t num_edges, const IndexLevels& index, const StartRecords& starts,
-                      int64_t* check_work, hipStream_t stream);
+                      int64_t* check_work, hipStream_t stream, int32_t* row32);
 // Start records of the uniform CSR walk; the same launch zeroes the call's
 // status words.
 int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
