@@ -15,9 +15,12 @@
 //   radix_scatter_kernel  stable rank of each key inside its tile (wavefront
 //                         match of the digit), reorder of the tile in LDS,
 //                         then stores in digit runs.
-// The first pass reads the caller's (row, col) arrays directly (and the
-// reversed pairs, for symmetrize); the last pass's keys go to csr_emit_kernel,
-// which writes col, marks row starts and, with dedup, drops repeated keys.
+// Each scatter also writes every key's digit of the next pass into a byte
+// array beside the keys, so that the next histogram reads 1 byte per key
+// instead of the key.  The first pass reads the caller's (row, col) arrays
+// directly (and the reversed pairs, for symmetrize); the last pass's keys go
+// to csr_emit_kernel, which writes col, marks row starts and, with dedup,
+// drops repeated keys.
 // rowptr is filled with the entry count, row starts are written into it, and a
 // reverse inclusive min-scan gives empty rows the start of the next row.
 #include "walk_host.h"
@@ -66,27 +69,44 @@ __device__ __forceinline__ int64_t clamp_id(int64_t v, int64_t num_nodes, bool& 
     return ok ? v : 0;
 }
 
-template <typename KeyT>
-__device__ __forceinline__ KeyT src_key(const EdgeSrc& s, int64_t i, bool& bad) {
-    int64_t r, c;
-    if (i < s.num_edges) {
-        r = s.row[i];
-        c = s.col[i];
-    } else {
-        r = s.col[i - s.num_edges];
-        c = s.row[i - s.num_edges];
-    }
-    r = clamp_id(r, s.num_nodes, bad);
-    c = clamp_id(c, s.num_nodes, bad);
-    return (static_cast<KeyT>(r) << s.cbits) | static_cast<KeyT>(c);
+// Addresses of entry i's row and col ids (i >= num_edges: the reversed pair
+// of entry i - num_edges), chosen by a select rather than a branch.
+__device__ __forceinline__ const int64_t* src_row_ptr(const EdgeSrc& s, int64_t i) {
+    return i < s.num_edges ? s.row + i : s.col + (i - s.num_edges);
+}
+__device__ __forceinline__ const int64_t* src_col_ptr(const EdgeSrc& s, int64_t i) {
+    return i < s.num_edges ? s.col + i : s.row + (i - s.num_edges);
 }
 
-// The col field of entry i's key alone (one array read): enough for the
-// digits of a pass that lies inside the col field.
-template <typename KeyT>
-__device__ __forceinline__ KeyT src_col(const EdgeSrc& s, int64_t i, bool& bad) {
-    const int64_t c = i < s.num_edges ? s.col[i] : s.row[i - s.num_edges];
-    return static_cast<KeyT>(clamp_id(c, s.num_nodes, bad));
+// How a pass reads entry i: the previous pass's keys, or (first pass) the
+// caller's arrays, both ids or the col id alone when the pass's digits lie in
+// the col field (row ids are then checked by the first scatter pass, which
+// reads both).
+enum class Src { kKeys, kBoth, kCol };
+
+template <typename KeyT, Src kSrc>
+__device__ __forceinline__ KeyT read_entry(const EdgeSrc& s, const KeyT* keys, int64_t i,
+                                           bool& bad) {
+    if (kSrc == Src::kKeys) return keys[i];
+    const KeyT c = static_cast<KeyT>(clamp_id(*src_col_ptr(s, i), s.num_nodes, bad));
+    if (kSrc == Src::kCol) return c;
+    const KeyT r = static_cast<KeyT>(clamp_id(*src_row_ptr(s, i), s.num_nodes, bad));
+    return (r << s.cbits) | c;
+}
+
+// A thread's entries base + q * stride (q < kItems), every load issued before
+// any value is used: an index at or past `total` reads entry total - 1 (the
+// caller ignores those slots), so that no load sits behind a branch.  (Behind
+// per-slot branches the compiler waits for each load before the next.)
+template <typename KeyT, Src kSrc>
+__device__ __forceinline__ void load_slots(KeyT (&key)[kItems], const EdgeSrc& s,
+                                           const KeyT* keys, int64_t base, int stride,
+                                           int64_t total, bool& bad) {
+#pragma unroll
+    for (int q = 0; q < kItems; ++q) {
+        const int64_t i = base + static_cast<int64_t>(q) * stride;
+        key[q] = read_entry<KeyT, kSrc>(s, keys, i < total ? i : total - 1, bad);
+    }
 }
 
 template <typename KeyT>
@@ -97,23 +117,32 @@ __device__ __forceinline__ uint32_t digit_of(KeyT k, int shift) {
 // Lanes of this wavefront that are active and hold the same digit d.  For
 // each bit, the lanes whose bit differs from this lane's are m ^ e, with m
 // the wavefront's ballot of the bit and e = 0 or ~0 this lane's bit: OR-ing
-// those over the bits (one XOR and one OR per 32-bit half) leaves the peers
-// as the lanes never marked.
+// those over the bits leaves the peers as the lanes never marked.  The OR of
+// an XOR is one v_bitop3_b32 per 32-bit half (gfx950): truth table index
+// S0 * 4 + S1 * 2 + S2 over (S0 = m, S1 = e, S2 = differ), value
+// S2 | (S0 ^ S1).  With the sign-extended bit e as the ballot's operand a bit
+// costs four VALU instructions.
+constexpr uint32_t bitop3_table_or_xor() {
+    uint32_t t = 0;
+    for (int i = 0; i < 8; ++i)
+        if ((i & 1) | (((i >> 2) ^ (i >> 1)) & 1)) t |= 1u << i;
+    return t;
+}
+static_assert(bitop3_table_or_xor() == 0xbe, "S2 | (S0 ^ S1)");
+
 __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool active) {
     uint32_t differ_lo = 0, differ_hi = 0;
 #pragma unroll
     for (int b = 0; b < kRadixBits; ++b) {
-        const uint32_t e = 0u - ((d >> b) & 1u);
-        const uint64_t m = __ballot(e != 0);
-        differ_lo |= static_cast<uint32_t>(m) ^ e;
-        differ_hi |= static_cast<uint32_t>(m >> 32) ^ e;
+        const uint32_t e = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int32_t>(d), b, 1));
+        const uint64_t m = __builtin_amdgcn_uicmp(e, 0u, 33);  // 33: not equal
+        differ_lo = __builtin_amdgcn_bitop3_b32(static_cast<uint32_t>(m), e, differ_lo,
+                                                bitop3_table_or_xor());
+        differ_hi = __builtin_amdgcn_bitop3_b32(static_cast<uint32_t>(m >> 32), e, differ_hi,
+                                                bitop3_table_or_xor());
     }
     const uint64_t act = __ballot(active);
     return act & ~((static_cast<uint64_t>(differ_hi) << 32) | differ_lo);
-}
-
-__device__ __forceinline__ bool is_leader(uint64_t peers) {
-    return static_cast<int>(__lane_id()) == __ffsll(static_cast<long long>(peers)) - 1;
 }
 
 template <int kOp>
@@ -155,9 +184,13 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t* wtot, int64_t* total
 
 // ------------------------------------------------------------- radix pass
 
+// Per 8192-key tile, the counts of its 256 digits.  The first pass reads the
+// caller's arrays; later passes read the digit bytes the previous scatter
+// wrote beside the keys (1 byte per key instead of 4 or 8), one 16-byte load
+// per thread.  The byte array is padded to whole tiles.
 template <typename KeyT, bool kFirst>
 __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(EdgeSrc src,
-                                                                  const KeyT* __restrict__ keys,
+                                                                  const uint8_t* __restrict__ digits,
                                                                   int shift, int64_t total,
                                                                   int64_t tiles,
                                                                   int64_t* __restrict__ hist,
@@ -166,29 +199,33 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(EdgeSrc src,
     const int t = threadIdx.x, w = t / kWave, lane = t % kWave;
     for (int k = t; k < kSortWaves * kRadix; k += kSortThreads) (&cnt[0][0])[k] = 0;
     const int64_t tile = blockIdx.x;
-    const int64_t base = tile * kSortTile + w * kWaveTile + lane;
     bool bad = false;
-    // the first pass's digits lie in the col field (bits 0..7) when it is 8
-    // bits wide or more: only that array is read (bad rows are reported by
-    // the first scatter pass, which reads both)
-    const bool col_only = kFirst && shift + kRadixBits <= src.cbits;
-    // all loads first, so that the whole tile is in flight at once
-    KeyT key[kItems];
+    // Counts do not depend on order, so plain LDS atomics do.
+    if (kFirst) {
+        // all loads first, so that the whole tile is in flight at once
+        const int64_t base = tile * kSortTile + w * kWaveTile + lane;
+        KeyT key[kItems];
+        if (shift + kRadixBits <= src.cbits)
+            load_slots<KeyT, Src::kCol>(key, src, static_cast<const KeyT*>(nullptr), base, kWave,
+                                        total, bad);
+        else
+            load_slots<KeyT, Src::kBoth>(key, src, static_cast<const KeyT*>(nullptr), base, kWave,
+                                         total, bad);
+        __syncthreads();
 #pragma unroll
-    for (int s = 0; s < kItems; ++s) {
-        const int64_t i = base + static_cast<int64_t>(s) * kWave;
-        key[s] = 0;
-        if (i < total)
-            key[s] = !kFirst ? keys[i] : col_only ? src_col<KeyT>(src, i, bad) : src_key<KeyT>(src, i, bad);
-    }
-    __syncthreads();
-    // Counts do not depend on order, so plain LDS atomics do (measured on
-    // MI355X: 0.52 ms per pass at 2^28 keys, against 0.71 ms with the
-    // wavefront match the scatter needs for its stable ranks).
+        for (int s = 0; s < kItems; ++s) {
+            if (base + static_cast<int64_t>(s) * kWave < total)
+                atomicAdd(&cnt[w][digit_of(key[s], shift)], 1);
+        }
+    } else {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const int64_t at = tile * kSortTile + static_cast<int64_t>(t) * kItems;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(digits + at);
+        __syncthreads();
 #pragma unroll
-    for (int s = 0; s < kItems; ++s) {
-        if (base + static_cast<int64_t>(s) * kWave < total)
-            atomicAdd(&cnt[w][digit_of(key[s], shift)], 1);
+        for (int q = 0; q < kItems; ++q) {
+            if (at + q < total) atomicAdd(&cnt[w][(v[q / 4] >> (8 * (q % 4))) & 0xffu], 1);
+        }
     }
     __syncthreads();
     if (t < kRadix) {
@@ -218,10 +255,12 @@ __device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t tiles) {
     return x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
 }
 
+// Two blocks per CU (their LDS fits): at most 128 VGPRs.
 template <typename KeyT, bool kFirst>
-__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
+__global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4))) void radix_scatter_kernel(
     EdgeSrc src, const KeyT* __restrict__ keys_in, KeyT* __restrict__ keys_out, int shift,
-    int64_t total, int64_t tiles, const int64_t* __restrict__ offsets, int64_t* __restrict__ work) {
+    int64_t total, int64_t tiles, const int64_t* __restrict__ offsets, int64_t* __restrict__ work,
+    uint8_t* __restrict__ next_digits, int next_shift) {
     __shared__ KeyT buf[kSortTile];
     __shared__ int32_t cnt[kSortWaves][kRadix];
     __shared__ int64_t goff[kRadix];
@@ -238,18 +277,20 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     KeyT key[kItems];
     int32_t pos[kItems];
     bool bad = false;
+    if (kFirst)
+        load_slots<KeyT, Src::kBoth>(key, src, keys_in, base, kWave, total, bad);
+    else
+        load_slots<KeyT, Src::kKeys>(key, src, keys_in, base, kWave, total, bad);
 #pragma unroll
     for (int s = 0; s < kItems; ++s) {
-        const int64_t i = base + static_cast<int64_t>(s) * kWave;
-        const bool active = i < total;
-        KeyT k = 0;
-        if (active) k = kFirst ? src_key<KeyT>(src, i, bad) : keys_in[i];
-        key[s] = k;
+        const bool active = base + static_cast<int64_t>(s) * kWave < total;
+        const KeyT k = key[s];
         const uint32_t d = digit_of(k, shift);
         const uint64_t peers = match_digit(d, active);
         const int32_t before = cnt[w][d];
-        pos[s] = before + lane_rank(peers);
-        if (active && is_leader(peers)) cnt[w][d] = before + __popcll(peers);
+        const int rank = lane_rank(peers);
+        pos[s] = before + rank;
+        if (active && rank == 0) cnt[w][d] = before + __popcll(peers);  // the lowest such lane
     }
     __syncthreads();
 
@@ -284,9 +325,12 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     // Consecutive entries of one digit go to consecutive output positions.
     const int64_t left = total - tile * kSortTile;
     const int n = left < kSortTile ? static_cast<int>(left) : kSortTile;
+    // With next_digits, each key's digit of the next pass goes beside it.
     for (int j = t; j < n; j += kSortThreads) {
         const KeyT k = buf[j];
-        keys_out[goff[digit_of(k, shift)] + j] = k;
+        const int64_t at = goff[digit_of(k, shift)] + j;
+        keys_out[at] = k;
+        if (next_digits) next_digits[at] = static_cast<uint8_t>(digit_of(k, next_shift));
     }
     if (kFirst && bad)
         atomicOr(reinterpret_cast<unsigned long long*>(work),
@@ -384,11 +428,20 @@ __global__ void set_word_kernel(int64_t* __restrict__ word, int64_t v) {
     if (threadIdx.x == 0) *word = v;
 }
 
-// Entry i of the sorted keys is kept unless dedup is on and it repeats
-// entry i - 1.
-template <typename KeyT, bool kDedup>
-__device__ __forceinline__ bool kept(const KeyT* __restrict__ keys, int64_t i, KeyT k) {
-    return !kDedup || i == 0 || keys[i - 1] != k;
+// key[s] = keys[i], prev[s] = keys[i - 1] for i = base + s * kBlock, all
+// loads issued before any is used (indices clamped into [0, total); the
+// caller ignores slots with i >= total, and prev of i = 0).
+template <typename KeyT>
+__device__ __forceinline__ void load_pairs(KeyT (&key)[kItems], KeyT (&prev)[kItems],
+                                           const KeyT* __restrict__ keys, int64_t base,
+                                           int64_t total) {
+#pragma unroll
+    for (int s = 0; s < kItems; ++s) {
+        int64_t i = base + s * kBlock;
+        i = i < total ? i : total - 1;
+        key[s] = keys[i];
+        prev[s] = keys[i > 0 ? i - 1 : 0];
+    }
 }
 
 // counts[chunk] <- kept entries of chunk (kChunk entries).
@@ -397,11 +450,14 @@ __global__ __launch_bounds__(kBlock) void dedup_count_kernel(const KeyT* __restr
                                                              int64_t total,
                                                              int64_t* __restrict__ counts) {
     __shared__ int64_t wtot[kWaves];
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk + threadIdx.x;
+    KeyT key[kItems], prev[kItems];
+    load_pairs(key, prev, keys, base, total);
     int64_t c = 0;
+#pragma unroll
     for (int s = 0; s < kItems; ++s) {
-        const int64_t i = base + s * kBlock + threadIdx.x;
-        if (i < total) c += kept<KeyT, true>(keys, i, keys[i]);
+        const int64_t i = base + s * kBlock;
+        c += i < total && (i == 0 || prev[s] != key[s]);
     }
     int64_t all;
     block_exclusive_scan<kOpSum>(c, wtot, &all);
@@ -422,18 +478,14 @@ __global__ __launch_bounds__(kBlock) void csr_emit_kernel(const KeyT* __restrict
     const int t = threadIdx.x, w = t / kWave;
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
     const KeyT cmask = cbits == 0 ? KeyT(0) : (~KeyT(0) >> (8 * sizeof(KeyT) - cbits));
-    KeyT key[kItems];
+    KeyT key[kItems], before[kItems];
+    load_pairs(key, before, keys, base + t, total);
     uint32_t keep_bits = 0, start_bits = 0;
 #pragma unroll
     for (int s = 0; s < kItems; ++s) {
         const int64_t i = base + s * kBlock + t;
         const bool valid = i < total;
-        KeyT k = 0, prev = 0;
-        if (valid) {
-            k = keys[i];
-            if (i > 0) prev = keys[i - 1];
-        }
-        key[s] = k;
+        const KeyT k = key[s], prev = before[s];
         const bool keep = valid && (!kDedup || i == 0 || prev != k);
         const bool row_start = valid && (i == 0 || (prev >> cbits) != (k >> cbits));
         keep_bits |= static_cast<uint32_t>(keep) << s;
@@ -489,7 +541,7 @@ struct CsrLayout {
     bool wide = false;  // 64-bit keys
     int64_t tiles = 0;   // radix tiles of kSortTile keys
     int64_t chunks = 0;  // finish chunks of kChunk keys
-    size_t keys0 = 0, keys1 = 0, hist = 0, sums = 0, bytes = 0;
+    size_t keys0 = 0, keys1 = 0, digits = 0, hist = 0, sums = 0, bytes = 0;
 };
 
 CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
@@ -513,6 +565,8 @@ CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
     at += round256(static_cast<size_t>(l.total) * ksz);
     l.keys1 = at;
     at += round256(static_cast<size_t>(l.total) * ksz);
+    l.digits = at;  // the next pass's digit of each key, padded to whole tiles
+    at += round256(static_cast<size_t>(l.tiles) * kSortTile);
     l.hist = at;
     at += round256(static_cast<size_t>(hist_n) * sizeof(int64_t));
     l.sums = at;
@@ -550,25 +604,29 @@ int csr_build_typed(const EdgeSrc& src, const CsrLayout& l, int32_t flags, int64
     KeyT* buf[2] = {reinterpret_cast<KeyT*>(ws + l.keys0), reinterpret_cast<KeyT*>(ws + l.keys1)};
     int64_t* hist = reinterpret_cast<int64_t*>(ws + l.hist);
     int64_t* sums = reinterpret_cast<int64_t*>(ws + l.sums);
+    uint8_t* digits = reinterpret_cast<uint8_t*>(ws + l.digits);
     const KeyT* in = nullptr;
     for (int p = 0; p < l.passes; ++p) {
         const int shift = p * kRadixBits;
         KeyT* out = buf[p & 1];
+        uint8_t* next_digits = p + 1 < l.passes ? digits : nullptr;
         if (p == 0)
             hipLaunchKernelGGL((radix_hist_kernel<KeyT, true>), dim3(l.tiles), dim3(kSortThreads), 0, s,
-                               src, in, shift, l.total, l.tiles, hist, work);
+                               src, digits, shift, l.total, l.tiles, hist, work);
         else
             hipLaunchKernelGGL((radix_hist_kernel<KeyT, false>), dim3(l.tiles), dim3(kSortThreads), 0, s,
-                               src, in, shift, l.total, l.tiles, hist, work);
+                               src, digits, shift, l.total, l.tiles, hist, work);
         MLXC_HIP_TRY(hipGetLastError());
         if (int rc = device_scan<kOpSum, false, true>(hist, kRadix * l.tiles, sums, nullptr, s))
             return rc;
         if (p == 0)
             hipLaunchKernelGGL((radix_scatter_kernel<KeyT, true>), dim3(l.tiles), dim3(kSortThreads), 0,
-                               s, src, in, out, shift, l.total, l.tiles, hist, work);
+                               s, src, in, out, shift, l.total, l.tiles, hist, work, next_digits,
+                               shift + kRadixBits);
         else
             hipLaunchKernelGGL((radix_scatter_kernel<KeyT, false>), dim3(l.tiles), dim3(kSortThreads), 0,
-                               s, src, in, out, shift, l.total, l.tiles, hist, work);
+                               s, src, in, out, shift, l.total, l.tiles, hist, work, next_digits,
+                               shift + kRadixBits);
         MLXC_HIP_TRY(hipGetLastError());
         in = out;
     }

@@ -62,6 +62,42 @@ def test_skewed_with_duplicates(sym, dedup, cuda):
     assert_parity(row, col, V, cuda, sym, dedup)
 
 
+def _rows_of_lengths(lengths, V, rng, col_range=None):
+    """An edge list, shuffled, whose rows 0, k, 2k, ... hold the given numbers
+    of entries (k spreads the rows over the node ids)."""
+    k = max(1, V // len(lengths))
+    row = np.repeat(np.arange(len(lengths), dtype=np.int64) * k, lengths)
+    col = rng.integers(0, col_range or V, row.size)
+    perm = rng.permutation(row.size)
+    return row[perm], col[perm]
+
+
+@pytest.mark.parametrize("V", [300, 65536, 3_000_001])
+def test_row_lengths_around_tiles(V, cuda):
+    """Rows of lengths around the radix passes' 8192-key tiles and their
+    4096-entry finish chunks (one entry to several tiles), shuffled, with
+    repeated pairs and a long last row: digit runs that cross tile and
+    chunk boundaries.  V = 300 and 65536 give 32-bit keys, 3_000_001 64-bit
+    keys."""
+    rng = np.random.default_rng(V)
+    base = [1, 2, 63, 64, 4095, 4096, 4097, 6000, 8191, 8192, 8193, 12_000, 20_000]
+    lengths = list(rng.permutation(base * 3)) + [3, 4100, 9000]
+    row, col = _rows_of_lengths(lengths, min(V, 300), rng, col_range=V)
+    for sym, dedup in ((False, False), (False, True), (True, True)):
+        assert_parity(row, col, V, cuda, sym, dedup)
+
+
+def test_many_long_rows(cuda):
+    """1500 rows of 8500 to 12000 entries over 5000 columns: every tile holds
+    one or two rows, whose columns repeat many times."""
+    rng = np.random.default_rng(3)
+    V = 1 << 20
+    lengths = rng.integers(8_500, 12_000, 1500)
+    row, col = _rows_of_lengths(lengths, V, rng, col_range=5000)
+    assert_parity(row, col, V, cuda)
+    assert_parity(row, col, V, cuda, dedup=True)
+
+
 def test_rmat_2_20(cuda):
     """The generator of configurations 2 and 3: R-MAT 2^20, 2^24 samples."""
     row, col = synth.rmat_edges(20, 1 << 24, seed=0, device=cuda)
