@@ -59,6 +59,36 @@ struct EdgeSrc {
     int cbits;          // bits of the col field of a key
 };
 
+// Key arrays.  Keys of up to 32 bits are stored whole; keys of 33 to 48 bits
+// as a 32-bit array of their low halves and a 16-bit array of their high
+// bits (6 bytes a key instead of 8, so every pass over them moves a quarter
+// fewer bytes); wider keys as 64-bit words.  A store is a pair of device
+// pointers passed by value; K is the key's type in registers.
+struct Keys32 {
+    using K = uint32_t;
+    uint32_t* p;
+    __device__ __forceinline__ K load(int64_t i) const { return p[i]; }
+    __device__ __forceinline__ void store(int64_t i, K k) const { p[i] = k; }
+};
+struct Keys48 {
+    using K = uint64_t;
+    uint32_t* lo;
+    uint16_t* hi;
+    __device__ __forceinline__ K load(int64_t i) const {
+        return (static_cast<uint64_t>(hi[i]) << 32) | lo[i];
+    }
+    __device__ __forceinline__ void store(int64_t i, K k) const {
+        lo[i] = static_cast<uint32_t>(k);
+        hi[i] = static_cast<uint16_t>(k >> 32);
+    }
+};
+struct Keys64 {
+    using K = uint64_t;
+    uint64_t* p;
+    __device__ __forceinline__ K load(int64_t i) const { return p[i]; }
+    __device__ __forceinline__ void store(int64_t i, K k) const { p[i] = k; }
+};
+
 // Key of entry i of the (optionally symmetrized) list: i < num_edges is
 // (row[i], col[i]); i >= num_edges the reversed pair of entry i - num_edges.
 // An id outside [0, num_nodes) sets `bad` and becomes 0 (each id on its own),
@@ -84,10 +114,10 @@ __device__ __forceinline__ const int64_t* src_col_ptr(const EdgeSrc& s, int64_t 
 // reads both).
 enum class Src { kKeys, kBoth, kCol };
 
-template <typename KeyT, Src kSrc>
-__device__ __forceinline__ KeyT read_entry(const EdgeSrc& s, const KeyT* keys, int64_t i,
+template <typename Store, Src kSrc, typename KeyT = typename Store::K>
+__device__ __forceinline__ KeyT read_entry(const EdgeSrc& s, const Store& keys, int64_t i,
                                            bool& bad) {
-    if (kSrc == Src::kKeys) return keys[i];
+    if (kSrc == Src::kKeys) return keys.load(i);
     const KeyT c = static_cast<KeyT>(clamp_id(*src_col_ptr(s, i), s.num_nodes, bad));
     if (kSrc == Src::kCol) return c;
     const KeyT r = static_cast<KeyT>(clamp_id(*src_row_ptr(s, i), s.num_nodes, bad));
@@ -98,14 +128,14 @@ __device__ __forceinline__ KeyT read_entry(const EdgeSrc& s, const KeyT* keys, i
 // any value is used: an index at or past `total` reads entry total - 1 (the
 // caller ignores those slots), so that no load sits behind a branch.  (Behind
 // per-slot branches the compiler waits for each load before the next.)
-template <typename KeyT, Src kSrc>
+template <typename Store, Src kSrc, typename KeyT = typename Store::K>
 __device__ __forceinline__ void load_slots(KeyT (&key)[kItems], const EdgeSrc& s,
-                                           const KeyT* keys, int64_t base, int stride,
+                                           const Store& keys, int64_t base, int stride,
                                            int64_t total, bool& bad) {
 #pragma unroll
     for (int q = 0; q < kItems; ++q) {
         const int64_t i = base + static_cast<int64_t>(q) * stride;
-        key[q] = read_entry<KeyT, kSrc>(s, keys, i < total ? i : total - 1, bad);
+        key[q] = read_entry<Store, kSrc>(s, keys, i < total ? i : total - 1, bad);
     }
 }
 
@@ -206,7 +236,7 @@ __device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t tiles) {
 // caller's arrays; later passes read the digit bytes the previous scatter
 // wrote beside the keys (1 byte per key instead of 4 or 8), one 16-byte load
 // per thread.  The byte array is padded to whole tiles.
-template <typename KeyT, bool kFirst>
+template <typename Store, bool kFirst>
 __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(EdgeSrc src,
                                                                   const uint8_t* __restrict__ digits,
                                                                   int shift, int64_t total,
@@ -225,13 +255,11 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(EdgeSrc src,
     if (kFirst) {
         // all loads first, so that the whole tile is in flight at once
         const int64_t base = tile * kSortTile + w * kWaveTile + lane;
-        KeyT key[kItems];
+        typename Store::K key[kItems];
         if (shift + kRadixBits <= src.cbits)
-            load_slots<KeyT, Src::kCol>(key, src, static_cast<const KeyT*>(nullptr), base, kWave,
-                                        total, bad);
+            load_slots<Store, Src::kCol>(key, src, Store{}, base, kWave, total, bad);
         else
-            load_slots<KeyT, Src::kBoth>(key, src, static_cast<const KeyT*>(nullptr), base, kWave,
-                                         total, bad);
+            load_slots<Store, Src::kBoth>(key, src, Store{}, base, kWave, total, bad);
         __syncthreads();
 #pragma unroll
         for (int s = 0; s < kItems; ++s) {
@@ -270,11 +298,12 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(EdgeSrc src,
 }
 
 // Two blocks per CU (their LDS fits): at most 128 VGPRs.
-template <typename KeyT, bool kFirst>
+template <typename Store, bool kFirst>
 __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4))) void radix_scatter_kernel(
-    EdgeSrc src, const KeyT* __restrict__ keys_in, KeyT* __restrict__ keys_out, int shift,
+    EdgeSrc src, Store keys_in, Store keys_out, int shift,
     int64_t total, int64_t tiles, const int64_t* __restrict__ offsets, int64_t* __restrict__ work,
     uint8_t* __restrict__ next_digits, int next_shift) {
+    using KeyT = typename Store::K;
     __shared__ KeyT buf[kSortTile];
     __shared__ int32_t cnt[kSortWaves][kRadix];
     __shared__ int64_t goff[kRadix];
@@ -292,9 +321,9 @@ __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4)
     int32_t pos[kItems];
     bool bad = false;
     if (kFirst)
-        load_slots<KeyT, Src::kBoth>(key, src, keys_in, base, kWave, total, bad);
+        load_slots<Store, Src::kBoth>(key, src, keys_in, base, kWave, total, bad);
     else
-        load_slots<KeyT, Src::kKeys>(key, src, keys_in, base, kWave, total, bad);
+        load_slots<Store, Src::kKeys>(key, src, keys_in, base, kWave, total, bad);
 #pragma unroll
     for (int s = 0; s < kItems; ++s) {
         const bool active = base + static_cast<int64_t>(s) * kWave < total;
@@ -343,7 +372,7 @@ __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4)
     for (int j = t; j < n; j += kSortThreads) {
         const KeyT k = buf[j];
         const int64_t at = goff[digit_of(k, shift)] + j;
-        keys_out[at] = k;
+        keys_out.store(at, k);
         if (next_digits) next_digits[at] = static_cast<uint8_t>(digit_of(k, next_shift));
     }
     if (kFirst && bad)
@@ -442,31 +471,47 @@ __global__ void set_word_kernel(int64_t* __restrict__ word, int64_t v) {
     if (threadIdx.x == 0) *word = v;
 }
 
-// key[s] = keys[i], prev[s] = keys[i - 1] for i = base + s * kBlock, all
-// loads issued before any is used (indices clamped into [0, total); the
-// caller ignores slots with i >= total, and prev of i = 0).
-template <typename KeyT>
+// key[s] = keys[i], prev[s] = keys[i - 1] for i = chunk + s * kBlock + t (the
+// block's kChunk entries from `chunk`), the keys' loads all issued before any
+// is used (indices clamped into [0, total); the caller ignores slots with
+// i >= total, and prev of i = 0).  prev is thread t - 1's key of the slot: a
+// lane shuffle inside a wavefront, `edge` (kItems x kWaves words of LDS) for
+// lane 0, and one more load for the chunk's first entry.  Contains a barrier.
+template <typename Store, typename KeyT = typename Store::K>
 __device__ __forceinline__ void load_pairs(KeyT (&key)[kItems], KeyT (&prev)[kItems],
-                                           const KeyT* __restrict__ keys, int64_t base,
-                                           int64_t total) {
+                                           const Store& keys, int64_t chunk, int64_t total,
+                                           KeyT (*edge)[kWaves]) {
+    const int t = threadIdx.x, w = t / kWave, lane = t % kWave;
 #pragma unroll
     for (int s = 0; s < kItems; ++s) {
-        int64_t i = base + s * kBlock;
-        i = i < total ? i : total - 1;
-        key[s] = keys[i];
-        prev[s] = keys[i > 0 ? i - 1 : 0];
+        const int64_t i = chunk + s * kBlock + t;
+        key[s] = keys.load(i < total ? i : total - 1);
+    }
+    const int64_t i0 = chunk > 0 ? (chunk - 1 < total ? chunk - 1 : total - 1) : 0;
+    const KeyT first_prev = keys.load(i0);
+#pragma unroll
+    for (int s = 0; s < kItems; ++s) {
+        prev[s] = __shfl_up(key[s], 1, kWave);
+        if (lane == kWave - 1) edge[s][w] = key[s];
+    }
+    __syncthreads();
+    if (lane == 0) {
+#pragma unroll
+        for (int s = 0; s < kItems; ++s)
+            prev[s] = w > 0 ? edge[s][w - 1] : s > 0 ? edge[s - 1][kWaves - 1] : first_prev;
     }
 }
 
 // counts[chunk] <- kept entries of chunk (kChunk entries).
-template <typename KeyT>
-__global__ __launch_bounds__(kBlock) void dedup_count_kernel(const KeyT* __restrict__ keys,
+template <typename Store>
+__global__ __launch_bounds__(kBlock) void dedup_count_kernel(Store keys,
                                                              int64_t total,
                                                              int64_t* __restrict__ counts) {
     __shared__ int64_t wtot[kWaves];
+    __shared__ typename Store::K edge[kItems][kWaves];
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk + threadIdx.x;
-    KeyT key[kItems], prev[kItems];
-    load_pairs(key, prev, keys, base, total);
+    typename Store::K key[kItems], prev[kItems];
+    load_pairs(key, prev, keys, static_cast<int64_t>(blockIdx.x) * kChunk, total, edge);
     int64_t c = 0;
 #pragma unroll
     for (int s = 0; s < kItems; ++s) {
@@ -482,18 +527,20 @@ __global__ __launch_bounds__(kBlock) void dedup_count_kernel(const KeyT* __restr
 // rowptr[row] = p at the first entry of each row present.  kDedup: the
 // chunk's first p comes from chunk_base (the exclusive scan of
 // dedup_count_kernel's counts).
-template <typename KeyT, bool kDedup>
-__global__ __launch_bounds__(kBlock) void csr_emit_kernel(const KeyT* __restrict__ keys,
+template <typename Store, bool kDedup>
+__global__ __launch_bounds__(kBlock) void csr_emit_kernel(Store keys,
                                                           int64_t total, int cbits,
                                                           const int64_t* __restrict__ chunk_base,
                                                           int64_t* __restrict__ rowptr,
                                                           int64_t* __restrict__ col_out) {
+    using KeyT = typename Store::K;
     __shared__ int32_t wkept[kItems][kWaves];
     const int t = threadIdx.x, w = t / kWave;
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
     const KeyT cmask = cbits == 0 ? KeyT(0) : (~KeyT(0) >> (8 * sizeof(KeyT) - cbits));
+    __shared__ KeyT edge[kItems][kWaves];
     KeyT key[kItems], before[kItems];
-    load_pairs(key, before, keys, base + t, total);
+    load_pairs(key, before, keys, base, total, edge);
     uint32_t keep_bits = 0, start_bits = 0;
 #pragma unroll
     for (int s = 0; s < kItems; ++s) {
@@ -552,10 +599,12 @@ struct CsrLayout {
     int64_t total = 0;  // entries to sort
     int cbits = 0;
     int passes = 0;
-    bool wide = false;  // 64-bit keys
+    int key_bytes = 4;   // 4, 6 (Keys48) or 8
     int64_t tiles = 0;   // radix tiles of kSortTile keys
     int64_t chunks = 0;  // finish chunks of kChunk keys
-    size_t keys0 = 0, keys1 = 0, digits = 0, hist = 0, sums = 0, bytes = 0;
+    size_t keys[2] = {0, 0};  // the two key arrays (Keys48: low halves)
+    size_t keys_hi[2] = {0, 0};  // Keys48: the high bits
+    size_t digits = 0, hist = 0, sums = 0, bytes = 0;
 };
 
 CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
@@ -563,11 +612,11 @@ CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
     l.total = (flags & MLXC_CSR_SYMMETRIZE) ? 2 * num_edges : num_edges;
     l.cbits = bits_for(num_nodes);
     const int key_bits = 2 * l.cbits;
-    l.wide = key_bits > 32;
+    l.key_bytes = key_bits <= 32 ? 4 : key_bits <= 48 ? 6 : 8;
     l.passes = key_bits == 0 ? 1 : (key_bits + kRadixBits - 1) / kRadixBits;
     l.tiles = (l.total + kSortTile - 1) / kSortTile;
     l.chunks = (l.total + kChunk - 1) / kChunk;
-    const size_t ksz = l.wide ? 8 : 4;
+    const size_t n = static_cast<size_t>(l.total);
     // the digit counts, and after the last pass the finish chunks' counts
     int64_t hist_n = kRadix * l.tiles;
     if (l.chunks > hist_n) hist_n = l.chunks;
@@ -575,10 +624,14 @@ CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
     if (num_nodes + 1 > scan_n) scan_n = num_nodes + 1;
     const int64_t chunks = (scan_n + kChunk - 1) / kChunk;
     size_t at = round256(MLXC_WORK_WORDS * sizeof(int64_t));
-    l.keys0 = at;
-    at += round256(static_cast<size_t>(l.total) * ksz);
-    l.keys1 = at;
-    at += round256(static_cast<size_t>(l.total) * ksz);
+    for (int b = 0; b < 2; ++b) {
+        l.keys[b] = at;
+        at += round256(n * (l.key_bytes == 6 ? 4 : l.key_bytes));
+        if (l.key_bytes == 6) {
+            l.keys_hi[b] = at;
+            at += round256(n * 2);
+        }
+    }
     l.digits = at;  // the next pass's digit of each key, padded to whole tiles
     at += round256(static_cast<size_t>(l.tiles) * kSortTile);
     l.hist = at;
@@ -611,34 +664,45 @@ int fill_words(int64_t* out, int64_t n, const int64_t* value, hipStream_t s) {
     return MLXC_OK;
 }
 
-template <typename KeyT>
+Keys32 key_store(char* ws, const CsrLayout& l, int b, Keys32) {
+    return Keys32{reinterpret_cast<uint32_t*>(ws + l.keys[b])};
+}
+Keys48 key_store(char* ws, const CsrLayout& l, int b, Keys48) {
+    return Keys48{reinterpret_cast<uint32_t*>(ws + l.keys[b]),
+                  reinterpret_cast<uint16_t*>(ws + l.keys_hi[b])};
+}
+Keys64 key_store(char* ws, const CsrLayout& l, int b, Keys64) {
+    return Keys64{reinterpret_cast<uint64_t*>(ws + l.keys[b])};
+}
+
+template <typename Store>
 int csr_build_typed(const EdgeSrc& src, const CsrLayout& l, int32_t flags, int64_t* rowptr,
                     int64_t* col_out, char* ws, hipStream_t s) {
     int64_t* work = reinterpret_cast<int64_t*>(ws);
-    KeyT* buf[2] = {reinterpret_cast<KeyT*>(ws + l.keys0), reinterpret_cast<KeyT*>(ws + l.keys1)};
+    const Store buf[2] = {key_store(ws, l, 0, Store{}), key_store(ws, l, 1, Store{})};
     int64_t* hist = reinterpret_cast<int64_t*>(ws + l.hist);
     int64_t* sums = reinterpret_cast<int64_t*>(ws + l.sums);
     uint8_t* digits = reinterpret_cast<uint8_t*>(ws + l.digits);
-    const KeyT* in = nullptr;
+    Store in{};
     for (int p = 0; p < l.passes; ++p) {
         const int shift = p * kRadixBits;
-        KeyT* out = buf[p & 1];
+        const Store out = buf[p & 1];
         uint8_t* next_digits = p + 1 < l.passes ? digits : nullptr;
         if (p == 0)
-            hipLaunchKernelGGL((radix_hist_kernel<KeyT, true>), dim3(l.tiles), dim3(kSortThreads), 0, s,
+            hipLaunchKernelGGL((radix_hist_kernel<Store, true>), dim3(l.tiles), dim3(kSortThreads), 0, s,
                                src, digits, shift, l.total, l.tiles, hist, work);
         else
-            hipLaunchKernelGGL((radix_hist_kernel<KeyT, false>), dim3(l.tiles), dim3(kSortThreads), 0, s,
+            hipLaunchKernelGGL((radix_hist_kernel<Store, false>), dim3(l.tiles), dim3(kSortThreads), 0, s,
                                src, digits, shift, l.total, l.tiles, hist, work);
         MLXC_HIP_TRY(hipGetLastError());
         if (int rc = device_scan<kOpSum, false, true>(hist, kRadix * l.tiles, sums, nullptr, s))
             return rc;
         if (p == 0)
-            hipLaunchKernelGGL((radix_scatter_kernel<KeyT, true>), dim3(l.tiles), dim3(kSortThreads), 0,
+            hipLaunchKernelGGL((radix_scatter_kernel<Store, true>), dim3(l.tiles), dim3(kSortThreads), 0,
                                s, src, in, out, shift, l.total, l.tiles, hist, work, next_digits,
                                shift + kRadixBits);
         else
-            hipLaunchKernelGGL((radix_scatter_kernel<KeyT, false>), dim3(l.tiles), dim3(kSortThreads), 0,
+            hipLaunchKernelGGL((radix_scatter_kernel<Store, false>), dim3(l.tiles), dim3(kSortThreads), 0,
                                s, src, in, out, shift, l.total, l.tiles, hist, work, next_digits,
                                shift + kRadixBits);
         MLXC_HIP_TRY(hipGetLastError());
@@ -650,7 +714,7 @@ int csr_build_typed(const EdgeSrc& src, const CsrLayout& l, int32_t flags, int64
     const int64_t chunks = l.chunks;
     int64_t* chunk_base = hist;
     if (flags & MLXC_CSR_DEDUP) {
-        hipLaunchKernelGGL((dedup_count_kernel<KeyT>), dim3(chunks), dim3(kBlock), 0, s, in,
+        hipLaunchKernelGGL((dedup_count_kernel<Store>), dim3(chunks), dim3(kBlock), 0, s, in,
                            l.total, chunk_base);
         MLXC_HIP_TRY(hipGetLastError());
         if (int rc = device_scan<kOpSum, false, true>(chunk_base, chunks, sums, work + 1, s))
@@ -661,10 +725,10 @@ int csr_build_typed(const EdgeSrc& src, const CsrLayout& l, int32_t flags, int64
     MLXC_HIP_TRY(hipGetLastError());
     if (int rc = fill_words(rowptr, src.num_nodes + 1, work + 1, s)) return rc;
     if (flags & MLXC_CSR_DEDUP)
-        hipLaunchKernelGGL((csr_emit_kernel<KeyT, true>), dim3(chunks), dim3(kBlock), 0, s, in,
+        hipLaunchKernelGGL((csr_emit_kernel<Store, true>), dim3(chunks), dim3(kBlock), 0, s, in,
                            l.total, l.cbits, chunk_base, rowptr, col_out);
     else
-        hipLaunchKernelGGL((csr_emit_kernel<KeyT, false>), dim3(chunks), dim3(kBlock), 0, s, in,
+        hipLaunchKernelGGL((csr_emit_kernel<Store, false>), dim3(chunks), dim3(kBlock), 0, s, in,
                            l.total, l.cbits, chunk_base, rowptr, col_out);
     MLXC_HIP_TRY(hipGetLastError());
     return device_scan<kOpMin, true, false>(rowptr, src.num_nodes + 1, sums, nullptr, s);
@@ -688,8 +752,9 @@ int launch_csr_build(const int64_t* row, const int64_t* col, int64_t num_edges, 
     if (int rc = launch_zero_work(work, stream)) return rc;
     if (l.total == 0) return fill_words(rowptr, num_nodes + 1, work + 1, stream);
     const EdgeSrc src{row, col, num_edges, num_nodes, l.cbits};
-    return l.wide ? csr_build_typed<uint64_t>(src, l, flags, rowptr, col_out, ws, stream)
-                  : csr_build_typed<uint32_t>(src, l, flags, rowptr, col_out, ws, stream);
+    if (l.key_bytes == 4) return csr_build_typed<Keys32>(src, l, flags, rowptr, col_out, ws, stream);
+    if (l.key_bytes == 6) return csr_build_typed<Keys48>(src, l, flags, rowptr, col_out, ws, stream);
+    return csr_build_typed<Keys64>(src, l, flags, rowptr, col_out, ws, stream);
 }
 
 }  // namespace mlxc

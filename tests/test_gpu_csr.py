@@ -48,6 +48,22 @@ def test_random_lists(E, V, cuda):
     assert_parity(row, col, V, cuda, symmetrize=True, dedup=True)
 
 
+def test_64_bit_keys(cuda):
+    """More than 2^24 nodes: keys wider than 48 bits, stored whole (smaller
+    graphs split theirs into 32 + 16 bits).  Ids near both ends of the range,
+    a hub row and repeated pairs."""
+    rng = np.random.default_rng(64)
+    V, E = (1 << 25) + 7, 150_003
+    row, col = rng.integers(0, V, E), rng.integers(0, V, E)
+    row[:20_000] = V - 1
+    col[20_000:24_000] = rng.integers(0, 3, 4000)
+    col[24_000:26_000] = V - 2
+    row[30_000:32_000] = row[40_000:42_000]
+    col[30_000:32_000] = col[40_000:42_000]
+    for sym, dedup in ((False, False), (True, True)):
+        assert_parity(row, col, V, cuda, sym, dedup)
+
+
 @pytest.mark.parametrize("sym,dedup", [(False, False), (False, True), (True, False),
                                        (True, True)])
 def test_skewed_with_duplicates(sym, dedup, cuda):
