@@ -360,15 +360,22 @@ def bench_csr(args, np, torch, mc, synth, dev):
     del prp, pc
 
     # Bytes: any CSR build reads the two id arrays and writes col and rowptr
-    # once.  The radix passes move more; their stream volume is reported too.
+    # once.  The radix passes move more; their stream volume is reported too:
+    # keys of k bytes (4, 6 as 32 + 16 bits, or 8), the first histogram reads
+    # the col ids (both ids below 8 col bits), each scatter but the last
+    # writes a digit byte per key that the next histogram reads, the finish
+    # reads the keys twice (dedup count, emit), and every pass writes, scans
+    # and reads 256 digit counts per 8192-key tile.
     algo_bytes = 16 * E + 8 * kept + 8 * (V + 1)
     cbits = (V - 1).bit_length()
-    k = 8 if 2 * cbits > 32 else 4
+    k = 4 if 2 * cbits <= 32 else 6 if 2 * cbits <= 48 else 8
     passes = max(1, -(-2 * cbits // 8))
-    tiles = -(-total // 4096)
-    pass_bytes = (total * (16 + 16 + k) + (passes - 1) * total * 3 * k
-                  + total * 2 * k + 8 * kept + 5 * 8 * (V + 1)
-                  + passes * 3 * 8 * 256 * tiles)
+    tiles = -(-total // 8192)
+    first_hist = 8 if cbits >= 8 else 16
+    pass_bytes = (total * (first_hist + 16 + k + (1 if passes > 1 else 0))
+                  + (passes - 1) * total * (1 + 2 * k) + max(passes - 2, 0) * total
+                  + total * 2 * k + 8 * kept + 4 * 8 * (V + 1)
+                  + passes * 4 * 8 * 256 * tiles)
     achieved = algo_bytes / (kernel_ms / 1e3) / 1e9
     traffic = traffic_from_profile(f"csr_build_{args.config}")
     roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
