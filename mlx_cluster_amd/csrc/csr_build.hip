@@ -6,7 +6,8 @@
 //
 // Method: an LSD radix sort of packed keys (row << cbits | col), cbits =
 // bits(num_nodes - 1), sorting only the 2 * cbits bits that can be non-zero,
-// 8 bits per pass.  Keys are 32-bit when they fit (num_nodes <= 65536).  Each
+// 8 bits per pass.  Keys are stored in 4 bytes when they fit (num_nodes <=
+// 65536), in 6 (a 32-bit and a 16-bit array) up to 48 bits, else in 8.  Each
 // pass is three launches and needs no inter-block waiting:
 //   radix_hist_kernel     per 8192-key tile, a 256-digit histogram, written
 //                         digit-major (hist[d * tiles + tile]);
