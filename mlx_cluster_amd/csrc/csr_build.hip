@@ -90,8 +90,6 @@ struct Keys64 {
     __device__ __forceinline__ void store(int64_t i, K k) const { p[i] = k; }
 };
 
-// Key of entry i of the (optionally symmetrized) list: i < num_edges is
-// (row[i], col[i]); i >= num_edges the reversed pair of entry i - num_edges.
 // An id outside [0, num_nodes) sets `bad` and becomes 0 (each id on its own),
 // so that every index derived from a key stays in bounds.
 __device__ __forceinline__ int64_t clamp_id(int64_t v, int64_t num_nodes, bool& bad) {
@@ -112,7 +110,9 @@ __device__ __forceinline__ const int64_t* src_col_ptr(const EdgeSrc& s, int64_t 
 // How a pass reads entry i: the previous pass's keys, or (first pass) the
 // caller's arrays, both ids or the col id alone when the pass's digits lie in
 // the col field (row ids are then checked by the first scatter pass, which
-// reads both).
+// reads both).  Entry i of the (optionally symmetrized) list is (row[i],
+// col[i]) for i < num_edges, else the reversed pair of entry i - num_edges;
+// its key is row << cbits | col.
 enum class Src { kKeys, kBoth, kCol };
 
 template <typename Store, Src kSrc, typename KeyT = typename Store::K>
