@@ -361,14 +361,14 @@ def bench_csr(args, np, torch, mc, synth, dev):
 
     # Bytes: any CSR build reads the two id arrays and writes col and rowptr
     # once.  The radix passes move more; their stream volume is reported too:
-    # keys of k bytes (4, 6 as 32 + 16 bits, or 8), the first histogram reads
+    # keys of k bytes (4, 5 or 6 as 32 + 8 or 16 bits, or 8), the first histogram reads
     # the col ids (both ids below 8 col bits), each scatter but the last
     # writes a digit byte per key that the next histogram reads, the finish
     # reads the keys twice (dedup count, emit), and every pass writes, scans
     # and reads 256 digit counts per 8192-key tile.
     algo_bytes = 16 * E + 8 * kept + 8 * (V + 1)
     cbits = (V - 1).bit_length()
-    k = 4 if 2 * cbits <= 32 else 6 if 2 * cbits <= 48 else 8
+    k = 4 if 2 * cbits <= 32 else 5 if 2 * cbits <= 40 else 6 if 2 * cbits <= 48 else 8
     passes = max(1, -(-2 * cbits // 8))
     tiles = -(-total // 8192)
     first_hist = 8 if cbits >= 8 else 16

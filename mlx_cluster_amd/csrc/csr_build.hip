@@ -7,8 +7,8 @@
 // Method: an LSD radix sort of packed keys (row << cbits | col), cbits =
 // bits(num_nodes - 1), sorting only the 2 * cbits bits that can be non-zero,
 // 8 bits per pass.  Keys are stored in 4 bytes when they fit (num_nodes <=
-// 65536), in 6 (a 32-bit and a 16-bit array) up to 48 bits, else in 8.  Each
-// pass is three launches and needs no inter-block waiting:
+// 65536), in 5 or 6 (a 32-bit and an 8- or 16-bit array) up to 40 or 48 bits,
+// else in 8.  Each pass is three launches and needs no inter-block waiting:
 //   radix_hist_kernel     per 8192-key tile, a 256-digit histogram, written
 //                         digit-major (hist[d * tiles + tile]);
 //   scan_*                one exclusive scan of that array, which turns it
@@ -60,16 +60,28 @@ struct EdgeSrc {
     int cbits;          // bits of the col field of a key
 };
 
-// Key arrays.  Keys of up to 32 bits are stored whole; keys of 33 to 48 bits
-// as a 32-bit array of their low halves and a 16-bit array of their high
-// bits (6 bytes a key instead of 8, so every pass over them moves a quarter
-// fewer bytes); wider keys as 64-bit words.  A store is a pair of device
-// pointers passed by value; K is the key's type in registers.
+// Key arrays.  Keys of up to 32 bits are stored whole; keys of 33 to 40 (48)
+// bits as a 32-bit array of their low halves and an 8-bit (16-bit) array of
+// their high bits, 5 (6) bytes a key instead of 8, so every pass over them
+// moves that many fewer bytes; wider keys as 64-bit words.  A store is a set
+// of device pointers passed by value; K is the key's type in registers.
 struct Keys32 {
     using K = uint32_t;
     uint32_t* p;
     __device__ __forceinline__ K load(int64_t i) const { return p[i]; }
     __device__ __forceinline__ void store(int64_t i, K k) const { p[i] = k; }
+};
+struct Keys40 {
+    using K = uint64_t;
+    uint32_t* lo;
+    uint8_t* hi;
+    __device__ __forceinline__ K load(int64_t i) const {
+        return (static_cast<uint64_t>(hi[i]) << 32) | lo[i];
+    }
+    __device__ __forceinline__ void store(int64_t i, K k) const {
+        lo[i] = static_cast<uint32_t>(k);
+        hi[i] = static_cast<uint8_t>(k >> 32);
+    }
 };
 struct Keys48 {
     using K = uint64_t;
@@ -600,11 +612,11 @@ struct CsrLayout {
     int64_t total = 0;  // entries to sort
     int cbits = 0;
     int passes = 0;
-    int key_bytes = 4;   // 4, 6 (Keys48) or 8
+    int key_bytes = 4;   // 4, 5 (Keys40), 6 (Keys48) or 8
     int64_t tiles = 0;   // radix tiles of kSortTile keys
     int64_t chunks = 0;  // finish chunks of kChunk keys
-    size_t keys[2] = {0, 0};  // the two key arrays (Keys48: low halves)
-    size_t keys_hi[2] = {0, 0};  // Keys48: the high bits
+    size_t keys[2] = {0, 0};  // the two key arrays (Keys40 / Keys48: low halves)
+    size_t keys_hi[2] = {0, 0};  // Keys40 / Keys48: the high bits
     size_t digits = 0, hist = 0, sums = 0, bytes = 0;
 };
 
@@ -613,7 +625,7 @@ CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
     l.total = (flags & MLXC_CSR_SYMMETRIZE) ? 2 * num_edges : num_edges;
     l.cbits = bits_for(num_nodes);
     const int key_bits = 2 * l.cbits;
-    l.key_bytes = key_bits <= 32 ? 4 : key_bits <= 48 ? 6 : 8;
+    l.key_bytes = key_bits <= 32 ? 4 : key_bits <= 40 ? 5 : key_bits <= 48 ? 6 : 8;
     l.passes = key_bits == 0 ? 1 : (key_bits + kRadixBits - 1) / kRadixBits;
     l.tiles = (l.total + kSortTile - 1) / kSortTile;
     l.chunks = (l.total + kChunk - 1) / kChunk;
@@ -626,11 +638,12 @@ CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
     const int64_t chunks = (scan_n + kChunk - 1) / kChunk;
     size_t at = round256(MLXC_WORK_WORDS * sizeof(int64_t));
     for (int b = 0; b < 2; ++b) {
+        const bool split = l.key_bytes == 5 || l.key_bytes == 6;
         l.keys[b] = at;
-        at += round256(n * (l.key_bytes == 6 ? 4 : l.key_bytes));
-        if (l.key_bytes == 6) {
+        at += round256(n * (split ? 4 : l.key_bytes));
+        if (split) {
             l.keys_hi[b] = at;
-            at += round256(n * 2);
+            at += round256(n * (l.key_bytes - 4));
         }
     }
     l.digits = at;  // the next pass's digit of each key, padded to whole tiles
@@ -667,6 +680,10 @@ int fill_words(int64_t* out, int64_t n, const int64_t* value, hipStream_t s) {
 
 Keys32 key_store(char* ws, const CsrLayout& l, int b, Keys32) {
     return Keys32{reinterpret_cast<uint32_t*>(ws + l.keys[b])};
+}
+Keys40 key_store(char* ws, const CsrLayout& l, int b, Keys40) {
+    return Keys40{reinterpret_cast<uint32_t*>(ws + l.keys[b]),
+                  reinterpret_cast<uint8_t*>(ws + l.keys_hi[b])};
 }
 Keys48 key_store(char* ws, const CsrLayout& l, int b, Keys48) {
     return Keys48{reinterpret_cast<uint32_t*>(ws + l.keys[b]),
@@ -754,6 +771,7 @@ int launch_csr_build(const int64_t* row, const int64_t* col, int64_t num_edges, 
     if (l.total == 0) return fill_words(rowptr, num_nodes + 1, work + 1, stream);
     const EdgeSrc src{row, col, num_edges, num_nodes, l.cbits};
     if (l.key_bytes == 4) return csr_build_typed<Keys32>(src, l, flags, rowptr, col_out, ws, stream);
+    if (l.key_bytes == 5) return csr_build_typed<Keys40>(src, l, flags, rowptr, col_out, ws, stream);
     if (l.key_bytes == 6) return csr_build_typed<Keys48>(src, l, flags, rowptr, col_out, ws, stream);
     return csr_build_typed<Keys64>(src, l, flags, rowptr, col_out, ws, stream);
 }

@@ -101,14 +101,16 @@ def test_abi_argument_checks():
 
 def test_workspace_bytes():
     lib = _lib.load()
-    # keys of 4 bytes up to 65536 nodes, 6 up to 2^24, 8 above; two key
-    # arrays each, plus a digit byte per entry
+    # keys of 4 bytes up to 65536 nodes, 5 up to 2^20, 6 up to 2^24, 8 above;
+    # two key arrays each, plus a digit byte per entry
     E = 1 << 20
     small = lib.mlxc_csr_build_workspace_bytes(65536, E, 0)
-    mid = lib.mlxc_csr_build_workspace_bytes(65537, E, 0)
+    k5 = lib.mlxc_csr_build_workspace_bytes(65537, E, 0)
+    k6 = lib.mlxc_csr_build_workspace_bytes((1 << 20) + 1, E, 0)
     wide = lib.mlxc_csr_build_workspace_bytes((1 << 24) + 1, E, 0)
-    assert small >= (2 * 4 + 1) * E and mid >= (2 * 6 + 1) * E and wide >= (2 * 8 + 1) * E
-    assert mid - small >= 2 * 2 * E and wide - mid >= 2 * 2 * E
+    assert small >= (2 * 4 + 1) * E and k5 >= (2 * 5 + 1) * E
+    assert k6 >= (2 * 6 + 1) * E and wide >= (2 * 8 + 1) * E
+    assert k5 - small >= 2 * E and k6 - k5 >= 2 * E and wide - k6 >= 2 * 2 * E
     sym = lib.mlxc_csr_build_workspace_bytes(65537, E, _lib.MLXC_CSR_SYMMETRIZE)
-    assert sym >= (2 * 6 + 1) * (2 * E)
+    assert sym >= (2 * 5 + 1) * (2 * E)
     assert lib.mlxc_csr_build_workspace_bytes(-1, 5, 0) == 0
