@@ -24,21 +24,25 @@ constexpr int64_t kQueueChunk = 256;  // walks taken per global atomic
 
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy
 // as 1, 2, 3", SC'11): ten rounds of two 32x32->64 multiplies with a Weyl
-// key schedule.
+// key schedule.  Each product is one v_mad_u64_u32 (both halves at once; a
+// 32-bit multiply is quarter rate, and separate low and high multiplies cost
+// two), and each three-way XOR one v_bitop3_b32 (gfx950; truth table 0x96).
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
+
 __device__ __forceinline__ void philox4x32_10(uint32_t& c0, uint32_t& c1, uint32_t& c2,
                                               uint32_t& c3, uint32_t k0, uint32_t k1) {
 #pragma unroll
     for (int round = 0; round < 10; ++round) {
-        const uint32_t lo0 = 0xD2511F53u * c0;
-        const uint32_t hi0 = __umulhi(0xD2511F53u, c0);
-        const uint32_t lo1 = 0xCD9E8D57u * c2;
-        const uint32_t hi1 = __umulhi(0xCD9E8D57u, c2);
-        const uint32_t n0 = hi1 ^ c1 ^ k0;
-        const uint32_t n2 = hi0 ^ c3 ^ k1;
+        const uint64_t p0 = static_cast<uint64_t>(0xD2511F53u) * c0;
+        const uint64_t p1 = static_cast<uint64_t>(0xCD9E8D57u) * c2;
+        const uint32_t n0 = xor3(static_cast<uint32_t>(p1 >> 32), c1, k0);
+        const uint32_t n2 = xor3(static_cast<uint32_t>(p0 >> 32), c3, k1);
         c0 = n0;
-        c1 = lo1;
+        c1 = static_cast<uint32_t>(p1);
         c2 = n2;
-        c3 = lo0;
+        c3 = static_cast<uint32_t>(p0);
         k0 += 0x9E3779B9u;
         k1 += 0xBB67AE85u;
     }
