@@ -33,8 +33,8 @@ extern "C" {
  * run; after the call has completed, word 0 holds the MLXC_STATUS_* bits of
  * that call (the other words are internal: the walk-queue counter).  A
  * workspace of the size the *_workspace_bytes queries return also holds
- * per-call layouts of the graph and the starts (16-byte records: node, row
- * begin, row degree) that cut the dependent reads per step; with a smaller
+ * per-call layouts of the graph and the starts (8- or 16-byte records: node,
+ * row begin, row degree) that cut the dependent reads per step; with a smaller
  * workspace the kernels read the CSR arrays directly.  For graphs small
  * enough (see the queries), a workspace of exactly the 256-byte header runs
  * the walk with the whole CSR in on-chip memory.  Same results every way. */
@@ -105,9 +105,10 @@ const char* mlxc_last_error(void);
  * call:
  *   256 when num_nodes + 1 + num_edges <= 14336 and the call takes 1 to 2^20
  *     steps (num_walks <= 2^20): the walk runs with rowptr and col in LDS;
- *   256 + 16 * (num_edges + num_walks) when the call takes at least
+ *   256 + R * (num_edges + num_walks) when the call takes at least
  *     4 * num_edges steps, or num_edges <= 32768 * walk_length (per-call edge
- *     records);
+ *     records): R = 8 when the bits of num_nodes - 1 and of num_edges add up
+ *     to at most 48 (node, row begin and degree packed in 64 bits), else 16;
  *   else 256 + 16 * num_walks (start records only);
  *   MLXC_WORK_WORDS * 8 when num_nodes or num_edges is 2^31 or more.
  * No reference counterpart (the reference allocates inside eval,

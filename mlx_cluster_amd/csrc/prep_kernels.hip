@@ -369,24 +369,28 @@ __global__ __launch_bounds__(kBlock) void edge_index_kernel(const int64_t* __res
 
 // The uniform record walk's whole preparation in one launch (a small call
 // is bound by launch latency): the call's status words zeroed, the edge
-// record of every CSR entry, then the start record of every walk.
+// record of every CSR entry, then the start record of every walk, as
+// EdgeRecord or (kPacked) in the 8-byte format fmt.  The start records
+// follow the edge records: init = recs + num_edges.
+template <bool kPacked>
 __global__ __launch_bounds__(kBlock) void record_prep_kernel(const int64_t* __restrict__ rowptr,
                                                              const int64_t* __restrict__ col,
                                                              const int64_t* __restrict__ start,
                                                              int64_t num_nodes, int64_t num_edges,
                                                              int64_t num_walks,
-                                                             EdgeRecord* __restrict__ recs,
-                                                             EdgeRecord* __restrict__ init,
+                                                             void* __restrict__ recs,
+                                                             PackedFormat fmt,
                                                              int64_t* __restrict__ work) {
     if (blockIdx.x == 0 && threadIdx.x < MLXC_WORK_WORDS) work[threadIdx.x] = 0;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
          i < num_edges + num_walks; i += stride) {
-        if (i < num_edges)
-            *reinterpret_cast<int4*>(recs + i) = node_record(rowptr, col[i], num_nodes, num_edges);
+        const int4 r = node_record(rowptr, i < num_edges ? col[i] : start[i - num_edges],
+                                   num_nodes, num_edges);
+        if (kPacked)
+            static_cast<uint64_t*>(recs)[i] = fmt.pack(r.x, r.y, r.z);
         else
-            *reinterpret_cast<int4*>(init + (i - num_edges)) =
-                node_record(rowptr, start[i - num_edges], num_nodes, num_edges);
+            static_cast<int4*>(recs)[i] = r;
     }
 }
 
@@ -601,12 +605,17 @@ int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_no
 }
 
 int launch_record_prep(const int64_t* rowptr, const int64_t* col, const int64_t* start,
-                       int64_t num_nodes, int64_t num_edges, int64_t num_walks, EdgeRecord* recs,
-                       EdgeRecord* init, int64_t* work, hipStream_t stream) {
+                       int64_t num_nodes, int64_t num_edges, int64_t num_walks, void* recs,
+                       const PackedFormat* packed, int64_t* work, hipStream_t stream) {
     int grid = 0;
     if (int rc = stream_grid(num_edges + num_walks, 16, grid)) return rc;
-    hipLaunchKernelGGL(record_prep_kernel, dim3(grid), dim3(kBlock), 0, stream, rowptr, col, start,
-                       num_nodes, num_edges, num_walks, recs, init, work);
+    if (packed)
+        hipLaunchKernelGGL(record_prep_kernel<true>, dim3(grid), dim3(kBlock), 0, stream, rowptr,
+                           col, start, num_nodes, num_edges, num_walks, recs, *packed, work);
+    else
+        hipLaunchKernelGGL(record_prep_kernel<false>, dim3(grid), dim3(kBlock), 0, stream, rowptr,
+                           col, start, num_nodes, num_edges, num_walks, recs, PackedFormat{0, 0, 0},
+                           work);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

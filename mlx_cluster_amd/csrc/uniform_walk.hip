@@ -7,6 +7,8 @@
 // next walk from a per-wavefront queue refilled by one global atomic per
 // kQueueChunk walks, so lanes never idle while walks remain and the kernel's
 // tail is about one walk long.  Grids are the device's resident capacity.
+#include <type_traits>
+
 #include "walk_host.h"
 
 namespace mlxc {
@@ -123,7 +125,8 @@ enum : int {
     kSlotStart = 1,  // reads the start record of walk n (and its first rand block)
     kSlotWalk = 2,   // record walk: reads the record of the chosen edge
     kSlotCol = 3,    // CSR walk: reads col[e] of the chosen edge
-    kSlotRow = 4,    // CSR walk: reads rowptr[v], rowptr[v+1] of the new node
+    kSlotRow = 4,    // CSR walk: reads rowptr[v], rowptr[v+1] of the new node; packed
+                     // record walk: reads rowptr[v+1] of a row too long for its record
     kSlotDone = 5,   // the queue is exhausted
 };
 
@@ -131,19 +134,22 @@ enum : int {
 // e_out, num_nodes and num_edges below 2^31, num_walks * walk_length a
 // multiple of 4 and at least RW).
 //
-// Loop invariant: every live slot issues exactly one dependent 16-byte read
-// per iteration (a start record or an edge record), plus at most one
-// independent rand block, and the wave waits once.  The rand value for a step
+// Loop invariant: every live slot issues exactly one dependent read per
+// iteration (a start record or an edge record; with packed records also the
+// end of a row too long for the degree field), plus at most one independent
+// rand block, and the wave waits once.  The rand value for a step
 // is taken from the window in the iteration before the read it addresses, so
 // a new rand block always travels together with a record read and never costs
 // a round trip of its own.  The whole blocks of output completed in one
 // iteration are stored by the wavefront (ow_drain) right after the next
 // iteration's reads are issued, so they overlap those reads.
-template <int W, int RW, bool kGen, bool kEdges, typename OutT>
+template <int W, int RW, bool kGen, bool kEdges, typename OutT, bool kPacked>
 __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
-                                                                  const EdgeRecord* __restrict__ recs,
-                                                                  const EdgeRecord* __restrict__ init) {
+                                                                  const void* __restrict__ recs,
+                                                                  const void* __restrict__ init,
+                                                                  PackedFormat fmt) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    typedef typename std::conditional<kPacked, uint64_t, i32x4>::type Rec;
     OutT* const nout = static_cast<OutT*>(a.n_out);
     OutT* const eout = static_cast<OutT*>(a.e_out);
     const int64_t L = a.walk_length;
@@ -154,7 +160,11 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
     WaveQueue q{0, 0};
     int phase[W];
     int64_t n[W];
-    int32_t l[W], e[W];        // e: record index read this iteration (kSlotWalk)
+    int32_t l[W];
+    const Rec* rp[W];          // what the slot reads next: a start or edge record, or
+                               // (kSlotRow) the end of a long row; idle slots reread
+                               // their last address
+    int32_t row_begin[W];      // kSlotRow: the begin of that row
     int64_t fr[W];             // rand index whose block the next read brings along
     bool need_block[W];        // ... if set
     LdsWindow<RW> rw[W];
@@ -170,7 +180,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
         phase[s] = kSlotIdle;
         n[s] = 0;
         l[s] = 0;
-        e[s] = 0;
+        rp[s] = static_cast<const Rec*>(init);
         fr[s] = 0;
         need_block[s] = false;
         rw[s].pos = 0;
@@ -180,18 +190,15 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
     }
 
     while (true) {
-        // 1. One record read per live slot (idle slots read init[0], so the
+        // 1. One read per slot (idle slots reread an earlier address, so the
         // load is unconditional and nothing merges with it before the wait in
         // step 3), and the rand blocks due.
         int ph[W];  // phase at issue: only these slots consume in step 3
-        i32x4 rec[W];
+        Rec rec[W];
 #pragma unroll
         for (int s = 0; s < W; ++s) {
             ph[s] = phase[s];
-            const EdgeRecord* p = ph[s] == kSlotStart ? init + n[s]
-                                  : ph[s] == kSlotWalk ? recs + e[s]
-                                                       : init;
-            rec[s] = *reinterpret_cast<const i32x4*>(p);
+            rec[s] = *rp[s];
         }
         RandWindow<RW> blk[W];  // due rand blocks, stored to LDS in step 3
 #pragma unroll
@@ -215,70 +222,97 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                 n[s] = id;
                 l[s] = 0;
                 phase[s] = id < N ? kSlotStart : kSlotDone;
+                if (id < N) rp[s] = static_cast<const Rec*>(init) + id;
                 fr[s] = id * L;  // the first step's uniform
             }
             alive |= phase[s] != kSlotDone;
         }
         if (!__any(alive)) break;  // every slot done: nothing was read above
         wait_vmem();
+        if constexpr (!kPacked) {
 #pragma unroll
-        for (int s = 0; s < W; ++s) keep_vgpr(rec[s].w);
+            for (int s = 0; s < W; ++s) keep_vgpr(rec[s].w);
+        }
 
         // 3. Consume: buffer the node, finish or pick the next edge.
 #pragma unroll
         for (int s = 0; s < W; ++s) {
-            if (ph[s] != kSlotStart && ph[s] != kSlotWalk) {
+            const int64_t e0 = n[s] * L;  // edge output index of the walk's step 0
+            bool pick = false;            // leave the node of row [begin, begin + deg)
+            int32_t begin = 0, deg = 0;
+            if (kPacked && ph[s] == kSlotRow) {  // the end of a long row
+                pick = true;
+                begin = row_begin[s];
+                if constexpr (kPacked) deg = static_cast<int32_t>(static_cast<int64_t>(rec[s]) - begin);
+            } else if (ph[s] != kSlotStart && ph[s] != kSlotWalk) {
                 // a slot that just drew a walk reads its start record and
                 // first rand block next iteration
                 need_block[s] = phase[s] == kSlotStart && L > 0;
-                continue;
-            }
-            const int64_t g0 = n[s] * L1;  // output index of the walk's start node
-            const int64_t g = g0 + l[s] + (ph[s] == kSlotWalk ? 1 : 0);
-            if (need_block[s]) {
-                // the block holding rand[fr]; fr is its entry k
-                const int k = static_cast<int>(fr[s] - rw_base<RW, kGen>(fr[s], rtotal));
-                lw_store(rand_area[s], rw[s], blk[s], k);
-                need_block[s] = false;
-            }
-            const int32_t node = rec[s].x, begin = rec[s].y, deg = rec[s].z;
-            const int64_t e0 = n[s] * L;  // edge output index of the walk's step 0
-            bool fill = false, flush = false;
-            if (ph[s] == kSlotStart) {
-                ow[s].count = 0;
-                ew[s].count = 0;
-            }
-            // a malformed start or col entry, or the malformed row of a node
-            // the walk is to leave: stop (outputs unspecified).  The row of the
-            // node a walk ends at is not read by the reference, nor checked.
-            if (deg == kRecBadNode || (deg < 0 && l[s] + (ph[s] == kSlotWalk ? 1 : 0) < L)) {
-                status |= deg == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
-                ow_fill(ow[s], nout, g, g0 + L, node);
-                // edges of steps 0 .. l are buffered after a pick, none at the start
-                if (kEdges) ow_fill(ew[s], eout, e0 + l[s] + (ph[s] == kSlotWalk ? 1 : 0),
-                                    e0 + L - 1, -1);
-                phase[s] = kSlotIdle;
-                continue;
-            }
-            ow_push(ow[s], nout, g, node);
-            if (ph[s] == kSlotWalk) l[s] += 1;
-            if (l[s] == L) flush = true;
-            else if (deg == 0) fill = true;  // absorbing node: the walk stays
-            if (fill) {
-                ow_fill(ow[s], nout, g + 1, g0 + L, node);
-                if (kEdges) ow_fill(ew[s], eout, e0 + l[s], e0 + L - 1, -1);
-            } else if (flush) {
-                if (ow[s].count) ow_flush(ow[s], nout, g);
-                if (kEdges && ew[s].count) ow_flush(ew[s], eout, e0 + L - 1);
             } else {
-                // step l (0-based) leaves this node with uniform rand[n*L + l]
-                e[s] = static_cast<int32_t>(begin + pick_index(lw_take(rand_area[s], rw[s]), deg));
-                if (kEdges) ow_push(ew[s], eout, e0 + l[s], e[s]);
+                const int64_t g0 = n[s] * L1;  // output index of the walk's start node
+                const int64_t g = g0 + l[s] + (ph[s] == kSlotWalk ? 1 : 0);
+                if (need_block[s]) {
+                    // the block holding rand[fr]; fr is its entry k
+                    const int k = static_cast<int>(fr[s] - rw_base<RW, kGen>(fr[s], rtotal));
+                    lw_store(rand_area[s], rw[s], blk[s], k);
+                    need_block[s] = false;
+                }
+                int32_t node;
+                if constexpr (kPacked) {
+                    fmt.unpack(rec[s], node, begin, deg);
+                } else {
+                    node = rec[s].x;
+                    begin = rec[s].y;
+                    deg = rec[s].z;
+                }
+                if (ph[s] == kSlotStart) {
+                    ow[s].count = 0;
+                    ew[s].count = 0;
+                }
+                // A malformed start or col entry, or the malformed row of a
+                // node the walk is to leave, stops the walk (outputs
+                // unspecified).  The row of the node a walk ends at is not
+                // read by the reference, nor checked.
+                const int32_t la = l[s] + (ph[s] == kSlotWalk ? 1 : 0);  // steps taken
+                status |= (deg == kRecBadNode ? MLXC_STATUS_BAD_NODE : 0u) |
+                          (deg == kRecBadRow && la < L ? MLXC_STATUS_BAD_ROW : 0u);
+                ow_push(ow[s], nout, g, node);
+                l[s] = la;
+                if (la == L) {
+                    if (ow[s].count) ow_flush(ow[s], nout, g);
+                    if (kEdges && ew[s].count) ow_flush(ew[s], eout, e0 + L - 1);
+                    phase[s] = kSlotIdle;
+                } else if (deg <= 0 && deg != kRecLongRow) {
+                    // an absorbing node (the walk stays) or a malformed record
+                    ow_fill(ow[s], nout, g + 1, g0 + L, node);
+                    if (kEdges) ow_fill(ew[s], eout, e0 + la, e0 + L - 1, -1);
+                    phase[s] = kSlotIdle;
+                } else if (kPacked && deg == kRecLongRow) {  // read the row's end first
+                    rp[s] = reinterpret_cast<const Rec*>(a.rowptr + node + 1);
+                    row_begin[s] = begin;
+                    phase[s] = kSlotRow;
+                } else {
+                    pick = true;
+                }
+            }
+            if (pick) {  // step l (0-based) leaves the node with uniform rand[n*L + l]
+                const float r = lw_take(rand_area[s], rw[s]);
+                int64_t idx;
+                if (kPacked && ph[s] != kSlotRow) {
+                    // a degree held in a packed record: the float32 rule's exact
+                    // branch only (the compiler drops the other)
+                    __builtin_assume(deg <= PackedFormat::kMaxInlineDegree);
+                    idx = pick_index(r, deg);
+                } else {
+                    idx = pick_index(r, deg);
+                }
+                const int32_t e = static_cast<int32_t>(begin + idx);
+                if (kEdges) ow_push(ew[s], eout, e0 + l[s], e);
+                rp[s] = static_cast<const Rec*>(recs) + e;
                 need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
                 fr[s] = n[s] * L + l[s] + 1;
                 phase[s] = kSlotWalk;
             }
-            if (fill || flush) phase[s] = kSlotIdle;
         }
     }
     if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
@@ -570,8 +604,12 @@ bool records_pay_off(int64_t num_edges, int64_t num_walks, int32_t walk_length) 
            num_edges <= kSmallGraphEdgesPerStep * walk_length;
 }
 
-size_t record_bytes(int64_t num_edges, int64_t num_walks) {
-    return kRecordOffset + static_cast<size_t>(num_edges + num_walks) * sizeof(EdgeRecord);
+// Edge and start records: 8 bytes each when the graph's ids pack
+// (packed_format), else 16.
+size_t record_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks) {
+    PackedFormat f;
+    const size_t each = packed_format(num_nodes, num_edges, f) ? sizeof(uint64_t) : sizeof(EdgeRecord);
+    return kRecordOffset + static_cast<size_t>(num_edges + num_walks) * each;
 }
 
 size_t init_bytes(int64_t num_walks) {
@@ -586,7 +624,7 @@ UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes, bool gen) {
                             reinterpret_cast<uintptr_t>(a.e_out) % 16 == 0;  // e_out may be null
     if (streams_ok && records_fit(a.num_nodes, a.num_edges)) {
         if (records_pay_off(a.num_edges, a.num_walks, a.walk_length) &&
-            workspace_bytes >= record_bytes(a.num_edges, a.num_walks))
+            workspace_bytes >= record_bytes(a.num_nodes, a.num_edges, a.num_walks))
             return UniformMode::kRecords;
         if (workspace_bytes >= init_bytes(a.num_walks)) return UniformMode::kCsr;
     }
@@ -631,8 +669,9 @@ size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num
         return minimum;
     if (lds_walk_fits(num_nodes, num_edges, num_walks, walk_length))
         return kRecordOffset;  // the LDS walk: its size selects it
-    return records_pay_off(num_edges, num_walks, walk_length) ? record_bytes(num_edges, num_walks)
-                                                              : init_bytes(num_walks);
+    return records_pay_off(num_edges, num_walks, walk_length)
+               ? record_bytes(num_nodes, num_edges, num_walks)
+               : init_bytes(num_walks);
 }
 
 namespace {
@@ -644,15 +683,22 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
     EdgeRecord* recs = reinterpret_cast<EdgeRecord*>(static_cast<char*>(workspace) + kRecordOffset);
     switch (uniform_mode(a, workspace_bytes, kGen)) {
     case UniformMode::kRecords: {
-        EdgeRecord* init = recs + a.num_edges;
+        PackedFormat f;
+        const bool packed = packed_format(a.num_nodes, a.num_edges, f);
         if (int rc = launch_record_prep(a.rowptr, a.col, a.start, a.num_nodes, a.num_edges,
-                                        a.num_walks, recs, init, a.work, stream))
+                                        a.num_walks, recs, packed ? &f : nullptr, a.work, stream))
             return rc;
-        return launch_walk_kernel(uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen, kEdges, OutT>,
-                                  MLXC_REC_SLOTS, MLXC_REC_BLOCKS_PER_CU, a,
-                                  stream,
-                                  static_cast<const EdgeRecord*>(recs),
-                                  static_cast<const EdgeRecord*>(init));
+        if (packed) {
+            const uint64_t* recs8 = reinterpret_cast<const uint64_t*>(recs);
+            return launch_walk_kernel(
+                uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen, kEdges, OutT, true>,
+                MLXC_REC_SLOTS, MLXC_REC_BLOCKS_PER_CU, a, stream,
+                static_cast<const void*>(recs8), static_cast<const void*>(recs8 + a.num_edges), f);
+        }
+        return launch_walk_kernel(
+            uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen, kEdges, OutT, false>,
+            MLXC_REC_SLOTS, MLXC_REC_BLOCKS_PER_CU, a, stream, static_cast<const void*>(recs),
+            static_cast<const void*>(recs + a.num_edges), f);
     }
     case UniformMode::kCsr: {
         EdgeRecord* init = recs;

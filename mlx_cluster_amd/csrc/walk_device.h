@@ -549,6 +549,63 @@ struct __attribute__((aligned(16))) EdgeRecord {
     int32_t deg;    // rowptr[col[e] + 1] - rowptr[col[e]]; < 0 marks a malformed entry
     int32_t pad;
 };
+
+constexpr int32_t kRecBadNode = -1;  // col[e] outside [0, num_nodes)
+constexpr int32_t kRecBadRow = -2;   // row of col[e] outside [0, num_edges] or decreasing
+constexpr int32_t kRecLongRow = -3;  // packed records: a row too long for the degree field
+
+// The uniform walk's edge record packed into 8 bytes, for graphs whose ids
+// leave at least kPackedMinDegreeBits for the degree.  With c the bits of
+// num_nodes - 1, s those of num_edges and d = min(24, 64 - c - s): bits
+// [0, d) hold a degree code, [d, d + s) the row begin and [64 - c, 64) the
+// node.  The code is the degree + 3; codes 2 and 1 mark a bad node and a bad
+// row, and code 0 a row longer than the field holds, whose end the walk then
+// reads from rowptr.  A 128-byte line holds 16 records instead of 8, so twice
+// the share of the graph stays in each XCD's L2 and in the Infinity Cache.
+// A degree the code holds is below 2^24, where the float32 index rule is
+// exact (pick_index).
+constexpr int kPackedMinDegreeBits = 16;
+struct PackedFormat {
+    static constexpr int kMaxDegreeBits = 24;
+    static constexpr int32_t kMaxInlineDegree = (1 << kMaxDegreeBits) - 4;
+    int32_t c;  // node bits, 1 .. 31
+    int32_t s;  // row-begin bits, 1 .. 31
+    int32_t d;  // degree-code bits, kPackedMinDegreeBits .. kMaxDegreeBits
+
+    __host__ __device__ uint64_t pack(int32_t node, int32_t begin, int32_t deg) const {
+        const uint32_t most = (1u << d) - 4;  // the largest degree the code holds
+        const uint32_t code = deg < 0 ? static_cast<uint32_t>(deg + 3)  // kRecBadNode, kRecBadRow
+                              : static_cast<uint32_t>(deg) > most ? 0u   // kRecLongRow
+                                                                  : static_cast<uint32_t>(deg) + 3;
+        return (static_cast<uint64_t>(static_cast<uint32_t>(node) & ((1u << c) - 1)) << (64 - c)) |
+               (static_cast<uint64_t>(static_cast<uint32_t>(begin)) << d) | code;
+    }
+
+    // deg: the degree, or kRecBadNode / kRecBadRow / kRecLongRow.  Five VALU
+    // operations: a shift, two masks, a funnel shift (v_alignbit_b32) and
+    // the subtraction.
+    __device__ __forceinline__ void unpack(uint64_t x, int32_t& node, int32_t& begin,
+                                           int32_t& deg) const {
+        const uint32_t lo = static_cast<uint32_t>(x), hi = static_cast<uint32_t>(x >> 32);
+        node = static_cast<int32_t>(hi >> (32 - c));
+        begin = static_cast<int32_t>(__builtin_amdgcn_alignbit(hi, lo, d) & ((1u << s) - 1));
+        deg = static_cast<int32_t>(lo & ((1u << d) - 1)) - 3;
+    }
+};
+
+// Whether a graph's records pack into 8 bytes, and the field widths.
+inline __host__ bool packed_format(int64_t num_nodes, int64_t num_edges, PackedFormat& f) {
+    auto bits = [](int64_t x) {
+        int b = 0;
+        while (x > 0) { ++b; x >>= 1; }
+        return b;
+    };
+    f.c = num_nodes > 2 ? bits(num_nodes - 1) : 1;
+    f.s = num_edges > 1 ? bits(num_edges) : 1;
+    f.d = 64 - f.c - f.s < PackedFormat::kMaxDegreeBits ? 64 - f.c - f.s
+                                                         : PackedFormat::kMaxDegreeBits;
+    return f.c <= 31 && f.s <= 31 && f.d >= kPackedMinDegreeBits;
+}
 // Search index of the node2vec walk over sorted rows: level 0 is col as
 // int32 (col32); level k >= 1 holds col32[16^k * i] for every i.  Every
 // level is padded to whole blocks of 16 entries (64 bytes).  Built by
@@ -601,8 +658,6 @@ struct StartRecords {
     EdgeRecord* init;
 };
 
-constexpr int32_t kRecBadNode = -1;  // col[e] outside [0, num_nodes)
-constexpr int32_t kRecBadRow = -2;   // row of col[e] outside [0, num_edges] or decreasing
 constexpr size_t kRecordOffset = 256;  // bytes of workspace before the records
 
 // Walks on graphs small enough for LDS (uniform_walk_lds_kernel,

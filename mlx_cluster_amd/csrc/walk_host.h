@@ -68,10 +68,11 @@ inline bool records_fit(int64_t num_nodes, int64_t num_edges) {
 // ---- prep_kernels.hip
 int launch_zero_work(int64_t* d_work, hipStream_t stream);
 // The uniform record walk's preparation in one launch: zeroes the status
-// words, writes the edge records and the start records.
+// words, writes the edge records and, after them, the start records; in the
+// 8-byte format *packed when packed is not null, else as EdgeRecord.
 int launch_record_prep(const int64_t* rowptr, const int64_t* col, const int64_t* start,
-                       int64_t num_nodes, int64_t num_edges, int64_t num_walks, EdgeRecord* recs,
-                       EdgeRecord* init, int64_t* work, hipStream_t stream);
+                       int64_t num_nodes, int64_t num_edges, int64_t num_walks, void* recs,
+                       const PackedFormat* packed, int64_t* work, hipStream_t stream);
 // Edge records and the search index levels (index.count > 0) of the node2vec
 // walk, and in the same pass the start records of `starts` (num_walks 0:
 // none); a non-null check_work also validates the CSR and counts row

@@ -122,21 +122,29 @@ def test_other_entry_points_reject_bad_arguments():
 
 
 def test_workspace_size_query():
+    """Edge and start records take 8 bytes each when node ids, row begins and
+    at least 16 bits of degree pack into 64 bits, else 16; start records
+    alone (the CSR walk) always take 16."""
     q = _lib.load().mlxc_random_walk_workspace_bytes
     E = 10**6                                     # above the small-graph size 32768 * 4
-    assert q(10, E, E, 4) == 256 + 16 * 2 * E     # 4E steps >= 4 * E edges: records
+    assert q(10, E, E, 4) == 256 + 8 * 2 * E      # 4E steps >= 4 * E edges: records
     assert q(10, E, E - 1, 4) == 256 + 16 * (E - 1)  # fewer steps: start records only
-    assert q(10, 32768 * 4, 1, 4) == 256 + 16 * (32768 * 4 + 1)   # small graph: records
+    assert q(10, 32768 * 4, 1, 4) == 256 + 8 * (32768 * 4 + 1)   # small graph: records
     assert q(10, 32768 * 4 + 1, 1, 4) == 256 + 16 * 1
     # graphs whose rowptr and col fit in LDS (V + 1 + E <= 14336 entries), on
     # calls of 1 to 2^20 steps: the LDS walk, selected by a 256-byte workspace
     assert q(10, 100, 1, 4) == 256
     assert q(10, 14336 - 11, 2000, 5) == 256
-    assert q(10, 14336 - 10, 2000, 5) == 256 + 16 * (14336 - 10 + 2000)   # one entry more
+    assert q(10, 14336 - 10, 2000, 5) == 256 + 8 * (14336 - 10 + 2000)   # one entry more
     assert q(10, 100, 2**18, 4) == 256
-    assert q(10, 100, 2**18 + 1, 4) == 256 + 16 * (100 + 2**18 + 1)      # > 2^20 steps
+    assert q(10, 100, 2**18 + 1, 4) == 256 + 8 * (100 + 2**18 + 1)      # > 2^20 steps
     assert q(10, 100, 5, 0) == 256 + 16 * 5              # no step: start records only
     assert q(10, 0, 0, 0) == 256 + 16 * 0
+    # 24 bits of node id + 24 of row begin leave 16 for the degree; 25 do not
+    assert q(1 << 24, (1 << 24) - 1, 1 << 24, 4) == 256 + 8 * ((1 << 24) - 1 + (1 << 24))
+    assert q(1 << 24, 1 << 24, 1 << 24, 4) == 256 + 16 * 2 * (1 << 24)
+    assert q((1 << 24) + 1, (1 << 24) - 1, 1 << 24, 4) == 256 + 16 * ((1 << 24) - 1 + (1 << 24))
+    assert q(2**31 - 1, E, E, 4) == 256 + 16 * 2 * E
     assert q(2**31, 5, 1, 1) == 32
     assert q(5, 2**31, 1, 1) == 32
     assert q(-1, 5, 1, 1) == 32
@@ -159,7 +167,7 @@ def test_noalloc_rejects_calls_beyond_its_scratch():
     text = open(HEADER).read()
     assert "#define MLXC_NOALLOC_SCRATCH_BYTES (64 * 1024 * 1024)" in text
     assert _lib.MLXC_NOALLOC_SCRATCH_BYTES == 64 * 1024 * 1024
-    V, E, N, L = 1 << 22, 1 << 24, 1 << 22, 80  # edge records: 16 * (E + N) bytes
+    V, E, N, L = 1 << 22, 1 << 24, 1 << 22, 80  # edge records: 8 * (E + N) bytes
     assert lib.mlxc_random_walk_workspace_bytes(V, E, N, L) > _lib.MLXC_NOALLOC_SCRATCH_BYTES
     rc = lib.mlxc_random_walk_noalloc(FAKE, V, FAKE, E, FAKE, N, FAKE, L, FAKE, None, 0, None,
                                       None)

@@ -258,6 +258,59 @@ def test_all_kernel_paths_agree(N, L, cuda):
     np.testing.assert_array_equal(e_view.view(N, L).cpu().numpy(), ref_e, err_msg="unaligned e")
 
 
+def _hub_graph(V, hub_degrees, core_entries, seed):
+    """V nodes, most of them isolated: 1000 core nodes spread over the id
+    range with core_entries entries between them (a fifth of them to the
+    hubs), and hubs at the top ids whose rows of the given lengths point back
+    into the core, so that walks keep entering and leaving the hubs."""
+    rng = np.random.default_rng(seed)
+    core = np.arange(1000, dtype=np.int64) * (V // 1000)
+    hubs = V - 1 - np.arange(len(hub_degrees), dtype=np.int64)
+    to_hub = rng.random(core_entries) < 0.2
+    pick = lambda ids, n: ids[rng.integers(0, ids.size, n)]  # noqa: E731
+    row = np.concatenate([np.repeat(hubs, hub_degrees), pick(core, core_entries)])
+    col = np.concatenate([pick(core, int(sum(hub_degrees))),
+                          np.where(to_hub, pick(hubs, core_entries), pick(core, core_entries))])
+    order = np.lexsort((col, row))
+    rowptr = np.zeros(V + 1, np.int64)
+    np.cumsum(np.bincount(row, minlength=V), out=rowptr[1:])
+    return rowptr, col[order], core, hubs
+
+
+@pytest.mark.parametrize("packed", [True, False])
+def test_record_formats_and_long_rows(packed, cuda):
+    """Edge records of 8 bytes (26 bits of node id, 22 of row begin and a
+    16-bit degree field) and of 16 bytes (one more bit of row begin leaves
+    15), on a graph of 2^26 nodes whose hub rows hold 65,532 entries (the
+    longest the 8-byte degree field holds), 65,533 (the shortest it does not)
+    and 100,000: a walk leaving a longer row reads the row's end from rowptr
+    first.  Sampled walks and edge ids against the oracle; generated
+    uniforms and the int32 output give the same walks."""
+    from mlx_cluster_amd import _lib
+    V, L = 1 << 26, 40
+    rowptr, col, core, hubs = _hub_graph(V, [65_532, 65_533, 100_000],
+                                         2_500_000 if packed else 4_300_000, seed=26)
+    E = col.size
+    assert (E < 1 << 22) == packed
+    N = 4 * E // L + 1001                  # >= 4 steps per edge: the record walk
+    start = np.where(np.arange(N) % 4 == 0, hubs[np.arange(N) % 3], core[np.arange(N) % 1000])
+    assert _lib.load().mlxc_random_walk_workspace_bytes(V, E, N, L) == \
+        256 + (8 if packed else 16) * (E + N)
+    rp, cl, st = (torch.from_numpy(a).to(cuda) for a in (rowptr, col, start))
+    rand = mc.philox_uniform((N, L), 31, device=cuda)
+    n, e = mc.random_walk(rp, cl, st, rand, L, return_edges=True)
+    sample = np.random.default_rng(1).choice(N, 3000, replace=False)
+    n_ref, e_ref, status, _ = oracle.uniform_walk(rowptr, col, start[sample],
+                                                  rand.cpu().numpy()[sample], L, with_edges=True)
+    assert status == 0
+    np.testing.assert_array_equal(n.cpu().numpy()[sample], n_ref)
+    np.testing.assert_array_equal(e.cpu().numpy()[sample], e_ref)
+    assert np.isin(n_ref[:, :-1], hubs[1:]).sum() > 1000   # steps leaving the long rows
+    assert torch.equal(mc.random_walk(rp, cl, st, None, L, seed=31), n)
+    n32 = mc.random_walk(rp, cl, st, None, L, seed=31, out_dtype=torch.int32)
+    assert torch.equal(n32.long(), n)
+
+
 @pytest.mark.parametrize("N,L", [(1, 1), (37, 5), (1000, 16), (4096, 23), (30_000, 80)])
 def test_seeded_uniforms_match_rand_tensor(N, L, cuda):
     """rand=None, seed=s generates in the kernel exactly the stream

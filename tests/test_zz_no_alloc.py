@@ -60,13 +60,13 @@ def test_noalloc_equals_workspace_entry_point(cuda):
     equal to mlxc_random_walk's, and the first also to the oracle's."""
     rowptr, col = synth.rmat_csr(14, 120_000, seed=21, device=cuda)
     V = rowptr.numel() - 1
-    # call 1: 200,000 walks x 16 steps (records: N*L >= 4E), 6.4 MB of workspace
+    # call 1: 200,000 walks x 16 steps (records: N*L >= 4E; 8 bytes each), 2.5 MB of workspace
     N, L = 200_000, 16
     start = (torch.arange(N, device=cuda) * 7) % V
     rand = mc.philox_uniform((N, L), 3, device=cuda)
     lib = _lib.load()
     E = col.numel()
-    assert lib.mlxc_random_walk_workspace_bytes(V, E, N, L) == 256 + 16 * (E + N)
+    assert lib.mlxc_random_walk_workspace_bytes(V, E, N, L) == 256 + 8 * (E + N)
     n, e, st = _same(rowptr, col, start, rand, L)
     assert st == 0
     ref, ref_e, rst, _ = oracle.uniform_walk(rowptr.cpu().numpy(), col.cpu().numpy(),
@@ -127,7 +127,7 @@ def test_noalloc_rejects_calls_beyond_the_scratch(cuda):
     """A call whose workspace would exceed MLXC_NOALLOC_SCRATCH_BYTES fails
     on the host with a clear error, before any launch."""
     lib = _lib.load()
-    V, E, N, L = 1 << 22, 1 << 24, 1 << 22, 80  # records: 16 * (E + N) > 64 MiB
+    V, E, N, L = 1 << 22, 1 << 24, 1 << 22, 80  # records: 8 * (E + N) > 64 MiB
     need = lib.mlxc_random_walk_workspace_bytes(V, E, N, L)
     assert need > _lib.MLXC_NOALLOC_SCRATCH_BYTES
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: the size check fails first
