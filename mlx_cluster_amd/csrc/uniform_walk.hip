@@ -366,7 +366,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
 
     while (true) {
         // 1. Reads: a 16-byte start record or rowptr pair (one instruction;
-        // idle slots read init[0]), an 8-byte col entry, and due rand blocks.
+        // idle slots read init[0]), an 8-byte col entry (other slots reread
+        // init[0]: both loads are unconditional), and due rand blocks.
         int ph[W];
         i32x4 row[W];
         int64_t cv[W];
@@ -377,7 +378,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                              : ph[s] == kSlotStart ? reinterpret_cast<const i32x4*>(init + n[s])
                                                    : reinterpret_cast<const i32x4*>(init);
             row[s] = *p;
-            if (ph[s] == kSlotCol) cv[s] = a.col[e[s]];
+            cv[s] = *(ph[s] == kSlotCol ? a.col + e[s] : reinterpret_cast<const int64_t*>(init));
         }
         RandWindow<RW> blk[W];  // due rand blocks, stored to LDS in step 3
 #pragma unroll
@@ -589,6 +590,15 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_lds_kernel(WalkArgs a) {
 #ifndef MLXC_GEN_WINDOW
 #define MLXC_GEN_WINDOW 4
 #endif
+// Uniforms per rand block of the packed record walk on walks of at least
+// kLongWalk steps: a whole 128-byte line per read, where a 64-byte block
+// leaves the line's other half to a later miss.  Configuration 2 (L = 80):
+// 7.43 -> 7.39 ms; on short walks most of a long block goes unused
+// (configuration 4's CSR walk, L = 20: 6.33 -> 6.85 ms).
+#ifndef MLXC_LONG_RAND_WINDOW
+#define MLXC_LONG_RAND_WINDOW 32
+#endif
+constexpr int32_t kLongWalk = 64;
 
 namespace {
 
@@ -689,11 +699,16 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
                                         a.num_walks, recs, packed ? &f : nullptr, a.work, stream))
             return rc;
         if (packed) {
-            const uint64_t* recs8 = reinterpret_cast<const uint64_t*>(recs);
+            const void* recs8 = recs;
+            const void* init8 = reinterpret_cast<const uint64_t*>(recs) + a.num_edges;
+            if (!kGen && a.walk_length >= kLongWalk)
+                return launch_walk_kernel(
+                    uniform_walk_rec_kernel<MLXC_REC_SLOTS, kGen ? RW : MLXC_LONG_RAND_WINDOW,
+                                            kGen, kEdges, OutT, true>,
+                    MLXC_REC_SLOTS, MLXC_REC_BLOCKS_PER_CU, a, stream, recs8, init8, f);
             return launch_walk_kernel(
                 uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen, kEdges, OutT, true>,
-                MLXC_REC_SLOTS, MLXC_REC_BLOCKS_PER_CU, a, stream,
-                static_cast<const void*>(recs8), static_cast<const void*>(recs8 + a.num_edges), f);
+                MLXC_REC_SLOTS, MLXC_REC_BLOCKS_PER_CU, a, stream, recs8, init8, f);
         }
         return launch_walk_kernel(
             uniform_walk_rec_kernel<MLXC_REC_SLOTS, RW, kGen, kEdges, OutT, false>,
