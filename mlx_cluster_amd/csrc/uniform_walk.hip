@@ -651,12 +651,13 @@ UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes, bool gen) {
 // register limit: measured on MI355X at configuration 2, 7.55 ms with 3
 // blocks per CU, 7.61 with 2 or 4, 7.68 with 5 and 7.73 with 6 (the same
 // order for the seeded and the int32-output variants).  The CSR walk runs
-// best at its limit (configuration 4: 6.31 ms at the limit or with 4).
+// best with 4 (configuration 4 on one MI355X: 6.07, 5.97, 6.02 and 6.01 ms
+// with 3, 4, 5 and 6 blocks per CU).
 #ifndef MLXC_REC_BLOCKS_PER_CU
 #define MLXC_REC_BLOCKS_PER_CU 3
 #endif
 #ifndef MLXC_CSR_BLOCKS_PER_CU
-#define MLXC_CSR_BLOCKS_PER_CU 0
+#define MLXC_CSR_BLOCKS_PER_CU 4
 #endif
 
 template <typename Kernel, typename... Extra>
