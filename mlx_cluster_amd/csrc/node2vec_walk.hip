@@ -763,18 +763,28 @@ int dispatch_n2v(const N2VArgs& a, bool edges, hipStream_t stream) {
 }
 
 // Resident blocks per compute unit of the node2vec record walk (0: as many
-// as its registers allow, 6).  Measured on MI355X: configuration 3 13.57 ms
-// with 4, 13.67 with 5 and 13.65 with 6; configuration 5 10.93, 10.97 and
-// 11.02 ms.
+// as its registers allow, 5), per rule: the two rules are different kernels.
+// Measured on MI355X with 4 blocks and at the limit: the reference chain at
+// configuration 3 11.95 and 12.15 ms, with the symmetric hint 11.33 and
+// 11.51, configuration 5 (CSR mode) 8.55 and 8.57; the analytic rule at
+// configuration 5x 18.25 and 17.55 ms, with the symmetric hint 17.31 and
+// 16.61.  The reference-chain walk at configuration 3 spends more of each
+// iteration in VALU work (more waves then contend), the analytic walk at 5x
+// more of it waiting on reads (more waves hide them).
 #ifndef MLXC_N2V_BLOCKS_PER_CU
 #define MLXC_N2V_BLOCKS_PER_CU 4
+#endif
+#ifndef MLXC_N2V_ANALYTIC_BLOCKS_PER_CU
+#define MLXC_N2V_ANALYTIC_BLOCKS_PER_CU 0
 #endif
 
 template <int kRule, bool kEdges, bool kCsr, typename OutT>
 int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
     auto kernel = node2vec_rec_kernel<kRule, kEdges, kCsr, OutT>;
+    constexpr int per_cu = kRule == MLXC_RULE_REF_CHAIN ? MLXC_N2V_BLOCKS_PER_CU
+                                                         : MLXC_N2V_ANALYTIC_BLOCKS_PER_CU;
     int grid = 0;
-    if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid, MLXC_N2V_BLOCKS_PER_CU)) return rc;
+    if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid, per_cu)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
