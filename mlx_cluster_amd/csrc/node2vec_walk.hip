@@ -633,33 +633,33 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
 // other layouts do (block 0 reports it); with MLXC_ROWS_DETECT each block
 // also checks the row order of its copy.
 template <int kRule, bool kEdges, typename OutT>
-__global__ __launch_bounds__(kBlock) void node2vec_lds_kernel(N2VRecArgs a) {
+__global__ __launch_bounds__(kLdsBlock) void node2vec_lds_kernel(N2VRecArgs a) {
     __shared__ int32_t graph[kLdsGraphEntries];
     const int64_t V = a.w.num_nodes, E = a.w.num_edges, N = a.w.num_walks, L = a.w.walk_length;
     int32_t* const rp = graph;          // rowptr, -1 for an entry outside [0, E]
     int32_t* const cl = graph + V + 1;  // col, -1 for a value outside [0, V)
     bool bad_row = false, bad_col = false;
-    for (int64_t i = threadIdx.x; i <= V; i += kBlock) {
+    for (int64_t i = threadIdx.x; i <= V; i += kLdsBlock) {
         const int64_t r = a.w.rowptr[i];
         const bool ok = r >= 0 && r <= E;
         rp[i] = ok ? static_cast<int32_t>(r) : -1;
         bad_row |= !ok || (i == 0 && r != 0) || (i == V && r != E);
     }
-    for (int64_t i = threadIdx.x; i < E; i += kBlock) {
+    for (int64_t i = threadIdx.x; i < E; i += kLdsBlock) {
         const int64_t c = a.w.col[i];
         const bool ok = node_ok(c, V);
         cl[i] = ok ? static_cast<int32_t>(c) : -1;
         bad_col |= !ok;
     }
     __syncthreads();
-    for (int64_t u = threadIdx.x; u < V; u += kBlock) bad_row |= rp[u + 1] < rp[u];
+    for (int64_t u = threadIdx.x; u < V; u += kLdsBlock) bad_row |= rp[u + 1] < rp[u];
     // (both reductions are block-wide barriers every thread reaches)
     const bool any_bad_row = __syncthreads_or(bad_row);
     const bool any_bad_col = __syncthreads_or(bad_col);
     bool sorted = a.rows == MLXC_ROWS_SORTED;
     if (a.rows == MLXC_ROWS_DETECT) {
         bool descent = false;  // inside some well-formed row
-        for (int64_t u = threadIdx.x; u < V; u += kBlock) {
+        for (int64_t u = threadIdx.x; u < V; u += kLdsBlock) {
             const int32_t b = rp[u], end = rp[u + 1];
             if (b < 0 || end < b) continue;
             for (int32_t i = b + 1; i < end; ++i) descent |= cl[i] < cl[i - 1];
@@ -671,8 +671,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_lds_kernel(N2VRecArgs a) {
     uint32_t status = 0;
     if (blockIdx.x == 0 && threadIdx.x == 0)
         status = (any_bad_row ? MLXC_STATUS_BAD_ROW : 0u) | (any_bad_col ? MLXC_STATUS_BAD_NODE : 0u);
-    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; n < N;
-         n += static_cast<int64_t>(gridDim.x) * kBlock) {
+    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kLdsBlock + threadIdx.x; n < N;
+         n += static_cast<int64_t>(gridDim.x) * kLdsBlock) {
         const int64_t s = a.w.start[n];
         OutT* const row = nout + n * (L + 1);
         OutT* const erow = kEdges ? eout + n * L : nullptr;
@@ -998,14 +998,14 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         a.thr2 = float_at_or_above(p.prob2);
         a.key0 = p.key0;
         a.key1 = p.key1;
-        const dim3 grid(static_cast<unsigned>((w.num_walks + kBlock - 1) / kBlock));  // <= 4096
+        const dim3 grid(static_cast<unsigned>((w.num_walks + kLdsBlock - 1) / kLdsBlock));  // <= 1024
         const bool edges = w.e_out != nullptr;
         if (p.rule == MLXC_RULE_REF_CHAIN) {
-            if (edges) hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, true, OutT>), grid, dim3(kBlock), 0, stream, a);
-            else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, false, OutT>), grid, dim3(kBlock), 0, stream, a);
+            if (edges) hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, true, OutT>), grid, dim3(kLdsBlock), 0, stream, a);
+            else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, false, OutT>), grid, dim3(kLdsBlock), 0, stream, a);
         } else {
-            if (edges) hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_NODE2VEC_EXACT, true, OutT>), grid, dim3(kBlock), 0, stream, a);
-            else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_NODE2VEC_EXACT, false, OutT>), grid, dim3(kBlock), 0, stream, a);
+            if (edges) hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_NODE2VEC_EXACT, true, OutT>), grid, dim3(kLdsBlock), 0, stream, a);
+            else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_NODE2VEC_EXACT, false, OutT>), grid, dim3(kLdsBlock), 0, stream, a);
         }
         MLXC_HIP_TRY(hipGetLastError());
         return MLXC_OK;

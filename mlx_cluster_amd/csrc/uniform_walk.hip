@@ -505,16 +505,16 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
 
 
 template <bool kGen, bool kEdges, typename OutT>
-__global__ __launch_bounds__(kBlock) void uniform_walk_lds_kernel(WalkArgs a) {
+__global__ __launch_bounds__(kLdsBlock) void uniform_walk_lds_kernel(WalkArgs a) {
     __shared__ int32_t graph[kLdsGraphEntries];
     const int64_t V = a.num_nodes, E = a.num_edges, N = a.num_walks, L = a.walk_length;
     int32_t* const rp = graph;          // rowptr, -1 for an entry outside [0, E]
     int32_t* const cl = graph + V + 1;  // col, -1 for a value outside [0, V)
-    for (int64_t i = threadIdx.x; i <= V; i += kBlock) {
+    for (int64_t i = threadIdx.x; i <= V; i += kLdsBlock) {
         const int64_t r = a.rowptr[i];
         rp[i] = r >= 0 && r <= E ? static_cast<int32_t>(r) : -1;
     }
-    for (int64_t i = threadIdx.x; i < E; i += kBlock) {
+    for (int64_t i = threadIdx.x; i < E; i += kLdsBlock) {
         const int64_t c = a.col[i];
         cl[i] = node_ok(c, V) ? static_cast<int32_t>(c) : -1;
     }
@@ -522,8 +522,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_lds_kernel(WalkArgs a) {
     OutT* const nout = static_cast<OutT*>(a.n_out);
     OutT* const eout = static_cast<OutT*>(a.e_out);
     uint32_t status = 0;
-    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; n < N;
-         n += static_cast<int64_t>(gridDim.x) * kBlock) {
+    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kLdsBlock + threadIdx.x; n < N;
+         n += static_cast<int64_t>(gridDim.x) * kLdsBlock) {
         const int64_t s = a.start[n];
         OutT* const row = nout + n * (L + 1);
         OutT* const erow = kEdges ? eout + n * L : nullptr;
@@ -728,9 +728,9 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
     }
     case UniformMode::kLds: {
         if (int rc = launch_zero_work(a.work, stream)) return rc;
-        const int64_t blocks = (a.num_walks + kBlock - 1) / kBlock;  // at most 4096
+        const int64_t blocks = (a.num_walks + kLdsBlock - 1) / kLdsBlock;  // at most 1024
         hipLaunchKernelGGL((uniform_walk_lds_kernel<kGen, kEdges, OutT>), dim3(static_cast<int>(blocks)),
-                           dim3(kBlock), 0, stream, a);
+                           dim3(kLdsBlock), 0, stream, a);
         MLXC_HIP_TRY(hipGetLastError());
         return MLXC_OK;
     }
