@@ -20,7 +20,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .walks import _check_stream_arg, _stream_handle, _workspace
+from .walks import _check_stream_arg, _on_device, _stream_handle, _workspace
 
 
 def to_csr(edge_index, num_nodes: Optional[int] = None, *, symmetrize: bool = False,
@@ -83,7 +83,7 @@ def to_csr(edge_index, num_nodes: Optional[int] = None, *, symmetrize: bool = Fa
         if nbytes == 0:
             raise ValueError("to_csr: num_nodes or the edge count is out of range")
         work = _workspace(nbytes, dev)
-        with torch.cuda.device(dev):
+        with _on_device(dev):
             rc = lib.mlxc_csr_build(row.data_ptr() if E else None, col.data_ptr() if E else None,
                                     E, V, flags, rowptr.data_ptr(),
                                     col_out.data_ptr() if total else None, work.data_ptr(),

@@ -22,6 +22,7 @@ fallback from one to the other.
 """
 from __future__ import annotations
 
+import contextlib
 import numbers
 from typing import Optional, Tuple, Union
 
@@ -51,6 +52,15 @@ def _resolve_device(stream, tensors) -> torch.device:
     return torch.device("cuda", torch.cuda.current_device())
 
 
+# torch's current stream of a device as a raw handle, without building a
+# torch.cuda.Stream object (a small call's overhead is mostly the Python layer)
+_current_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
 def _stream_handle(stream, device: torch.device) -> int:
     """hipStream_t for `stream`: None -> torch's current stream on device."""
     _check_stream_arg(stream)
@@ -58,10 +68,21 @@ def _stream_handle(stream, device: torch.device) -> int:
         raise ValueError("this operation runs on the GPU only; stream='cpu' is for "
                          "random_walk and rejection_sampling")
     if stream is None:
+        if _current_raw_stream is not None:
+            return _current_raw_stream(_device_index(device))
         return torch.cuda.current_stream(device).cuda_stream
     if isinstance(stream, torch.cuda.Stream):
         return stream.cuda_stream
     return torch.cuda.current_stream(torch.device(stream)).cuda_stream
+
+
+def _on_device(device: torch.device):
+    """The library's calls query and launch on the current device: make it
+    `device` (a no-op context when it already is)."""
+    index = _device_index(device)
+    if index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(index)
 
 
 def _as_tensor(x: TensorLike, dtype: torch.dtype, name: str) -> torch.Tensor:
@@ -249,7 +270,7 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     graph = (_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N)
     outs = (_ptr(n_out), _ptr(e_out) if return_edges else None, otype, work.data_ptr(),
             work.numel() * 8, handle)
-    with torch.cuda.device(device):
+    with _on_device(device):
         if rand is None:
             rc = lib.mlxc_random_walk_seeded(*graph, L, seed, *outs)
         else:
@@ -273,7 +294,7 @@ def csr_check(rowptr: TensorLike, col: TensorLike, *, stream=None) -> int:
     rowptr, col = _on(rowptr, device), _on(col, device)
     work = _workspace(_lib.MLXC_WORK_WORDS * 8, device)
     flags = _lib.ctypes.c_int32(0)
-    with torch.cuda.device(device):
+    with _on_device(device):
         rc = _lib.load().mlxc_csr_check(_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(),
                                         work.data_ptr(), work.numel() * 8,
                                         _lib.ctypes.addressof(flags), handle)
@@ -358,7 +379,7 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     lib = _lib.load()
     work = _workspace(lib.mlxc_rejection_sampling_workspace_bytes(
         rowptr.numel() - 1, col.numel(), N, L, float(p), float(q), _RULES[rule]), device)
-    with torch.cuda.device(device):
+    with _on_device(device):
         rc = lib.mlxc_rejection_sampling(
             _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,
             p, q, seed, _RULES[rule], rows, _ptr(n_out),
@@ -384,7 +405,7 @@ def philox_uniform(shape, seed: int, *, device=None, stream=None) -> torch.Tenso
     dev = torch.device(device) if device is not None else _resolve_device(stream, ())
     handle = _stream_handle(stream, dev)
     out = torch.empty(tuple(shape), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         rc = _lib.load().mlxc_philox_uniform(_ptr(out), out.numel(), int(seed) & (2**64 - 1), handle)
     _lib.check(rc, "philox_uniform")
     return out
