@@ -311,6 +311,31 @@ def test_record_formats_and_long_rows(packed, cuda):
     assert torch.equal(n32.long(), n)
 
 
+def test_packed_degree_field_cap(cuda):
+    """The widest degree code (24 bits: 14 bits of node id and 26 of row
+    begin leave more): a row of 2^24 - 4 entries, the longest the code
+    holds, and one of 2^24 - 3, read through the long-row phase.  Sampled
+    walks and edge ids against the oracle."""
+    from mlx_cluster_amd import _lib
+    V, L = 1 << 14, 40
+    rowptr, col, core, hubs = _hub_graph(V, [(1 << 24) - 4, (1 << 24) - 3], 200_000, seed=24)
+    E = col.size
+    assert (1 << 25) < E < (1 << 26)
+    N = 4 * E // L + 1001
+    start = np.where(np.arange(N) % 2 == 0, hubs[np.arange(N) % 2], core[np.arange(N) % 1000])
+    assert _lib.load().mlxc_random_walk_workspace_bytes(V, E, N, L) == 256 + 8 * (E + N)
+    rp, cl, st = (torch.from_numpy(a).to(cuda) for a in (rowptr, col, start))
+    rand = mc.philox_uniform((N, L), 5, device=cuda)
+    n, e = mc.random_walk(rp, cl, st, rand, L, return_edges=True)
+    sample = np.random.default_rng(2).choice(N, 2000, replace=False)
+    n_ref, e_ref, status, _ = oracle.uniform_walk(rowptr, col, start[sample],
+                                                  rand.cpu().numpy()[sample], L, with_edges=True)
+    assert status == 0
+    np.testing.assert_array_equal(n.cpu().numpy()[sample], n_ref)
+    np.testing.assert_array_equal(e.cpu().numpy()[sample], e_ref)
+    assert np.isin(n_ref[:, :-1], hubs).sum() > 1000
+
+
 @pytest.mark.parametrize("N,L", [(1, 1), (37, 5), (1000, 16), (4096, 23), (30_000, 80)])
 def test_seeded_uniforms_match_rand_tensor(N, L, cuda):
     """rand=None, seed=s generates in the kernel exactly the stream
