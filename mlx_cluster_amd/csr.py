@@ -20,7 +20,8 @@ import numpy as np
 import torch
 
 from . import _lib
-from .walks import _check_stream_arg, _on_device, _stream_handle, _workspace
+from .walks import (_check_stream_arg, _enter_side_stream, _leave_side_stream, _on_device,
+                    _side_stream, _stream_handle, _workspace)
 
 
 def to_csr(edge_index, num_nodes: Optional[int] = None, *, symmetrize: bool = False,
@@ -83,11 +84,14 @@ def to_csr(edge_index, num_nodes: Optional[int] = None, *, symmetrize: bool = Fa
         if nbytes == 0:
             raise ValueError("to_csr: num_nodes or the edge count is out of range")
         work = _workspace(nbytes, dev)
+        side = _side_stream(stream, dev)
+        _enter_side_stream(side, dev)
         with _on_device(dev):
             rc = lib.mlxc_csr_build(row.data_ptr() if E else None, col.data_ptr() if E else None,
                                     E, V, flags, rowptr.data_ptr(),
                                     col_out.data_ptr() if total else None, work.data_ptr(),
                                     work.numel() * 8, handle)
+        _leave_side_stream(side, row, col, rowptr, col_out, work)
         _lib.check(rc, "to_csr")
         if isinstance(stream, torch.cuda.Stream):
             stream.synchronize()

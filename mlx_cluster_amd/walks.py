@@ -76,6 +76,36 @@ def _stream_handle(stream, device: torch.device) -> int:
     return torch.cuda.current_stream(torch.device(stream)).cuda_stream
 
 
+def _side_stream(stream, device: torch.device) -> Optional[torch.cuda.Stream]:
+    """`stream` when a call runs on a torch.cuda.Stream that is not torch's
+    current stream of `device`, else None."""
+    if isinstance(stream, torch.cuda.Stream) and \
+            stream.cuda_stream != torch.cuda.current_stream(device).cuda_stream:
+        return stream
+    return None
+
+
+def _enter_side_stream(side: Optional[torch.cuda.Stream], device: torch.device) -> None:
+    """A call copies its inputs and allocates its outputs and workspace on
+    torch's current stream: the side stream it launches on waits for that
+    work first, so no kernel reads a copy still in flight or writes memory
+    the allocator handed over while an earlier kernel on the current stream
+    still used it."""
+    if side is not None:
+        side.wait_stream(torch.cuda.current_stream(device))
+
+
+def _leave_side_stream(side: Optional[torch.cuda.Stream], *tensors) -> None:
+    """Marks every device tensor a side-stream call touched as used on that
+    stream, so the caching allocator reuses none of them (the workspace and
+    input copies are freed when the call returns) before the stream's
+    kernels have finished."""
+    if side is not None:
+        for t in tensors:
+            if isinstance(t, torch.Tensor) and t.is_cuda and t.numel():
+                t.record_stream(side)
+
+
 def _on_device(device: torch.device):
     """The library's calls query and launch on the current device: make it
     `device` (a no-op context when it already is)."""
@@ -207,9 +237,12 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
             seed), without the rand tensor's memory traffic.
         walk_length: steps per walk (>= 0).
         stream: None (torch's current stream), a torch.cuda.Stream or a
-            device.  'cpu' evaluates on CPU threads (the reference's
-            eval_cpu) with results bit-identical to the GPU's; inputs are
-            copied to host memory and outputs are CPU tensors.
+            device.  On a torch.cuda.Stream the kernels run after the work
+            already queued on torch's current stream (where inputs are
+            copied and outputs allocated), and every tensor of the call is
+            recorded as used there.  'cpu' evaluates on CPU threads (the
+            reference's eval_cpu) with results bit-identical to the GPU's;
+            inputs are copied to host memory and outputs are CPU tensors.
         return_edges: also return the edge ids [num_walks, walk_length]
             (-1 where the walk stayed in a node of out-degree 0), the
             reference's discarded second output (RandomWalk.cpp:58).
@@ -270,12 +303,16 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     graph = (_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N)
     outs = (_ptr(n_out), _ptr(e_out) if return_edges else None, otype, work.data_ptr(),
             work.numel() * 8, handle)
+    if rand is not None:
+        rand = _on(rand, device)
+    side = _side_stream(stream, device)
+    _enter_side_stream(side, device)
     with _on_device(device):
         if rand is None:
             rc = lib.mlxc_random_walk_seeded(*graph, L, seed, *outs)
         else:
-            rand = _on(rand, device)
             rc = lib.mlxc_random_walk(*graph, _ptr(rand), L, *outs)
+    _leave_side_stream(side, rowptr, col, start, rand, n_out, e_out, work)
     _lib.check(rc, "random_walk")
     if check:
         _raise_status(work, stream, "random_walk")
@@ -294,10 +331,13 @@ def csr_check(rowptr: TensorLike, col: TensorLike, *, stream=None) -> int:
     rowptr, col = _on(rowptr, device), _on(col, device)
     work = _workspace(_lib.MLXC_WORK_WORDS * 8, device)
     flags = _lib.ctypes.c_int32(0)
+    side = _side_stream(stream, device)
+    _enter_side_stream(side, device)
     with _on_device(device):
         rc = _lib.load().mlxc_csr_check(_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(),
                                         work.data_ptr(), work.numel() * 8,
                                         _lib.ctypes.addressof(flags), handle)
+    _leave_side_stream(side, rowptr, col, work)
     _lib.check(rc, "csr_check")
     return int(flags.value)
 
@@ -379,12 +419,15 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     lib = _lib.load()
     work = _workspace(lib.mlxc_rejection_sampling_workspace_bytes(
         rowptr.numel() - 1, col.numel(), N, L, float(p), float(q), _RULES[rule]), device)
+    side = _side_stream(stream, device)
+    _enter_side_stream(side, device)
     with _on_device(device):
         rc = lib.mlxc_rejection_sampling(
             _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,
             p, q, seed, _RULES[rule], rows, _ptr(n_out),
             _ptr(e_out) if return_edges else None, otype, work.data_ptr(), work.numel() * 8,
             handle)
+    _leave_side_stream(side, rowptr, col, start, n_out, e_out, work)
     _lib.check(rc, "rejection_sampling")
     if check:
         _raise_status(work, stream, "rejection_sampling")
@@ -405,7 +448,10 @@ def philox_uniform(shape, seed: int, *, device=None, stream=None) -> torch.Tenso
     dev = torch.device(device) if device is not None else _resolve_device(stream, ())
     handle = _stream_handle(stream, dev)
     out = torch.empty(tuple(shape), dtype=torch.float32, device=dev)
+    side = _side_stream(stream, dev)
+    _enter_side_stream(side, dev)
     with _on_device(dev):
         rc = _lib.load().mlxc_philox_uniform(_ptr(out), out.numel(), int(seed) & (2**64 - 1), handle)
+    _leave_side_stream(side, out)
     _lib.check(rc, "philox_uniform")
     return out

@@ -17,8 +17,9 @@ import numpy as np
 import torch
 
 from . import _lib
-from .walks import (_as_tensor, _check_stream_arg, _on, _on_cpu, _on_device, _out_type,
-                    _resolve_device, _stream_handle)
+from .walks import (_as_tensor, _check_stream_arg, _enter_side_stream, _leave_side_stream, _on,
+                    _on_cpu, _on_device, _out_type, _resolve_device, _side_stream,
+                    _stream_handle)
 
 _ELEM = {torch.int64: _lib.MLXC_OUT_INT64, torch.int32: _lib.MLXC_OUT_INT32}
 
@@ -60,9 +61,12 @@ def context_windows(walks, context_size: int, *, stream=None) -> torch.Tensor:
     handle = _stream_handle(stream, device)
     walks = _on(walks, device)
     out = torch.empty((W * N, C), dtype=walks.dtype, device=device)
+    side = _side_stream(stream, device)
+    _enter_side_stream(side, device)
     with _on_device(device):
         rc = lib.mlxc_context_windows(walks.data_ptr() if N else None, N, nodes, C,
                                       _ELEM[walks.dtype], out.data_ptr() if N else None, handle)
+    _leave_side_stream(side, walks, out)
     _lib.check(rc, "context_windows")
     return out
 
@@ -104,8 +108,11 @@ def negative_windows(start, walk_length: int, context_size: int, num_nodes: int,
     handle = _stream_handle(stream, device)
     start = _on(start, device)
     out = torch.empty((W * N, C), dtype=out_dtype, device=device)
+    side = _side_stream(stream, device)
+    _enter_side_stream(side, device)
     with _on_device(device):
         rc = lib.mlxc_negative_windows(start.data_ptr() if N else None, N, L, C, V, seed,
                                        out_type, out.data_ptr() if N else None, handle)
+    _leave_side_stream(side, start, out)
     _lib.check(rc, "negative_windows")
     return out

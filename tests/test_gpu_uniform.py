@@ -111,6 +111,43 @@ def test_repeatable_and_side_stream(cuda):
     assert torch.equal(a, b)
 
 
+def test_side_stream_call_is_ordered_and_keeps_its_memory(cuda):
+    """A call on a side stream with check=False: its kernels run after the
+    work queued on torch's current stream (here an input written there
+    behind a spin kernel of bounded length), and the allocator hands out
+    none of the call's memory (workspace, input copies) while they run: a
+    zero-fill of the workspace's size queued on the current stream right
+    after the call must not reach the walk's edge records.  Nodes, edges and
+    node2vec walks equal the oracle's."""
+    rowptr, col = synth.rmat_csr(12, 40_000, seed=5)
+    rowptr, col = rowptr.numpy(), col.numpy()
+    V, L = rowptr.size - 1, 30
+    start = (np.arange(20 * V) % V).astype(np.int64)   # many steps per edge: records
+    rand = oracle.philox_uniform(start.size * L, 6).reshape(start.size, L)
+    n_ref, e_ref, _, _ = oracle.uniform_walk(rowptr, col, start, rand, L, with_edges=True)
+    n2v_ref, _, _, _ = oracle.node2vec_walk(rowptr, col, start, L, 0.5, 2.0, 9)
+    cur = torch.cuda.current_stream(cuda)
+    s = torch.cuda.Stream(device=cuda)
+    rand_dev = torch.full(rand.shape, 0.5, dtype=torch.float32, device=cuda)
+    lib = mc._lib.load()
+    ws_words = lib.mlxc_random_walk_workspace_bytes(V, col.size, start.size, L) // 8 + 1
+    torch.cuda._sleep(20_000_000)          # bounded spin on the current stream
+    rand_dev.copy_(torch.from_numpy(rand).to(cuda, non_blocking=False))
+    n, e = mc.random_walk(rowptr, col, start, rand_dev, L, stream=s, check=False,
+                          return_edges=True)
+    junk = torch.zeros(ws_words, dtype=torch.int64, device=cuda)
+    torch.cuda._sleep(20_000_000)
+    junk.fill_(0)
+    w = mc.rejection_sampling(rowptr, col, start, L, 0.5, 2.0, seed=9, stream=s, check=False)
+    junk2 = torch.zeros(ws_words * 2, dtype=torch.int64, device=cuda)
+    s.synchronize()
+    cur.synchronize()
+    np.testing.assert_array_equal(n.cpu().numpy(), n_ref)
+    np.testing.assert_array_equal(e.cpu().numpy(), e_ref)
+    np.testing.assert_array_equal(w.cpu().numpy(), n2v_ref)
+    del junk, junk2
+
+
 def test_numpy_inputs_are_copied(c1, cuda):
     n = mc.random_walk(c1["rowptr"], c1["col"], c1["start"], c1["rand"], int(c1["walk_length"]))
     assert n.is_cuda
