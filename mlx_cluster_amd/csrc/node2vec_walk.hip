@@ -631,7 +631,9 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
 // bisection (sorted rows) or a linear scan (unsorted rows) in LDS.  Every
 // block validates its copy of the whole CSR, as the preparation passes of the
 // other layouts do (block 0 reports it); with MLXC_ROWS_DETECT each block
-// also checks the row order of its copy.
+// also decides the row order of its copy by the preparation passes' rule
+// (CsrCheck: every position i >= 1 with col[i] < col[i-1] starts a non-empty
+// row), checked entry-parallel.
 template <int kRule, bool kEdges, typename OutT>
 __global__ __launch_bounds__(kLdsBlock) void node2vec_lds_kernel(N2VRecArgs a) {
     __shared__ int32_t graph[kLdsGraphEntries];
@@ -653,18 +655,25 @@ __global__ __launch_bounds__(kLdsBlock) void node2vec_lds_kernel(N2VRecArgs a) {
     }
     __syncthreads();
     for (int64_t u = threadIdx.x; u < V; u += kLdsBlock) bad_row |= rp[u + 1] < rp[u];
-    // (both reductions are block-wide barriers every thread reaches)
+    // (every reduction below is a block-wide barrier every thread reaches)
     const bool any_bad_row = __syncthreads_or(bad_row);
     const bool any_bad_col = __syncthreads_or(bad_col);
     bool sorted = a.rows == MLXC_ROWS_SORTED;
     if (a.rows == MLXC_ROWS_DETECT) {
-        bool descent = false;  // inside some well-formed row
+        // the block's descents minus those at a row start (each of which is
+        // also a descent): zero exactly when the rows are sorted
+        __shared__ int extra;
+        if (threadIdx.x == 0) extra = 0;
+        __syncthreads();
+        int d = 0;
+        for (int64_t i = 1 + threadIdx.x; i < E; i += kLdsBlock) d += cl[i] < cl[i - 1];
         for (int64_t u = threadIdx.x; u < V; u += kLdsBlock) {
             const int32_t b = rp[u], end = rp[u + 1];
-            if (b < 0 || end < b) continue;
-            for (int32_t i = b + 1; i < end; ++i) descent |= cl[i] < cl[i - 1];
+            d -= b >= 1 && end > b && cl[b] < cl[b - 1];
         }
-        sorted = !__syncthreads_or(descent);
+        if (d) atomicAdd(&extra, d);
+        __syncthreads();
+        sorted = extra == 0;
     }
     OutT* const nout = static_cast<OutT*>(a.w.n_out);
     OutT* const eout = static_cast<OutT*>(a.w.e_out);
@@ -989,7 +998,7 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
     // (it stores single elements: no alignment needed)
     if (workspace_bytes >= kRecordOffset &&
         lds_walk_fits(w.num_nodes, w.num_edges, w.num_walks, w.walk_length)) {
-        if (int rc = launch_zero_work(w.work, stream)) return rc;
+        // (mlxc_rejection_sampling cleared the status words before this launch)
         N2VRecArgs a{};
         a.w = w;
         a.rows = p.rows;
@@ -999,13 +1008,14 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         a.key0 = p.key0;
         a.key1 = p.key1;
         const dim3 grid(static_cast<unsigned>((w.num_walks + kLdsBlock - 1) / kLdsBlock));  // <= 1024
+        const dim3 block(kLdsBlock);
         const bool edges = w.e_out != nullptr;
         if (p.rule == MLXC_RULE_REF_CHAIN) {
-            if (edges) hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, true, OutT>), grid, dim3(kLdsBlock), 0, stream, a);
-            else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, false, OutT>), grid, dim3(kLdsBlock), 0, stream, a);
+            if (edges) hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, true, OutT>), grid, block, 0, stream, a);
+            else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, false, OutT>), grid, block, 0, stream, a);
         } else {
-            if (edges) hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_NODE2VEC_EXACT, true, OutT>), grid, dim3(kLdsBlock), 0, stream, a);
-            else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_NODE2VEC_EXACT, false, OutT>), grid, dim3(kLdsBlock), 0, stream, a);
+            if (edges) hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_NODE2VEC_EXACT, true, OutT>), grid, block, 0, stream, a);
+            else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_NODE2VEC_EXACT, false, OutT>), grid, block, 0, stream, a);
         }
         MLXC_HIP_TRY(hipGetLastError());
         return MLXC_OK;
