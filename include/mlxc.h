@@ -312,7 +312,9 @@ int mlxc_csr_build_cpu(const int64_t* row, const int64_t* col, int64_t num_edges
  * d_walks    [N, walk_nodes] row-major, element type elem_type (MLXC_OUT_*)
  * d_out      [W * N, C], the same element type
  * walk_nodes in [1, 65536 / element size]; context_size in [1, min(32,
- * walk_nodes)].
+ * walk_nodes)].  One launch takes at most 16,777,215 tiles of walks (a tile
+ * is min(64, 65536 / (walk_nodes * element size)) walks): larger calls fail
+ * with MLXC_ERR_INVALID_ARGUMENT and are split by the caller.
  * Asynchronous on `stream`; no workspace.
  */
 int mlxc_context_windows(const void* d_walks, int64_t num_walks, int32_t walk_nodes,

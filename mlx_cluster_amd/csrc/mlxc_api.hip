@@ -151,6 +151,19 @@ int check_windows(const void* walks, int64_t num_walks, int32_t walk_nodes, int3
     return MLXC_OK;
 }
 
+// The window kernels launch one block of kBlock threads per tile of walks,
+// and a launch holds fewer than 2^32 work-items per grid dimension.
+int check_window_grid(int64_t num_walks, int32_t walk_nodes, int32_t elem_type) {
+    const int per_block = tile_walks(walk_nodes, elem_type == MLXC_OUT_INT32 ? 4 : 8);
+    const int64_t max_blocks = static_cast<int64_t>(UINT32_MAX) / kBlock;
+    if (per_block >= 1 && (num_walks + per_block - 1) / per_block > max_blocks)
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "too many walks for one window launch: at most " +
+                        std::to_string(max_blocks * per_block) +
+                        " walks of this length; split the call");
+    return MLXC_OK;
+}
+
 int check_negative(const int64_t* start, int64_t num_walks, int32_t walk_length, int32_t ctx,
                    int64_t num_nodes, int32_t out_type, const void* out) {
     if (walk_length < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "walk_length must be >= 0");
@@ -366,6 +379,7 @@ int mlxc_context_windows(const void* d_walks, int64_t num_walks, int32_t walk_no
                          int32_t context_size, int32_t elem_type, void* d_out, void* stream) {
     if (int rc = check_windows(d_walks, num_walks, walk_nodes, context_size, elem_type, d_out))
         return rc;
+    if (int rc = check_window_grid(num_walks, walk_nodes, elem_type)) return rc;
     if (num_walks == 0) return MLXC_OK;
     return launch_context_windows(d_walks, num_walks, walk_nodes, context_size, elem_type, d_out,
                                   static_cast<hipStream_t>(stream));
@@ -377,6 +391,7 @@ int mlxc_negative_windows(const int64_t* d_start, int64_t num_walks, int32_t wal
     if (int rc = check_negative(d_start, num_walks, walk_length, context_size, num_nodes,
                                 out_type, d_out))
         return rc;
+    if (int rc = check_window_grid(num_walks, walk_length + 1, out_type)) return rc;
     if (num_walks == 0) return MLXC_OK;
     return launch_negative_windows(d_start, num_walks, walk_length, context_size, num_nodes, seed,
                                    out_type, d_out, static_cast<hipStream_t>(stream));

@@ -161,6 +161,8 @@ int launch_negative_windows(const int64_t* start, int64_t num_walks, int32_t wal
 // Most nodes per walk the window kernels accept for this element type (a
 // walk row must fit the LDS tile).
 int windows_max_nodes(int32_t elem_type);
+// Walks per block of the window kernels (one block per tile of walks).
+int tile_walks(int32_t walk_nodes, size_t esz);
 
 // ---- host_walk.cpp (host pointers; the same walks on CPU threads)
 struct HostWalk {

@@ -121,6 +121,22 @@ def test_other_entry_points_reject_bad_arguments():
         == _lib.MLXC_ERR_INVALID_ARGUMENT
 
 
+def test_window_launches_beyond_the_grid_limit_are_rejected():
+    """A window launch runs one 256-thread block per tile of walks (64 walks
+    of up to 128 int64 nodes, one walk of 8192): more tiles than a grid
+    dimension holds (2^32 - 1 work-items) fail with a message before any
+    device call; the largest call that fits passes the check."""
+    lib = _lib.load()
+    max_tiles = (2**32 - 1) // 256
+    for nodes, per_tile in ((2, 64), (8192, 1)):
+        too_many = max_tiles * per_tile + 1
+        rc = lib.mlxc_context_windows(FAKE, too_many, nodes, 2, _lib.MLXC_OUT_INT64, FAKE, None)
+        assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT and "split the call" in _lib.last_error()
+        rc = lib.mlxc_negative_windows(FAKE, too_many, nodes - 1, 2, 10, 1, _lib.MLXC_OUT_INT64,
+                                       FAKE, None)
+        assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT and "split the call" in _lib.last_error()
+
+
 def test_workspace_size_query():
     """Edge and start records take 8 bytes each when node ids, row begins and
     at least 16 bits of degree pack into 64 bits, else 16; start records
