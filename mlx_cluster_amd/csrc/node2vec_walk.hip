@@ -680,74 +680,114 @@ __global__ __launch_bounds__(kLdsBlock) void node2vec_lds_kernel(N2VRecArgs a) {
     uint32_t status = 0;
     if (blockIdx.x == 0 && threadIdx.x == 0)
         status = (any_bad_row ? MLXC_STATUS_BAD_ROW : 0u) | (any_bad_col ? MLXC_STATUS_BAD_NODE : 0u);
-    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kLdsBlock + threadIdx.x; n < N;
-         n += static_cast<int64_t>(gridDim.x) * kLdsBlock) {
-        const int64_t s = a.w.start[n];
-        OutT* const row = nout + n * (L + 1);
-        OutT* const erow = kEdges ? eout + n * L : nullptr;
-        row[0] = static_cast<OutT>(s);
-        int64_t l = 0;                    // steps taken
-        int32_t v = static_cast<int32_t>(s), t = v;
-        bool stop = !node_ok(s, V);       // a sink or an error ends the walk
-        if (stop) status |= MLXC_STATUS_BAD_NODE;
-        while (l < L && !stop) {
-            const int32_t b = rp[v], end = rp[v + 1];
-            if (b < 0 || end < b) {
-                status |= MLXC_STATUS_BAD_ROW;
-                break;
-            }
-            const int32_t deg = end - b;
-            if (deg == 0) break;  // absorbing node: the walk stays
-            int32_t e = b, x = 0;
-            for (uint32_t trial = 0;; ++trial) {
-                // the first step and forced steps accept (BiasedRandomWalk.cpp:60-66, 76-78)
-                const bool test = l > 0 && deg > 1;
-                float r = 0.0f;
-                if (l == 0 || deg > 1) {
-                    float u0;
-                    n2v_uniforms(n, static_cast<int32_t>(l), trial, a.key0, a.key1, u0, r);
-                    e = b + static_cast<int32_t>(pick_index(u0, deg));
-                }
-                x = cl[e];
-                const int32_t bx = x >= 0 ? rp[x] : -1, ex = x >= 0 ? rp[x + 1] : -1;
-                if (x < 0 || bx < 0 || ex < bx) {
-                    status |= x < 0 ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
-                    stop = true;
-                    break;
-                }
-                if (!test) break;
-                int d = n2v_decide<kRule>(a, r, x, t);
-                if (d < 0) {  // is t in row(x)?
-                    bool adjacent = false;
-                    if (sorted) {
-                        int32_t lo = bx, count = ex - bx;
-                        while (count > 0) {  // lower_bound
-                            const int32_t half = count >> 1;
-                            if (cl[lo + half] < t) {
-                                lo += half + 1;
-                                count -= half + 1;
-                            } else {
-                                count = half;
-                            }
-                        }
-                        adjacent = lo < ex && cl[lo] == t;
-                    } else {
-                        for (int32_t i = bx; i < ex && !adjacent; ++i) adjacent = cl[i] == t;
-                    }
-                    d = n2v_resolve<kRule>(a, r, adjacent) ? 1 : 0;
-                }
-                if (d == 1 || trial + 1 >= MLXC_MAX_TRIALS) break;  // (the cap keeps the last candidate)
-            }
-            if (stop) break;
-            row[l + 1] = static_cast<OutT>(x);
-            if (kEdges) erow[l] = static_cast<OutT>(e);
-            t = v;
-            v = x;
-            l += 1;
-        }
-        for (int64_t j = l + 1; j <= L; ++j) row[j] = static_cast<OutT>(v);  // the walk stays
+    // One trial per loop iteration and lane: a lane whose walk takes its
+    // step goes on with the next step (or its next walk) in the next
+    // iteration, so a wavefront runs as long as its longest walk, not as
+    // long as the longest trial run of each step summed over the steps.
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kLdsBlock;
+    int64_t n = static_cast<int64_t>(blockIdx.x) * kLdsBlock + threadIdx.x;
+    OutT* row = nullptr;
+    OutT* erow = nullptr;
+    int64_t l = 0;           // steps taken
+    int32_t v = 0, t = 0;    // current and previous node
+    int32_t b = 0, deg = 0;  // row of v
+    uint32_t trial = 0;
+    bool walking = false;    // walk n has a trial due
+    // the walk stays at v from step l on; then the lane takes its next walk
+    auto finish = [&]() {
+        for (int64_t j = l + 1; j <= L; ++j) row[j] = static_cast<OutT>(v);
         if (kEdges)
             for (int64_t j = l; j < L; ++j) erow[j] = static_cast<OutT>(-1);
+        walking = false;
+        n += stride;
+    };
+    while (true) {
+        if (!walking) {
+            if (n >= N) break;
+            const int64_t s = a.w.start[n];
+            row = nout + n * (L + 1);
+            erow = kEdges ? eout + n * L : nullptr;
+            row[0] = static_cast<OutT>(s);
+            l = 0;
+            v = static_cast<int32_t>(s);
+            t = v;
+            if (!node_ok(s, V)) {
+                status |= MLXC_STATUS_BAD_NODE;
+                finish();
+                continue;
+            }
+            if (L == 0) {
+                finish();
+                continue;
+            }
+            b = rp[v];
+            const int32_t end = rp[v + 1];
+            if (b < 0 || end < b) {
+                status |= MLXC_STATUS_BAD_ROW;
+                finish();
+                continue;
+            }
+            deg = end - b;
+            if (deg == 0) {  // absorbing start node: the walk stays
+                finish();
+                continue;
+            }
+            trial = 0;
+            walking = true;
+        }
+        // trial `trial` of step l from v; the first step and forced steps
+        // accept (BiasedRandomWalk.cpp:60-66, 76-78)
+        const bool test = l > 0 && deg > 1;
+        float r = 0.0f;
+        int32_t e = b;
+        if (l == 0 || deg > 1) {
+            float u0;
+            n2v_uniforms(n, static_cast<int32_t>(l), trial, a.key0, a.key1, u0, r);
+            e = b + static_cast<int32_t>(pick_index(u0, deg));
+        }
+        const int32_t x = cl[e];
+        const int32_t bx = x >= 0 ? rp[x] : -1, ex = x >= 0 ? rp[x + 1] : -1;
+        if (x < 0 || bx < 0 || ex < bx) {
+            status |= x < 0 ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
+            finish();
+            continue;
+        }
+        if (test) {
+            int d = n2v_decide<kRule>(a, r, x, t);
+            if (d < 0) {  // is t in row(x)?
+                bool adjacent = false;
+                if (sorted) {
+                    int32_t lo = bx, count = ex - bx;
+                    while (count > 0) {  // lower_bound
+                        const int32_t half = count >> 1;
+                        if (cl[lo + half] < t) {
+                            lo += half + 1;
+                            count -= half + 1;
+                        } else {
+                            count = half;
+                        }
+                    }
+                    adjacent = lo < ex && cl[lo] == t;
+                } else {
+                    for (int32_t i = bx; i < ex && !adjacent; ++i) adjacent = cl[i] == t;
+                }
+                d = n2v_resolve<kRule>(a, r, adjacent) ? 1 : 0;
+            }
+            if (d != 1 && trial + 1 < MLXC_MAX_TRIALS) {  // (the cap keeps the last candidate)
+                ++trial;
+                continue;
+            }
+        }
+        // the step to x, whose row the trial has read and checked
+        row[l + 1] = static_cast<OutT>(x);
+        if (kEdges) erow[l] = static_cast<OutT>(e);
+        t = v;
+        v = x;
+        l += 1;
+        b = bx;
+        deg = ex - bx;
+        trial = 0;
+        if (l == L || deg == 0) finish();  // (deg 0: an absorbing node, the walk stays)
     }
     if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.w.work), static_cast<unsigned long long>(status));
 }
