@@ -63,9 +63,17 @@ __device__ __forceinline__ bool accept(const N2VArgs& a, bool sorted, double r, 
     return is_neighbor(a.w.rowptr, a.w.col, a.w.num_edges, sorted, x, t, status) ? lt1 : lt2;
 }
 
-// node2vec walk on the CSR arrays (the fallback of the record walk).  The row
-// order comes from the device: csr_status_kernel leaves work[2] = 1 when the
-// CSR check found every row sorted, so the call needs no host round trip.
+// node2vec walk on the CSR arrays (the fallback of the record walk, and the
+// walk of graphs whose ids exceed int32).  The row order comes from the
+// device: csr_status_kernel leaves work[2] = 1 when the CSR check found every
+// row sorted, so the call needs no host round trip.
+//
+// Each lane takes its own walks from the wave queue and does one trial of
+// its current step per loop iteration (reading the step's row first when it
+// enters the step), so lanes never wait for each other's rejection runs or
+// walk ends.  A walk that meets an out-of-range id or row, or a node of
+// out-degree 0, repeats its node to the end: a bad candidate id is written
+// once, then repeated.
 template <int kRule, bool kEdges, typename OutT>
 __global__ __launch_bounds__(kBlock) void node2vec_walk_kernel(N2VArgs a) {
     const int64_t L = a.w.walk_length;
@@ -76,75 +84,123 @@ __global__ __launch_bounds__(kBlock) void node2vec_walk_kernel(N2VArgs a) {
     unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.w.work + 1);
     WaveQueue q{0, 0};
     uint32_t status = 0;
+    OutT* out = nullptr;
+    OutT* eout = nullptr;
+    int64_t n = 0, l = 0;     // walk and its step (1 .. L-1 while walking)
+    int64_t t = 0, v = 0;     // previous and current node
+    RowBounds rb{0, 0};       // row of v, once the step has been entered
+    uint32_t n_lo = 0, n_hi = 0, trial = 0;
+    bool walking = false;     // walk n has step l to take
+    bool entered = false;     // ... and has read v's row (rb)
+    bool exhausted = false;   // the queue has no walk left for this lane
+    // steps l .. L-1 stay at node x with no edge
+    auto stay = [&](int64_t from, int64_t x) {
+        for (int64_t j = from; j < L; ++j) {
+            out[j + 1] = static_cast<OutT>(x);
+            if (kEdges) eout[j] = static_cast<OutT>(-1);
+        }
+        walking = false;
+    };
     while (true) {
-        const int64_t n = queue_take(q, true, counter);
-        if (n >= N) break;  // wave-uniform: every lane asked, ids are consecutive
-        OutT* out = static_cast<OutT*>(a.w.n_out) + n * (L + 1);
-        OutT* eout = kEdges ? static_cast<OutT*>(a.w.e_out) + n * L : nullptr;
-        int64_t t = a.w.start[n];
-        out[0] = static_cast<OutT>(t);
-        if (L == 0) {
-            if (!node_ok(t, V)) status |= MLXC_STATUS_BAD_NODE;
-            continue;
-        }
-        bool bad = !node_ok(t, V);
-        int64_t v = t, e = -1;
-        const uint32_t n_lo = static_cast<uint32_t>(n), n_hi = static_cast<uint32_t>(n >> 32);
-        if (bad) {
-            status |= MLXC_STATUS_BAD_NODE;
-        } else {
-            // First step: uniform, no acceptance test (BiasedRandomWalk.cpp:60-66).
-            const RowBounds rb = load_row(a.w.rowptr, t);
-            if (!row_ok(rb, a.w.num_edges)) {
-                status |= MLXC_STATUS_BAD_ROW;
-                bad = true;
-            } else if (rb.end > rb.begin) {
-                uint32_t c0 = n_lo, c1 = n_hi, c2 = 0, c3 = 0;
-                philox4x32_10(c0, c1, c2, c3, a.key0, a.key1);
-                e = rb.begin + pick_index(unit_float(c0), rb.end - rb.begin);
-                v = a.w.col[e];
-            }
-        }
-        out[1] = static_cast<OutT>(v);
-        if (kEdges) eout[0] = static_cast<OutT>(e);
-        for (int64_t l = 1; l < L; ++l) {
-            int64_t x = v;
-            e = -1;
-            if (!bad && !node_ok(v, V)) {
-                status |= MLXC_STATUS_BAD_NODE;
-                bad = true;
-            }
-            if (!bad) {
-                const RowBounds rb = load_row(a.w.rowptr, v);
-                const int64_t deg = rb.end - rb.begin;
-                if (!row_ok(rb, a.w.num_edges)) {
-                    status |= MLXC_STATUS_BAD_ROW;
-                    bad = true;
-                } else if (deg == 1) {  // BiasedRandomWalk.cpp:76-78: forced, no draw
-                    e = rb.begin;
-                    x = a.w.col[e];
-                } else if (deg > 1) {   // :80-92 rejection loop
-                    for (uint32_t trial = 0;; ++trial) {
-                        uint32_t c0 = n_lo, c1 = n_hi, c2 = static_cast<uint32_t>(l), c3 = trial;
-                        philox4x32_10(c0, c1, c2, c3, a.key0, a.key1);
-                        e = rb.begin + pick_index(unit_float(c0), deg);
-                        x = a.w.col[e];
-                        const double r = static_cast<double>(unit_float(c1));
-                        if (!node_ok(x, V)) {
-                            status |= MLXC_STATUS_BAD_NODE;
+        const bool need = !walking && !exhausted;
+        const int64_t id = queue_take(q, need, counter);
+        if (need) {
+            if (id >= N) {
+                exhausted = true;
+            } else {
+                n = id;
+                n_lo = static_cast<uint32_t>(n);
+                n_hi = static_cast<uint32_t>(n >> 32);
+                out = static_cast<OutT*>(a.w.n_out) + n * (L + 1);
+                eout = kEdges ? static_cast<OutT*>(a.w.e_out) + n * L : nullptr;
+                t = a.w.start[n];
+                out[0] = static_cast<OutT>(t);
+                if (L == 0) {
+                    if (!node_ok(t, V)) status |= MLXC_STATUS_BAD_NODE;
+                } else {
+                    // first step: uniform, no acceptance test (BiasedRandomWalk.cpp:60-66)
+                    bool bad = !node_ok(t, V);
+                    int64_t e = -1;
+                    v = t;
+                    if (bad) {
+                        status |= MLXC_STATUS_BAD_NODE;
+                    } else {
+                        const RowBounds r0 = load_row(a.w.rowptr, t);
+                        if (!row_ok(r0, a.w.num_edges)) {
+                            status |= MLXC_STATUS_BAD_ROW;
                             bad = true;
-                            break;
+                        } else if (r0.end > r0.begin) {
+                            uint32_t c0 = n_lo, c1 = n_hi, c2 = 0, c3 = 0;
+                            philox4x32_10(c0, c1, c2, c3, a.key0, a.key1);
+                            e = r0.begin + pick_index(unit_float(c0), r0.end - r0.begin);
+                            v = a.w.col[e];
                         }
-                        if (accept<kRule>(a, sorted, r, x, t, status)) break;
-                        if (trial + 1 >= MLXC_MAX_TRIALS) break;
                     }
+                    out[1] = static_cast<OutT>(v);
+                    if (kEdges) eout[0] = static_cast<OutT>(e);
+                    l = 1;
+                    walking = true;
+                    entered = false;
+                    if (bad) stay(1, v);
+                    else if (L == 1) walking = false;
                 }
             }
-            out[l + 1] = static_cast<OutT>(x);
-            if (kEdges) eout[l] = static_cast<OutT>(e);
-            t = v;
-            v = x;
         }
+        if (!__any(walking || !exhausted)) break;
+        if (!walking) continue;
+        if (!entered) {
+            if (!node_ok(v, V)) {
+                status |= MLXC_STATUS_BAD_NODE;
+                stay(l, v);
+                continue;
+            }
+            rb = load_row(a.w.rowptr, v);
+            const int64_t deg = rb.end - rb.begin;
+            if (!row_ok(rb, a.w.num_edges)) {
+                status |= MLXC_STATUS_BAD_ROW;
+                stay(l, v);
+                continue;
+            }
+            if (deg == 0) {
+                stay(l, v);  // an absorbing node: the walk stays
+                continue;
+            }
+            entered = true;
+            trial = 0;
+        }
+        const int64_t deg = rb.end - rb.begin;
+        int64_t e, x;
+        bool take;
+        if (deg == 1) {  // BiasedRandomWalk.cpp:76-78: forced, no draw
+            e = rb.begin;
+            x = a.w.col[e];
+            take = true;
+        } else {         // :80-92, one trial of the rejection loop
+            uint32_t c0 = n_lo, c1 = n_hi, c2 = static_cast<uint32_t>(l), c3 = trial;
+            philox4x32_10(c0, c1, c2, c3, a.key0, a.key1);
+            e = rb.begin + pick_index(unit_float(c0), deg);
+            x = a.w.col[e];
+            const double r = static_cast<double>(unit_float(c1));
+            if (!node_ok(x, V)) {
+                status |= MLXC_STATUS_BAD_NODE;
+                out[l + 1] = static_cast<OutT>(x);
+                if (kEdges) eout[l] = static_cast<OutT>(e);
+                stay(l + 1, x);
+                continue;
+            }
+            take = accept<kRule>(a, sorted, r, x, t, status) || trial + 1 >= MLXC_MAX_TRIALS;
+        }
+        if (!take) {
+            ++trial;
+            continue;
+        }
+        out[l + 1] = static_cast<OutT>(x);
+        if (kEdges) eout[l] = static_cast<OutT>(e);
+        t = v;
+        v = x;
+        ++l;
+        entered = false;
+        if (l == L) walking = false;
     }
     if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.w.work), static_cast<unsigned long long>(status));
 }
