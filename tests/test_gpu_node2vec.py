@@ -383,13 +383,18 @@ def test_c3_full_size_properties(cuda):
     col[e] is the next node) or stays, with edge id -1, at a node of
     out-degree 0; and three blocks of 2,000 walks (start, middle and end of
     the walk-id range, hence of the Philox counters) are bit-exact against the
-    oracle, nodes and edges."""
+    oracle, nodes and edges.  The direct kernel (the path of graphs beyond
+    int32 ids, forced by a minimal workspace) gives the same walks in full."""
     rowptr, col = synth.rmat_csr(20, 1 << 24, seed=0, device=cuda, symmetrize=True)
     V, E = rowptr.numel() - 1, col.numel()
     N, L = 4 * V, 40
     start = torch.arange(N, device=cuda) % V
     n, e = mc.rejection_sampling(rowptr, col, start, L, 0.5, 2.0, seed=3, return_edges=True)
     assert torch.equal(n[:, 0], start)
+    dn, de = _abi_walk(rowptr, col, start, L, 0.5, 2.0, 3, oracle.RULE_REF_CHAIN,
+                       mc._lib.MLXC_ROWS_DETECT, "direct")
+    assert torch.equal(dn, n) and torch.equal(de, e)
+    del dn, de
     bad = 0
     for l in range(L):
         u, v, el = n[:, l], n[:, l + 1], e[:, l]
@@ -416,7 +421,8 @@ def test_c5_full_size_properties(rule, cuda):
     rule (edge records, frequent searches of hub rows).  Every step follows
     its recorded edge or stays at a node of out-degree 0, and three blocks of
     1,000 walks spread over the walk-id range are bit-exact against the
-    oracle."""
+    oracle.  The direct kernel (the path of graphs beyond int32 ids, forced
+    by a minimal workspace) gives the same walks in full."""
     rowptr, col = synth.ba_hub_csr(4_000_000, 20, 64, 500_000, seed=0, device=cuda)
     V, E = rowptr.numel() - 1, col.numel()
     N, L = 2 * V, 30
@@ -424,6 +430,11 @@ def test_c5_full_size_properties(rule, cuda):
     n, e = mc.rejection_sampling(rowptr, col, start, L, 4.0, 0.25, seed=5, rule=rule,
                                  return_edges=True)
     assert torch.equal(n[:, 0], start)
+    rule_id = {name: k for k, name in RULE_NAME.items()}[rule]
+    dn, de = _abi_walk(rowptr, col, start, L, 4.0, 0.25, 5, rule_id, mc._lib.MLXC_ROWS_DETECT,
+                       "direct")
+    assert torch.equal(dn, n) and torch.equal(de, e)
+    del dn, de
     bad = 0
     for l in range(L):
         u, v, el = n[:, l], n[:, l + 1], e[:, l]
@@ -433,7 +444,6 @@ def test_c5_full_size_properties(rule, cuda):
         bad += int((~(stay | move)).sum())
     assert bad == 0
     rp, cl = rowptr.cpu().numpy(), col.cpu().numpy()
-    rule_id = {name: k for k, name in RULE_NAME.items()}[rule]
     for s0 in (0, N // 2, N - 1000):
         ref, ref_e, st, _ = oracle.node2vec_walk(rp, cl, start[s0:s0 + 1000].cpu().numpy(), L,
                                                  4.0, 0.25, 5, rule=rule_id, rows_sorted=True,

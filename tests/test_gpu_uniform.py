@@ -171,7 +171,7 @@ def test_c2_full_size_properties(cuda):
     """Configuration 2 at full size (R-MAT 2^20, 10 walks per node, L=80):
     every one of the 838,860,800 steps is checked against numpy-free torch
     float32 arithmetic on the device, and a sample of walks bit-exactly
-    against the oracle."""
+    against the oracle; the unwindowed kernel gives the same walks in full."""
     rowptr, col = synth.rmat_csr(20, 1 << 24, seed=0, device=cuda)
     V = rowptr.numel() - 1
     N, L = 10 * V, 80
@@ -197,6 +197,11 @@ def test_c2_full_size_properties(cuda):
                                           rand[sample].cpu().numpy(), L)
     assert st == 0
     np.testing.assert_array_equal(n[sample].cpu().numpy(), n_ref)
+    # the unwindowed kernel (the path of graphs beyond int32 ids, forced by a
+    # minimal workspace) gives the same walks in full
+    n2 = torch.empty_like(n)
+    _abi_walk(rowptr, col, start, rand.data_ptr(), L, n2.data_ptr(), ws_bytes=32)
+    assert torch.equal(n2, n)
 
 
 def test_c4_full_size_properties(cuda):
@@ -204,7 +209,8 @@ def test_c4_full_size_properties(cuda):
     per node, L=20), which the workspace query sends to the CSR walk (fewer
     than 4 steps per edge): every one of the 335,544,320 steps and its edge id
     is checked against torch float32 arithmetic on the device, and 4,000
-    sampled walks bit-exactly against the oracle, nodes and edges."""
+    sampled walks bit-exactly against the oracle, nodes and edges; the
+    unwindowed kernel gives the same walks and edges in full."""
     rowptr, col = synth.rmat_csr(24, 1 << 28, seed=0, device=cuda)
     V, E = rowptr.numel() - 1, col.numel()
     N, L = V, 20
@@ -236,6 +242,11 @@ def test_c4_full_size_properties(cuda):
     assert st == 0
     np.testing.assert_array_equal(n[sample].cpu().numpy(), n_ref)
     np.testing.assert_array_equal(e[sample].cpu().numpy(), e_ref)
+    # the unwindowed kernel (the path of graphs beyond int32 ids, forced by a
+    # minimal workspace) gives the same walks and edges in full
+    n2, e2 = torch.empty_like(n), torch.empty_like(e)
+    _abi_walk(rowptr, col, start, rand.data_ptr(), L, n2.data_ptr(), e_out=e2, ws_bytes=32)
+    assert torch.equal(n2, n) and torch.equal(e2, e)
 
 
 def _abi_walk(rowptr, col, start, rand_t, L, n_out_t, *, e_out=None, ws_bytes=None,
