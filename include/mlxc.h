@@ -110,7 +110,9 @@ const char* mlxc_last_error(void);
  *     records): R = 8 when the bits of num_nodes - 1 and of num_edges add up
  *     to at most 48 (node, row begin and degree packed in 64 bits), else 16;
  *   else 256 + 16 * num_walks (start records only);
- *   MLXC_WORK_WORDS * 8 when num_nodes or num_edges is 2^31 or more.
+ *   256 + 16 * num_walks also when num_edges is 2^31 or more (and num_nodes
+ *     below 2^31): start records with 64-bit row begins for the CSR walk;
+ *   MLXC_WORK_WORDS * 8 when num_nodes is 2^31 or more.
  * No reference counterpart (the reference allocates inside eval,
  * RandomWalk.cpp:28-29). */
 size_t mlxc_random_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges,

@@ -318,17 +318,60 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
     if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.work), static_cast<unsigned long long>(status));
 }
 
+// Start record of the wide CSR walk, for graphs of 2^31 or more CSR entries
+// (node ids below 2^31): {node, degree, row begin as int64}.  The degree
+// field holds kRecBadNode or kRecBadRow for a malformed start or row, and
+// kRecLongRow for a row of 2^31 or more entries, whose end the walk reads
+// from rowptr first.
+struct __attribute__((aligned(16))) WideStart {
+    int32_t node, deg;
+    int64_t begin;
+};
+static_assert(sizeof(WideStart) == sizeof(EdgeRecord), "both start layouts take 16 bytes a walk");
+
+// Zeroes the status words and writes one WideStart per walk (one coalesced
+// pass over start, one row read per walk).
+__global__ __launch_bounds__(kBlock) void wide_init_kernel(const int64_t* __restrict__ rowptr,
+                                                           const int64_t* __restrict__ start,
+                                                           int64_t num_nodes, int64_t num_edges,
+                                                           int64_t num_walks,
+                                                           WideStart* __restrict__ init,
+                                                           int64_t* __restrict__ work) {
+    if (blockIdx.x == 0 && threadIdx.x < MLXC_WORK_WORDS) work[threadIdx.x] = 0;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; n < num_walks;
+         n += stride) {
+        const int64_t v = start[n];
+        WideStart r{static_cast<int32_t>(v), kRecBadNode, 0};
+        if (node_ok(v, num_nodes)) {
+            const RowBounds rb = load_row(rowptr, v);
+            if (!row_ok(rb, num_edges)) {
+                r.deg = kRecBadRow;
+            } else {
+                const int64_t deg = rb.end - rb.begin;
+                r.begin = rb.begin;
+                r.deg = deg > INT32_MAX ? kRecLongRow : static_cast<int32_t>(deg);
+            }
+        }
+        init[n] = r;
+    }
+}
+
 // Uniform walk over the CSR arrays, for calls whose edge records would not
 // pay for themselves (few steps per edge) or do not fit int32.  Same loop
 // shape as the record walk — one dependent read per slot per iteration, one
 // wait — but a step costs two reads: col[e] of the chosen edge, then the row
 // of the new node.  Start records (walk_init_kernel) give the first row.
 // Requirements as for the record walk except num_edges may be any size the
-// int32 start records hold (num_nodes, num_edges below 2^31).
-template <int W, int RW, bool kGen, bool kEdges, typename OutT>
+// int32 start records hold (num_nodes, num_edges below 2^31).  kWide: graphs
+// of 2^31 or more entries (node ids still below 2^31), with WideStart records
+// and int64 edge ids, which are stored directly instead of through a window.
+template <int W, int RW, bool kGen, bool kEdges, typename OutT, bool kWide>
 __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
-                                                                  const EdgeRecord* __restrict__ init) {
+                                                                  const void* __restrict__ init_v) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4), aligned(8)));
+    typedef typename std::conditional<kWide, int64_t, int32_t>::type EIdx;
+    const EdgeRecord* const init = static_cast<const EdgeRecord*>(init_v);  // 16 bytes either way
     OutT* const nout = static_cast<OutT*>(a.n_out);
     OutT* const eout = static_cast<OutT*>(a.e_out);
     const int64_t L = a.walk_length;
@@ -339,7 +382,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
     WaveQueue q{0, 0};
     int phase[W];
     int64_t n[W], fr[W];
-    int32_t l[W], e[W], v[W];  // steps, edge and node ids fit in int32 here
+    int32_t l[W], v[W];        // steps and node ids fit in int32 here
+    EIdx e[W];                 // edge ids: int32 unless kWide
     bool need_block[W];
     LdsWindow<RW> rw[W];
     __shared__ float rand_area[W][RW][kBlock];
@@ -434,15 +478,22 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                 ew[s].count = 0;
                 v[s] = row[s].x;
                 push = true;
-                if (row[s].z == kRecBadNode) {
+                // {node, begin, degree, pad}, or WideStart {node, degree, begin}
+                const int32_t code = kWide ? row[s].y : row[s].z;
+                if (code == kRecBadNode) {
                     bad = MLXC_STATUS_BAD_NODE;
                 } else if (L == 0) {
                     flush = true;  // (the start's row is not read)
-                } else if (row[s].z < 0) {
+                } else if (kWide && code == kRecLongRow) {
+                    phase[s] = kSlotRow;  // the row's bounds come from rowptr
+                } else if (code < 0) {
                     bad = MLXC_STATUS_BAD_ROW;
                 } else {
-                    begin = row[s].y;
-                    deg = row[s].z;
+                    begin = kWide ? static_cast<int64_t>(
+                                        (static_cast<uint64_t>(static_cast<uint32_t>(row[s].w)) << 32) |
+                                        static_cast<uint32_t>(row[s].z))
+                                  : row[s].y;
+                    deg = code;
                 }
             } else if (ph[s] == kSlotCol) {
                 eg += 1;  // step l's edge was buffered at its pick
@@ -475,8 +526,11 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
             } else if (deg == 0) {
                 fill = true;  // absorbing node: the walk stays
             } else if (deg > 0) {
-                e[s] = static_cast<int32_t>(begin + pick_index(lw_take(rand_area[s], rw[s]), deg));
-                if (kEdges) ow_push(ew[s], eout, eg, e[s]);
+                e[s] = static_cast<EIdx>(begin + pick_index(lw_take(rand_area[s], rw[s]), deg));
+                if (kEdges) {
+                    if constexpr (kWide) eout[eg] = static_cast<OutT>(e[s]);
+                    else ow_push(ew[s], eout, eg, e[s]);
+                }
                 need_block[s] = rw[s].valid == 0 && l[s] + 1 < L;
                 fr[s] = n[s] * L + l[s] + 1;
                 phase[s] = kSlotCol;
@@ -484,10 +538,16 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
             if (push) ow_push(ow[s], nout, g, v[s]);
             if (fill) {
                 ow_fill(ow[s], nout, g + 1, g0 + L, v[s]);
-                if (kEdges) ow_fill(ew[s], eout, eg, e0 + L - 1, -1);
+                if (kEdges) {
+                    if constexpr (kWide) {
+                        for (int64_t j = eg; j < e0 + L; ++j) eout[j] = static_cast<OutT>(-1);
+                    } else {
+                        ow_fill(ew[s], eout, eg, e0 + L - 1, -1);
+                    }
+                }
             } else if (flush) {
                 if (ow[s].count) ow_flush(ow[s], nout, g);
-                if (kEdges && ew[s].count) ow_flush(ew[s], eout, e0 + L - 1);
+                if (kEdges && !kWide && ew[s].count) ow_flush(ew[s], eout, e0 + L - 1);
             }
             if (fill || flush) phase[s] = kSlotIdle;
         }
@@ -602,7 +662,7 @@ constexpr int32_t kLongWalk = 64;
 
 namespace {
 
-enum class UniformMode { kRecords, kCsr, kLds, kPlain };
+enum class UniformMode { kRecords, kCsr, kCsrWide, kLds, kPlain };
 
 // Edge records cost one random read per edge to build; they pay off when the
 // call takes several steps per edge, or when the graph is small enough that
@@ -637,6 +697,9 @@ UniformMode uniform_mode(const WalkArgs& a, size_t workspace_bytes, bool gen) {
             workspace_bytes >= record_bytes(a.num_nodes, a.num_edges, a.num_walks))
             return UniformMode::kRecords;
         if (workspace_bytes >= init_bytes(a.num_walks)) return UniformMode::kCsr;
+    } else if (streams_ok && a.num_nodes <= INT32_MAX &&
+               workspace_bytes >= init_bytes(a.num_walks)) {
+        return UniformMode::kCsrWide;  // 2^31 or more entries
     }
     // the LDS walk reads rand and stores its outputs one element at a time:
     // any alignment and length will do
@@ -675,9 +738,9 @@ int launch_walk_kernel(Kernel kernel, int slots, int max_per_cu, const WalkArgs&
 size_t uniform_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
                                int32_t walk_length) {
     const size_t minimum = MLXC_WORK_WORDS * sizeof(int64_t);
-    if (num_nodes < 0 || num_edges < 0 || num_walks < 0 || walk_length < 0 ||
-        !records_fit(num_nodes, num_edges))
-        return minimum;
+    if (num_nodes < 0 || num_edges < 0 || num_walks < 0 || walk_length < 0) return minimum;
+    if (!records_fit(num_nodes, num_edges))  // the wide CSR walk, while node ids fit int32
+        return num_nodes <= INT32_MAX ? init_bytes(num_walks) : minimum;
     if (lds_walk_fits(num_nodes, num_edges, num_walks, walk_length))
         return kRecordOffset;  // the LDS walk: its size selects it
     return records_pay_off(num_edges, num_walks, walk_length)
@@ -721,10 +784,21 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
         if (int rc = launch_walk_init(a.rowptr, a.start, a.num_nodes, a.num_edges, a.num_walks,
                                       init, a.work, stream))
             return rc;
-        return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW, kGen, kEdges, OutT>,
+        return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW, kGen, kEdges, OutT, false>,
                                   MLXC_CSR_SLOTS, MLXC_CSR_BLOCKS_PER_CU, a,
                                   stream,
-                                  static_cast<const EdgeRecord*>(init));
+                                  static_cast<const void*>(init));
+    }
+    case UniformMode::kCsrWide: {
+        WideStart* init = reinterpret_cast<WideStart*>(recs);  // 16 bytes per walk, as EdgeRecord
+        int grid = 0;
+        if (int rc = stream_grid(a.num_walks, 16, grid)) return rc;
+        hipLaunchKernelGGL(wide_init_kernel, dim3(grid), dim3(kBlock), 0, stream, a.rowptr, a.start,
+                           a.num_nodes, a.num_edges, a.num_walks, init, a.work);
+        MLXC_HIP_TRY(hipGetLastError());
+        return launch_walk_kernel(uniform_walk_csr_kernel<MLXC_CSR_SLOTS, RW, kGen, kEdges, OutT, true>,
+                                  MLXC_CSR_SLOTS, MLXC_CSR_BLOCKS_PER_CU, a, stream,
+                                  static_cast<const void*>(init));
     }
     case UniformMode::kLds: {
         if (int rc = launch_zero_work(a.work, stream)) return rc;

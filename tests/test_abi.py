@@ -140,7 +140,8 @@ def test_window_launches_beyond_the_grid_limit_are_rejected():
 def test_workspace_size_query():
     """Edge and start records take 8 bytes each when node ids, row begins and
     at least 16 bits of degree pack into 64 bits, else 16; start records
-    alone (the CSR walk) always take 16."""
+    alone (the CSR walk, and the wide CSR walk of graphs with 2^31 or more
+    entries) always take 16."""
     q = _lib.load().mlxc_random_walk_workspace_bytes
     E = 10**6                                     # above the small-graph size 32768 * 4
     assert q(10, E, E, 4) == 256 + 8 * 2 * E      # 4E steps >= 4 * E edges: records
@@ -161,8 +162,9 @@ def test_workspace_size_query():
     assert q(1 << 24, 1 << 24, 1 << 24, 4) == 256 + 16 * 2 * (1 << 24)
     assert q((1 << 24) + 1, (1 << 24) - 1, 1 << 24, 4) == 256 + 16 * ((1 << 24) - 1 + (1 << 24))
     assert q(2**31 - 1, E, E, 4) == 256 + 16 * 2 * E
-    assert q(2**31, 5, 1, 1) == 32
-    assert q(5, 2**31, 1, 1) == 32
+    assert q(2**31, 5, 1, 1) == 32                 # node ids beyond int32: the plain walk
+    assert q(5, 2**31, 3, 1) == 256 + 16 * 3       # 2^31 entries: the wide CSR walk's starts
+    assert q(2**31, 2**31, 3, 1) == 32
     assert q(-1, 5, 1, 1) == 32
     assert q(5, 5, -1, 1) == 32
     assert q(5, 5, 1, -1) == 32

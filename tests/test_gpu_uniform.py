@@ -543,3 +543,88 @@ def test_lds_walk_flags_bad_input(cuda):
     # the same graph, well formed: no error
     n = mc.random_walk(t(rowptr), t(col), t([0, 1]), rand, 3)
     np.testing.assert_array_equal(n.cpu().numpy(), [[0, 1, 2, 3], [1, 2, 3, 0]])
+
+
+def _check_steps(rowptr, col, rand, n, e, L):
+    """Mismatches between the walks and their steps re-derived with torch
+    float32 arithmetic on the device (RandomWalk.cpp:45-58: the degree
+    rounded to float32, multiplied by r, truncated)."""
+    bad = 0
+    for l in range(L):
+        u, v = n[:, l], n[:, l + 1]
+        rs = rowptr[u]
+        deg = rowptr[u + 1] - rs
+        idx = torch.minimum((rand[:, l] * deg.to(torch.float32)).to(torch.int64),
+                            (deg - 1).clamp_min(0))
+        moving = deg > 0
+        edge = torch.where(moving, rs + idx, -1)
+        expect = torch.where(moving, col[edge.clamp_min(0)], u)
+        bad += int((expect != v).sum()) + int((edge != e[:, l]).sum())
+    return bad
+
+
+def test_graph_beyond_int32_edge_ids(cuda):
+    """A graph of 2^31 + 2^20 CSR entries (2^20 nodes of degree 2049, 17.2 GB
+    of col): the workspace query asks for 16-byte start records, and the
+    wide CSR walk runs with int64 edge ids.  Every step and edge id is
+    re-derived on the device, the unwindowed kernel gives the same walks and
+    edges, and 2,000 walks are bit-exact against the oracle; a bad col entry
+    and a bad rowptr entry met by a walk raise.  Then a row of 2^31 + 5
+    entries: its start record marks it long, the walk reads its bounds from
+    rowptr and picks with the float32 rule's rounded degree."""
+    from mlx_cluster_amd import _lib
+    q = _lib.load().mlxc_random_walk_workspace_bytes
+    V, deg, L = 1 << 20, 2049, 20
+    E = V * deg
+    assert E > 2**31 - 1
+    rowptr = torch.arange(V + 1, device=cuda, dtype=torch.int64) * deg
+    g = torch.Generator(device=cuda).manual_seed(11)
+    col = torch.randint(0, V, (E,), device=cuda, generator=g, dtype=torch.int64)
+    N = V
+    start = torch.arange(N, device=cuda, dtype=torch.int64)
+    rand = mc.philox_uniform((N, L), 7, device=cuda)
+    assert q(V, E, N, L) == 256 + 16 * N
+    n, e = mc.random_walk(rowptr, col, start, rand, L, return_edges=True)
+    assert torch.equal(n[:, 0], start)
+    assert _check_steps(rowptr, col, rand, n, e, L) == 0
+    assert int(e.max()) > 2**31  # edge ids beyond int32
+    n2, e2 = torch.empty_like(n), torch.empty_like(e)
+    _abi_walk(rowptr, col, start, rand.data_ptr(), L, n2.data_ptr(), e_out=e2, ws_bytes=32)
+    assert torch.equal(n2, n) and torch.equal(e2, e)
+    del n2, e2
+    sample = torch.randint(0, N, (2000,), generator=torch.Generator().manual_seed(3)).to(cuda)
+    rp, cl = rowptr.cpu().numpy(), col.cpu().numpy()
+    n_ref, e_ref, st, _ = oracle.uniform_walk(rp, cl, start[sample].cpu().numpy(),
+                                              rand[sample].cpu().numpy(), L, with_edges=True)
+    assert st == 0
+    np.testing.assert_array_equal(n[sample].cpu().numpy(), n_ref)
+    np.testing.assert_array_equal(e[sample].cpu().numpy(), e_ref)
+    del cl, rp
+    # malformed input met by a walk: walk 0's first edge, then its start's row
+    first = int(e[0, 0])
+    col[first] = V
+    with pytest.raises(ValueError, match="outside"):
+        mc.random_walk(rowptr, col, start[:64], rand[:64], L)
+    col[first] = 0
+    rowptr[1] = E + 1
+    with pytest.raises(ValueError, match="rowptr"):
+        mc.random_walk(rowptr, col, start[:64], rand[:64], L)
+    del col, n, e, rowptr
+    torch.cuda.empty_cache()
+
+    # one row of 2^31 + 5 entries (node 0) and one of 3 (node 1)
+    E2 = 2**31 + 8
+    rowptr = torch.tensor([0, E2 - 3, E2], device=cuda, dtype=torch.int64)
+    col = torch.randint(0, 2, (E2,), device=cuda, generator=g, dtype=torch.int64)
+    N, L = 4096, 6
+    start = torch.arange(N, device=cuda, dtype=torch.int64) % 2
+    rand = mc.philox_uniform((N, L), 8, device=cuda)
+    assert q(2, E2, N, L) == 256 + 16 * N
+    n, e = mc.random_walk(rowptr, col, start, rand, L, return_edges=True)
+    assert _check_steps(rowptr, col, rand, n, e, L) == 0
+    assert int(e[start == 0, 0].max()) > 2**30  # first steps spread over the long row
+    n2, e2 = torch.empty_like(n), torch.empty_like(e)
+    _abi_walk(rowptr, col, start, rand.data_ptr(), L, n2.data_ptr(), e_out=e2, ws_bytes=32)
+    assert torch.equal(n2, n) and torch.equal(e2, e)
+    del col, n, e, n2, e2
+    torch.cuda.empty_cache()
