@@ -568,8 +568,9 @@ def test_graph_beyond_int32_edge_ids(cuda):
     of col): the workspace query asks for 16-byte start records, and the
     wide CSR walk runs with int64 edge ids.  Every step and edge id is
     re-derived on the device, the unwindowed kernel gives the same walks and
-    edges, and 2,000 walks are bit-exact against the oracle; a bad col entry
-    and a bad rowptr entry met by a walk raise.  Then a row of 2^31 + 5
+    edges, and 2,000 walks are bit-exact against the oracle; 4,096 node2vec
+    walks (the direct kernel, linear scans of the unsorted rows) are too; a
+    bad col entry and a bad rowptr entry met by a walk raise.  Then a row of 2^31 + 5
     entries: its start record marks it long, the walk reads its bounds from
     rowptr and picks with the float32 rule's rounded degree."""
     from mlx_cluster_amd import _lib
@@ -599,7 +600,16 @@ def test_graph_beyond_int32_edge_ids(cuda):
     assert st == 0
     np.testing.assert_array_equal(n[sample].cpu().numpy(), n_ref)
     np.testing.assert_array_equal(e[sample].cpu().numpy(), e_ref)
-    del cl, rp
+    # node2vec on the same graph takes its direct kernel (int64 positions);
+    # the rows are unsorted, so the device check picks linear scans
+    w = mc.rejection_sampling(rowptr, col, start[:4096], 5, 0.5, 2.0, seed=13, return_edges=True)
+    w_ref, we_ref, st, _ = oracle.node2vec_walk(rp, cl, start[:4096].cpu().numpy(), 5, 0.5, 2.0,
+                                                13, rule=oracle.RULE_REF_CHAIN, rows_sorted=False,
+                                                with_edges=True)
+    assert st == 0
+    np.testing.assert_array_equal(w[0].cpu().numpy(), w_ref)
+    np.testing.assert_array_equal(w[1].cpu().numpy(), we_ref)
+    del cl, rp, w
     # malformed input met by a walk: walk 0's first edge, then its start's row
     first = int(e[0, 0])
     col[first] = V
