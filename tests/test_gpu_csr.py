@@ -1,6 +1,8 @@
 """Parity of the HIP CSR build (mlxc_csr_build, via to_csr on a GPU) with the
 oracle's restatement of the reference tests' pipeline
 (tests/test_random_walk.py:23-28): bit-exact rowptr and col."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -189,3 +191,49 @@ def test_c4_full_size_properties(cuda):
     out_key = out_row * V + c
     assert bool((out_key[1:] > out_key[:-1]).all())
     assert torch.equal(out_key, key)
+
+
+def test_build_beyond_int32_entries(cuda):
+    """A build whose input and output both pass int32 positions, against an
+    answer known in closed form (torch's unique and boolean indexing are not
+    usable at this size): the n = 2^31 + 2^20 distinct keys
+    k_j = j * 2^16 + 12345 (row k >> 24 of 2^24 nodes, 256 entries a row),
+    laid out in the order pi(i) = (a * i + b) mod n with a coprime to n, then
+    2^20 of them repeated: 2^31 + 2^21 pairs, two 17 GB arrays.  Sorting and
+    deduplicating must give col = k_j mod 2^24 for every j and
+    rowptr = min(256 * r, n)."""
+    from mlx_cluster_amd import _lib
+    lib = _lib.load()
+    V = 1 << 24
+    n, dup = (1 << 31) + (1 << 20), 1 << 20
+    E = n + dup
+    a, b = 1_000_000_007, 77_777
+    assert math.gcd(a, n) == 1
+    pos = torch.arange(E, device=cuda, dtype=torch.int64)
+    j = torch.where(pos < n, (pos * a + b) % n, pos - n)  # a * i < 2^63
+    del pos
+    key = j * (1 << 16) + 12345
+    del j
+    row, col = key >> 24, key & (V - 1)
+    del key
+    flags = _lib.MLXC_CSR_DEDUP
+    nbytes = lib.mlxc_csr_build_workspace_bytes(V, E, flags)
+    work = torch.empty((nbytes + 7) // 8, dtype=torch.int64, device=cuda)
+    rowptr = torch.empty(V + 1, dtype=torch.int64, device=cuda)
+    out = torch.empty(E, dtype=torch.int64, device=cuda)
+    rc = lib.mlxc_csr_build(row.data_ptr(), col.data_ptr(), E, V, flags, rowptr.data_ptr(),
+                            out.data_ptr(), work.data_ptr(), nbytes,
+                            torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    bits, count = (int(x) for x in work[:2].tolist())
+    del work, row, col
+    torch.cuda.empty_cache()
+    assert bits == 0 and count == n
+    expect_rowptr = torch.clamp(torch.arange(V + 1, device=cuda, dtype=torch.int64) * 256, max=n)
+    assert torch.equal(rowptr, expect_rowptr)
+    del expect_rowptr
+    expect_col = (torch.arange(n, device=cuda, dtype=torch.int64) * (1 << 16) + 12345) & (V - 1)
+    assert torch.equal(out[:n], expect_col)
+    del expect_col, out, rowptr
+    torch.cuda.empty_cache()
