@@ -346,8 +346,9 @@ int mlxc_negative_windows_cpu(const int64_t* start, int64_t num_walks, int32_t w
 
 /*
  * Host twins of the three walk entry points: the same walks, the same
- * arguments with host pointers, evaluated on `threads` CPU threads (<= 0:
- * one per hardware thread) and returning when done.  Outputs are
+ * arguments with host pointers, evaluated on up to `threads` CPU threads
+ * (<= 0: one per hardware thread; small calls use fewer, since starting a
+ * thread costs more than thousands of steps) and returning when done.  Outputs are
  * bit-identical to the device entry points for the same inputs and seed.
  * *status (may be NULL) receives the MLXC_STATUS_* bits that the device
  * entry points leave in workspace word 0; no workspace is needed.

@@ -105,6 +105,20 @@ int resolve_threads(int32_t threads) {
 
 constexpr int64_t kHostChunk = 1024;  // walks per chunk
 
+// Threads worth starting for a call of `steps` walk steps: starting one costs
+// tens of microseconds, as much as ~3,000 uniform steps, so small calls (the
+// reference tests' 2,000 walks of 5 steps) run on fewer threads than allowed.
+// Measured on an 8-core host with the Cora-like graph: a uniform call of
+// 10,000 steps 127 us on one thread against 180 us on eight; a node2vec call
+// of 10,000 steps (about 18,000 trials and linear row scans) 700 us on two
+// against 1,000 us on one.
+constexpr int64_t kUniformStepsPerThread = int64_t{1} << 16;
+constexpr int64_t kNode2vecStepsPerThread = int64_t{1} << 12;
+int threads_for(int allowed, int64_t steps, int64_t steps_per_thread) {
+    const int64_t useful = steps / steps_per_thread;
+    return useful < 1 ? 1 : useful < allowed ? static_cast<int>(useful) : allowed;
+}
+
 // Uniform walks [first, last): the loop of RandomWalk.cpp:41-60, with the
 // out-of-range handling of uniform_walk_kernel (the walk stops and repeats
 // its node, edge id -1).
@@ -393,19 +407,22 @@ void host_negative_windows(const int64_t* start, int64_t num_walks, int32_t walk
 }
 
 int host_uniform(const HostWalk& w, bool generate, int32_t threads, uint32_t& status) {
-    const int t = resolve_threads(threads);
+    const int t = threads_for(resolve_threads(threads), w.num_walks * w.walk_length,
+                              kUniformStepsPerThread);
     return w.out_type == MLXC_OUT_INT32 ? host_uniform_typed<int32_t>(w, generate, t, status)
                                         : host_uniform_typed<int64_t>(w, generate, t, status);
 }
 
 int host_node2vec(const HostWalk& w, const N2VParams& prm, int32_t threads, uint32_t& status) {
-    const int t = resolve_threads(threads);
-    // the whole CSR is validated on every call, as the device layouts do
+    const int all = resolve_threads(threads);
+    const int t = threads_for(all, w.num_walks * w.walk_length, kNode2vecStepsPerThread);
+    // the whole CSR is validated on every call, as the device layouts do (its
+    // chunks of 2^16 entries set how many of the threads it uses)
     uint32_t prep = 0;
     bool sorted = prm.rows == MLXC_ROWS_SORTED;
     if (w.num_walks > 0) {
         bool detected = false;
-        prep = host_csr_scan(w, t, detected);
+        prep = host_csr_scan(w, all, detected);
         if (prm.rows == MLXC_ROWS_DETECT) sorted = detected;
     }
     const int rc = w.out_type == MLXC_OUT_INT32

@@ -250,8 +250,8 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
             rowptr entry was out of range (the reference reads out of bounds
             there).  With check=False the call stays asynchronous.
         seed: key of the generated uniforms when rand is None.
-        threads: CPU threads for stream='cpu' (None: one per hardware
-            thread); ignored on the GPU.
+        threads: the most CPU threads stream='cpu' may use (None: one per
+            hardware thread; small calls use fewer); ignored on the GPU.
         out_dtype: torch.int64 (the reference's output) or torch.int32, a
             compact output with half the bytes (node ids, and edge ids with
             return_edges, must be below 2^31).
