@@ -219,7 +219,9 @@ def cpu_all_cores_context(np, torch, mc, kind, rowptr_h, col_h, start, rand, L, 
                               rule=extra["rule"], rows_sorted=True, stream="cpu", threads=threads)
     dt = time.perf_counter() - t0
     return {"value": walks * L / dt, "unit": "walk-steps/s", "threads": threads,
-            "seconds": dt, "what": "mlx_cluster_amd host twin (stream='cpu'), same sample"}
+            "seconds": dt,
+            "what": "mlx_cluster_amd host twin (stream='cpu'), same sample, on up to `threads` "
+                    "threads (small calls use fewer: one per 2^16 uniform or 2^12 node2vec steps)"}
 
 
 def gather_ceiling(torch, dev):
