@@ -14,6 +14,15 @@ struct N2VArgs {
     int32_t rows;  // MLXC_ROWS_*; DETECT: work[2] != 0 when the rows are sorted
 };
 
+// Entries per round of the direct kernel's scan of an unsorted row (one
+// 128-byte line of int64).  Configuration 3's graph with every row scanned
+// (2^18 walks of 10 steps) on MI355X: 152, 112 and 104 ms with rounds of 4,
+// 8 and 16 entries, 256 ms one entry at a time.
+#ifndef MLXC_SCAN_ROUND
+#define MLXC_SCAN_ROUND 16
+#endif
+constexpr int kScanRound = MLXC_SCAN_ROUND;
+
 // Is t in row(x)?  BiasedRandomWalk.cpp:20-28 scans the row linearly; on a
 // sorted row lower_bound gives the same answer in log2(deg) probes.
 __device__ __forceinline__ bool is_neighbor(const int64_t* __restrict__ rowptr,
@@ -25,8 +34,19 @@ __device__ __forceinline__ bool is_neighbor(const int64_t* __restrict__ rowptr,
         return false;
     }
     if (!sorted) {
-        for (int64_t i = rb.begin; i < rb.end; ++i)
-            if (col[i] == t) return true;
+        // kScanRound entries per round, loaded unconditionally (indices past
+        // the row's end are clamped to its last entry): the loads are
+        // independent, so a round costs one memory round trip, where one
+        // entry at a time waits for each load
+        for (int64_t i = rb.begin; i < rb.end; i += kScanRound) {
+            int64_t v[kScanRound];
+#pragma unroll
+            for (int k = 0; k < kScanRound; ++k) v[k] = col[i + k < rb.end ? i + k : rb.end - 1];
+            bool hit = false;
+#pragma unroll
+            for (int k = 0; k < kScanRound; ++k) hit |= v[k] == t;  // (a clamped entry repeats one in the row)
+            if (hit) return true;
+        }
         return false;
     }
     int64_t lo = rb.begin, count = rb.end - rb.begin;
