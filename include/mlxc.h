@@ -263,8 +263,9 @@ int mlxc_philox_uniform(float* d_out, int64_t n, uint64_t seed, void* stream);
 /* Workspace bytes mlxc_csr_build needs (at least 16-byte aligned): two key
  * arrays of 4 bytes per entry (5 when num_nodes > 65536, 6 when num_nodes >
  * 2^20, 8 when num_nodes > 2^24), entries = num_edges, or 2 * num_edges with
- * MLXC_CSR_SYMMETRIZE, plus 1 byte per entry of digits and 8 bytes per 16
- * entries of digit counts.  No reference counterpart. */
+ * MLXC_CSR_SYMMETRIZE, plus 1 byte per entry of digits, 8 bytes per 16
+ * entries of digit counts and a few KB of totals and block sums.  No
+ * reference counterpart. */
 size_t mlxc_csr_build_workspace_bytes(int64_t num_nodes, int64_t num_edges, int32_t flags);
 
 /*

@@ -11,11 +11,13 @@
 // else in 8.  Each pass is three launches and needs no inter-block waiting:
 //   radix_hist_kernel     per 8192-key tile, a 256-digit histogram, written
 //                         digit-major (hist[d * tiles + tile]);
-//   scan_*                one exclusive scan of that array, which turns it
-//                         into every (digit, tile)'s first output position;
+//   row_scan_kernel       an exclusive scan of each digit's row of tile
+//                         counts, one block per digit, and the digit totals;
 //   radix_scatter_kernel  stable rank of each key inside its tile (wavefront
 //                         match of the digit), reorder of the tile in LDS,
-//                         then stores in digit runs.
+//                         then stores in digit runs; a (digit, tile)'s first
+//                         output position is its row prefix plus the digit
+//                         totals before it.
 // Each scatter also writes every key's digit of the next pass into a byte
 // array beside the keys, so that the next histogram reads 1 byte per key
 // instead of the key.  The first pass reads the caller's (row, col) arrays
@@ -314,7 +316,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(EdgeSrc src,
 template <typename Store, bool kFirst>
 __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4))) void radix_scatter_kernel(
     EdgeSrc src, Store keys_in, Store keys_out, int shift,
-    int64_t total, int64_t tiles, const int64_t* __restrict__ offsets, int64_t* __restrict__ work,
+    int64_t total, int64_t tiles, const int64_t* __restrict__ offsets,
+    const int64_t* __restrict__ digit_totals, int64_t* __restrict__ work,
     uint8_t* __restrict__ next_digits, int next_shift) {
     using KeyT = typename Store::K;
     __shared__ KeyT buf[kSortTile];
@@ -325,6 +328,8 @@ __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4)
     const int64_t tile = xcd_tile(blockIdx.x, tiles);
     for (int k = t; k < kSortWaves * kRadix; k += kSortThreads) (&cnt[0][0])[k] = 0;
     if (t < kRadix) goff[t] = offsets[static_cast<int64_t>(t) * tiles + tile];
+    // read now, used after the ranking: the load overlaps the key loads
+    const int64_t dtot = digit_totals && t < kRadix ? digit_totals[t] : 0;
     __syncthreads();
 
     // Rank of every key among the keys of its digit that come before it in
@@ -352,18 +357,29 @@ __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4)
 
     // Thread t < 256 owns digit t: its first position in the reordered tile,
     // and the first position of each wavefront's keys of that digit.
+    // offsets[] holds each tile's position inside its digit's output range;
+    // the ranges start at the exclusive prefix of digit_totals (with no
+    // digit_totals, offsets[] holds the whole position).  Both
+    // prefixes come from one scan: the tile counts (at most kSortTile, whose
+    // sum fits kTileBits) in the low bits, the digit totals above them.
+    constexpr int kTileBits = 14;
+    static_assert(kSortTile < (1 << kTileBits), "tile counts fit the low field");
     int32_t c[kSortWaves];
     int32_t tot = 0;
+    int64_t packed = 0;
     if (t < kRadix) {
 #pragma unroll
         for (int k = 0; k < kSortWaves; ++k) {
             c[k] = cnt[k][t];
             tot += c[k];
         }
+        packed = (dtot << kTileBits) | tot;
     }
-    int32_t at = static_cast<int32_t>(block_exclusive_scan<kOpSum, kSortThreads>(tot, wtot));
+    const int64_t ex = block_exclusive_scan<kOpSum, kSortThreads>(packed, wtot);
+    int32_t at = static_cast<int32_t>(ex & ((1 << kTileBits) - 1));
     if (t < kRadix) {
-        goff[t] -= at;  // output position of tile entry j of digit t: goff[t] + j
+        // output position of tile entry j of digit t: goff[t] + j
+        goff[t] += (ex >> kTileBits) - at;
 #pragma unroll
         for (int k = 0; k < kSortWaves; ++k) {
             cnt[k][t] = at;
@@ -394,6 +410,60 @@ __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4)
 }
 
 // ------------------------------------------------------------- device scan
+
+// Exclusive sum scan of each of gridDim.x rows of len values, in place, one
+// block per row; totals[row] <- the row's sum.  The digit counts are 256 such
+// rows (digit-major), so one launch replaces the three of a scan over the
+// whole array.  Each chunk's loads are issued before the previous chunk is
+// scanned.
+__global__ __launch_bounds__(kBlock) void row_scan_kernel(int64_t* __restrict__ data, int64_t len,
+                                                          int64_t* __restrict__ totals) {
+    __shared__ int64_t vals[kChunk + kChunk / kItems];
+    __shared__ int64_t wtot[kWaves];
+    const int t = threadIdx.x;
+    int64_t* row = data + static_cast<int64_t>(blockIdx.x) * len;
+    auto slot = [](int j) { return j + j / kItems; };
+    int64_t next[kItems];
+#pragma unroll
+    for (int s = 0; s < kItems; ++s) {
+        const int64_t j = s * kBlock + t;
+        next[s] = j < len ? row[j] : 0;
+    }
+    int64_t carry = 0;
+    for (int64_t base = 0; base < len; base += kChunk) {
+#pragma unroll
+        for (int s = 0; s < kItems; ++s) vals[slot(s * kBlock + t)] = next[s];
+        __syncthreads();
+        if (base + kChunk < len) {
+#pragma unroll
+            for (int s = 0; s < kItems; ++s) {
+                const int64_t j = base + kChunk + s * kBlock + t;
+                next[s] = j < len ? row[j] : 0;
+            }
+        }
+        int64_t run = 0;
+#pragma unroll
+        for (int s = 0; s < kItems; ++s) run += vals[slot(t * kItems + s)];
+        int64_t total;
+        int64_t acc = carry + block_exclusive_scan<kOpSum>(run, wtot, &total);
+#pragma unroll
+        for (int s = 0; s < kItems; ++s) {
+            const int j = slot(t * kItems + s);
+            const int64_t v = vals[j];
+            vals[j] = acc;
+            acc += v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < kItems; ++s) {
+            const int64_t j = base + s * kBlock + t;
+            if (j < len) row[j] = vals[slot(s * kBlock + t)];
+        }
+        carry += total;
+        __syncthreads();
+    }
+    if (t == 0) totals[blockIdx.x] = carry;
+}
 // In place over n int64 values, chunks of kChunk per block.  kRev scans from
 // the end (logical element j is data[n - 1 - j]).
 
@@ -617,7 +687,7 @@ struct CsrLayout {
     int64_t chunks = 0;  // finish chunks of kChunk keys
     size_t keys[2] = {0, 0};  // the two key arrays (Keys40 / Keys48: low halves)
     size_t keys_hi[2] = {0, 0};  // Keys40 / Keys48: the high bits
-    size_t digits = 0, hist = 0, sums = 0, bytes = 0;
+    size_t digits = 0, hist = 0, totals = 0, sums = 0, bytes = 0;
 };
 
 CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
@@ -650,11 +720,26 @@ CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
     at += round256(static_cast<size_t>(l.tiles) * kSortTile);
     l.hist = at;
     at += round256(static_cast<size_t>(hist_n) * sizeof(int64_t));
+    l.totals = at;  // the digit totals of a pass
+    at += round256(kRadix * sizeof(int64_t));
     l.sums = at;
     at += round256(static_cast<size_t>(chunks + 1) * sizeof(int64_t));
     l.bytes = at;
     return l;
 }
+
+// Up to this many values, one block scans faster than the three launches of
+// device_scan.
+#ifndef MLXC_ROW_SCAN_MAX
+#define MLXC_ROW_SCAN_MAX (4 * kChunk)
+#endif
+constexpr int64_t kRowScanMax = MLXC_ROW_SCAN_MAX;
+// The digit counts are scanned by rows (one block per digit) up to this many
+// tiles per row.
+#ifndef MLXC_ROW_SCAN_TILES
+#define MLXC_ROW_SCAN_TILES kChunk
+#endif
+constexpr int64_t kRowScanTiles = MLXC_ROW_SCAN_TILES;
 
 template <int kOp, bool kRev, bool kExcl>
 int device_scan(int64_t* data, int64_t n, int64_t* sums, int64_t* total_out, hipStream_t s) {
@@ -699,6 +784,7 @@ int csr_build_typed(const EdgeSrc& src, const CsrLayout& l, int32_t flags, int64
     int64_t* work = reinterpret_cast<int64_t*>(ws);
     const Store buf[2] = {key_store(ws, l, 0, Store{}), key_store(ws, l, 1, Store{})};
     int64_t* hist = reinterpret_cast<int64_t*>(ws + l.hist);
+    int64_t* totals = reinterpret_cast<int64_t*>(ws + l.totals);
     int64_t* sums = reinterpret_cast<int64_t*>(ws + l.sums);
     uint8_t* digits = reinterpret_cast<uint8_t*>(ws + l.digits);
     Store in{};
@@ -713,16 +799,23 @@ int csr_build_typed(const EdgeSrc& src, const CsrLayout& l, int32_t flags, int64
             hipLaunchKernelGGL((radix_hist_kernel<Store, false>), dim3(l.tiles), dim3(kSortThreads), 0, s,
                                src, digits, shift, l.total, l.tiles, hist, work);
         MLXC_HIP_TRY(hipGetLastError());
-        if (int rc = device_scan<kOpSum, false, true>(hist, kRadix * l.tiles, sums, nullptr, s))
+        // short rows: one block per digit; long rows: a scan of the whole
+        // array, which spreads each row over many blocks
+        const bool by_rows = l.tiles <= kRowScanTiles;
+        if (by_rows)
+            hipLaunchKernelGGL(row_scan_kernel, dim3(kRadix), dim3(kBlock), 0, s, hist, l.tiles,
+                               totals);
+        else if (int rc = device_scan<kOpSum, false, true>(hist, kRadix * l.tiles, sums, nullptr, s))
             return rc;
+        const int64_t* digit_totals = by_rows ? totals : nullptr;
         if (p == 0)
             hipLaunchKernelGGL((radix_scatter_kernel<Store, true>), dim3(l.tiles), dim3(kSortThreads), 0,
-                               s, src, in, out, shift, l.total, l.tiles, hist, work, next_digits,
-                               shift + kRadixBits);
+                               s, src, in, out, shift, l.total, l.tiles, hist, digit_totals, work,
+                               next_digits, shift + kRadixBits);
         else
             hipLaunchKernelGGL((radix_scatter_kernel<Store, false>), dim3(l.tiles), dim3(kSortThreads), 0,
-                               s, src, in, out, shift, l.total, l.tiles, hist, work, next_digits,
-                               shift + kRadixBits);
+                               s, src, in, out, shift, l.total, l.tiles, hist, digit_totals, work,
+                               next_digits, shift + kRadixBits);
         MLXC_HIP_TRY(hipGetLastError());
         in = out;
     }
@@ -735,8 +828,12 @@ int csr_build_typed(const EdgeSrc& src, const CsrLayout& l, int32_t flags, int64
         hipLaunchKernelGGL((dedup_count_kernel<Store>), dim3(chunks), dim3(kBlock), 0, s, in,
                            l.total, chunk_base);
         MLXC_HIP_TRY(hipGetLastError());
-        if (int rc = device_scan<kOpSum, false, true>(chunk_base, chunks, sums, work + 1, s))
+        if (chunks <= kRowScanMax) {
+            hipLaunchKernelGGL(row_scan_kernel, dim3(1), dim3(kBlock), 0, s, chunk_base, chunks,
+                               work + 1);
+        } else if (int rc = device_scan<kOpSum, false, true>(chunk_base, chunks, sums, work + 1, s)) {
             return rc;
+        }
     } else {
         hipLaunchKernelGGL(set_word_kernel, dim3(1), dim3(kWave), 0, s, work + 1, l.total);
     }
