@@ -8,11 +8,14 @@
 // bits(num_nodes - 1), sorting only the 2 * cbits bits that can be non-zero,
 // 8 bits per pass.  Keys are stored in 4 bytes when they fit (num_nodes <=
 // 65536), in 5 or 6 (a 32-bit and an 8- or 16-bit array) up to 40 or 48 bits,
-// else in 8.  Each pass is three launches and needs no inter-block waiting:
+// else in 8.  Each pass is three launches (five when rows of counts are long,
+// below) and needs no inter-block waiting:
 //   radix_hist_kernel     per 8192-key tile, a 256-digit histogram, written
 //                         digit-major (hist[d * tiles + tile]);
 //   row_scan_kernel       an exclusive scan of each digit's row of tile
-//                         counts, one block per digit, and the digit totals;
+//                         counts, one block per digit, and the digit totals
+//                         (rows over kRowScanTiles tiles: a scan of the whole
+//                         array, three launches, positions included);
 //   radix_scatter_kernel  stable rank of each key inside its tile (wavefront
 //                         match of the digit), reorder of the tile in LDS,
 //                         then stores in digit runs; a (digit, tile)'s first
