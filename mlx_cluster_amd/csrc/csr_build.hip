@@ -8,14 +8,14 @@
 // bits(num_nodes - 1), sorting only the 2 * cbits bits that can be non-zero,
 // 8 bits per pass.  Keys are stored in 4 bytes when they fit (num_nodes <=
 // 65536), in 5 or 6 (a 32-bit and an 8- or 16-bit array) up to 40 or 48 bits,
-// else in 8.  Each pass is three launches (five when rows of counts are long,
+// else in 8.  Each pass is three launches (four when rows of counts are long,
 // below) and needs no inter-block waiting:
 //   radix_hist_kernel     per 8192-key tile, a 256-digit histogram, written
 //                         digit-major (hist[d * tiles + tile]);
 //   row_scan_kernel       an exclusive scan of each digit's row of tile
 //                         counts, one block per digit, and the digit totals
 //                         (rows over kRowScanTiles tiles: a scan of the whole
-//                         array, three launches, positions included);
+//                         array, two launches, positions included);
 //   radix_scatter_kernel  stable rank of each key inside its tile (wavefront
 //                         match of the digit), reorder of the tile in LDS,
 //                         then stores in digit runs; a (digit, tile)'s first
@@ -490,27 +490,14 @@ __global__ __launch_bounds__(kBlock) void scan_reduce_kernel(const int64_t* __re
     if (threadIdx.x == 0) sums[blockIdx.x] = total;
 }
 
-// One block: sums[b] <- reduction of sums[0..b) (exclusive); *total_out (if
-// given) <- reduction of all nb values.
-template <int kOp>
-__global__ __launch_bounds__(kBlock) void scan_top_kernel(int64_t* __restrict__ sums, int64_t nb,
-                                                          int64_t* __restrict__ total_out) {
-    __shared__ int64_t wtot[kWaves];
-    int64_t carry = op_identity<kOp>();
-    for (int64_t base = 0; base < nb; base += kBlock) {
-        const int64_t j = base + threadIdx.x;
-        const int64_t v = j < nb ? sums[j] : op_identity<kOp>();
-        int64_t total;
-        const int64_t ex = block_exclusive_scan<kOp>(v, wtot, &total);
-        if (j < nb) sums[j] = op_apply<kOp>(carry, ex);
-        carry = op_apply<kOp>(carry, total);
-    }
-    if (total_out && threadIdx.x == 0) *total_out = carry;
-}
-
 template <int kOp, bool kRev, bool kExcl>
+// Each block reduces the chunk sums of the blocks before it itself (at most a
+// few thousand values, read from L2), so no single-block launch has to scan
+// them in between; the last block writes the whole reduction to *total_out
+// (if given).
 __global__ __launch_bounds__(kBlock) void scan_down_kernel(int64_t* __restrict__ data, int64_t n,
-                                                           const int64_t* __restrict__ sums) {
+                                                           const int64_t* __restrict__ sums,
+                                                           int64_t* __restrict__ total_out) {
     // Padded so that thread t's 16 consecutive values sit in distinct banks.
     __shared__ int64_t vals[kChunk + kChunk / kItems];
     __shared__ int64_t wtot[kWaves];
@@ -521,10 +508,15 @@ __global__ __launch_bounds__(kBlock) void scan_down_kernel(int64_t* __restrict__
         const int j = s * kBlock + t;
         vals[slot(j)] = scan_load<kOp, kRev>(data, n, base + j);
     }
-    __syncthreads();
+    int64_t part = op_identity<kOp>();
+    for (int64_t k = t; k < blockIdx.x; k += kBlock) part = op_apply<kOp>(part, sums[k]);
+    int64_t carry;
+    block_exclusive_scan<kOp>(part, wtot, &carry);  // its two barriers also cover vals
     int64_t run = op_identity<kOp>();
     for (int s = 0; s < kItems; ++s) run = op_apply<kOp>(run, vals[slot(t * kItems + s)]);
-    int64_t acc = op_apply<kOp>(sums[blockIdx.x], block_exclusive_scan<kOp>(run, wtot));
+    int64_t own;
+    int64_t acc = op_apply<kOp>(carry, block_exclusive_scan<kOp>(run, wtot, &own));
+    if (total_out && t == 0 && blockIdx.x == gridDim.x - 1) *total_out = op_apply<kOp>(carry, own);
     for (int s = 0; s < kItems; ++s) {
         const int j = slot(t * kItems + s);
         const int64_t v = vals[j];
@@ -731,7 +723,7 @@ CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
     return l;
 }
 
-// Up to this many values, one block scans faster than the three launches of
+// Up to this many values, one block scans faster than the two launches of
 // device_scan.
 #ifndef MLXC_ROW_SCAN_MAX
 #define MLXC_ROW_SCAN_MAX (4 * kChunk)
@@ -750,10 +742,8 @@ int device_scan(int64_t* data, int64_t n, int64_t* sums, int64_t* total_out, hip
     const int64_t chunks = (n + kChunk - 1) / kChunk;
     hipLaunchKernelGGL((scan_reduce_kernel<kOp, kRev>), dim3(chunks), dim3(kBlock), 0, s, data, n,
                        sums);
-    hipLaunchKernelGGL((scan_top_kernel<kOp>), dim3(1), dim3(kBlock), 0, s, sums, chunks,
-                       total_out);
     hipLaunchKernelGGL((scan_down_kernel<kOp, kRev, kExcl>), dim3(chunks), dim3(kBlock), 0, s,
-                       data, n, sums);
+                       data, n, sums, total_out);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }
