@@ -197,17 +197,23 @@ int mlxc_random_walk_noalloc(const int64_t* d_rowptr, int64_t num_nodes,
  * Uniform random walk that generates its uniforms instead of reading a rand
  * tensor: the same walk as mlxc_random_walk with
  *   rand[n*L + l] = (w >> 8) * 2^-24, w = word (i % 4) of
- *   Philox4x32-10(key = seed; counter = (i/4 lo, i/4 hi, 0, 0)), i = n*L + l,
- * i.e. bit-identical to mlxc_random_walk on the output of
- * mlxc_philox_uniform(rand, num_walks * walk_length, seed).  Saves the
- * 4-byte-per-step rand stream and the pass that writes it.
+ *   Philox4x32-10(key = seed; counter = (i/4 lo, i/4 hi, 0, 0)),
+ *   i = (first_walk + n)*L + l,
+ * i.e. bit-identical to mlxc_random_walk on elements [first_walk * L,
+ * (first_walk + num_walks) * L) of the output of mlxc_philox_uniform(rand,
+ * (first_walk + num_walks) * walk_length, seed).  Saves the 4-byte-per-step
+ * rand stream and the pass that writes it.
+ * first_walk (>= 0) is the index of this call's walk 0 in a larger batch:
+ * walks [i0, i1) of a batch are rows i0 .. i1-1 of the whole batch's call
+ * when called on start[i0:i1] with first_walk = i0, so a batch can be run in
+ * slices (on one GPU, or one slice per GPU) with bit-identical results.
  * Extends: the reference's rand input, made by mx.random.uniform before the
  *   call (/root/reference/tests/test_random_walk.py:31-36).
  */
 int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes,
                             const int64_t* d_col, int64_t num_edges,
                             const int64_t* d_start, int64_t num_walks,
-                            int32_t walk_length, uint64_t seed,
+                            int32_t walk_length, uint64_t seed, int64_t first_walk,
                             void* d_n_out, void* d_e_out, int32_t out_type,
                             void* d_workspace, size_t workspace_bytes, void* stream);
 
@@ -222,8 +228,10 @@ int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes,
  *
  * The reference draws from libc rand(); this entry point draws from the
  * counter-based stream Philox4x32-10(key = seed; counter = (walk lo, walk hi,
- * step, trial)): word 0 picks the candidate as in mlxc_random_walk, word 1
- * gives r = (x1 >> 8) * 2^-24 for the acceptance test against the FP64
+ * step, trial)) with walk = first_walk + n for walk n of the call (>= 0; a
+ * call on start[i0:i1] with first_walk = i0 gives rows i0 .. i1-1 of the
+ * whole batch's call): word 0 picks the candidate as in mlxc_random_walk,
+ * word 1 gives r = (x1 >> 8) * 2^-24 for the acceptance test against the FP64
  * constants of BiasedRandomWalk.cpp:52-55.  `rows` is one of MLXC_ROWS_*:
  * sorted rows are searched through a 16-ary index, unsorted rows scanned
  * linearly as the reference does; MLXC_ROWS_DETECT decides on the device in
@@ -235,7 +243,7 @@ int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes,
                             const int64_t* d_col, int64_t num_edges,
                             const int64_t* d_start, int64_t num_walks,
                             int32_t walk_length, double p, double q,
-                            uint64_t seed, int32_t rule, int32_t rows,
+                            uint64_t seed, int64_t first_walk, int32_t rule, int32_t rows,
                             void* d_n_out, void* d_e_out, int32_t out_type,
                             void* d_workspace, size_t workspace_bytes, void* stream);
 
@@ -369,7 +377,7 @@ int mlxc_random_walk_cpu(const int64_t* rowptr, int64_t num_nodes,
 int mlxc_random_walk_seeded_cpu(const int64_t* rowptr, int64_t num_nodes,
                                 const int64_t* col, int64_t num_edges,
                                 const int64_t* start, int64_t num_walks,
-                                int32_t walk_length, uint64_t seed,
+                                int32_t walk_length, uint64_t seed, int64_t first_walk,
                                 void* n_out, void* e_out, int32_t out_type,
                                 int32_t threads, int64_t* status);
 
@@ -377,7 +385,7 @@ int mlxc_rejection_sampling_cpu(const int64_t* rowptr, int64_t num_nodes,
                                 const int64_t* col, int64_t num_edges,
                                 const int64_t* start, int64_t num_walks,
                                 int32_t walk_length, double p, double q,
-                                uint64_t seed, int32_t rule, int32_t rows,
+                                uint64_t seed, int64_t first_walk, int32_t rule, int32_t rows,
                                 void* n_out, void* e_out, int32_t out_type,
                                 int32_t threads, int64_t* status);
 

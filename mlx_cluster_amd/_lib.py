@@ -62,11 +62,12 @@ SIGNATURES = {
     ),
     "mlxc_random_walk_seeded": (
         ctypes.c_int,
-        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _u64, _ptr, _ptr, _i32, _ptr, _size, _ptr],
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _u64, _i64, _ptr, _ptr, _i32, _ptr, _size,
+         _ptr],
     ),
     "mlxc_rejection_sampling": (
         ctypes.c_int,
-        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _dbl, _dbl, _u64, _i32, _i32,
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _dbl, _dbl, _u64, _i64, _i32, _i32,
          _ptr, _ptr, _i32, _ptr, _size, _ptr],
     ),
     "mlxc_csr_check": (ctypes.c_int, [_ptr, _i64, _ptr, _i64, _ptr, _size, _ptr, _ptr]),
@@ -90,11 +91,11 @@ SIGNATURES = {
     ),
     "mlxc_random_walk_seeded_cpu": (
         ctypes.c_int,
-        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _u64, _ptr, _ptr, _i32, _i32, _ptr],
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _u64, _i64, _ptr, _ptr, _i32, _i32, _ptr],
     ),
     "mlxc_rejection_sampling_cpu": (
         ctypes.c_int,
-        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _dbl, _dbl, _u64, _i32, _i32,
+        [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _dbl, _dbl, _u64, _i64, _i32, _i32,
          _ptr, _ptr, _i32, _i32, _ptr],
     ),
 }

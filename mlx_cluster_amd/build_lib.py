@@ -38,15 +38,36 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None, out: str = OUT) -> str:
-    cmd = [HIPCC, *FLAGS, *(extra_flags or []), "-I", INCLUDE, "-I", CSRC, *SOURCES,
-           "-o", out + ".tmp"]
+BUILD_DIR = os.path.join(REPO_DIR, "_build")
+
+
+def _run(cmd: list[str], verbose: bool, what: str) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed building {out}")
+        raise RuntimeError(f"hipcc failed building {what}")
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None, out: str = OUT) -> str:
+    """Compiles every source to an object (in parallel; each translation unit
+    carries its own gfx950 code object, no cross-unit device calls) and links
+    them into `out`."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    tag = hashlib.sha256(" ".join(extra_flags or []).encode()).hexdigest()[:8]
+    obj_dir = os.path.join(BUILD_DIR, f"{os.path.basename(out)}-{tag}")
+    os.makedirs(obj_dir, exist_ok=True)
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    objs = [os.path.join(obj_dir, os.path.basename(src) + ".o") for src in SOURCES]
+    jobs = max(1, min(len(SOURCES), os.cpu_count() or 1, 16))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(lambda so: _run([HIPCC, *compile_flags, *(extra_flags or []), "-I", INCLUDE,
+                                       "-I", CSRC, "-c", so[0], "-o", so[1]], verbose, so[0]),
+                      zip(SOURCES, objs)))
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", out + ".tmp"],
+         verbose, out)
     os.replace(out + ".tmp", out)
     return out
 
@@ -68,11 +89,13 @@ def _code_only(text: str) -> str:
 # launchers, the preparation kernels the walks run first, the shared device
 # helpers): a profile stays matched to a build as long as these files' code
 # is unchanged.
+# walk_host.h is in every family: its constants (records_fit,
+# kSmallGraphEdgesPerStep) choose which kernels a call runs.
 KERNEL_SOURCES = {
-    "uniform_walk": ["walk_device.h", "prep_kernels.hip", "uniform_walk.hip"],
-    "node2vec_walk": ["walk_device.h", "prep_kernels.hip", "node2vec_walk.hip"],
-    "csr_build": ["walk_device.h", "csr_build.hip"],
-    "context_windows": ["walk_device.h", "windows.hip"],
+    "uniform_walk": ["walk_device.h", "walk_host.h", "prep_kernels.hip", "uniform_walk.hip"],
+    "node2vec_walk": ["walk_device.h", "walk_host.h", "prep_kernels.hip", "node2vec_walk.hip"],
+    "csr_build": ["walk_device.h", "walk_host.h", "csr_build.hip"],
+    "context_windows": ["walk_device.h", "walk_host.h", "windows.hip"],
 }
 
 

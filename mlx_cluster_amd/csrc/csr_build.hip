@@ -490,11 +490,17 @@ __global__ __launch_bounds__(kBlock) void scan_reduce_kernel(const int64_t* __re
     if (threadIdx.x == 0) sums[blockIdx.x] = total;
 }
 
-template <int kOp, bool kRev, bool kExcl>
-// Each block reduces the chunk sums of the blocks before it itself (at most a
-// few thousand values, read from L2), so no single-block launch has to scan
-// them in between; the last block writes the whole reduction to *total_out
-// (if given).
+// Up to this many chunks, each block of scan_down_kernel reduces the chunk
+// sums of the blocks before it itself (at most kScanFlatChunks values, read
+// from L2), so no launch has to scan the sums in between.  That costs
+// chunks^2 / 2 loads in all; above it the sums are scanned first (by the same
+// two launches, one level up) and each block reads its own carry.
+constexpr int64_t kScanFlatChunks = 4096;
+
+// kPre: sums[b] already holds the exclusive scan of the chunk sums before
+// chunk b.  Otherwise each block reduces sums[0 .. b) itself.  The last block
+// writes the whole reduction to *total_out (if given).
+template <int kOp, bool kRev, bool kExcl, bool kPre>
 __global__ __launch_bounds__(kBlock) void scan_down_kernel(int64_t* __restrict__ data, int64_t n,
                                                            const int64_t* __restrict__ sums,
                                                            int64_t* __restrict__ total_out) {
@@ -508,10 +514,15 @@ __global__ __launch_bounds__(kBlock) void scan_down_kernel(int64_t* __restrict__
         const int j = s * kBlock + t;
         vals[slot(j)] = scan_load<kOp, kRev>(data, n, base + j);
     }
-    int64_t part = op_identity<kOp>();
-    for (int64_t k = t; k < blockIdx.x; k += kBlock) part = op_apply<kOp>(part, sums[k]);
     int64_t carry;
-    block_exclusive_scan<kOp>(part, wtot, &carry);  // its two barriers also cover vals
+    if (kPre) {
+        carry = sums[blockIdx.x];
+        __syncthreads();  // covers vals
+    } else {
+        int64_t part = op_identity<kOp>();
+        for (int64_t k = t; k < blockIdx.x; k += kBlock) part = op_apply<kOp>(part, sums[k]);
+        block_exclusive_scan<kOp>(part, wtot, &carry);  // its two barriers also cover vals
+    }
     int64_t run = op_identity<kOp>();
     for (int s = 0; s < kItems; ++s) run = op_apply<kOp>(run, vals[slot(t * kItems + s)]);
     int64_t own;
@@ -685,6 +696,13 @@ struct CsrLayout {
     size_t digits = 0, hist = 0, totals = 0, sums = 0, bytes = 0;
 };
 
+// Words of chunk sums device_scan needs for n values: one per chunk, plus
+// those of the sums' own scan when it takes the levelled form.
+int64_t scan_sums_words(int64_t n) {
+    const int64_t chunks = (n + kChunk - 1) / kChunk;
+    return chunks + (chunks > kScanFlatChunks ? scan_sums_words(chunks) : 0);
+}
+
 CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
     CsrLayout l;
     l.total = (flags & MLXC_CSR_SYMMETRIZE) ? 2 * num_edges : num_edges;
@@ -700,7 +718,7 @@ CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
     if (l.chunks > hist_n) hist_n = l.chunks;
     int64_t scan_n = hist_n;
     if (num_nodes + 1 > scan_n) scan_n = num_nodes + 1;
-    const int64_t chunks = (scan_n + kChunk - 1) / kChunk;
+    const int64_t sum_words = scan_sums_words(scan_n);
     size_t at = round256(MLXC_WORK_WORDS * sizeof(int64_t));
     for (int b = 0; b < 2; ++b) {
         const bool split = l.key_bytes == 5 || l.key_bytes == 6;
@@ -718,7 +736,7 @@ CsrLayout csr_layout(int64_t num_nodes, int64_t num_edges, int32_t flags) {
     l.totals = at;  // the digit totals of a pass
     at += round256(kRadix * sizeof(int64_t));
     l.sums = at;
-    at += round256(static_cast<size_t>(chunks + 1) * sizeof(int64_t));
+    at += round256(static_cast<size_t>(sum_words + 1) * sizeof(int64_t));
     l.bytes = at;
     return l;
 }
@@ -736,14 +754,27 @@ constexpr int64_t kRowScanMax = MLXC_ROW_SCAN_MAX;
 #endif
 constexpr int64_t kRowScanTiles = MLXC_ROW_SCAN_TILES;
 
+// Scan of n int64 values in place: two launches up to kScanFlatChunks
+// chunks of kChunk values, and two more per level of chunk sums above that.
+// `sums` holds scan_sums_words(n) words.
 template <int kOp, bool kRev, bool kExcl>
 int device_scan(int64_t* data, int64_t n, int64_t* sums, int64_t* total_out, hipStream_t s) {
     if (n <= 0) return MLXC_OK;
     const int64_t chunks = (n + kChunk - 1) / kChunk;
     hipLaunchKernelGGL((scan_reduce_kernel<kOp, kRev>), dim3(chunks), dim3(kBlock), 0, s, data, n,
                        sums);
-    hipLaunchKernelGGL((scan_down_kernel<kOp, kRev, kExcl>), dim3(chunks), dim3(kBlock), 0, s,
-                       data, n, sums, total_out);
+    MLXC_HIP_TRY(hipGetLastError());
+    if (chunks <= kScanFlatChunks) {
+        hipLaunchKernelGGL((scan_down_kernel<kOp, kRev, kExcl, false>), dim3(chunks), dim3(kBlock),
+                           0, s, data, n, sums, total_out);
+    } else {
+        // the chunk sums, exclusive and in chunk order, with the next level's
+        // sums after them
+        if (int rc = device_scan<kOp, false, true>(sums, chunks, sums + chunks, nullptr, s))
+            return rc;
+        hipLaunchKernelGGL((scan_down_kernel<kOp, kRev, kExcl, true>), dim3(chunks), dim3(kBlock),
+                           0, s, data, n, sums, total_out);
+    }
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
 }

@@ -147,8 +147,9 @@ uint32_t uniform_range(const HostWalk& w, int64_t first, int64_t last) {
                 const int64_t i = n * L + l;
                 float r;
                 if (kGen) {
-                    if ((i >> 2) != block) {
-                        block = i >> 2;
+                    const int64_t g = (w.walk_base + n) * L + l;  // stream position
+                    if ((g >> 2) != block) {
+                        block = g >> 2;
                         uint32_t c0 = static_cast<uint32_t>(block);
                         uint32_t c1 = static_cast<uint32_t>(static_cast<uint64_t>(block) >> 32);
                         uint32_t c2 = 0, c3 = 0;
@@ -158,7 +159,7 @@ uint32_t uniform_range(const HostWalk& w, int64_t first, int64_t last) {
                         u[2] = unit_float_host(c2);
                         u[3] = unit_float_host(c3);
                     }
-                    r = u[i & 3];
+                    r = u[g & 3];
                 } else {
                     r = w.rand[i];
                 }
@@ -228,8 +229,9 @@ uint32_t node2vec_range(const HostWalk& w, const N2VParams& prm, bool sorted, in
             if (!node_in(t, V)) status |= MLXC_STATUS_BAD_NODE;
             continue;
         }
-        const uint32_t n_lo = static_cast<uint32_t>(n);
-        const uint32_t n_hi = static_cast<uint32_t>(static_cast<uint64_t>(n) >> 32);
+        const uint64_t sn = static_cast<uint64_t>(w.walk_base + n);  // Philox stream index
+        const uint32_t n_lo = static_cast<uint32_t>(sn);
+        const uint32_t n_hi = static_cast<uint32_t>(sn >> 32);
         bool bad = !node_in(t, V);
         int64_t v = t, e = -1;
         if (bad) {

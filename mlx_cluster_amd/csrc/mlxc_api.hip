@@ -90,6 +90,17 @@ int check_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col, int
     return check_workspace(work, work_bytes);
 }
 
+// first_walk of the seeded entry points: the Philox stream index of walk 0,
+// with every stream position (first_walk + num_walks) * walk_length in int64.
+int check_first_walk(int64_t first_walk, int64_t num_walks, int32_t walk_length) {
+    if (first_walk < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "first_walk must be >= 0");
+    const int64_t per = walk_length > 0 ? walk_length : 1;
+    if (first_walk > INT64_MAX / per - num_walks)
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "(first_walk + num_walks) * walk_length overflows int64");
+    return MLXC_OK;
+}
+
 // Parameters of one node2vec call; the acceptance constants exactly as
 // BiasedRandomWalk.cpp:52-55, in FP64.
 int n2v_params(double p, double q, uint64_t seed, int32_t rule, int32_t rows, N2VParams& prm) {
@@ -196,11 +207,11 @@ int noalloc_scratch(void** out) {
 
 HostWalk host_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                    int64_t num_edges, const int64_t* start, int64_t num_walks, const float* rand,
-                   int32_t walk_length, uint64_t seed, void* n_out, void* e_out,
-                   int32_t out_type) {
+                   int32_t walk_length, uint64_t seed, int64_t first_walk, void* n_out,
+                   void* e_out, int32_t out_type) {
     return HostWalk{rowptr, col, start, rand, n_out, e_out, out_type, num_nodes, num_edges,
                     num_walks, walk_length, static_cast<uint32_t>(seed),
-                    static_cast<uint32_t>(seed >> 32)};
+                    static_cast<uint32_t>(seed >> 32), first_walk};
 }
 
 }  // namespace
@@ -210,7 +221,7 @@ using namespace mlxc;
 
 extern "C" {
 
-int mlxc_version(void) { return 200; }
+int mlxc_version(void) { return 300; }
 
 const char* mlxc_last_error(void) { return g_last_error.c_str(); }
 
@@ -243,7 +254,7 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* 
     int64_t* d_work = static_cast<int64_t*>(d_workspace);
     if (num_walks == 0) return launch_zero_work(d_work, s);  // (else the walk's launches zero it)
     const WalkArgs a{d_rowptr, d_col, d_start, d_rand, d_n_out, d_e_out, d_work,
-                     num_nodes, num_edges, num_walks, walk_length, 0u, 0u};
+                     num_nodes, num_edges, num_walks, walk_length, 0u, 0u, 0};
     return launch_uniform(a, d_workspace, workspace_bytes, false, out_type, s);
 }
 
@@ -280,30 +291,32 @@ int mlxc_random_walk_noalloc(const int64_t* d_rowptr, int64_t num_nodes, const i
 
 int mlxc_random_walk_seeded(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
                             int64_t num_edges, const int64_t* d_start, int64_t num_walks,
-                            int32_t walk_length, uint64_t seed, void* d_n_out, void* d_e_out,
-                            int32_t out_type, void* d_workspace, size_t workspace_bytes,
-                            void* stream) {
+                            int32_t walk_length, uint64_t seed, int64_t first_walk,
+                            void* d_n_out, void* d_e_out, int32_t out_type, void* d_workspace,
+                            size_t workspace_bytes, void* stream) {
     if (int rc = check_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
                             walk_length, d_n_out, d_e_out, out_type, d_workspace, workspace_bytes))
         return rc;
+    if (int rc = check_first_walk(first_walk, num_walks, walk_length)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     int64_t* d_work = static_cast<int64_t*>(d_workspace);
     if (num_walks == 0) return launch_zero_work(d_work, s);  // (else the walk's launches zero it)
     const WalkArgs a{d_rowptr, d_col, d_start, nullptr, d_n_out, d_e_out, d_work,
                      num_nodes, num_edges, num_walks, walk_length,
-                     static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32)};
+                     static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32), first_walk};
     return launch_uniform(a, d_workspace, workspace_bytes, true, out_type, s);
 }
 
 int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
                             int64_t num_edges, const int64_t* d_start, int64_t num_walks,
                             int32_t walk_length, double p, double q, uint64_t seed,
-                            int32_t rule, int32_t rows, void* d_n_out, void* d_e_out,
-                            int32_t out_type, void* d_workspace, size_t workspace_bytes,
-                            void* stream) {
+                            int64_t first_walk, int32_t rule, int32_t rows, void* d_n_out,
+                            void* d_e_out, int32_t out_type, void* d_workspace,
+                            size_t workspace_bytes, void* stream) {
     if (int rc = check_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
                             walk_length, d_n_out, d_e_out, out_type, d_workspace, workspace_bytes))
         return rc;
+    if (int rc = check_first_walk(first_walk, num_walks, walk_length)) return rc;
     N2VParams prm;
     if (int rc = n2v_params(p, q, seed, rule, rows, prm)) return rc;
     prm.out_type = out_type;
@@ -312,7 +325,7 @@ int mlxc_rejection_sampling(const int64_t* d_rowptr, int64_t num_nodes, const in
     if (int rc = launch_zero_work(d_work, s)) return rc;
     if (num_walks == 0) return MLXC_OK;
     const WalkArgs a{d_rowptr, d_col, d_start, nullptr, d_n_out, d_e_out, d_work,
-                     num_nodes, num_edges, num_walks, walk_length, 0u, 0u};
+                     num_nodes, num_edges, num_walks, walk_length, 0u, 0u, first_walk};
     return launch_node2vec(a, prm, d_workspace, workspace_bytes, s);
 }
 
@@ -428,7 +441,7 @@ int mlxc_random_walk_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t
         return fail(MLXC_ERR_INVALID_ARGUMENT, "rand must not be NULL");
     uint32_t bits = 0;
     const HostWalk w = host_walk(rowptr, num_nodes, col, num_edges, start, num_walks, rand,
-                                 walk_length, 0, n_out, e_out, out_type);
+                                 walk_length, 0, 0, n_out, e_out, out_type);
     const int rc = host_uniform(w, false, threads, bits);
     if (status) *status = bits;
     return rc;
@@ -436,15 +449,17 @@ int mlxc_random_walk_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t
 
 int mlxc_random_walk_seeded_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                                 int64_t num_edges, const int64_t* start, int64_t num_walks,
-                                int32_t walk_length, uint64_t seed, void* n_out, void* e_out,
-                                int32_t out_type, int32_t threads, int64_t* status) {
+                                int32_t walk_length, uint64_t seed, int64_t first_walk,
+                                void* n_out, void* e_out, int32_t out_type, int32_t threads,
+                                int64_t* status) {
     if (int rc = check_graph(rowptr, num_nodes, col, num_edges, start, num_walks, walk_length,
                              n_out))
         return rc;
     if (int rc = check_out_type(out_type, num_nodes, num_edges, e_out)) return rc;
+    if (int rc = check_first_walk(first_walk, num_walks, walk_length)) return rc;
     uint32_t bits = 0;
     const HostWalk w = host_walk(rowptr, num_nodes, col, num_edges, start, num_walks, nullptr,
-                                 walk_length, seed, n_out, e_out, out_type);
+                                 walk_length, seed, first_walk, n_out, e_out, out_type);
     const int rc = host_uniform(w, true, threads, bits);
     if (status) *status = bits;
     return rc;
@@ -453,18 +468,20 @@ int mlxc_random_walk_seeded_cpu(const int64_t* rowptr, int64_t num_nodes, const 
 int mlxc_rejection_sampling_cpu(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                                 int64_t num_edges, const int64_t* start, int64_t num_walks,
                                 int32_t walk_length, double p, double q, uint64_t seed,
-                                int32_t rule, int32_t rows, void* n_out, void* e_out,
-                                int32_t out_type, int32_t threads, int64_t* status) {
+                                int64_t first_walk, int32_t rule, int32_t rows, void* n_out,
+                                void* e_out, int32_t out_type, int32_t threads,
+                                int64_t* status) {
     if (int rc = check_graph(rowptr, num_nodes, col, num_edges, start, num_walks, walk_length,
                              n_out))
         return rc;
     if (int rc = check_out_type(out_type, num_nodes, num_edges, e_out)) return rc;
+    if (int rc = check_first_walk(first_walk, num_walks, walk_length)) return rc;
     N2VParams prm;
     if (int rc = n2v_params(p, q, seed, rule, rows, prm)) return rc;
     prm.out_type = out_type;
     uint32_t bits = 0;
     const HostWalk w = host_walk(rowptr, num_nodes, col, num_edges, start, num_walks, nullptr,
-                                 walk_length, seed, n_out, e_out, out_type);
+                                 walk_length, seed, first_walk, n_out, e_out, out_type);
     const int rc = host_node2vec(w, prm, threads, bits);
     if (status) *status = bits;
     return rc;

@@ -129,8 +129,9 @@ __global__ __launch_bounds__(kBlock) void node2vec_walk_kernel(N2VArgs a) {
                 exhausted = true;
             } else {
                 n = id;
-                n_lo = static_cast<uint32_t>(n);
-                n_hi = static_cast<uint32_t>(n >> 32);
+                const int64_t sn = a.w.walk_base + n;  // the walk's Philox stream index
+                n_lo = static_cast<uint32_t>(sn);
+                n_hi = static_cast<uint32_t>(sn >> 32);
                 out = static_cast<OutT*>(a.w.n_out) + n * (L + 1);
                 eout = kEdges ? static_cast<OutT*>(a.w.e_out) + n * L : nullptr;
                 t = a.w.start[n];
@@ -246,7 +247,8 @@ enum : int {
 };
 
 // The two uniforms of a trial: Philox4x32-10 with key = seed and counter =
-// (walk lo, walk hi, step, trial); word 0 picks the candidate, word 1 is
+// (walk lo, walk hi, step, trial), walk being the stream index walk_base + n
+// of walk n of the call; word 0 picks the candidate, word 1 is
 // the acceptance test's r (the reference's rand() % deg and rand()/RAND_MAX,
 // BiasedRandomWalk.cpp:81,84).
 __device__ __forceinline__ void n2v_uniforms(int64_t n, int32_t step, uint32_t trial,
@@ -684,7 +686,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
         // places that draw (a wavefront executes each site any lane needs).
         if (draw) {
             float u0;
-            n2v_uniforms(n, l, trial, a.key0, a.key1, u0, r);
+            n2v_uniforms(a.w.walk_base + n, l, trial, a.key0, a.key1, u0, r);
             e = bv + static_cast<int32_t>(pick_index(u0, dv));
         }
         if (push) ow_push(ow, nout, g, v);
@@ -818,7 +820,7 @@ __global__ __launch_bounds__(kLdsBlock) void node2vec_lds_kernel(N2VRecArgs a) {
         int32_t e = b;
         if (l == 0 || deg > 1) {
             float u0;
-            n2v_uniforms(n, static_cast<int32_t>(l), trial, a.key0, a.key1, u0, r);
+            n2v_uniforms(a.w.walk_base + n, static_cast<int32_t>(l), trial, a.key0, a.key1, u0, r);
             e = b + static_cast<int32_t>(pick_index(u0, deg));
         }
         const int32_t x = cl[e];

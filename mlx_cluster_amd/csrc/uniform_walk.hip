@@ -22,6 +22,7 @@ template <int W, bool kEdges, bool kGen, typename OutT>
 __global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
     const int64_t L = a.walk_length;
     const int64_t N = a.num_walks;
+    const int64_t goff = kGen ? a.walk_base * L : 0;  // stream position of uniform 0
     OutT* const nout = static_cast<OutT*>(a.n_out);
     OutT* const eout = static_cast<OutT*>(a.e_out);
     unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.work + 1);
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_kernel(WalkArgs a) {
             r[s] = 0.0f;
             if (live) {
                 rb[s] = load_row(a.rowptr, v[s]);
-                r[s] = kGen ? philox_uniform_at(n[s] * L + l[s], a.key0, a.key1)
+                r[s] = kGen ? philox_uniform_at(goff + n[s] * L + l[s], a.key0, a.key1)
                             : __builtin_nontemporal_load(a.rand + n[s] * L + l[s]);
             }
         }
@@ -156,6 +157,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
     const int64_t L1 = L + 1;
     const int64_t N = a.num_walks;
     const int64_t rtotal = N * L;
+    const int64_t goff = kGen ? a.walk_base * L : 0;  // stream position of uniform 0
     unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.work + 1);
     WaveQueue q{0, 0};
     int phase[W];
@@ -203,7 +205,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
         RandWindow<RW> blk[W];  // due rand blocks, stored to LDS in step 3
 #pragma unroll
         for (int s = 0; s < W; ++s)
-            if (need_block[s]) rw_fetch<RW, kGen>(blk[s], a, fr[s], rtotal);
+            if (need_block[s]) rw_fetch<RW, kGen>(blk[s], a, fr[s], rtotal, goff);
         // ... and the output blocks the last iteration completed are stored.
 #pragma unroll
         for (int s = 0; s < W; ++s) {
@@ -253,7 +255,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                 const int64_t g = g0 + l[s] + (ph[s] == kSlotWalk ? 1 : 0);
                 if (need_block[s]) {
                     // the block holding rand[fr]; fr is its entry k
-                    const int k = static_cast<int>(fr[s] - rw_base<RW, kGen>(fr[s], rtotal));
+                    const int k = static_cast<int>(fr[s] - rw_base<RW, kGen>(fr[s], rtotal, goff));
                     lw_store(rand_area[s], rw[s], blk[s], k);
                     need_block[s] = false;
                 }
@@ -378,6 +380,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
     const int64_t L1 = L + 1;
     const int64_t N = a.num_walks;
     const int64_t rtotal = N * L;
+    const int64_t goff = kGen ? a.walk_base * L : 0;  // stream position of uniform 0
     unsigned long long* counter = reinterpret_cast<unsigned long long*>(a.work + 1);
     WaveQueue q{0, 0};
     int phase[W];
@@ -428,7 +431,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
 #pragma unroll
         for (int s = 0; s < W; ++s)  // a block due after a pick travels with the col read
             if (need_block[s] && ph[s] != kSlotRow)
-                rw_fetch<RW, kGen>(blk[s], a, fr[s], rtotal);
+                rw_fetch<RW, kGen>(blk[s], a, fr[s], rtotal, goff);
         // ... and the output blocks the last iteration completed are stored.
 #pragma unroll
         for (int s = 0; s < W; ++s) {
@@ -462,7 +465,7 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                 continue;
             }
             if (need_block[s] && ph[s] != kSlotRow) {  // the block fetched above
-                const int k = static_cast<int>(fr[s] - rw_base<RW, kGen>(fr[s], rtotal));
+                const int k = static_cast<int>(fr[s] - rw_base<RW, kGen>(fr[s], rtotal, goff));
                 lw_store(rand_area[s], rw[s], blk[s], k);
                 need_block[s] = false;
             }
@@ -568,6 +571,7 @@ template <bool kGen, bool kEdges, typename OutT>
 __global__ __launch_bounds__(kLdsBlock) void uniform_walk_lds_kernel(WalkArgs a) {
     __shared__ int32_t graph[kLdsGraphEntries];
     const int64_t V = a.num_nodes, E = a.num_edges, N = a.num_walks, L = a.walk_length;
+    const int64_t goff = kGen ? a.walk_base * L : 0;  // stream position of uniform 0
     int32_t* const rp = graph;          // rowptr, -1 for an entry outside [0, E]
     int32_t* const cl = graph + V + 1;  // col, -1 for a value outside [0, V)
     for (int64_t i = threadIdx.x; i <= V; i += kLdsBlock) {
@@ -597,7 +601,7 @@ __global__ __launch_bounds__(kLdsBlock) void uniform_walk_lds_kernel(WalkArgs a)
 #pragma unroll
             for (int j = 0; j < 8; ++j)
                 if (l + j < L)
-                    r[j] = kGen ? philox_uniform_at(n * L + l + j, a.key0, a.key1) : a.rand[n * L + l + j];
+                    r[j] = kGen ? philox_uniform_at(goff + n * L + l + j, a.key0, a.key1) : a.rand[n * L + l + j];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 if (stop || l >= L) break;

@@ -158,6 +158,10 @@ struct WalkArgs {
     int64_t num_walks;
     int32_t walk_length;
     uint32_t key0, key1;  // Philox key (the seed) when the kernel generates its uniforms
+    // Philox walk index of walk 0 of this call: walk n draws from the stream
+    // of walk walk_base + n, so a call over any slice of a larger batch gives
+    // that slice's walks.  Generated uniform streams only (0 with a rand tensor).
+    int64_t walk_base;
 };
 
 // ------------------------------------------------- stream windows
@@ -235,18 +239,21 @@ __device__ __forceinline__ void rw_gen_at(RandWindow<RW>& r, int64_t base, uint3
     }
 }
 
-// Block start for rand[f]: generated streams have no array end to respect.
+// Block start for rand[f].  A generated stream has no array end to respect;
+// its uniform f is stream position f + off (off = walk_base * walk_length),
+// and its blocks are aligned in stream positions, so the block start may lie
+// before f = 0 (a negative index, never read: the block is generated).
 template <int RW, bool kGen>
-__device__ __forceinline__ int64_t rw_base(int64_t f, int64_t total) {
-    return kGen ? (f & ~static_cast<int64_t>(RW - 1)) : rw_block_base<RW>(f, total);
+__device__ __forceinline__ int64_t rw_base(int64_t f, int64_t total, int64_t off) {
+    return kGen ? ((f + off) & ~static_cast<int64_t>(RW - 1)) - off : rw_block_base<RW>(f, total);
 }
 
 // Fills the window with the block that serves rand[f], read or generated.
 template <int RW, bool kGen>
 __device__ __forceinline__ void rw_fetch(RandWindow<RW>& r, const WalkArgs& a, int64_t f,
-                                         int64_t total) {
-    if (kGen) rw_gen_at(r, rw_base<RW, kGen>(f, total), a.key0, a.key1);
-    else rw_load_at(r, a.rand, rw_base<RW, kGen>(f, total));
+                                         int64_t total, int64_t off) {
+    if (kGen) rw_gen_at(r, rw_base<RW, kGen>(f, total, off) + off, a.key0, a.key1);
+    else rw_load_at(r, a.rand, rw_base<RW, kGen>(f, total, off));
 }
 
 // The walk loops keep each slot's rand window in LDS rather than in

@@ -175,6 +175,7 @@ struct HostWalk {
     int32_t out_type;   // MLXC_OUT_*
     int64_t num_nodes, num_edges, num_walks, walk_length;
     uint32_t key0, key1;  // Philox key of generated uniforms
+    int64_t walk_base;    // Philox stream index of walk 0 (WalkArgs::walk_base)
 };
 // threads <= 0: one per hardware thread.  status receives MLXC_STATUS_* bits.
 int host_uniform(const HostWalk& w, bool generate, int32_t threads, uint32_t& status);

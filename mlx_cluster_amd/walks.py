@@ -214,12 +214,166 @@ def _raise_bits(bits: int, what: str) -> None:
     raise ValueError(f"{what}: " + "; ".join(reasons))
 
 
+def _walk_offset(walk_offset) -> int:
+    if isinstance(walk_offset, bool) or not isinstance(walk_offset, numbers.Integral):
+        raise TypeError("walk_offset must be an int")
+    if walk_offset < 0 or walk_offset >= 2**63:
+        raise ValueError("walk_offset must lie in [0, 2^63)")
+    return int(walk_offset)
+
+
+def _memory_budget(budget) -> Optional[int]:
+    if budget is None:
+        return None
+    if isinstance(budget, bool) or not isinstance(budget, numbers.Integral) or budget < 1:
+        raise ValueError("memory_budget must be None or a positive int (bytes)")
+    return int(budget)
+
+
+def _available_bytes(device: torch.device) -> int:
+    """Device memory a call can take: the driver's free memory plus what
+    torch's caching allocator holds unused."""
+    index = _device_index(device)
+    free, _ = torch.cuda.mem_get_info(index)
+    return int(free) + torch.cuda.memory_reserved(index) - torch.cuda.memory_allocated(index)
+
+
+# Smallest workspace a walk entry point accepts (MLXC_WORK_WORDS int64
+# words): the direct kernels, which read the CSR arrays as they are.
+_MIN_WORKSPACE = _lib.MLXC_WORK_WORDS * 8
+# Chunks of a chunked call are whole multiples of this many walks, so every
+# chunk's rows of the rand tensor and of the staging outputs start 16-byte
+# aligned (the windowed kernels' requirement).
+_CHUNK_ALIGN = 64
+
+
+def _plan(N: int, row_bytes: int, ws_query, budget: int):
+    """How a call of N walks runs within `budget` bytes of device memory for
+    its outputs (row_bytes per walk) and workspace (ws_query(n) bytes for n
+    walks at the fastest layout; any smaller workspace of at least
+    _MIN_WORKSPACE bytes runs too, at a slower layout with the same results).
+
+    Returns ("device", None, ws): one call with device outputs and a
+    workspace of ws bytes; or ("host", chunk, ws): chunks of `chunk` walks
+    into two device staging buffers, copied into pinned host outputs."""
+    out = N * row_bytes
+    if out + ws_query(N) <= budget:
+        return "device", None, ws_query(N)
+    if out + _MIN_WORKSPACE <= budget:
+        return "device", None, (budget - out) // 16 * 16
+    cost = lambda c: 2 * c * row_bytes + ws_query(c)
+    hi = N // _CHUNK_ALIGN
+    if hi >= 1 and cost(_CHUNK_ALIGN) <= budget:
+        lo = 1  # the largest multiple k of _CHUNK_ALIGN with cost(k * _CHUNK_ALIGN) <= budget
+        while lo < hi:
+            mid = (lo + hi + 1) // 2
+            if cost(mid * _CHUNK_ALIGN) <= budget:
+                lo = mid
+            else:
+                hi = mid - 1
+        chunk = lo * _CHUNK_ALIGN
+        return "host", chunk, ws_query(chunk)
+    chunk = min(N, (budget - _MIN_WORKSPACE) // (2 * row_bytes))
+    if chunk >= _CHUNK_ALIGN:
+        chunk -= chunk % _CHUNK_ALIGN
+    if chunk < 1:
+        raise ValueError(f"memory_budget of {budget} bytes holds no chunk: one walk needs "
+                         f"{2 * row_bytes + _MIN_WORKSPACE} bytes (two staging rows and the "
+                         f"minimal workspace)")
+    return "host", chunk, min(ws_query(chunk), (budget - 2 * chunk * row_bytes) // 16 * 16)
+
+
+def _run_walks(device, stream, handle, N: int, L: int, out_dtype, return_edges: bool,
+               ws_query, launch, budget: Optional[int], check: bool, what: str, inputs):
+    """Runs a walk call on the device.  launch(i0, n, n_ptr, e_ptr, ws_ptr,
+    ws_bytes) enqueues walks [i0, i0 + n) of the call on `handle` and returns
+    the library's code.  Without a budget the call runs once, with device
+    outputs and the fastest workspace; when that allocation fails, or when
+    the outputs and workspace would exceed `budget` bytes, _plan decides."""
+    esize = 8 if out_dtype == torch.int64 else 4
+    row_bytes = (2 * L + 1 if return_edges else L + 1) * esize
+    if budget is None:
+        try:
+            return _run_once(device, stream, N, L, out_dtype, return_edges, ws_query(N), launch,
+                             check, what, inputs)
+        except torch.cuda.OutOfMemoryError:
+            budget = _available_bytes(device)
+    mode, chunk, ws_bytes = _plan(N, row_bytes, ws_query, budget)
+    if mode == "device":
+        return _run_once(device, stream, N, L, out_dtype, return_edges, ws_bytes, launch, check,
+                         what, inputs)
+    return _run_chunked(device, stream, N, L, out_dtype, return_edges, chunk, ws_bytes, launch,
+                        check, what, inputs)
+
+
+def _run_once(device, stream, N, L, out_dtype, return_edges, ws_bytes, launch, check, what,
+              inputs):
+    n_out = torch.empty((N, L + 1), dtype=out_dtype, device=device)
+    e_out = torch.empty((N, L), dtype=out_dtype, device=device) if return_edges else None
+    work = _workspace(ws_bytes, device)
+    side = _side_stream(stream, device)
+    _enter_side_stream(side, device)
+    with _on_device(device):
+        rc = launch(0, N, _ptr(n_out), _ptr(e_out) if return_edges else None, work.data_ptr(),
+                    work.numel() * 8)
+    _leave_side_stream(side, *inputs, n_out, e_out, work)
+    _lib.check(rc, what)
+    if check:
+        _raise_status(work, stream, what)
+    return n_out, e_out
+
+
+def _run_chunked(device, stream, N, L, out_dtype, return_edges, chunk, ws_bytes, launch, check,
+                 what, inputs):
+    """Walks in chunks of `chunk`, each written into one of two device staging
+    buffers and copied on a copy stream into pinned host outputs while the
+    next chunk runs.  Synchronises before returning (the outputs are host
+    memory); the status bits of every chunk are OR-ed on the device."""
+    n_host = torch.empty((N, L + 1), dtype=out_dtype, pin_memory=True)
+    e_host = torch.empty((N, L), dtype=out_dtype, pin_memory=True) if return_edges else None
+    compute = stream if isinstance(stream, torch.cuda.Stream) else torch.cuda.current_stream(device)
+    _enter_side_stream(_side_stream(stream, device), device)
+    with _on_device(device), torch.cuda.stream(compute):
+        n_stage = torch.empty((2, chunk, L + 1), dtype=out_dtype, device=device)
+        e_stage = (torch.empty((2, chunk, L), dtype=out_dtype, device=device) if return_edges
+                   else None)
+        work = _workspace(ws_bytes, device)
+        status = torch.zeros(1, dtype=torch.int64, device=device)
+        copy = torch.cuda.Stream(device)
+        copied = [None, None]  # copy-stream events after which a staging buffer is free
+        for k, i0 in enumerate(range(0, N, chunk)):
+            n, b = min(chunk, N - i0), k % 2
+            if copied[b] is not None:
+                compute.wait_event(copied[b])
+            rc = launch(i0, n, n_stage[b].data_ptr(),
+                        e_stage[b].data_ptr() if return_edges else None, work.data_ptr(),
+                        work.numel() * 8)
+            if rc != _lib.MLXC_OK:
+                copy.synchronize()
+                _lib.check(rc, what)
+            status.bitwise_or_(work[:1])
+            done = torch.cuda.Event()
+            done.record(compute)
+            copy.wait_event(done)
+            with torch.cuda.stream(copy):
+                n_host[i0:i0 + n].copy_(n_stage[b, :n], non_blocking=True)
+                if return_edges:
+                    e_host[i0:i0 + n].copy_(e_stage[b, :n], non_blocking=True)
+                copied[b] = torch.cuda.Event()
+                copied[b].record(copy)
+        copy.synchronize()
+    if check:
+        _raise_bits(int(status.item()), what)
+    return n_host, e_host
+
+
 # ------------------------------------------------------------------- API
 
 def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
                 rand: Optional[TensorLike], walk_length: int, *, stream=None,
                 return_edges: bool = False, check: bool = True, seed: Optional[int] = None,
-                threads: Optional[int] = None, out_dtype: torch.dtype = torch.int64
+                threads: Optional[int] = None, out_dtype: torch.dtype = torch.int64,
+                walk_offset: int = 0, memory_budget: Optional[int] = None
                 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """Uniform random walks over a CSR graph.
 
@@ -255,12 +409,28 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
         out_dtype: torch.int64 (the reference's output) or torch.int32, a
             compact output with half the bytes (node ids, and edge ids with
             return_edges, must be below 2^31).
+        walk_offset: with seed, the index of this call's first walk in a
+            larger batch: walk n draws the uniforms of walk walk_offset + n,
+            so the call on start[i0:i1] with walk_offset=i0 returns rows
+            i0 .. i1-1 of the whole batch's call, bit for bit.  (With a rand
+            tensor, pass the slice's rows of rand instead.)
+        memory_budget: bytes of device memory the call may allocate for its
+            outputs and workspace (None: whatever it needs, and if that
+            allocation fails, what the device has free).  Outputs that fit
+            stay on the device, with the workspace shrunk to the rest if
+            needed (a slower kernel layout, the same walks).  Outputs that do
+            not fit are computed in chunks of walks, each with its walk
+            offset, through two device staging buffers, and returned in
+            pinned host memory (the call then synchronises).  Ignored for
+            stream='cpu'.
 
     Returns:
         [num_walks, walk_length + 1] node sequences (and edge ids) of out_dtype.
     """
     L = _walk_length(walk_length)
     otype = _out_type(out_dtype)
+    offset = _walk_offset(walk_offset)
+    budget = _memory_budget(memory_budget)
     _check_stream_arg(stream)
     rowptr, col, start = _graph(rowptr, col, start)
     N = start.numel()
@@ -271,6 +441,9 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     else:
         if seed is not None:
             raise ValueError("pass either rand or seed, not both")
+        if offset:
+            raise ValueError("walk_offset applies to generated uniforms (seed=); with a rand "
+                             "tensor, pass the rows of rand that belong to these walks")
         rand = _as_tensor(rand, torch.float32, "rand")
         if rand.numel() != N * L:
             raise ValueError(f"rand must hold num_walks * walk_length = {N * L} values, "
@@ -284,7 +457,7 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
         outs = (_ptr(n_out), _ptr(e_out), otype, _threads(threads),
                 _lib.ctypes.addressof(status))
         if rand is None:
-            rc = _lib.load().mlxc_random_walk_seeded_cpu(*graph, L, seed, *outs)
+            rc = _lib.load().mlxc_random_walk_seeded_cpu(*graph, L, seed, offset, *outs)
         else:
             rand = _host(rand)
             rc = _lib.load().mlxc_random_walk_cpu(*graph, _ptr(rand), L, *outs)
@@ -295,27 +468,28 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     device = _resolve_device(stream, (rowptr, col, start, rand))
     handle = _stream_handle(stream, device)
     rowptr, col, start = (_on(t, device) for t in (rowptr, col, start))
-    n_out = torch.empty((N, L + 1), dtype=out_dtype, device=device)
-    e_out = torch.empty((N, L), dtype=out_dtype, device=device) if return_edges else None
-    lib = _lib.load()
-    work = _workspace(lib.mlxc_random_walk_workspace_bytes(rowptr.numel() - 1, col.numel(), N, L),
-                      device)
-    graph = (_ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N)
-    outs = (_ptr(n_out), _ptr(e_out) if return_edges else None, otype, work.data_ptr(),
-            work.numel() * 8, handle)
     if rand is not None:
         rand = _on(rand, device)
-    side = _side_stream(stream, device)
-    _enter_side_stream(side, device)
-    with _on_device(device):
+    lib = _lib.load()
+    V, E = rowptr.numel() - 1, col.numel()
+    rowptr_p, col_p = _ptr(rowptr), _ptr(col)
+    start_p = start.data_ptr() if N else None
+    rand_p = rand.data_ptr() if rand is not None and rand.numel() else None
+
+    def launch(i0, n, n_p, e_p, ws_p, ws_bytes):
+        s_p = start_p + 8 * i0 if start_p else None
         if rand is None:
-            rc = lib.mlxc_random_walk_seeded(*graph, L, seed, *outs)
-        else:
-            rc = lib.mlxc_random_walk(*graph, _ptr(rand), L, *outs)
-    _leave_side_stream(side, rowptr, col, start, rand, n_out, e_out, work)
-    _lib.check(rc, "random_walk")
-    if check:
-        _raise_status(work, stream, "random_walk")
+            return lib.mlxc_random_walk_seeded(rowptr_p, V, col_p, E, s_p, n, L, seed,
+                                               offset + i0, n_p, e_p, otype, ws_p, ws_bytes,
+                                               handle)
+        r_p = rand_p + 4 * L * i0 if rand_p else None
+        return lib.mlxc_random_walk(rowptr_p, V, col_p, E, s_p, n, r_p, L, n_p, e_p, otype, ws_p,
+                                    ws_bytes, handle)
+
+    n_out, e_out = _run_walks(
+        device, stream, handle, N, L, out_dtype, return_edges,
+        lambda n: lib.mlxc_random_walk_workspace_bytes(V, E, n, L), launch, budget, check,
+        "random_walk", (rowptr, col, start, rand))
     return (n_out, e_out) if return_edges else n_out
 
 
@@ -347,7 +521,8 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
                        seed: Optional[int] = None, rule: str = "ref_chain",
                        rows_sorted: Optional[bool] = None, return_edges: bool = False,
                        check: bool = True, threads: Optional[int] = None,
-                       out_dtype: torch.dtype = torch.int64, symmetric: bool = False
+                       out_dtype: torch.dtype = torch.int64, symmetric: bool = False,
+                       walk_offset: int = 0, memory_budget: Optional[int] = None
                        ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """node2vec random walks by rejection sampling.
 
@@ -380,9 +555,18 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
             the reference does; on a graph that is not symmetric True gives
             unspecified walks.  csr_check(rowptr, col) & MLXC_CSR_ASYMMETRIC
             (8) tells whether the promise holds (for sorted rows).
+        walk_offset: the index of this call's first walk in a larger batch:
+            walk n draws from the Philox stream of walk walk_offset + n, so
+            the call on start[i0:i1] with walk_offset=i0 (and the same seed)
+            returns rows i0 .. i1-1 of the whole batch's call, bit for bit.
+        memory_budget: as in random_walk.  A workspace shrunk to fit runs
+            the edge records without hub bitmaps, then the CSR mode, then the
+            direct kernel: the same walks each way.
     """
     L = _walk_length(walk_length)
     otype = _out_type(out_dtype)
+    offset = _walk_offset(walk_offset)
+    budget = _memory_budget(memory_budget)
     p, q = float(p), float(q)
     if not (np.isfinite(p) and np.isfinite(q) and p > 0 and q > 0):
         raise ValueError("p and q must be finite and > 0")
@@ -405,8 +589,8 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
         status = _lib.ctypes.c_int64(0)
         rc = _lib.load().mlxc_rejection_sampling_cpu(
             _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,
-            p, q, seed, _RULES[rule], rows, _ptr(n_out), _ptr(e_out), otype, _threads(threads),
-            _lib.ctypes.addressof(status))
+            p, q, seed, offset, _RULES[rule], rows, _ptr(n_out), _ptr(e_out), otype,
+            _threads(threads), _lib.ctypes.addressof(status))
         _lib.check(rc, "rejection_sampling")
         if check:
             _raise_bits(int(status.value), "rejection_sampling")
@@ -414,23 +598,21 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     device = _resolve_device(stream, (rowptr, col, start))
     handle = _stream_handle(stream, device)
     rowptr, col, start = (_on(t, device) for t in (rowptr, col, start))
-    n_out = torch.empty((N, L + 1), dtype=out_dtype, device=device)
-    e_out = torch.empty((N, L), dtype=out_dtype, device=device) if return_edges else None
     lib = _lib.load()
-    work = _workspace(lib.mlxc_rejection_sampling_workspace_bytes(
-        rowptr.numel() - 1, col.numel(), N, L, float(p), float(q), _RULES[rule]), device)
-    side = _side_stream(stream, device)
-    _enter_side_stream(side, device)
-    with _on_device(device):
-        rc = lib.mlxc_rejection_sampling(
-            _ptr(rowptr), rowptr.numel() - 1, _ptr(col), col.numel(), _ptr(start), N, L,
-            p, q, seed, _RULES[rule], rows, _ptr(n_out),
-            _ptr(e_out) if return_edges else None, otype, work.data_ptr(), work.numel() * 8,
-            handle)
-    _leave_side_stream(side, rowptr, col, start, n_out, e_out, work)
-    _lib.check(rc, "rejection_sampling")
-    if check:
-        _raise_status(work, stream, "rejection_sampling")
+    V, E, rid = rowptr.numel() - 1, col.numel(), _RULES[rule]
+    rowptr_p, col_p = _ptr(rowptr), _ptr(col)
+    start_p = start.data_ptr() if N else None
+
+    def launch(i0, n, n_p, e_p, ws_p, ws_bytes):
+        s_p = start_p + 8 * i0 if start_p else None
+        return lib.mlxc_rejection_sampling(rowptr_p, V, col_p, E, s_p, n, L, p, q, seed,
+                                           offset + i0, rid, rows, n_p, e_p, otype, ws_p,
+                                           ws_bytes, handle)
+
+    n_out, e_out = _run_walks(
+        device, stream, handle, N, L, out_dtype, return_edges,
+        lambda n: lib.mlxc_rejection_sampling_workspace_bytes(V, E, n, L, p, q, rid), launch,
+        budget, check, "rejection_sampling", (rowptr, col, start))
     return (n_out, e_out) if return_edges else n_out
 
 

@@ -57,6 +57,7 @@ def _load():
         lib.oracle_u32_to_unit_float.argtypes = [u32]
         lib.oracle_u32_to_unit_float.restype = ctypes.c_float
         lib.oracle_philox_uniform_fill.argtypes = [P, i64, u64]
+        lib.oracle_philox_uniform_fill_at.argtypes = [P, i64, i64, u64]
         lib.oracle_node2vec_trial0_u0.argtypes = [P, i64, i32, u64]
         lib.oracle_pick_index.argtypes = [ctypes.c_float, i64]
         lib.oracle_pick_index.restype = i64
@@ -95,9 +96,13 @@ def u32_to_unit_float(x: int) -> float:
     return float(np.float32(_load().oracle_u32_to_unit_float(int(x))))
 
 
-def philox_uniform(n: int, seed: int) -> np.ndarray:
+def philox_uniform(n: int, seed: int, first: int = 0) -> np.ndarray:
+    """Elements [first, first + n) of the Philox uniform stream of `seed`."""
     out = np.empty(int(n), dtype=np.float32)
-    _load().oracle_philox_uniform_fill(_p(out), int(n), int(seed) & (2**64 - 1))
+    if first == 0:
+        _load().oracle_philox_uniform_fill(_p(out), int(n), int(seed) & (2**64 - 1))
+    else:
+        _load().oracle_philox_uniform_fill_at(_p(out), int(first), int(n), int(seed) & (2**64 - 1))
     return out
 
 

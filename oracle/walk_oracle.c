@@ -42,13 +42,22 @@ float oracle_u32_to_unit_float(uint32_t x) {
 }
 
 void oracle_philox_uniform_fill(float* out, int64_t n, uint64_t seed) {
+    oracle_philox_uniform_fill_at(out, 0, n, seed);
+}
+
+void oracle_philox_uniform_fill_at(float* out, int64_t first, int64_t n, uint64_t seed) {
     uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
-    for (int64_t base = 0; base < n; base += 4) {
-        uint64_t blk = (uint64_t)base >> 2;
-        uint32_t ctr[4] = {(uint32_t)blk, (uint32_t)(blk >> 32), 0u, 0u};
-        uint32_t w[4];
-        oracle_philox4x32_10(ctr, key, w);
-        for (int k = 0; k < 4 && base + k < n; ++k) out[base + k] = oracle_u32_to_unit_float(w[k]);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    uint64_t have = UINT64_MAX;  /* block whose words are in w */
+    for (int64_t i = 0; i < n; ++i) {
+        uint64_t pos = (uint64_t)(first + i);
+        uint64_t blk = pos >> 2;
+        if (blk != have) {
+            uint32_t ctr[4] = {(uint32_t)blk, (uint32_t)(blk >> 32), 0u, 0u};
+            oracle_philox4x32_10(ctr, key, w);
+            have = blk;
+        }
+        out[i] = oracle_u32_to_unit_float(w[pos & 3]);
     }
 }
 

@@ -50,6 +50,11 @@ float oracle_u32_to_unit_float(uint32_t x);
  * key = (seed lo, seed hi)). */
 void oracle_philox_uniform_fill(float* out, int64_t n, uint64_t seed);
 
+/* Elements [first, first + n) of the same stream: out[i] is element
+ * first + i (the uniforms of walks [w0, w1) of an L-step seeded uniform walk
+ * are elements [w0 * L, w1 * L)). */
+void oracle_philox_uniform_fill_at(float* out, int64_t first, int64_t n, uint64_t seed);
+
 /* Trial-0 candidate uniform of the node2vec stream, materialised as a
  * [N, L] rand tensor: out[n*L + l] = u0(seed; n, l, 0). */
 void oracle_node2vec_trial0_u0(float* out, int64_t N, int32_t L, uint64_t seed);

@@ -21,7 +21,7 @@ int main(void) {
     const int64_t row[] = {2, 0, 3, 1, 0, 0};
     const int64_t col[] = {3, 2, 0, 2, 1, 2};
     int64_t rowptr[5], cols[6], count = 0, status = -1;
-    CHECK(mlxc_version() >= 200);
+    CHECK(mlxc_version() >= 300);
     CHECK(mlxc_csr_build_cpu(row, col, 6, 4, MLXC_CSR_DEDUP, rowptr, cols, &count, &status) ==
           MLXC_OK);
     CHECK(status == 0 && count == 5);
@@ -41,7 +41,7 @@ int main(void) {
 
     /* node2vec with p = q = 1 accepts the first candidate of every step */
     int64_t n2v[2 * 4];
-    CHECK(mlxc_rejection_sampling_cpu(rowptr, 4, cols, 5, start, 2, 3, 1.0, 1.0, 42,
+    CHECK(mlxc_rejection_sampling_cpu(rowptr, 4, cols, 5, start, 2, 3, 1.0, 1.0, 42, 0,
                                       MLXC_RULE_REF_CHAIN, MLXC_ROWS_DETECT, n2v, NULL,
                                       MLXC_OUT_INT64, 2, &status) == MLXC_OK);
     CHECK(status == 0 && n2v[0] == 0 && n2v[4] == 3);

@@ -88,7 +88,7 @@ def host_uniform_status(lib, rowptr, col, start, L, *, seed=None, rand=None):
                                       ctypes.addressof(status))
     else:
         rc = lib.mlxc_random_walk_seeded_cpu(p(rowptr), rowptr.size - 1, p(col), col.size,
-                                             p(start), N, L, seed, p(n_out), p(e_out), 0, 2,
+                                             p(start), N, L, seed, 0, p(n_out), p(e_out), 0, 2,
                                              ctypes.addressof(status))
     assert rc == 0
     return int(status.value)
@@ -103,7 +103,7 @@ def host_node2vec_status(lib, rowptr, col, start, L, p, q, seed, rule, rows):
     status = ctypes.c_int64(-1)
     ptr = lambda a: a.ctypes.data
     rc = lib.mlxc_rejection_sampling_cpu(ptr(rowptr), rowptr.size - 1, ptr(col), col.size,
-                                         ptr(start), N, L, p, q, seed, rule, rows, ptr(n_out),
+                                         ptr(start), N, L, p, q, seed, 0, rule, rows, ptr(n_out),
                                          ptr(e_out), 0, 2, ctypes.addressof(status))
     assert rc == 0
     return int(status.value)

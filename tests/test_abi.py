@@ -47,7 +47,7 @@ def test_header_constants_match_binding():
 
 
 def test_version():
-    assert _lib.load().mlxc_version() == 200
+    assert _lib.load().mlxc_version() == 300
 
 
 FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
@@ -95,7 +95,7 @@ def test_out_type_is_checked(num_nodes, num_edges, e_out, out_type, msg):
 ])
 def test_rejection_sampling_rejects_bad_arguments(p, q, rule, msg):
     lib = _lib.load()
-    rc = lib.mlxc_rejection_sampling(FAKE, 1, FAKE, 0, FAKE, 0, 3, p, q, 1, rule, 1, FAKE, None,
+    rc = lib.mlxc_rejection_sampling(FAKE, 1, FAKE, 0, FAKE, 0, 3, p, q, 1, 0, rule, 1, FAKE, None,
                                      0, FAKE, WS, None)
     assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT
     assert msg in _lib.last_error()
@@ -103,7 +103,7 @@ def test_rejection_sampling_rejects_bad_arguments(p, q, rule, msg):
 
 def test_rejection_sampling_rejects_bad_row_mode():
     lib = _lib.load()
-    rc = lib.mlxc_rejection_sampling(FAKE, 1, FAKE, 0, FAKE, 0, 3, 1.0, 1.0, 1, 0, 3, FAKE, None,
+    rc = lib.mlxc_rejection_sampling(FAKE, 1, FAKE, 0, FAKE, 0, 3, 1.0, 1.0, 1, 0, 0, 3, FAKE, None,
                                      0, FAKE, WS, None)
     assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT and "rows" in _lib.last_error()
 

@@ -68,3 +68,63 @@ def test_rejection_sampling_validation(p, q, rule, exc):
 def test_no_gpu_fails_loudly():
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         mc.random_walk(ROWPTR, COL, START, RAND, 4)
+
+
+def test_walk_offset_validation():
+    with pytest.raises(ValueError, match="walk_offset"):
+        mc.random_walk(ROWPTR, COL, START, RAND, 4, walk_offset=3, stream="cpu")
+    with pytest.raises(ValueError, match="walk_offset"):
+        mc.random_walk(ROWPTR, COL, START, None, 4, seed=1, walk_offset=-1, stream="cpu")
+    with pytest.raises(TypeError, match="walk_offset"):
+        mc.rejection_sampling(ROWPTR, COL, START, 4, 1.0, 1.0, walk_offset=1.5, stream="cpu")
+    with pytest.raises(ValueError, match="memory_budget"):
+        mc.random_walk(ROWPTR, COL, START, None, 4, seed=1, memory_budget=0, stream="cpu")
+
+
+# -------------------------------------------------- chunk planning (host logic)
+
+def _records_query(E):
+    """A workspace query shaped like the uniform walk's: records (8 bytes per
+    edge and walk) when the call takes at least 4 steps per edge, else 16
+    bytes per walk."""
+    return lambda n: 256 + (8 * (E + n) if n * 20 >= 4 * E else 16 * n)
+
+
+def test_plan_one_call_when_everything_fits():
+    from mlx_cluster_amd.walks import _plan
+    q = _records_query(1000)
+    assert _plan(10_000, 168, q, 10_000 * 168 + q(10_000)) == ("device", None, q(10_000))
+
+
+def test_plan_shrinks_the_workspace_before_chunking():
+    from mlx_cluster_amd.walks import _MIN_WORKSPACE, _plan
+    q = _records_query(10**6)
+    N, row = 10_000, 168
+    budget = N * row + 5000
+    mode, chunk, ws = _plan(N, row, q, budget)
+    assert (mode, chunk) == ("device", None) and _MIN_WORKSPACE <= ws <= 5000 and ws % 16 == 0
+
+
+@pytest.mark.parametrize("N,row,E,budget", [
+    (100_000, 168, 1000, 4_000_000), (100_000, 168, 10**6, 4_000_000),
+    (1_000_000, 656, 16 * 10**6, 300 * 2**20), (777, 48, 10, 20_000), (50, 8, 10, 300)])
+def test_plan_chunks_fit_the_budget(N, row, E, budget):
+    """Outputs larger than the budget: chunks whose two staging buffers and
+    workspace fit it, whole multiples of 64 walks when a chunk holds that
+    many, as large as the budget allows."""
+    from mlx_cluster_amd.walks import _CHUNK_ALIGN, _MIN_WORKSPACE, _plan
+    q = _records_query(E)
+    mode, chunk, ws = _plan(N, row, q, budget)
+    assert mode == "host" and 1 <= chunk <= N
+    assert 2 * chunk * row + ws <= budget and ws >= _MIN_WORKSPACE
+    if chunk >= _CHUNK_ALIGN:
+        assert chunk % _CHUNK_ALIGN == 0
+        bigger = chunk + _CHUNK_ALIGN
+        assert bigger > N or 2 * bigger * row + min(q(bigger), _MIN_WORKSPACE) > budget or \
+            2 * bigger * row + q(bigger) > budget
+
+
+def test_plan_rejects_a_budget_below_one_walk():
+    from mlx_cluster_amd.walks import _plan
+    with pytest.raises(ValueError, match="memory_budget"):
+        _plan(10, 1000, lambda n: 256 + 16 * n, 1000)

@@ -46,7 +46,7 @@ def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode, out_dtype=tor
     ws = torch.zeros((nbytes + 7) // 8, dtype=torch.int64, device=start.device)
     ptr = lambda t: t.data_ptr() if t.numel() else None
     rc = lib.mlxc_rejection_sampling(ptr(rowptr), V, ptr(col), E,
-                                     ptr(start), N, L, p, q, seed, rule, rows, ptr(n), ptr(e),
+                                     ptr(start), N, L, p, q, seed, 0, rule, rows, ptr(n), ptr(e),
                                      out_type, ws.data_ptr(), nbytes,
                                      torch.cuda.current_stream().cuda_stream)
     assert rc == 0, _lib.last_error()

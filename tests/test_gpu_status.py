@@ -37,7 +37,7 @@ def _n2v_status(rowptr, col, start, L, seed, rows, mode, cuda):
     n = torch.empty((N, L + 1), dtype=torch.int64, device=cuda)
     e = torch.empty((N, L), dtype=torch.int64, device=cuda)
     rc = lib.mlxc_rejection_sampling(rowptr.data_ptr(), V, col.data_ptr(), E, start.data_ptr(),
-                                     N, L, p, q, seed, rule, rows, n.data_ptr(), e.data_ptr(),
+                                     N, L, p, q, seed, 0, rule, rows, n.data_ptr(), e.data_ptr(),
                                      _lib.MLXC_OUT_INT64, ws.data_ptr(), nbytes,
                                      torch.cuda.current_stream().cuda_stream)
     assert rc == 0, _lib.last_error()
@@ -78,7 +78,7 @@ def _uniform_status(rowptr, col, start, L, mode, seeded, cuda):
     graph = (rowptr.data_ptr(), V, col.data_ptr(), E, start.data_ptr(), N)
     outs = (n.data_ptr(), e.data_ptr(), _lib.MLXC_OUT_INT64, ws.data_ptr(), nbytes, stream)
     if seeded:
-        rc = lib.mlxc_random_walk_seeded(*graph, L, 5, *outs)
+        rc = lib.mlxc_random_walk_seeded(*graph, L, 5, 0, *outs)
     else:
         rand = torch.full((max(N * L, 1),), 0.5, dtype=torch.float32, device=cuda)
         rc = lib.mlxc_random_walk(*graph, rand.data_ptr(), L, *outs)

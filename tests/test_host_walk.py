@@ -125,12 +125,12 @@ def test_symmetric_flag_is_accepted_and_checked():
     ptr = lambda t: t.data_ptr()
     for rows in (3, 7, 8, -1):
         rc = lib.mlxc_rejection_sampling_cpu(ptr(rowptr), rowptr.numel() - 1, ptr(col), col.numel(),
-                                             ptr(start), 1, 2, 1.0, 1.0, 1, 0, rows, ptr(out), None,
+                                             ptr(start), 1, 2, 1.0, 1.0, 1, 0, 0, rows, ptr(out), None,
                                              _lib.MLXC_OUT_INT64, 1, None)
         assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT, rows
     for rows in (4, 5, 6):
         rc = lib.mlxc_rejection_sampling_cpu(ptr(rowptr), rowptr.numel() - 1, ptr(col), col.numel(),
-                                             ptr(start), 1, 2, 1.0, 1.0, 1, 0, rows, ptr(out), None,
+                                             ptr(start), 1, 2, 1.0, 1.0, 1, 0, 0, rows, ptr(out), None,
                                              _lib.MLXC_OUT_INT64, 1, None)
         assert rc == _lib.MLXC_OK, rows
 
@@ -256,3 +256,84 @@ def test_uniform_status_bits(case):
     for seed in (None, 5):
         got = status_cases.host_uniform_status(_lib.load(), rowptr, col, start, L, seed=seed)
         assert got == want, (name, seed, got)
+
+
+# ------------------------------------------------------------ walk offsets
+
+
+@pytest.mark.parametrize("cuts", [(0, 1000), (0, 1, 64, 999, 1000), (0, 333, 334, 1000)])
+def test_seeded_uniform_slices_equal_whole_call(cuts):
+    """walk_offset: the call on start[i0:i1] with walk_offset=i0 gives rows
+    i0 .. i1-1 of the whole call, and those rows are the oracle's walk on the
+    stream elements [i0 * L, i1 * L)."""
+    rowptr, col = synth.rmat_csr(11, 20000, seed=8)
+    rowptr_h, col_h = rowptr.numpy(), col.numpy()
+    V, L, seed = rowptr.numel() - 1, 11, 31
+    start = torch.arange(1000) * 7 % V
+    whole_n, whole_e = mc.random_walk(rowptr, col, start, None, L, seed=seed, stream="cpu",
+                                      return_edges=True)
+    for i0, i1 in zip(cuts[:-1], cuts[1:]):
+        n, e = mc.random_walk(rowptr, col, start[i0:i1], None, L, seed=seed, walk_offset=i0,
+                              stream="cpu", return_edges=True)
+        assert torch.equal(n, whole_n[i0:i1]) and torch.equal(e, whole_e[i0:i1])
+        rand = oracle.philox_uniform((i1 - i0) * L, seed, first=i0 * L).reshape(-1, L)
+        n_ref, e_ref, st, _ = oracle.uniform_walk(rowptr_h, col_h, start[i0:i1].numpy(), rand, L,
+                                                  with_edges=True)
+        assert st == 0
+        np.testing.assert_array_equal(n.numpy(), n_ref)
+        np.testing.assert_array_equal(e.numpy(), e_ref)
+
+
+@pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
+def test_node2vec_slices_equal_whole_call(rule):
+    """walk_offset on the node2vec walk: slices equal the whole call and the
+    oracle's walk with first_walk = i0 (Philox counter = global walk index)."""
+    rowptr, col = synth.rmat_csr(11, 20000, seed=9, symmetrize=True)
+    rowptr_h, col_h = rowptr.numpy(), col.numpy()
+    V, L, seed, p, q = rowptr.numel() - 1, 9, 12, 0.5, 2.0
+    start = torch.arange(900) * 5 % V
+    whole_n, whole_e = n2v_cpu(rowptr, col, start, L, p, q, seed, rule)
+    for i0, i1 in ((0, 300), (300, 301), (301, 900)):
+        n, e = n2v_cpu(rowptr, col, start[i0:i1], L, p, q, seed, rule, walk_offset=i0)
+        np.testing.assert_array_equal(n, whole_n[i0:i1])
+        np.testing.assert_array_equal(e, whole_e[i0:i1])
+        n_ref, e_ref, st, _ = oracle.node2vec_walk(rowptr_h, col_h, start[i0:i1].numpy(), L, p,
+                                                   q, seed, rule=rule, with_edges=True,
+                                                   first_walk=i0)
+        assert st == 0
+        np.testing.assert_array_equal(n, n_ref)
+        np.testing.assert_array_equal(e, e_ref)
+
+
+def test_walk_offset_far_into_the_stream():
+    """An offset past 2^32 walks reaches the counter's high word: the host
+    twin equals the oracle there."""
+    rowptr, col = synth.rmat_csr(9, 4000, seed=2, symmetrize=True)
+    rowptr_h, col_h = rowptr.numpy(), col.numpy()
+    start = torch.arange(50) % (rowptr.numel() - 1)
+    first, L = (1 << 33) + 17, 6
+    n = mc.random_walk(rowptr, col, start, None, L, seed=5, walk_offset=first, stream="cpu")
+    rand = oracle.philox_uniform(50 * L, 5, first=first * L).reshape(50, L)
+    np.testing.assert_array_equal(n.numpy(),
+                                  oracle.uniform_walk(rowptr_h, col_h, start.numpy(), rand, L)[0])
+    n, _ = n2v_cpu(rowptr, col, start, L, 2.0, 0.5, 3, oracle.RULE_NODE2VEC_EXACT,
+                   walk_offset=first)
+    np.testing.assert_array_equal(n, oracle.node2vec_walk(
+        rowptr_h, col_h, start.numpy(), L, 2.0, 0.5, 3, rule=oracle.RULE_NODE2VEC_EXACT,
+        first_walk=first)[0])
+
+
+def test_first_walk_checked_by_the_abi():
+    from mlx_cluster_amd import _lib
+    lib = _lib.load()
+    rowptr, col = csr(3, [(0, 1), (1, 2), (2, 0)])
+    start = np.array([0, 1], dtype=np.int64)
+    out = np.empty((2, 5), np.int64)
+    p = lambda a: a.ctypes.data
+    for first in (-1, 2**63 // 4):  # negative; (first + N) * L past int64
+        rc = lib.mlxc_random_walk_seeded_cpu(p(rowptr), 3, p(col), 3, p(start), 2, 4, 1, first,
+                                             p(out), None, 0, 1, None)
+        assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT and "first_walk" in _lib.last_error()
+        rc = lib.mlxc_rejection_sampling_cpu(p(rowptr), 3, p(col), 3, p(start), 2, 4, 1.0, 1.0,
+                                             1, first, 0, 1, p(out), None, 0, 1, None)
+        assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT and "first_walk" in _lib.last_error()

@@ -64,6 +64,23 @@ def test_uniform_fill_layout():
     assert u.min() >= 0.0 and u.max() < 1.0
 
 
+@pytest.mark.parametrize("first", [1, 6, 4096 * 80 + 3, (1 << 34) + 5])
+def test_uniform_fill_at_offset(first):
+    """Elements [first, first + n) of the stream: each rebuilt from one
+    Philox block (counter (pos//4 lo, pos//4 hi, 0, 0)), the high counter
+    word included past 2^34; and equal to the slice of the fill from 0."""
+    seed = 0x0BAD_5EED_0000_0042
+    n = 13
+    u = oracle.philox_uniform(n, seed, first=first)
+    key = [seed & 0xFFFFFFFF, seed >> 32]
+    for i in range(n):
+        pos = first + i
+        w = oracle.philox4x32_10([(pos >> 2) & 0xFFFFFFFF, pos >> 34, 0, 0], key)[pos % 4]
+        assert u[i] == np.float32((int(w) >> 8) * 2.0 ** -24)
+    if first < 1 << 20:
+        assert np.array_equal(oracle.philox_uniform(first + n, seed)[first:], u)
+
+
 def test_uniform_fill_is_uniform():
     u = oracle.philox_uniform(200_000, 7)
     assert stats.kstest(u, "uniform").pvalue > 0.01
