@@ -224,42 +224,158 @@ def cpu_all_cores_context(np, torch, mc, kind, rowptr_h, col_h, start, rand, L, 
                     "threads (small calls use fewer: one per 2^16 uniform or 2^12 node2vec steps)"}
 
 
-def gather_ceiling(torch, dev):
-    """Random-gather ceiling: out[i] = table[idx[i]] with 2^26 independent
-    uniform int64 indices (torch.take), for tables from 32 MiB (L2/MALL
-    resident) to 8 GiB (HBM).  Reports gathered lines/s and the equivalent
-    GB/s at 64 and 128 bytes per line; the idx and out streams are included
-    in the time, not in the line count."""
-    res = []
-    n = 1 << 26
-    for mib in (32, 128, 256, 1024, 8192):
-        table = torch.arange(mib << 17, dtype=torch.int64, device=dev)
-        g = torch.Generator(device=dev).manual_seed(mib)
-        idx = torch.randint(0, table.numel(), (n,), generator=g, device=dev)
-        out = torch.take(table, idx)
-        torch.cuda.synchronize()
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        ev[0].record()
-        reps = 10
-        for _ in range(reps):
-            torch.take(table, idx, out=out) if hasattr(torch, "take") else None
-        ev[1].record()
-        torch.cuda.synchronize()
-        ms = ev[0].elapsed_time(ev[1]) / reps
-        lines = n / (ms / 1e3)
-        res.append({"table_MiB": mib, "ms": ms, "gathers_per_s": lines,
-                    "GBs_at_64B": lines * 64 / 1e9, "GBs_at_128B": lines * 128 / 1e9,
-                    "stream_GBs": n * 16 / (ms / 1e3) / 1e9})
-        log(f"gather table {mib} MiB: {ms:.3f} ms, {lines:.3e} gathers/s")
-        del table, idx, out
-    return {"gather_ceiling": res}
+# Table sizes of the random-read ceiling: from tables the L2s and the
+# Infinity Cache hold to ones only HBM holds (the walk configurations' random
+# footprints lie between 100 MB and 6 GB).
+CEILING_MIB = (32, 128, 256, 512, 1024, 2048, 4096, 8192)
+
+
+def gather_ceiling(torch, dev, variant=None, target_loads=150_000_000):
+    """Random-read ceiling of the device (mlxc_gather_probe): for each table
+    size, reads at addresses uniform over the table, swept over independent
+    and dependent chains (each address depending on the value the chain read
+    before, as in a walk), 1 to 8 chains per lane, 2 to 8 blocks of 256 threads
+    per compute unit and 16- or 4-byte reads; HIP events over 3 launches after
+    a warm-up, median.  Every read of a table beyond the L2s costs one 128-byte
+    line between the L2 and the fabric, so reads/s is the line rate a walk
+    kernel can reach at most.  variant = (dependent, chains, blocks_per_cu,
+    bytes) runs that one variant per size (for counter passes)."""
+    import statistics
+    from mlx_cluster_amd import _lib
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    table = torch.randint(-2**31, 2**31 - 1, (max(CEILING_MIB) << 18,), dtype=torch.int32,
+                          device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    issued = _lib.ctypes.c_int64(0)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    variants = ([variant] if variant else
+                [(d, k, b, 16) for d in (0, 1) for k in (1, 2, 4, 8) for b in (2, 4, 8)])
+
+    def run(mib, d, k, b, nbytes):
+        iters = max(1, -(-target_loads // (cus * b * 256 * k)))
+        args = (table.data_ptr(), mib << 20, nbytes, k, d, b, iters, 12345, sink.data_ptr(),
+                _lib.ctypes.addressof(issued), stream.cuda_stream)
+        if lib.mlxc_gather_probe(*args) != 0:
+            raise RuntimeError(_lib.last_error())
+        ms = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            lib.mlxc_gather_probe(*args)
+            e1.record(stream)
+            e1.synchronize()
+            ms.append(e0.elapsed_time(e1))
+        t = statistics.median(ms)
+        return {"dependent": d, "chains_per_lane": k, "blocks_per_cu": b, "load_bytes": nbytes,
+                "reads": issued.value, "ms": t, "reads_per_s": issued.value / (t / 1e3)}
+
+    sizes = []
+    for mib in CEILING_MIB:
+        runs = [run(mib, *v) for v in variants]
+        if variant is None:  # the best independent variant again with 4-byte reads
+            best = max((r for r in runs if not r["dependent"]), key=lambda r: r["reads_per_s"])
+            runs.append(run(mib, 0, best["chains_per_lane"], best["blocks_per_cu"], 4))
+        top = max(runs, key=lambda r: r["reads_per_s"])
+        dep = [r for r in runs if r["dependent"]]
+        sizes.append({"table_MiB": mib, "lines_per_s": top["reads_per_s"], "best": top,
+                      "dependent_lines_per_s": max(r["reads_per_s"] for r in dep) if dep else None,
+                      "runs": runs})
+        log(f"ceiling {mib} MiB: {top['reads_per_s']:.3e} reads/s "
+            f"(dependent={top['dependent']} k={top['chains_per_lane']} "
+            f"blocks/CU={top['blocks_per_cu']} {top['load_bytes']} B)")
+    from mlx_cluster_amd.build_lib import source_hash
+    return {"gather_ceiling": sizes, "kernel_family": "gather_probe",
+            "kernel_source_sha256_16": source_hash("gather_probe"),
+            "device": torch.cuda.get_device_name(dev), "compute_units": cus}
+
+
+def line_ceiling(table_bytes):
+    """Random-read ceiling (lines/s) at a random footprint of table_bytes,
+    interpolated log-linearly in size between the committed measurements
+    (profiles/gather_ceiling.json, for the current probe source), clamped to
+    the measured range; None without a matching measurement."""
+    import math
+    from mlx_cluster_amd.build_lib import source_hash
+    path = os.path.join(REPO, "profiles", "gather_ceiling.json")
+    if not table_bytes or not os.path.exists(path):
+        return None
+    d = json.load(open(path))
+    if d.get("kernel_source_sha256_16") != source_hash("gather_probe"):
+        return None
+    pts = sorted((s["table_MiB"] * 2**20, s["lines_per_s"]) for s in d["gather_ceiling"])
+    if table_bytes <= pts[0][0]:
+        return pts[0][1]
+    for (b0, r0), (b1, r1) in zip(pts, pts[1:]):
+        if table_bytes <= b1:
+            f = math.log(table_bytes / b0) / math.log(b1 / b0)
+            return r0 + f * (r1 - r0)
+    return pts[-1][1]
+
+
+def random_footprint(mc, kind, V, E, N, L, extra):
+    """Bytes of the tables a walk call reads at random addresses, by the layout
+    its workspace query selects: the uniform record walk its edge records (8
+    or 16 bytes each), the uniform CSR walk col and rowptr; the node2vec walk
+    its workspace less the start records (edge records or the CSR mode's row
+    starts, the search index, the hub bitmaps).  None for the LDS walks, which
+    read no global table at random."""
+    lib = mc._lib.load()
+    if kind == "uniform":
+        ws = lib.mlxc_random_walk_workspace_bytes(V, E, N, L)
+        if ws <= 256:
+            return None
+        rec = 8 if (V - 1).bit_length() + E.bit_length() <= 48 else 16
+        return rec * E if ws >= 256 + rec * (E + N) else 8 * E + 8 * (V + 1)
+    ws = lib.mlxc_rejection_sampling_workspace_bytes(V, E, N, L, extra["p"], extra["q"],
+                                                     RULE_ID[extra["rule"]])
+    return None if ws <= 256 else ws - 256 - 16 * N
+
+
+def line_roofline(mc, kind, config, V, E, N, L, extra):
+    """lines/s of the walk kernel and its fraction of the ceiling at the call's
+    random footprint (nulls where a profile or the ceiling is missing)."""
+    foot = random_footprint(mc, kind, V, E, N, L, extra)
+    ceiling = line_ceiling(foot)
+    prof = walk_profile(f"{kind}_walk_{config}")
+    rate = prof["walk_kernel_ea_rdreq"] / (prof["walk_kernel_avg_ms"] / 1e3) if prof else None
+    return {"random_table_bytes": foot, "line_ceiling_per_s": ceiling,
+            "walk_kernel": prof["walk_kernel"] if prof else None,
+            "walk_kernel_ms_rocprof": prof["walk_kernel_avg_ms"] if prof else None,
+            "walk_kernel_lines_per_launch": prof["walk_kernel_ea_rdreq"] if prof else None,
+            "lines_per_s": rate,
+            "line_frac": rate / ceiling if rate and ceiling else None,
+            "line_frac_source": "TCC_EA0_RDREQ of the walk kernel per dispatch / its rocprofv3 "
+                                "average duration, over the random-read ceiling "
+                                "(profiles/gather_ceiling.json) at random_table_bytes"}
+
+
+def walk_profile(name: str):
+    """The committed rocprofv3 figures of a walk configuration's main kernel
+    (its average duration and TCC_EA0_RDREQ per dispatch), when the summary
+    matches the current kernel source; else None."""
+    from mlx_cluster_amd.build_lib import KERNEL_SOURCES
+    family = next((k for k in KERNEL_SOURCES if name.startswith(k + "_")), None)
+    path = os.path.join(REPO, "profiles", f"{name}_traffic.json")
+    if family is None or not os.path.exists(path):
+        return None
+    d = json.load(open(path))
+    if (d.get("kernel_family") != family or
+            d.get("kernel_source_sha256_16") != kernel_source_hash(family) or
+            "walk_kernel_ea_rdreq" not in d):
+        return None
+    return d
 
 
 def node2vec_bytes(np, oracle, rowptr_h, col_h, start_h, L, extra, walks=200_000):
-    """Roofline bytes of a node2vec call, 64*(S_move+Z) + 64*T + 64*(Q+P) + 8*N*(L+1) + 8*N
-    (each dependent random read of the reference loop charged one 64-byte line, streams
-    their bytes), with the counts from the oracle over an evenly strided sample of walks
-    scaled to N."""
+    """Roofline bytes of a node2vec call under the measurement contract's
+    formula, 64*S_move + 64*T + 64*P + 8*N*(L+1) (a 64-byte line per moving
+    step's row read, per trial's candidate read and per col line a lower_bound
+    search touches; the output stream at its bytes), with the counts from the
+    oracle over an evenly strided sample of walks scaled to N.  Also returns
+    the bytes of a wider formula that adds a row line per membership test and
+    per sink walk and the start stream, 64*(S+Z) + 64*T + 64*(Q+P) +
+    8*N*(L+1) + 8*N."""
     N = start_h.shape[0]
     idx = np.linspace(0, N - 1, min(N, walks)).astype(np.int64)
     _, _, st, c = oracle.node2vec_walk(rowptr_h, col_h, start_h[idx], L, extra["p"], extra["q"],
@@ -268,11 +384,14 @@ def node2vec_bytes(np, oracle, rowptr_h, col_h, start_h, L, extra, walks=200_000
     f = N / idx.size
     S, Z, T = c["moving_steps"] * f, c["sink_walks"] * f, c["trials"] * f
     Q, P = c["member_tests"] * f, c["member_lines"] * f
-    b = LINE * (S + Z) + LINE * T + LINE * (Q + P) + 8 * N * (L + 1) + 8 * N
+    b = LINE * S + LINE * T + LINE * P + 8 * N * (L + 1)
+    wide = LINE * (S + Z) + LINE * T + LINE * (Q + P) + 8 * N * (L + 1) + 8 * N
     useful = 16 * (S + Z) + 8 * T + 8 * P + 8 * N * (L + 1) + 8 * N
     return int(b), int(useful), dict(moving_steps=int(S), sink_walks=int(Z), trials=int(T),
                         member_tests=int(Q), member_lines=int(P), counts_sample_walks=int(idx.size),
-                        bytes_formula="64*(S+Z) + 64*T + 64*(Q+P) + 8*N*(L+1) + 8*N")
+                        bytes_formula="64*S + 64*T + 64*P + 8*N*(L+1)",
+                        wide_bytes_per_launch=int(wide),
+                        wide_bytes_formula="64*(S+Z) + 64*T + 64*(Q+P) + 8*N*(L+1) + 8*N")
 
 
 def cpu_baseline_node2vec(np, oracle, rowptr_h, col_h, start, L, extra, target_s=12.0):
@@ -558,7 +677,10 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (rocprof counter scale)")
     ap.add_argument("--gather-ceiling", action="store_true",
-                    help="measure independent random 8-byte gathers over tables of several sizes")
+                    help="measure the random-read ceiling over tables of 32 MiB to 8 GiB")
+    ap.add_argument("--gather-variant", default=None,
+                    help="with --gather-ceiling: one variant 'dependent,chains,blocks_per_cu,"
+                         "bytes' per size instead of the sweep")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the walks need no cross-GPU exchange, so k GPUs would "
@@ -586,7 +708,8 @@ def main():
         return
 
     if args.gather_ceiling:
-        print(json.dumps(gather_ceiling(torch, dev)), flush=True)
+        v = tuple(int(x) for x in args.gather_variant.split(",")) if args.gather_variant else None
+        print(json.dumps(gather_ceiling(torch, dev, v)), flush=True)
         return
 
     if args.config in CSR_CONFIGS:
@@ -689,8 +812,16 @@ def main():
                                            extra)
     achieved = roof_bytes / (kernel_ms / 1e3) / 1e9 if roof_bytes else None
     traffic = traffic_from_profile(f"{kind}_walk_{args.config}")
+    if "wide_bytes_per_launch" in units:
+        units["frac_wide_formula"] = units["wide_bytes_per_launch"] / (kernel_ms / 1e3) / 1e9 / \
+            PEAK_HBM_GBS
+    # The walk kernel's own line rate (TCC_EA0_RDREQ per dispatch over its
+    # average duration, from the committed profile of this source) against the
+    # random-read ceiling at the call's random footprint.
+    lines = line_roofline(mc, kind, args.config, V, E, N, L, extra)
     roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": (achieved / PEAK_HBM_GBS) if achieved else None, "traffic": traffic,
+                **lines,
                 "algorithmic_bytes_per_launch": roof_bytes,
                 "kernel_ms": kernel_ms, "kernel_ms_median": kernel_ms_median,
                 "e2e_ms_with_allocation": e2e_alloc_ms,

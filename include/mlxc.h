@@ -389,6 +389,29 @@ int mlxc_rejection_sampling_cpu(const int64_t* rowptr, int64_t num_nodes,
                                 void* n_out, void* e_out, int32_t out_type,
                                 int32_t threads, int64_t* status);
 
+/*
+ * Diagnostic: random reads from a device table, the measurement behind the
+ * walks' random-read ceiling (a walk step is one or two dependent reads at
+ * random addresses, so the walk kernels are bound by how many such reads the
+ * device completes per second).  Launches blocks_per_cu blocks of 256
+ * threads per compute unit; each thread runs `iterations` rounds of
+ * loads_per_lane (1, 2, 4 or 8) reads of load_bytes (4 or 16) bytes at
+ * addresses uniform over the table (aligned to load_bytes).  dependent = 1
+ * makes each read's address depend on the value the same chain read in the
+ * round before, as a walk's next read depends on the record it just read.
+ * *loads_issued (host) receives the number of reads the launch makes; time
+ * the launch on `stream` to get reads per second.  d_table is 16-byte
+ * aligned, table_bytes in [load_bytes, load_bytes * (2^32 - 1)]; iterations
+ * in [1, 2^24]; blocks_per_cu in [1, 32].  d_sink (one uint32 of device
+ * memory) is written only in the unlikely event that the XOR of the values
+ * read equals a fixed constant, which keeps the reads from being removed.
+ * No reference counterpart.
+ */
+int mlxc_gather_probe(const void* d_table, int64_t table_bytes, int32_t load_bytes,
+                      int32_t loads_per_lane, int32_t dependent, int32_t blocks_per_cu,
+                      int64_t iterations, uint64_t seed, uint32_t* d_sink,
+                      int64_t* loads_issued, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

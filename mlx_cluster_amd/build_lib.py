@@ -15,7 +15,7 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 SOURCES = [os.path.join(CSRC, f) for f in
            ("mlxc_api.hip", "prep_kernels.hip", "uniform_walk.hip", "node2vec_walk.hip",
-            "csr_build.hip", "windows.hip", "host_walk.cpp", "host_csr.cpp")]
+            "csr_build.hip", "windows.hip", "gather_probe.hip", "host_walk.cpp", "host_csr.cpp")]
 OUT = os.path.join(PKG_DIR, "libmlxc.so")
 INCLUDE = os.path.join(REPO_DIR, "include")
 
@@ -96,6 +96,7 @@ KERNEL_SOURCES = {
     "node2vec_walk": ["walk_device.h", "walk_host.h", "prep_kernels.hip", "node2vec_walk.hip"],
     "csr_build": ["walk_device.h", "walk_host.h", "csr_build.hip"],
     "context_windows": ["walk_device.h", "walk_host.h", "windows.hip"],
+    "gather_probe": ["walk_device.h", "walk_host.h", "gather_probe.hip"],
 }
 
 

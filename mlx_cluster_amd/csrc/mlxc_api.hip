@@ -410,6 +410,32 @@ int mlxc_negative_windows(const int64_t* d_start, int64_t num_walks, int32_t wal
                                    out_type, d_out, static_cast<hipStream_t>(stream));
 }
 
+int mlxc_gather_probe(const void* d_table, int64_t table_bytes, int32_t load_bytes,
+                      int32_t loads_per_lane, int32_t dependent, int32_t blocks_per_cu,
+                      int64_t iterations, uint64_t seed, uint32_t* d_sink,
+                      int64_t* loads_issued, void* stream) {
+    if (!d_table || !d_sink || !loads_issued)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "table, sink and loads_issued must not be NULL");
+    if (reinterpret_cast<uintptr_t>(d_table) % 16 != 0)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "table must be 16-byte aligned");
+    if (load_bytes != 4 && load_bytes != 16)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "load_bytes must be 4 or 16");
+    if (table_bytes < load_bytes || table_bytes / load_bytes > int64_t{UINT32_MAX})
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "table_bytes must lie in [load_bytes, load_bytes * (2^32 - 1)]");
+    if (loads_per_lane != 1 && loads_per_lane != 2 && loads_per_lane != 4 && loads_per_lane != 8)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "loads_per_lane must be 1, 2, 4 or 8");
+    if (dependent != 0 && dependent != 1)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "dependent must be 0 or 1");
+    if (blocks_per_cu < 1 || blocks_per_cu > 32)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "blocks_per_cu must lie in [1, 32]");
+    if (iterations < 1 || iterations > (int64_t{1} << 24))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "iterations must lie in [1, 2^24]");
+    return launch_gather_probe(d_table, table_bytes, load_bytes, loads_per_lane, dependent,
+                               blocks_per_cu, iterations, seed, d_sink, loads_issued,
+                               static_cast<hipStream_t>(stream));
+}
+
 int mlxc_context_windows_cpu(const void* walks, int64_t num_walks, int32_t walk_nodes,
                              int32_t context_size, int32_t elem_type, void* out) {
     if (int rc = check_windows(walks, num_walks, walk_nodes, context_size, elem_type, out))

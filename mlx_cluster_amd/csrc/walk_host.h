@@ -164,6 +164,14 @@ int windows_max_nodes(int32_t elem_type);
 // Walks per block of the window kernels (one block per tile of walks).
 int tile_walks(int32_t walk_nodes, size_t esz);
 
+// ---- gather_probe.hip
+// Random reads from a device table (mlxc_gather_probe; arguments checked by
+// the caller); *loads_issued receives the number of loads the launch makes.
+int launch_gather_probe(const void* table, int64_t table_bytes, int32_t load_bytes,
+                        int32_t loads_per_lane, int32_t dependent, int32_t blocks_per_cu,
+                        int64_t iterations, uint64_t seed, uint32_t* sink, int64_t* loads_issued,
+                        hipStream_t stream);
+
 // ---- host_walk.cpp (host pointers; the same walks on CPU threads)
 struct HostWalk {
     const int64_t* rowptr;

@@ -237,3 +237,32 @@ def test_build_beyond_int32_entries(cuda):
     assert torch.equal(out[:n], expect_col)
     del expect_col, out, rowptr
     torch.cuda.empty_cache()
+
+
+def test_rowptr_of_2_28_nodes(cuda):
+    """num_nodes = 2^28 + 3 (a rowptr of 2 GB): the rowptr scans take the
+    levelled form (65,537 chunks, whose sums are scanned first).  A few
+    thousand pairs, clustered at both ends of the id range, equal the oracle;
+    rowptr equals bincount + cumsum of the rows, and the call's time is
+    printed."""
+    import time
+    V = (1 << 28) + 3
+    rng = np.random.default_rng(28)
+    row = np.concatenate([rng.integers(0, 5000, 3000), rng.integers(V - 5000, V, 3000),
+                          rng.integers(0, V, 2000)])
+    col = rng.integers(0, V, row.size)
+    ei = torch.from_numpy(np.stack([row, col])).to(cuda)
+    for dedup in (False, True):
+        mc.to_csr(ei, V, dedup=dedup)  # warm
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        rowptr, c = mc.to_csr(ei, V, dedup=dedup)
+        torch.cuda.synchronize()
+        print(f"to_csr, {row.size} pairs over {V} nodes (dedup={dedup}): "
+              f"{(time.perf_counter() - t0) * 1e3:.2f} ms", flush=True)
+        ref = torch.zeros(V + 1, dtype=torch.int64, device=cuda)
+        torch.cumsum(torch.bincount(ei[0], minlength=V), 0, out=ref[1:])
+        assert torch.equal(rowptr, ref)
+        order = np.lexsort((col, row))
+        np.testing.assert_array_equal(c.cpu().numpy(), col[order])
+        del rowptr, c, ref
