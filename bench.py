@@ -819,6 +819,10 @@ def main():
     # average duration, from the committed profile of this source) against the
     # random-read ceiling at the call's random footprint.
     lines = line_roofline(mc, kind, args.config, V, E, N, L, extra)
+    # the call's whole L2-to-fabric traffic (reads and writes of all its
+    # kernels) against the ceiling's line traffic (128 bytes a line)
+    lines["fabric_frac"] = (traffic / (kernel_ms / 1e3) / (lines["line_ceiling_per_s"] * 128)
+                            if traffic and lines["line_ceiling_per_s"] else None)
     roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": (achieved / PEAK_HBM_GBS) if achieved else None, "traffic": traffic,
                 **lines,

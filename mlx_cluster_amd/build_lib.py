@@ -96,7 +96,9 @@ KERNEL_SOURCES = {
     "node2vec_walk": ["walk_device.h", "walk_host.h", "prep_kernels.hip", "node2vec_walk.hip"],
     "csr_build": ["walk_device.h", "walk_host.h", "csr_build.hip"],
     "context_windows": ["walk_device.h", "walk_host.h", "windows.hip"],
-    "gather_probe": ["walk_device.h", "walk_host.h", "gather_probe.hip"],
+    # the probe's kernel uses nothing from the walk headers (its launcher only
+    # their host helpers)
+    "gather_probe": ["gather_probe.hip"],
 }
 
 

@@ -11,6 +11,8 @@ namespace mlxc {
 
 namespace {
 
+constexpr int kProbeBlock = 256;  // threads per block
+
 // 64-bit LCG step (Knuth's MMIX constants); its high 32 bits are the draw.
 __device__ __forceinline__ uint64_t lcg(uint64_t x) {
     return x * 6364136223846793005ull + 1442695040888963407ull;
@@ -38,11 +40,11 @@ struct ProbeLoad<16> {
 // it equals a value no table of random words makes likely, which keeps the
 // loads live without storing per thread.
 template <int K, int kBytes, bool kDep>
-__global__ __launch_bounds__(kBlock) void gather_probe_kernel(const uint8_t* __restrict__ table,
+__global__ __launch_bounds__(kProbeBlock) void gather_probe_kernel(const uint8_t* __restrict__ table,
                                                               uint64_t slots, int64_t iterations,
                                                               uint64_t seed,
                                                               uint32_t* __restrict__ sink) {
-    const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * kProbeBlock + threadIdx.x;
     uint64_t x[K];
     uint32_t last[K];
 #pragma unroll
@@ -73,10 +75,10 @@ template <int K, int kBytes>
 int launch_probe_k(bool dep, dim3 grid, const uint8_t* table, uint64_t slots, int64_t iterations,
                    uint64_t seed, uint32_t* sink, hipStream_t stream) {
     if (dep)
-        hipLaunchKernelGGL((gather_probe_kernel<K, kBytes, true>), grid, dim3(kBlock), 0, stream,
+        hipLaunchKernelGGL((gather_probe_kernel<K, kBytes, true>), grid, dim3(kProbeBlock), 0, stream,
                            table, slots, iterations, seed, sink);
     else
-        hipLaunchKernelGGL((gather_probe_kernel<K, kBytes, false>), grid, dim3(kBlock), 0, stream,
+        hipLaunchKernelGGL((gather_probe_kernel<K, kBytes, false>), grid, dim3(kProbeBlock), 0, stream,
                            table, slots, iterations, seed, sink);
     MLXC_HIP_TRY(hipGetLastError());
     return MLXC_OK;
@@ -103,7 +105,7 @@ int launch_gather_probe(const void* table, int64_t table_bytes, int32_t load_byt
     if (int rc = device_info(info)) return rc;
     const int64_t blocks = static_cast<int64_t>(info.cus) * blocks_per_cu;
     const uint64_t slots = static_cast<uint64_t>(table_bytes / load_bytes);
-    *loads_issued = blocks * kBlock * iterations * loads_per_lane;
+    *loads_issued = blocks * kProbeBlock * iterations * loads_per_lane;
     const dim3 grid(static_cast<unsigned>(blocks));
     const uint8_t* t = static_cast<const uint8_t*>(table);
     return load_bytes == 4

@@ -418,11 +418,14 @@ def test_c5_full_size_properties(rule, cuda):
     """Configuration 5 at full size (BA graph of 4,000,000 nodes, m = 20, plus
     64 hubs of 500,000 neighbours; p = 4, q = 0.25, 2 walks per node, L = 30),
     with the reference chain (CSR mode: every draw accepts) and the analytic
-    rule (edge records, frequent searches of hub rows).  Every step follows
-    its recorded edge or stays at a node of out-degree 0, and three blocks of
-    1,000 walks spread over the walk-id range are bit-exact against the
-    oracle.  The direct kernel (the path of graphs beyond int32 ids, forced
-    by a minimal workspace) gives the same walks in full."""
+    rule (edge records, frequent searches of hub rows, which the hub bitmaps
+    answer).  Every step follows its recorded edge or stays at a node of
+    out-degree 0.  52,128 walks are bit-exact against the oracle, nodes and
+    edges: 25 blocks of 1,000 spread over the walk-id range, both walks of
+    each of the 64 hubs, and the first walks of 27,000 nodes drawn from the
+    hubs' neighbours (their walks step onto hubs, whose rows the acceptance
+    test searches).  The direct kernel (the path of graphs beyond int32 ids,
+    forced by a minimal workspace) gives the same walks in full."""
     rowptr, col = synth.ba_hub_csr(4_000_000, 20, 64, 500_000, seed=0, device=cuda)
     V, E = rowptr.numel() - 1, col.numel()
     N, L = 2 * V, 30
@@ -444,13 +447,34 @@ def test_c5_full_size_properties(rule, cuda):
         bad += int((~(stay | move)).sum())
     assert bad == 0
     rp, cl = rowptr.cpu().numpy(), col.cpu().numpy()
-    for s0 in (0, N // 2, N - 1000):
+    n_h, e_h = n.cpu().numpy(), e.cpu().numpy()
+    checked = 0
+    for s0 in np.linspace(0, N - 1000, 25).astype(np.int64):
         ref, ref_e, st, _ = oracle.node2vec_walk(rp, cl, start[s0:s0 + 1000].cpu().numpy(), L,
                                                  4.0, 0.25, 5, rule=rule_id, rows_sorted=True,
-                                                 with_edges=True, first_walk=s0)
+                                                 with_edges=True, first_walk=int(s0))
         assert st == 0
-        np.testing.assert_array_equal(n[s0:s0 + 1000].cpu().numpy(), ref)
-        np.testing.assert_array_equal(e[s0:s0 + 1000].cpu().numpy(), ref_e)
+        np.testing.assert_array_equal(n_h[s0:s0 + 1000], ref)
+        np.testing.assert_array_equal(e_h[s0:s0 + 1000], ref_e)
+        checked += 1000
+    # walk n starts at node n % V: the hubs' walks, and the first walks of hub
+    # neighbours (each checked with the oracle told its walk id)
+    deg = np.diff(rp)
+    hubs = np.flatnonzero(deg >= 500_000)
+    assert hubs.size == 64
+    nbrs = np.unique(np.concatenate([cl[rp[h]:rp[h + 1]] for h in hubs]))
+    picks = np.random.default_rng(5).choice(nbrs, 27_000, replace=False)
+    ids = np.concatenate([hubs, hubs + V, picks])
+    for w in ids:
+        ref, ref_e, st, _ = oracle.node2vec_walk(rp, cl, np.array([w % V]), L, 4.0, 0.25, 5,
+                                                 rule=rule_id, rows_sorted=True, with_edges=True,
+                                                 first_walk=int(w))
+        assert st == 0
+        np.testing.assert_array_equal(n_h[w], ref[0])
+        np.testing.assert_array_equal(e_h[w], ref_e[0])
+        checked += 1
+    assert checked >= 50_000
+    print(f"c5 {rule}: {checked} walks bit-exact against the oracle", flush=True)
 
 
 @pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
