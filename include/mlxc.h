@@ -130,15 +130,36 @@ size_t mlxc_random_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges,
  * CSR mode read).
  * Records are also chosen when num_edges <= 32768 * walk_length, and 256
  * bytes (the LDS walk) under the same conditions as for mlxc_random_walk.
- * The record layout ends with room for dense neighbour bitmaps of the rows
- * of highest degree (ceil(num_nodes / 32) words each, at most 1 GiB and one
- * per 256 entries, plus 4 * num_nodes bytes of slot map): membership tests
- * on those rows then take one read.  A workspace that holds the record
- * layout without that room runs with records and no bitmaps; one that holds
- * all of it always runs with records.  No reference counterpart. */
+ * When the call makes row searches (w > 0), the record layout ends with two
+ * more parts: per-row hash tables (64 * (num_edges / 8 + num_nodes + 2)
+ * bytes), which answer a membership test on a row of 2 to 1023 entries in
+ * one read, then dense neighbour bitmaps of the rows of highest degree
+ * (ceil(num_nodes / 32) words each, at most 1 GiB and one per 256 entries,
+ * plus 4 * num_nodes bytes of slot map), which do the same for those rows.
+ * A workspace that ends before the bitmaps runs without them, one that ends
+ * before the tables without both; mlxc_rejection_sampling_layout_bytes gives
+ * each size.  No reference counterpart. */
 size_t mlxc_rejection_sampling_workspace_bytes(int64_t num_nodes, int64_t num_edges,
                                                int64_t num_walks, int32_t walk_length,
                                                double p, double q, int32_t rule);
+
+/* Layouts of mlxc_rejection_sampling, smallest first.  The call runs the
+ * largest one its workspace holds, with the same results every way. */
+#define MLXC_N2V_LAYOUT_DIRECT 0        /* MLXC_WORK_WORDS words: the direct CSR kernel */
+#define MLXC_N2V_LAYOUT_LDS 1           /* the 256-byte header: the LDS walk (small graphs) */
+#define MLXC_N2V_LAYOUT_CSR 2           /* CSR mode: start records, search index, row starts */
+#define MLXC_N2V_LAYOUT_RECORDS 3       /* edge records instead of CSR mode */
+#define MLXC_N2V_LAYOUT_RECORDS_HASH 4  /* ... and the row hash tables */
+#define MLXC_N2V_LAYOUT_RECORDS_FULL 5  /* ... and the hub bitmaps */
+
+/* Workspace bytes of one MLXC_N2V_LAYOUT_* layout for these sizes (0 when it
+ * does not apply: the LDS walk beyond its size limits, the CSR-mode and
+ * record layouts for ids of 2^31 or more), for callers that trade speed for
+ * memory and for tests that run every kernel path.  No reference
+ * counterpart. */
+size_t mlxc_rejection_sampling_layout_bytes(int64_t num_nodes, int64_t num_edges,
+                                            int64_t num_walks, int32_t walk_length,
+                                            int32_t layout);
 
 /*
  * Uniform random walk.

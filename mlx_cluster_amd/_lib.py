@@ -38,6 +38,12 @@ MLXC_CSR_SYMMETRIZE = 1
 MLXC_CSR_DEDUP = 2
 MLXC_MAX_TRIALS = 65536
 MLXC_NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024
+MLXC_N2V_LAYOUT_DIRECT = 0
+MLXC_N2V_LAYOUT_LDS = 1
+MLXC_N2V_LAYOUT_CSR = 2
+MLXC_N2V_LAYOUT_RECORDS = 3
+MLXC_N2V_LAYOUT_RECORDS_HASH = 4
+MLXC_N2V_LAYOUT_RECORDS_FULL = 5
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -52,6 +58,7 @@ SIGNATURES = {
     "mlxc_last_error": (ctypes.c_char_p, []),
     "mlxc_random_walk_workspace_bytes": (_size, [_i64, _i64, _i64, _i32]),
     "mlxc_rejection_sampling_workspace_bytes": (_size, [_i64, _i64, _i64, _i32, _dbl, _dbl, _i32]),
+    "mlxc_rejection_sampling_layout_bytes": (_size, [_i64, _i64, _i64, _i32, _i32]),
     "mlxc_random_walk": (
         ctypes.c_int,
         [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i32, _ptr, _ptr, _i32, _ptr, _size, _ptr],

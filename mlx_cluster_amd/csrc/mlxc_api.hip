@@ -241,6 +241,12 @@ size_t mlxc_rejection_sampling_workspace_bytes(int64_t num_nodes, int64_t num_ed
     return node2vec_workspace_bytes(num_nodes, num_edges, num_walks, walk_length, width);
 }
 
+size_t mlxc_rejection_sampling_layout_bytes(int64_t num_nodes, int64_t num_edges,
+                                            int64_t num_walks, int32_t walk_length,
+                                            int32_t layout) {
+    return node2vec_layout_bytes(num_nodes, num_edges, num_walks, walk_length, layout);
+}
+
 int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes, const int64_t* d_col,
                      int64_t num_edges, const int64_t* d_start, int64_t num_walks,
                      const float* d_rand, int32_t walk_length, void* d_n_out, void* d_e_out,

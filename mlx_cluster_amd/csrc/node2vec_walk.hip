@@ -238,6 +238,7 @@ enum : int {
     kN2vDone = 5,    // the queue is exhausted
     kN2vRow = 6,     // CSR mode: reads rowptr[x], rowptr[x + 1] of the candidate
     kN2vBit = 7,     // reads the word of a hub bitmap that answers the neighbour test
+    kN2vHash = 8,    // reads one bucket of a row hash table
 };
 
 // What a CSR-mode slot does once the candidate's row has been read.
@@ -340,6 +341,9 @@ struct N2VRecArgs {
     const uint32_t* hub_bits;
     int64_t hub_words;
     const int32_t* row32;  // int32 row starts (row32_kernel): the CSR mode's row reads
+    // Row hash tables (record mode; null: none), kSearchBlock slots a bucket:
+    // rows without a hub bitmap whose search would take more than one read.
+    const int32_t* hash;
 };
 
 // Smallest float >= p (p > 0), the float threshold of N2VRecArgs.
@@ -477,6 +481,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             // the aligned 16 bytes holding word tgt / 32 of bitmap blk
             bp = reinterpret_cast<const int32_t*>(a.hub_bits + blk * a.hub_words +
                                                   ((tgt >> 5) & ~3));
+        } else if (!kCsr && ph == kN2vHash) {
+            bp = a.hash + static_cast<int64_t>(kSearchBlock) * blk;  // bucket blk
         } else {
             bp = reinterpret_cast<const int32_t*>(a.init);
         }
@@ -487,7 +493,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             qb[0] = reinterpret_cast<const i32x4*>(bp)[0];
         // the other 48 bytes of the block only for the search phases (reading
         // them for every phase costs registers and measured slower at C5)
-        if (ph == kN2vLevel || ph == kN2vScan) {
+        if (ph == kN2vLevel || ph == kN2vScan || (!kCsr && ph == kN2vHash)) {
 #pragma unroll
             for (int i = 1; i < 4; ++i) qb[i] = reinterpret_cast<const i32x4*>(bp)[i];
         }
@@ -609,6 +615,17 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
                         blk = s_t;  // bit x of row(t)'s bitmap: the same answer on a symmetric graph
                         tgt = x;
                         phase = kN2vBit;
+                    } else if (!one_block && a.hash && hi - lo < kHashMaxDegree) {
+                        // the row searched has no bitmap (it would have been
+                        // taken above) and a hash table: lo <- its first
+                        // bucket, hi <- its bucket count, blk <- tgt's bucket
+                        const int32_t node = tgt == t ? x : t;
+                        const int32_t nb = hash_buckets(hi - lo);
+                        lo = static_cast<int32_t>(hash_region(lo, node));
+                        hi = nb;
+                        blk = lo + hash_bucket(tgt, nb);
+                        lvl = 0;  // buckets read
+                        phase = kN2vHash;
                     } else if (!sorted) {
                         phase = kN2vScan;
                     } else {
@@ -625,6 +642,26 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             const uint32_t word = static_cast<uint32_t>(rec[(tgt >> 5) & 3]);
             accept = n2v_resolve<kRule>(a, r, ((word >> (tgt & 31)) & 1u) != 0);
             next_trial = !accept;
+        } else if (!kCsr && ph == kN2vHash) {
+            // tgt in the bucket: adjacent; an empty slot (-1): not adjacent;
+            // a full bucket without tgt: the next bucket of the table.  A
+            // table always has an empty slot; the bound on the buckets read
+            // only keeps a malformed CSR (rows that overlap, whose tables
+            // then overwrite each other) from looping.
+            bool found = false, open = false;
+#pragma unroll
+            for (int i = 0; i < kSearchBlock; ++i) {
+                const int32_t v16 = qb[i / 4][i % 4];
+                found |= v16 == tgt;
+                open |= v16 < 0;
+            }
+            lvl += 1;
+            if (found || open || lvl >= hi) {
+                accept = n2v_resolve<kRule>(a, r, found);
+                next_trial = !accept;
+            } else {
+                blk = blk + 1 == lo + hi ? lo : blk + 1;
+            }
         } else {  // the neighbour search: is t in row(x)?
             int32_t vals[kSearchBlock];
 #pragma unroll
@@ -921,14 +958,20 @@ int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
 // records, then (128-byte aligned) the levels of the search index — col as
 // int32, then its samples every 16^k entries — each padded to whole blocks of
 // kSearchBlock entries, then 64 bytes of slack for the block reads of the
-// last start records.  Record mode then adds the hub bitmaps: the info words,
-// slot_of [V], node_of [max] and the bitmaps [max][words], up to
-// kHubBudgetBytes of bitmaps and at most one slot per kHubMinDegree entries.
+// last start records.  Record mode then adds, in this order, the row hash
+// tables (num_edges / 8 + num_nodes + 2 buckets of 64 bytes; see row_hashed)
+// and the hub bitmaps: the info words, slot_of [V], node_of [max] and the
+// bitmaps [max][words], up to kHubBudgetBytes of bitmaps and at most one slot
+// per kHubMinDegree entries.  A workspace that ends before the bitmaps runs
+// without them, one that ends before the tables without both.
 struct N2VLayout {
     size_t level[kMaxLevels];
     int count;
     size_t row32;          // the int32 row starts (row32_kernel), num_nodes + 3 entries
-    size_t total_no_hubs;  // the layout without hub bitmaps
+    size_t total_base;     // records (or CSR mode), start records, index, row32
+    size_t hash;           // the row hash tables (record mode)
+    size_t hash_count, hash_list;  // the tables' build: long rows, counted and listed
+    size_t total_no_hubs;  // the layout without hub bitmaps (with the tables)
     size_t hub_info, hub_slot_of, hub_node_of, hub_bits;
     int32_t hub_max;
     int64_t hub_words;
@@ -960,6 +1003,16 @@ N2VLayout n2v_layout(int64_t num_nodes, int64_t num_edges, int64_t num_walks, bo
     // the int32 row starts, two entries of slack for the CSR walk's 16-byte reads
     lay.row32 = align128(pos);
     pos = lay.row32 + static_cast<size_t>(num_nodes + 3) * sizeof(int32_t);
+    lay.total_base = pos;
+    lay.hash = lay.hash_list = lay.hash_count = 0;
+    if (records) {
+        lay.hash = align128(pos);
+        pos = lay.hash + static_cast<size_t>(num_edges / 8 + num_nodes + 2) * kSearchBlock *
+                             sizeof(int32_t);
+        lay.hash_count = align128(pos);  // the build's count of long rows, then its list
+        lay.hash_list = lay.hash_count + 128;
+        pos = lay.hash_list + static_cast<size_t>(num_nodes) * sizeof(int32_t);
+    }
     lay.total_no_hubs = pos;
     lay.hub_words = ((num_nodes + 31) / 32 + 3) / 4 * 4;
     const int64_t bitmap_bytes = lay.hub_words * 4;
@@ -1007,9 +1060,31 @@ size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t nu
         return MLXC_WORK_WORDS * sizeof(int64_t);
     if (lds_walk_fits(num_nodes, num_edges, num_walks, walk_length))
         return kRecordOffset;  // the LDS walk: its size selects it
-    return n2v_layout(num_nodes, num_edges, num_walks,
-                      n2v_records_pay_off(num_edges, num_walks, walk_length, search_width))
-        .total;
+    const bool records = n2v_records_pay_off(num_edges, num_walks, walk_length, search_width);
+    const N2VLayout lay = n2v_layout(num_nodes, num_edges, num_walks, records);
+    // the hash tables and hub bitmaps serve only row searches: none without
+    return search_width > 0.0 ? lay.total : lay.total_base;
+}
+
+size_t node2vec_layout_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
+                             int32_t walk_length, int32_t layout) {
+    if (num_nodes < 0 || num_edges < 0 || num_walks < 0 || walk_length < 0) return 0;
+    switch (layout) {
+    case MLXC_N2V_LAYOUT_DIRECT:
+        return MLXC_WORK_WORDS * sizeof(int64_t);
+    case MLXC_N2V_LAYOUT_LDS:
+        return lds_walk_fits(num_nodes, num_edges, num_walks, walk_length) ? kRecordOffset : 0;
+    default:
+        break;
+    }
+    if (!records_fit(num_nodes, num_edges)) return 0;
+    if (layout == MLXC_N2V_LAYOUT_CSR)
+        return n2v_layout(num_nodes, num_edges, num_walks, false).total_base;
+    const N2VLayout lay = n2v_layout(num_nodes, num_edges, num_walks, true);
+    if (layout == MLXC_N2V_LAYOUT_RECORDS) return lay.total_base;
+    if (layout == MLXC_N2V_LAYOUT_RECORDS_HASH) return lay.total_no_hubs;
+    if (layout == MLXC_N2V_LAYOUT_RECORDS_FULL) return lay.total;
+    return 0;
 }
 
 namespace {
@@ -1040,11 +1115,14 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
     const N2VLayout lay_rec = n2v_layout(w.num_nodes, w.num_edges, w.num_walks, true);
     const N2VLayout lay_csr = n2v_layout(w.num_nodes, w.num_edges, w.num_walks, false);
     // Records whenever the workspace holds them: node2vec_workspace_bytes
-    // asks for them only when they pay off; hub bitmaps too when it holds them.
-    const bool records = workspace_bytes >= lay_rec.total_no_hubs;
+    // asks for them only when they pay off; the row hash tables and the hub
+    // bitmaps too when it holds them.  Both serve only the row searches,
+    // which a call of search width 0 never makes.
+    const bool records = workspace_bytes >= lay_rec.total_base;
     const int64_t hub_min_degree = n2v_hub_min_degree(w, p);
-    const bool hub_bitmaps = records && lay_rec.hub_max > 0 && workspace_bytes >= lay_rec.total &&
-                             hub_min_degree < INT64_MAX;
+    const bool searches = hub_min_degree < INT64_MAX;
+    const bool hash_tables = records && searches && workspace_bytes >= lay_rec.total_no_hubs;
+    const bool hub_bitmaps = hash_tables && lay_rec.hub_max > 0 && workspace_bytes >= lay_rec.total;
     if (aligned && records_fit(w.num_nodes, w.num_edges) &&
         (records || workspace_bytes >= lay_csr.total)) {
         const N2VLayout& lay = records ? lay_rec : lay_csr;
@@ -1087,6 +1165,17 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         if (hub_bitmaps)
             if (int rc = launch_hub_build(w.rowptr, w.col, w.num_nodes, hubs, p.rows, w.work, stream))
                 return rc;
+        a.hash = nullptr;
+        if (hash_tables) {
+            int32_t* table = reinterpret_cast<int32_t*>(base + lay.hash);
+            if (int rc = launch_hash_build(row32, index.level[0], w.num_nodes,
+                                           hub_bitmaps ? hubs.info : nullptr, table,
+                                           reinterpret_cast<int32_t*>(base + lay.hash_list),
+                                           reinterpret_cast<int64_t*>(base + lay.hash_count),
+                                           stream))
+                return rc;
+            a.hash = table;
+        }
         a.recs = recs;
         a.init = init;
         a.index = index;

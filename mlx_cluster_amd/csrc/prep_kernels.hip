@@ -313,6 +313,209 @@ __global__ __launch_bounds__(kBlock) void hub_build_kernel(const int64_t* __rest
     }
 }
 
+// Row hash tables (see row_hashed in walk_device.h), built in LDS by one
+// wavefront per table and stored whole with 16-byte stores: clear the table,
+// insert the row's entries (col32; -1, a malformed id, is left out) with an
+// LDS counter per bucket, moving on to the next bucket of the row when one is
+// full, store.  A table holds fewer than 2 entries per 16 slots of capacity
+// (or its whole row in one bucket), so an insertion always finds a bucket.
+//
+// Two launches.  hash_short_kernel: each wavefront reads the row starts of
+// groups of 64 consecutive rows, builds the tables of the short rows (at most
+// 64 entries) kHashBatch at a time, their entry loads issued together so that
+// one memory round trip serves the batch, and appends the long rows to a list
+// (one atomic per group).  hash_long_kernel: the wavefronts take the listed
+// rows round robin, one row at a time with all of its loads issued first.
+// The list spreads the long rows evenly: they crowd together where degrees
+// are skewed (R-MAT gives low ids, and ids of few set bits, high degrees),
+// and handed out by row id a few wavefronts got most of them
+// (configuration 3: 71 long rows on one wavefront against 6.6 on average,
+// 0.47 ms for the long rows).  Each launch gives its waves only the LDS its
+// rows need.  hub_info: rows of at least the hub threshold info[0] have
+// bitmaps and no table (null: no bitmaps in this call).
+constexpr int kHashTableMax = ((kHashMaxDegree - 1) >> 3) + 1;  // buckets of the longest table
+constexpr int kHashBatch = 8;
+constexpr int kHashShortMax = kWave;                            // entries of a short row
+constexpr int kHashShortBuckets = (kHashShortMax >> 3) + 1;     // buckets of its table
+
+// Inserts c (>= 0) into the table of nb buckets at sl / fl (wave-local LDS).
+__device__ __forceinline__ void hash_insert(int32_t* sl, int32_t* fl, int32_t nb, int32_t c) {
+    int32_t bk = hash_bucket(c, nb);
+    while (true) {
+        const int32_t at = atomicAdd(&fl[bk], 1);
+        if (at < kSearchBlock) {
+            sl[bk * kSearchBlock + at] = c;
+            return;
+        }
+        bk = bk + 1 == nb ? 0 : bk + 1;
+    }
+}
+
+// Stores the table of nb buckets at sl to its region (all lanes).
+__device__ __forceinline__ void hash_store(int32_t* __restrict__ table, const int32_t* sl,
+                                           int32_t nb, int32_t begin, int32_t node, int lane) {
+    int4* out = reinterpret_cast<int4*>(table + hash_region(begin, node) * kSearchBlock);
+    for (int q = lane; q < nb * (kSearchBlock / 4); q += kWave)
+        out[q] = make_int4(sl[4 * q], sl[4 * q + 1], sl[4 * q + 2], sl[4 * q + 3]);
+}
+
+__global__ __launch_bounds__(kBlock) void hash_short_kernel(const int32_t* __restrict__ row32,
+                                                            const int32_t* __restrict__ col32,
+                                                            int64_t num_nodes,
+                                                            const int64_t* __restrict__ hub_info,
+                                                            int32_t* __restrict__ table,
+                                                            int32_t* __restrict__ long_rows,
+                                                            unsigned long long* long_count) {
+    constexpr int kWaves = kBlock / kWave;
+    constexpr int kArea = kHashBatch * kHashShortBuckets;  // buckets of a wave's batch
+    constexpr int kPend = 2 * kWave;  // long rows a wave lists before appending them
+    __shared__ int32_t slots[kWaves][kArea * kSearchBlock];
+    __shared__ int32_t fill[kWaves][kArea];
+    __shared__ int32_t pend[kWaves][kPend];
+    const int w = threadIdx.x / kWave;
+    const int lane = static_cast<int>(__lane_id());
+    const int64_t h = hub_info ? hub_info[0] : INT64_MAX;
+    int32_t* const sl = slots[w];
+    int32_t* const fl = fill[w];
+    int32_t* const pl = pend[w];
+    int npend = 0;  // wave-uniform
+    // the listed long rows go to the list with one atomic per flush, not one
+    // per group (whose return each group would otherwise wait for)
+    auto flush = [&]() {
+        uint32_t at = 0;
+        if (lane == 0)
+            at = static_cast<uint32_t>(atomicAdd(long_count, static_cast<unsigned long long>(npend)));
+        at = __builtin_amdgcn_readlane(at, 0);
+        for (int k = lane; k < npend; k += kWave) long_rows[at + k] = pl[k];
+        npend = 0;
+        wave_sync();
+    };
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * kWaves;
+    for (int64_t g = static_cast<int64_t>(blockIdx.x) * kWaves + w; g * kWave < num_nodes;
+         g += waves) {
+        const int64_t base = g * kWave;
+        const int64_t u = base + lane;
+        int32_t b = 0, d = 0;
+        bool mine = false;
+        if (u < num_nodes) {
+            const int32_t rb = row32[u], re = row32[u + 1];
+            if (rb >= 0 && re >= rb) {
+                b = rb;
+                d = re - rb;
+                mine = row_hashed(rb, d, h);
+            }
+        }
+        const bool is_long = mine && d > kHashShortMax;
+        const uint64_t longs = __ballot(is_long);
+        if (longs) {  // list the group's long rows (at most num_nodes in all)
+            if (npend + __popcll(longs) > kPend) flush();
+            if (is_long) pl[npend + lane_rank(longs)] = static_cast<int32_t>(u);
+            npend += __popcll(longs);
+            wave_sync();
+        }
+        uint64_t shorts = __ballot(mine && !is_long);
+        while (shorts) {  // wave-uniform
+            int32_t rb[kHashBatch], rd[kHashBatch], node[kHashBatch], v[kHashBatch];
+#pragma unroll
+            for (int j = 0; j < kHashBatch; ++j) {
+                rb[j] = 0;
+                rd[j] = 0;
+                node[j] = 0;
+                if (shorts) {
+                    const int src = __builtin_ctzll(shorts);
+                    shorts &= shorts - 1;
+                    rb[j] = __builtin_amdgcn_readlane(b, src);
+                    rd[j] = __builtin_amdgcn_readlane(d, src);
+                    node[j] = static_cast<int32_t>(base + src);
+                }
+                // unconditional (the index clamped into the row, or entry 0
+                // for an unused batch place), so the loads are in flight together
+                v[j] = col32[rb[j] + min(lane, max(rd[j] - 1, 0))];
+            }
+#pragma unroll
+            for (int j = 0; j < kHashBatch; ++j) {
+                const int32_t nb = rd[j] > 0 ? hash_buckets(rd[j]) : 0;
+                int32_t* const tj = sl + j * kHashShortBuckets * kSearchBlock;
+                for (int i = lane; i < nb * kSearchBlock; i += kWave) tj[i] = -1;
+                if (lane < nb) fl[j * kHashShortBuckets + lane] = 0;
+            }
+            wave_sync();
+#pragma unroll
+            for (int j = 0; j < kHashBatch; ++j)
+                if (lane < rd[j] && v[j] >= 0)
+                    hash_insert(sl + j * kHashShortBuckets * kSearchBlock, fl + j * kHashShortBuckets,
+                                hash_buckets(rd[j]), v[j]);
+            wave_sync();
+#pragma unroll
+            for (int j = 0; j < kHashBatch; ++j)
+                if (rd[j] > 0)
+                    hash_store(table, sl + j * kHashShortBuckets * kSearchBlock,
+                               hash_buckets(rd[j]), rb[j], node[j], lane);
+            wave_sync();
+        }
+    }
+    if (npend > 0) flush();
+}
+
+__global__ __launch_bounds__(kBlock) void hash_long_kernel(const int32_t* __restrict__ row32,
+                                                           const int32_t* __restrict__ col32,
+                                                           int32_t* __restrict__ table,
+                                                           const int32_t* __restrict__ long_rows,
+                                                           const unsigned long long* long_count) {
+    constexpr int kWaves = kBlock / kWave;
+    __shared__ int32_t slots[kWaves][kHashTableMax * kSearchBlock];
+    __shared__ int32_t fill[kWaves][kHashTableMax];
+    const int w = threadIdx.x / kWave;
+    const int lane = static_cast<int>(__lane_id());
+    int32_t* const sl = slots[w];
+    int32_t* const fl = fill[w];
+    const int64_t n = static_cast<int64_t>(*long_count);
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * kWaves;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kWaves + w; i < n; i += waves) {
+        const int32_t u = long_rows[i];
+        const int32_t rb = row32[u], rd = row32[u + 1] - rb;  // a listed row: valid, 65..1023
+        const int32_t nb = hash_buckets(rd);
+        // every round's load first (indices clamped into the row), then the
+        // inserts: a load behind an insert would wait for it
+        constexpr int kRounds = (kHashMaxDegree + kWave - 1) / kWave;
+        const int rounds = (rd + kWave - 1) / kWave;
+        int32_t v[kRounds];
+#pragma unroll
+        for (int r = 0; r < kRounds; ++r)
+            if (r < rounds) v[r] = col32[rb + min(lane + r * kWave, rd - 1)];
+        for (int k = lane; k < nb * kSearchBlock; k += kWave) sl[k] = -1;
+        for (int k = lane; k < nb; k += kWave) fl[k] = 0;
+        wave_sync();
+#pragma unroll
+        for (int r = 0; r < kRounds; ++r)
+            if (r < rounds && lane + r * kWave < rd && v[r] >= 0) hash_insert(sl, fl, nb, v[r]);
+        wave_sync();
+        hash_store(table, sl, nb, rb, u, lane);
+        wave_sync();
+    }
+}
+
+int launch_hash_build(const int32_t* row32, const int32_t* col32, int64_t num_nodes,
+                      const int64_t* hub_info, int32_t* table, int32_t* long_rows,
+                      int64_t* long_count, hipStream_t stream) {
+    if (num_nodes <= 0) return MLXC_OK;
+    DeviceInfo info;
+    if (int rc = device_info(info)) return rc;
+    const int64_t groups = (num_nodes + kWave - 1) / kWave;  // one per wavefront and round
+    const int64_t want = (groups + kBlock / kWave - 1) / (kBlock / kWave);
+    const int64_t cap = static_cast<int64_t>(info.cus) * 8;
+    const int grid = static_cast<int>(want < cap ? want : cap);
+    hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(kWave), 0, stream, long_count, 1);
+    hipLaunchKernelGGL(hash_short_kernel, dim3(grid), dim3(kBlock), 0, stream, row32, col32,
+                       num_nodes, hub_info, table, long_rows,
+                       reinterpret_cast<unsigned long long*>(long_count));
+    hipLaunchKernelGGL(hash_long_kernel, dim3(static_cast<int>(cap)), dim3(kBlock), 0, stream,
+                       row32, col32, table, long_rows,
+                       reinterpret_cast<const unsigned long long*>(long_count));
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
+
 // The search index alone (the node2vec walk's CSR mode: no records, no rowptr
 // read per edge): col32 = col with -1 for a value outside [0, num_nodes),
 // plus its samples col32[16^k * i]; with a non-null work pointer the same

@@ -657,6 +657,45 @@ struct HubBitmaps {
     int32_t max;       // slots reserved; 0: no bitmaps
 };
 
+// Row hash tables of the node2vec record walk: an exact membership table per
+// row of kHashMinSpan.. entries below kHashMaxDegree, so that "is t in
+// row(x)" costs one 64-byte read instead of a descent through the index
+// levels (two or three reads for such rows).  Row x of begin b and degree d
+// has B = d / 8 + 1 buckets of kSearchBlock int32 slots (fewer than half of
+// them used; one bucket, which holds the whole row, when d <= 16), starting
+// at bucket b / 8 + x: the buckets of consecutive rows follow each other
+// without overlap (b / 8 + x + B <= (b + d) / 8 + x + 1), and all of them
+// lie below num_edges / 8 + num_nodes + 1.  Node t sits in
+// bucket hash_bucket(t, B), or when that bucket was full at insertion, in the
+// first bucket after it (cyclically) that was not; an empty slot holds -1.
+// So a lookup reads bucket hash_bucket(t, B): t found answers yes, an empty
+// slot no, and a full bucket without t sends it to the next bucket.
+// A row gets a table when its search would take more than one read (it
+// spans more than one aligned 16-entry block of col32) and it has no hub
+// bitmap (degree below the call's hub threshold).
+constexpr int32_t kHashMaxDegree = 1024;
+
+__host__ __device__ __forceinline__ bool row_hashed(int64_t begin, int64_t deg,
+                                                    int64_t hub_threshold) {
+    return deg > 1 && deg < kHashMaxDegree && deg < hub_threshold &&
+           ((begin ^ (begin + deg - 1)) >> 4) != 0;
+}
+
+__host__ __device__ __forceinline__ int32_t hash_buckets(int32_t deg) {
+    return deg <= kSearchBlock ? 1 : (deg >> 3) + 1;
+}
+
+__host__ __device__ __forceinline__ int64_t hash_region(int32_t begin, int32_t node) {
+    return (static_cast<int64_t>(begin) >> 3) + node;
+}
+
+// Bucket of node t among B: the high word of (t * golden ratio mod 2^32) * B
+// (Fibonacci hashing: consecutive ids spread over the buckets).
+__host__ __device__ __forceinline__ int32_t hash_bucket(int32_t t, int32_t buckets) {
+    const uint32_t h = static_cast<uint32_t>(t) * 0x9E3779B1u;
+    return static_cast<int32_t>((static_cast<uint64_t>(h) * static_cast<uint32_t>(buckets)) >> 32);
+}
+
 // Start records a preparation pass writes besides its edge pass: walk n's
 // start node in the record format, into init[n].
 struct StartRecords {

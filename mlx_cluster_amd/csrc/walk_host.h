@@ -95,6 +95,13 @@ int launch_hub_bitmaps(const int64_t* rowptr, const int64_t* col, int64_t num_no
 int launch_hub_build(const int64_t* rowptr, const int64_t* col, int64_t num_nodes,
                      const HubBitmaps& hubs, int32_t rows, const int64_t* work,
                      hipStream_t stream);
+// The row hash tables (see row_hashed) from the int32 row starts and col32,
+// after launch_edge_records wrote both; hub_info (null: no hub bitmaps in
+// this call) gives the hub threshold, above which rows get no table.
+// long_rows (num_nodes int32) and *long_count: scratch of the build.
+int launch_hash_build(const int32_t* row32, const int32_t* col32, int64_t num_nodes,
+                      const int64_t* hub_info, int32_t* table, int32_t* long_rows,
+                      int64_t* long_count, hipStream_t stream);
 // The index levels alone, from col (node2vec CSR mode), and the start records;
 // a 16-byte aligned col uses four entries per thread, any other alignment the
 // record pass.
@@ -143,6 +150,9 @@ struct N2VParams {
 double n2v_search_width(const N2VParams& p);
 size_t node2vec_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
                                 int32_t walk_length, double search_width);
+// Bytes of one MLXC_N2V_LAYOUT_* layout (0: not available for this call).
+size_t node2vec_layout_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
+                             int32_t walk_length, int32_t layout);
 int launch_node2vec(const WalkArgs& a, const N2VParams& p, void* workspace,
                     size_t workspace_bytes, hipStream_t stream);
 

@@ -7,6 +7,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 
 from mlx_cluster_amd import _lib
@@ -197,3 +198,54 @@ def test_noalloc_rejects_calls_beyond_its_scratch():
     rc = lib.mlxc_random_walk_noalloc(FAKE, 4, FAKE, 3, FAKE, 2, FAKE, 5, FAKE, None, 7, None,
                                       None)
     assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT and "out_type" in _lib.last_error()
+
+
+def test_row_hash_table_regions_are_disjoint():
+    """The node2vec walk's row hash tables: row x of begin b and degree d has
+    d // 8 + 1 buckets starting at bucket b // 8 + x.  Over random degree
+    sequences (empty rows, rows inside one 16-entry block, rows up to past the
+    1,024-entry limit) the tables of consecutive rows never overlap and all of
+    them end by bucket E // 8 + V + 1; the layout query reserves that many
+    64-byte buckets between the record layout and the hash layout."""
+    lib = _lib.load()
+    rng = np.random.default_rng(7)
+    for trial in range(20):
+        V = int(rng.integers(1, 3000))
+        deg = rng.choice([0, 1, 2, 15, 16, 17, 100, 1023, 1024, 1500], V) * (trial % 2) + \
+            rng.integers(0, 40, V)
+        rowptr = np.concatenate([[0], np.cumsum(deg)])
+        E = int(rowptr[-1])
+        b, d, x = rowptr[:-1], deg, np.arange(V)
+        start, count = b // 8 + x, d // 8 + 1
+        hashed = (d > 1) & (d < 1024) & (((b ^ (b + d - 1)) >> 4) != 0)
+        s, c = start[hashed], count[hashed]
+        assert np.all(s[1:] >= s[:-1] + c[:-1])
+        if hashed.any():
+            assert (s + c).max() <= E // 8 + V + 1
+        base = lib.mlxc_rejection_sampling_layout_bytes(V, E, 100, 10, _lib.MLXC_N2V_LAYOUT_RECORDS)
+        with_tables = lib.mlxc_rejection_sampling_layout_bytes(
+            V, E, 100, 10, _lib.MLXC_N2V_LAYOUT_RECORDS_HASH)
+        assert with_tables - base >= 64 * (E // 8 + V + 2)
+
+
+def test_layout_query_orders_the_layouts():
+    """Each layout of mlxc_rejection_sampling holds the one before it; the
+    LDS walk is offered only within its limits, the CSR-mode and record
+    layouts only for ids below 2^31."""
+    lib = _lib.load()
+    q = lambda V, E, N, L, k: lib.mlxc_rejection_sampling_layout_bytes(V, E, N, L, k)
+    sizes = [q(2**20, 31_000_000, 4 * 2**20, 40, k) for k in range(6)]
+    assert sizes[0] == 32 and sizes[1] == 0
+    assert sizes[2] < sizes[3] < sizes[4] <= sizes[5]
+    assert q(2708, 10556, 2000, 5, _lib.MLXC_N2V_LAYOUT_LDS) == 256
+    assert q(2**31, 10, 10, 5, _lib.MLXC_N2V_LAYOUT_RECORDS) == 0
+    assert q(10, 2**31, 10, 5, _lib.MLXC_N2V_LAYOUT_CSR) == 0
+    assert q(10, 10, 10, 5, 6) == 0 and q(-1, 10, 10, 5, 3) == 0
+    # the fastest layout the workspace query returns is one of these
+    full = lib.mlxc_rejection_sampling_workspace_bytes(2**20, 31_000_000, 4 * 2**20, 40, 0.5,
+                                                       2.0, 0)
+    assert full == sizes[5]
+    # a call that never searches a row (p = q = 1: every draw accepts) gets
+    # the records without tables or bitmaps
+    assert lib.mlxc_rejection_sampling_workspace_bytes(2**20, 31_000_000, 4 * 2**20, 40, 1.0,
+                                                       1.0, 0) == sizes[3]

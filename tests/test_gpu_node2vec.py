@@ -22,13 +22,13 @@ RULE_NAME = {oracle.RULE_REF_CHAIN: "ref_chain", oracle.RULE_NODE2VEC_EXACT: "no
 def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode, out_dtype=torch.int64,
               expect_status=0):
     """mlxc_rejection_sampling through the C ABI, with edge output, in the
-    mode the workspace selects: "direct" (minimal workspace: the direct CSR
-    kernel), "csr" (the CSR-mode layout: the record kernel without edge
-    records), "records" (the edge-record layout with its hub bitmaps),
-    "records_nohub" (one byte less: the edge records without the bitmaps,
-    when the layout has any) or "lds" (the 256-byte header: the LDS walk, for
-    graphs and calls small enough).  Asserts the call's status word equals
-    expect_status."""
+    layout the workspace selects (mlxc_rejection_sampling_layout_bytes):
+    "direct" (the direct CSR kernel), "lds" (the LDS walk, for graphs and
+    calls small enough), "csr" (the record kernel in CSR mode), "records_plain"
+    (edge records, index-level searches), "records_nohub" (edge records and
+    the row hash tables) or "records" (the tables and the hub bitmaps; the
+    tables and bitmaps serve calls that search rows).  Asserts the call's
+    status word equals expect_status."""
     from mlx_cluster_amd import _lib
     lib = _lib.load()
     N = start.numel()
@@ -36,13 +36,12 @@ def _abi_walk(rowptr, col, start, L, p, q, seed, rule, rows, mode, out_dtype=tor
     n = torch.empty((N, L + 1), dtype=out_dtype, device=start.device)
     e = torch.empty((N, L), dtype=out_dtype, device=start.device)
     out_type = _lib.MLXC_OUT_INT32 if out_dtype == torch.int32 else _lib.MLXC_OUT_INT64
-    query = lambda N_, L_: lib.mlxc_rejection_sampling_workspace_bytes(V, E, N_, L_, p, q, rule)
-    # the query sizes records only for calls of many steps per edge
-    full = query(max(N, 1), 2**31 - 1)
-    nbytes = {"direct": 32, "csr": query(N, 0), "records": full, "records_nohub": full - 1,
-              "lds": 256}[mode]
-    if mode == "csr" and E > 0:
-        assert nbytes < query(max(N, 1), 2**31 - 1)
+    layout = {"direct": _lib.MLXC_N2V_LAYOUT_DIRECT, "lds": _lib.MLXC_N2V_LAYOUT_LDS,
+              "csr": _lib.MLXC_N2V_LAYOUT_CSR, "records_plain": _lib.MLXC_N2V_LAYOUT_RECORDS,
+              "records_nohub": _lib.MLXC_N2V_LAYOUT_RECORDS_HASH,
+              "records": _lib.MLXC_N2V_LAYOUT_RECORDS_FULL}[mode]
+    nbytes = lib.mlxc_rejection_sampling_layout_bytes(V, E, N, L, layout)
+    assert nbytes > 0, mode
     ws = torch.zeros((nbytes + 7) // 8, dtype=torch.int64, device=start.device)
     ptr = lambda t: t.data_ptr() if t.numel() else None
     rc = lib.mlxc_rejection_sampling(ptr(rowptr), V, ptr(col), E,
@@ -69,7 +68,7 @@ def gpu_walk(rowptr, col, start, L, p, q, seed, rule, cuda, **kw):
     rows = {None: 2, True: 1, False: 0}[kw.get("rows_sorted")]
     if kw.get("symmetric"):
         rows |= 4  # MLXC_ROWS_SYMMETRIC
-    for mode in ("direct", "csr", "records", "records_nohub"):
+    for mode in ("direct", "csr", "records_plain", "records_nohub", "records"):
         nm, em = _abi_walk(*args[:3], L, p, q, seed, rule, rows, mode)
         np.testing.assert_array_equal(nm.cpu().numpy(), n.cpu().numpy(),
                                       err_msg=f"{mode} walk nodes differ")
@@ -580,3 +579,39 @@ def test_lds_walks_random_sweep(cuda):
                 np.testing.assert_array_equal(n.cpu().numpy(), n_ref,
                                               err_msg=f"node2vec case {case} {p} {q} {rule}")
                 np.testing.assert_array_equal(e.cpu().numpy(), e_ref)
+
+
+@pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
+def test_row_hash_tables_overflow_and_size_limit(rule, cuda):
+    """Row hash tables at their edges.  Node 0's row holds 20 ids that all
+    fall in bucket 0 of its 3-bucket table: 16 fill that bucket and 4 move on
+    to bucket 1, and a lookup of an absent id whose bucket is the full one
+    reads bucket 1 too.  Node 1's row has 1,023 entries (the longest row with
+    a table) and node 2's 1,024 (none: index levels).  The 20 ids are joined
+    in a chain and the hub rows are linked, so walks step from one of the ids
+    to node 0 and test the previous node against row 0.  Walks starting at
+    the 20 ids and at random nodes are bit-exact against the oracle in every
+    layout, sorted and unsorted rows."""
+    B = 3
+
+    def bucket(t):
+        return (((t * 0x9E3779B1) & 0xFFFFFFFF) * B) >> 32
+
+    V = 3000
+    ids = [t for t in range(3, V) if bucket(t) == 0][:20]
+    rng = np.random.default_rng(rule + 17)
+    others = [t for t in range(3, V) if t not in set(ids)]
+    pairs = [(0, c) for c in ids] + list(zip(ids[:-1], ids[1:]))
+    pairs += [(1, c) for c in rng.choice(others, 1023 - 1, replace=False)] + [(1, 2)]
+    pairs += [(2, c) for c in rng.choice(others, 1024 - 1, replace=False)]
+    pairs += [(int(a), int(b)) for a, b in rng.integers(3, V, (4000, 2)) if a != b]
+    rowptr, col = undirected(V, pairs)
+    deg = np.diff(rowptr)
+    assert (deg[0], deg[1], deg[2]) == (20, 1023, 1024)
+    start = np.concatenate([np.repeat(ids, 200), rng.integers(0, V, 6000)])
+    for sorted_rows in (True, False):
+        r, c = rowptr, col
+        if not sorted_rows:  # the same rows, each reversed
+            c = np.concatenate([col[rowptr[v]:rowptr[v + 1]][::-1] for v in range(V)])
+        assert_parity(r, c, start, 12, 0.5, 2.0, 99, rule, cuda, sorted_rows=sorted_rows,
+                      rows_sorted=sorted_rows)

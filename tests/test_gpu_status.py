@@ -30,7 +30,9 @@ def _n2v_status(rowptr, col, start, L, seed, rows, mode, cuda):
     V, E, N = rowptr.numel() - 1, col.numel(), start.numel()
     p, q, rule = 0.5, 2.0, _lib.MLXC_RULE_REF_CHAIN
     query = lambda n_, l_: lib.mlxc_rejection_sampling_workspace_bytes(V, E, n_, l_, p, q, rule)
-    nbytes = {"direct": 32, "csr": query(N, 0), "records": query(N, 2**31 - 1), "lds": 256}[mode]
+    layout = {"direct": _lib.MLXC_N2V_LAYOUT_DIRECT, "csr": _lib.MLXC_N2V_LAYOUT_CSR,
+              "records": _lib.MLXC_N2V_LAYOUT_RECORDS_FULL, "lds": _lib.MLXC_N2V_LAYOUT_LDS}[mode]
+    nbytes = max(lib.mlxc_rejection_sampling_layout_bytes(V, E, N, L, layout), 32)
     if mode == "lds":
         assert query(N, L) == 256  # the query itself selects the LDS walk here
     ws = torch.full(((nbytes + 7) // 8,), -1, dtype=torch.int64, device=cuda)
