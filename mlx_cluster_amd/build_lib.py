@@ -72,6 +72,41 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, out: str 
     return out
 
 
+BINDING_SRC = os.path.join(CSRC, "torch_binding.cpp")
+
+
+def binding_path() -> str:
+    import sysconfig
+    return os.path.join(PKG_DIR, "_mlxc_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_binding(verbose: bool = False, lib: str = OUT) -> str:
+    """Compiles the compiled fast path (torch_binding.cpp, host code only)
+    against torch's headers and libraries and the in-tree libmlxc.so, with
+    hipcc and no source translation step."""
+    import sysconfig
+
+    import torch
+    import torch.utils.cpp_extension as ce
+    out = binding_path()
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-DTORCH_EXTENSION_NAME=_mlxc_torch", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           "-I", INCLUDE, "-I", sysconfig.get_paths()["include"]]
+    for d in ce.include_paths(device_type="cuda"):
+        cmd += ["-isystem", d]
+    cmd += [BINDING_SRC, "-o", out + ".tmp"]
+    for d in ce.library_paths(device_type="cuda"):
+        cmd += ["-L", d, f"-Wl,-rpath,{d}"]
+    cmd += ["-L", os.path.dirname(lib), "-Wl,-rpath,$ORIGIN", "-lmlxc",
+            "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+            "-lamdhip64"]
+    _run(cmd, verbose, out)
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def source_files() -> list[str]:
     """Every file the library is built from (kernels, headers, C ABI)."""
     return sorted([os.path.join(CSRC, f) for f in os.listdir(CSRC)] +
@@ -120,3 +155,4 @@ def source_hash(kind: str | None = None) -> str:
 
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(build_binding(verbose=True))

@@ -35,6 +35,15 @@ TensorLike = Union[torch.Tensor, np.ndarray]
 
 _RULES = {"ref_chain": _lib.MLXC_RULE_REF_CHAIN, "node2vec": _lib.MLXC_RULE_NODE2VEC_EXACT}
 
+# The compiled fast path (csrc/torch_binding.cpp): the same calls into
+# libmlxc.so for the common case (tensors of the right dtype on the current
+# device, torch's current stream), without this layer's per-call cost; it
+# returns None for any other call.  Without it every call takes the path below.
+try:
+    from . import _mlxc_torch as _fast
+except ImportError:
+    _fast = None
+
 
 # ---------------------------------------------------------------- helpers
 
@@ -427,6 +436,17 @@ def random_walk(rowptr: TensorLike, col: TensorLike, start: TensorLike,
     Returns:
         [num_walks, walk_length + 1] node sequences (and edge ids) of out_dtype.
     """
+    if (_fast is not None and stream is None and walk_offset == 0 and memory_budget is None and
+            type(rowptr) is torch.Tensor and type(col) is torch.Tensor and
+            type(start) is torch.Tensor and type(walk_length) is int and
+            (rand is None or type(rand) is torch.Tensor) and
+            (seed is None or type(seed) is int) and
+            (out_dtype is torch.int64 or out_dtype is torch.int32)):
+        res = _fast.random_walk(rowptr, col, start, rand, walk_length,
+                                None if seed is None else seed & (2**64 - 1), bool(check),
+                                bool(return_edges), out_dtype is torch.int32)
+        if res is not None:
+            return res
     L = _walk_length(walk_length)
     otype = _out_type(out_dtype)
     offset = _walk_offset(walk_offset)
@@ -581,6 +601,13 @@ def rejection_sampling(rowptr: TensorLike, col: TensorLike, start: TensorLike,
             _lib.MLXC_ROWS_SORTED if rows_sorted else _lib.MLXC_ROWS_UNSORTED)
     if symmetric:
         rows |= _lib.MLXC_ROWS_SYMMETRIC
+    if (_fast is not None and stream is None and walk_offset == 0 and memory_budget is None and
+            type(rowptr) is torch.Tensor and type(col) is torch.Tensor and
+            type(start) is torch.Tensor and (out_dtype is torch.int64 or out_dtype is torch.int32)):
+        res = _fast.rejection_sampling(rowptr, col, start, L, p, q, seed, _RULES[rule], rows,
+                                       bool(check), bool(return_edges), out_dtype is torch.int32)
+        if res is not None:
+            return res
     N = start.numel()
     if _on_cpu(stream):
         rowptr, col, start = (_host(t) for t in (rowptr, col, start))

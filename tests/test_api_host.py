@@ -128,3 +128,21 @@ def test_plan_rejects_a_budget_below_one_walk():
     from mlx_cluster_amd.walks import _plan
     with pytest.raises(ValueError, match="memory_budget"):
         _plan(10, 1000, lambda n: 256 + 16 * n, 1000)
+
+
+def test_binding_declines_cpu_tensors():
+    """The compiled fast path takes only device tensors: given CPU tensors it
+    returns None, and the general path then reports the missing GPU (or, for
+    stream='cpu', runs the host twins)."""
+    from mlx_cluster_amd import walks
+    if walks._fast is None:
+        pytest.skip("the compiled fast path is not built")
+    r = torch.from_numpy(ROWPTR)
+    c = torch.from_numpy(COL)
+    s = torch.from_numpy(START)
+    assert walks._fast.random_walk(r, c, s, torch.from_numpy(RAND), 4, None, True, False,
+                                   False) is None
+    assert walks._fast.rejection_sampling(r, c, s, 4, 1.0, 1.0, 1, 0, 2, True, False,
+                                          False) is None
+    n = mc.random_walk(r, c, s, torch.from_numpy(RAND), 4, stream="cpu")
+    assert n.shape == (2, 5)
