@@ -758,16 +758,22 @@ def main():
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)  # the walk kernels launch on this stream
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(args.steps)]
+    # Wall time of K calls back to back, with nothing else between them; then
+    # K more calls bracketed by HIP events for the per-call GPU time (the
+    # event records would otherwise add to the wall time of short calls).
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
     for ev0, ev1 in events:
         ev0.record(stream)
         out = step()
         ev1.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     event_ms = [a.elapsed_time(b) for a, b in events]
     kernel_ms = float(np.mean(event_ms))
     kernel_ms_median = float(np.median(event_ms))

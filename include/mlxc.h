@@ -197,10 +197,11 @@ int mlxc_random_walk(const int64_t* d_rowptr, int64_t num_nodes,
  * memory around the call (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc).  The kernels, layouts and results are
  * those of mlxc_random_walk with a workspace of
- * mlxc_random_walk_workspace_bytes(num_nodes, num_edges, num_walks,
- * walk_length) bytes; that workspace lives in a file-scope device array of
- * MLXC_NOALLOC_SCRATCH_BYTES per GPU instead.  A call whose workspace would
- * be larger fails with MLXC_ERR_INVALID_ARGUMENT (use mlxc_random_walk).
+ * min(mlxc_random_walk_workspace_bytes(num_nodes, num_edges, num_walks,
+ * walk_length), MLXC_NOALLOC_SCRATCH_BYTES) bytes; that workspace lives in a
+ * file-scope device array of MLXC_NOALLOC_SCRATCH_BYTES per GPU instead.  A
+ * call whose fastest layout needs more runs the largest one the array holds
+ * (start records only, or the direct kernel): the same walks, more slowly.
  * d_status (device pointer to one int64, or NULL) receives the call's
  * MLXC_STATUS_* bits on `stream`.  Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (different streams, or host threads

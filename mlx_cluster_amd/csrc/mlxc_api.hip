@@ -274,18 +274,16 @@ int mlxc_random_walk_noalloc(const int64_t* d_rowptr, int64_t num_nodes, const i
     if (int rc = check_out_type(out_type, num_nodes, num_edges, d_e_out)) return rc;
     if (num_walks > 0 && walk_length > 0 && !d_rand)
         return fail(MLXC_ERR_INVALID_ARGUMENT, "rand must not be NULL");
-    const size_t need = uniform_workspace_bytes(num_nodes, num_edges, num_walks, walk_length);
-    if (need > static_cast<size_t>(MLXC_NOALLOC_SCRATCH_BYTES))
-        return fail(MLXC_ERR_INVALID_ARGUMENT,
-                    "this call needs " + std::to_string(need) +
-                        " bytes of workspace, more than the MLXC_NOALLOC_SCRATCH_BYTES (" +
-                        std::to_string(MLXC_NOALLOC_SCRATCH_BYTES) +
-                        ") of mlxc_random_walk_noalloc; call mlxc_random_walk with a workspace");
+    // the queried size, or the whole array when the fastest layout needs more:
+    // the walk then runs the largest layout the array holds (start records
+    // only, or none), with the same results
+    size_t need = uniform_workspace_bytes(num_nodes, num_edges, num_walks, walk_length);
+    if (need > static_cast<size_t>(MLXC_NOALLOC_SCRATCH_BYTES)) need = MLXC_NOALLOC_SCRATCH_BYTES;
     void* ws = nullptr;
     if (int rc = noalloc_scratch(&ws)) return rc;
-    // the same call as mlxc_random_walk with a workspace of the queried size;
-    // its launches clear the status words first, so stale contents of the
-    // shared array do not matter
+    // the same call as mlxc_random_walk with a workspace of that size; its
+    // launches clear the status words first, so stale contents of the shared
+    // array do not matter
     if (int rc = mlxc_random_walk(d_rowptr, num_nodes, d_col, num_edges, d_start, num_walks,
                                   d_rand, walk_length, d_n_out, d_e_out, out_type, ws, need,
                                   stream))

@@ -123,15 +123,18 @@ def test_noalloc_status_is_per_call(cuda):
     assert torch.equal(out, n_a)
 
 
-def test_noalloc_rejects_calls_beyond_the_scratch(cuda):
-    """A call whose workspace would exceed MLXC_NOALLOC_SCRATCH_BYTES fails
-    on the host with a clear error, before any launch."""
+def test_noalloc_beyond_the_scratch_runs_a_smaller_layout(cuda):
+    """Calls whose fastest layout exceeds MLXC_NOALLOC_SCRATCH_BYTES run the
+    largest layout the scratch holds: configuration 2's graph with 2^20 walks
+    of 80 steps (packed records of 137 MB; the start records of 16 MB fit),
+    then 2^23 walks of 6 steps (start records of 134 MB: the direct kernel),
+    each equal to mlxc_random_walk with the full workspace, nodes, edges and
+    status."""
     lib = _lib.load()
-    V, E, N, L = 1 << 22, 1 << 24, 1 << 22, 80  # records: 8 * (E + N) > 64 MiB
-    need = lib.mlxc_random_walk_workspace_bytes(V, E, N, L)
-    assert need > _lib.MLXC_NOALLOC_SCRATCH_BYTES
-    fake = ctypes.c_void_p(0x1000)  # never dereferenced: the size check fails first
-    rc = lib.mlxc_random_walk_noalloc(fake, V, fake, E, fake, N, fake, L, fake, None, 0, None,
-                                      None)
-    assert rc == _lib.MLXC_ERR_INVALID_ARGUMENT
-    assert "MLXC_NOALLOC_SCRATCH_BYTES" in _lib.last_error()
+    rowptr, col = synth.rmat_csr(20, 1 << 24, seed=0, device=cuda)
+    V, E = rowptr.numel() - 1, col.numel()
+    for N, L in ((1 << 20, 80), (1 << 23, 6)):
+        assert lib.mlxc_random_walk_workspace_bytes(V, E, N, L) > _lib.MLXC_NOALLOC_SCRATCH_BYTES
+        start = torch.arange(N, device=cuda) % V
+        rand = mc.philox_uniform((N, L), 11, device=cuda)
+        _same(rowptr, col, start, rand, L)
