@@ -13,8 +13,8 @@ import torch  # noqa: F401  (must be loaded first: provides the HIP runtime)
 
 # MLXC_LIB selects another build of the same library (for example one
 # compiled with different tuning macros); the default is the in-tree build.
-LIB_PATH = os.environ.get("MLXC_LIB") or os.path.join(
-    os.path.dirname(os.path.abspath(__file__)), "libmlxc.so")
+IN_TREE_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmlxc.so")
+LIB_PATH = os.environ.get("MLXC_LIB") or IN_TREE_LIB
 
 MLXC_OK = 0
 MLXC_ERR_INVALID_ARGUMENT = -1

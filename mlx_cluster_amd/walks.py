@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import contextlib
 import numbers
+import os
 from typing import Optional, Tuple, Union
 
 import numpy as np
@@ -39,10 +40,14 @@ _RULES = {"ref_chain": _lib.MLXC_RULE_REF_CHAIN, "node2vec": _lib.MLXC_RULE_NODE
 # libmlxc.so for the common case (tensors of the right dtype on the current
 # device, torch's current stream), without this layer's per-call cost; it
 # returns None for any other call.  Without it every call takes the path below.
-try:
-    from . import _mlxc_torch as _fast
-except ImportError:
-    _fast = None
+# It is linked to the in-tree libmlxc.so, so another build selected by
+# MLXC_LIB takes the path below for every call.
+_fast = None
+if os.path.realpath(_lib.LIB_PATH) == os.path.realpath(_lib.IN_TREE_LIB):
+    try:
+        from . import _mlxc_torch as _fast
+    except ImportError:
+        _fast = None
 
 
 # ---------------------------------------------------------------- helpers

@@ -146,3 +146,18 @@ def test_binding_declines_cpu_tensors():
                                           False) is None
     n = mc.random_walk(r, c, s, torch.from_numpy(RAND), 4, stream="cpu")
     assert n.shape == (2, 5)
+
+
+def test_fast_path_only_with_the_in_tree_library(tmp_path):
+    """The compiled fast path is linked to the in-tree libmlxc.so: another
+    build selected by MLXC_LIB must not be bypassed through it."""
+    import os
+    import subprocess
+    import sys
+    code = "import mlx_cluster_amd.walks as w; print(w._fast is None)"
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, MLXC_LIB=str(tmp_path / "libmlxc.so"))
+    out = subprocess.run([sys.executable, "-c", code], cwd=repo, env=env, capture_output=True,
+                         text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip() == "True"
