@@ -5,8 +5,9 @@
 // arithmetic.  Every lane runs a small state machine over W walk slots; a
 // slot whose walk ends (or is absorbed by a node of out-degree 0) takes the
 // next walk from a per-wavefront queue refilled by one global atomic per
-// kQueueChunk walks, so lanes never idle while walks remain and the kernel's
-// tail is about one walk long.  Grids are the device's resident capacity.
+// kQueueChunk (64) walks, so lanes never idle while walks remain and the
+// kernel's tail is about one walk long.  Grids are the device's resident
+// capacity.
 #include <type_traits>
 
 #include "walk_host.h"
