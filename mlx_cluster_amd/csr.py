@@ -36,8 +36,9 @@ def to_csr(edge_index, num_nodes: Optional[int] = None, *, symmetrize: bool = Fa
         device: where to build (default: edge_index's device).  A GPU builds
             with mlxc_csr_build, the CPU with mlxc_csr_build_cpu.
         stream: GPU only: a torch.cuda.Stream to run on (default: torch's
-            current stream).  The call synchronises with it once, to read the
-            entry count and the id check.
+            current stream); without device=, the build runs on the
+            stream's device.  The call synchronises with it once, to read
+            the entry count and the id check.
 
     Raises ValueError when an id lies outside [0, num_nodes).
     """
@@ -49,8 +50,16 @@ def to_csr(edge_index, num_nodes: Optional[int] = None, *, symmetrize: bool = Fa
             edge_index.dtype == torch.bool:
         raise TypeError(f"edge_index must hold integers, got {edge_index.dtype}")
     _check_stream_arg(stream)
+    if stream is not None and not isinstance(stream, torch.cuda.Stream):
+        raise TypeError("to_csr: stream must be None or a torch.cuda.Stream (name the build's "
+                        "device with device=)")
+    if device is None and stream is not None:
+        device = stream.device  # build where the stream runs
     if device is not None:
         edge_index = edge_index.to(device)
+    if stream is not None and edge_index.device != stream.device:
+        raise ValueError(f"to_csr: stream runs on {stream.device}, the build on "
+                         f"{edge_index.device}")
     row = edge_index[0].to(torch.int64).contiguous()
     col = edge_index[1].to(torch.int64).contiguous()
     E = row.numel()
@@ -69,8 +78,6 @@ def to_csr(edge_index, num_nodes: Optional[int] = None, *, symmetrize: bool = Fa
     rowptr = torch.empty(V + 1, dtype=torch.int64, device=dev)
     col_out = torch.empty(total, dtype=torch.int64, device=dev)
     if dev.type == "cpu":
-        if stream is not None:
-            raise ValueError("stream applies to GPU edge lists only")
         count, status = ctypes.c_int64(0), ctypes.c_int64(0)
         rc = lib.mlxc_csr_build_cpu(row.data_ptr() if E else None, col.data_ptr() if E else None,
                                     E, V, flags, rowptr.data_ptr(),

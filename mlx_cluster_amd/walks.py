@@ -58,6 +58,15 @@ def _resolve_device(stream, tensors) -> torch.device:
                          "random_walk and rejection_sampling")
     if isinstance(stream, torch.cuda.Stream):
         return stream.device
+    if isinstance(stream, (str, torch.device)):  # a GPU named as the stream: run there
+        named = torch.device(stream)
+        if named.type != "cuda":
+            raise ValueError(f"stream names device {named}; expected a GPU or 'cpu'")
+        if named.index is not None:
+            return named
+        if not torch.cuda.is_available():
+            raise RuntimeError("mlx_cluster_amd needs a ROCm GPU; none is visible")
+        return torch.device("cuda", torch.cuda.current_device())
     for t in tensors:
         if isinstance(t, torch.Tensor) and t.is_cuda:
             return t.device

@@ -54,6 +54,20 @@ def test_bad_stream_type():
         mc.random_walk(ROWPTR, COL, START, RAND, 4, stream=3.5)
 
 
+def test_device_named_as_stream_is_where_the_call_runs():
+    from mlx_cluster_amd.walks import _resolve_device
+    host_tensor = torch.zeros(1)
+    assert _resolve_device("cuda:1", (host_tensor,)) == torch.device("cuda", 1)
+    assert _resolve_device(torch.device("cuda", 3), ()) == torch.device("cuda", 3)
+    with pytest.raises(ValueError, match="expected a GPU"):
+        _resolve_device("meta", ())
+
+
+def test_to_csr_stream_must_be_a_stream():
+    with pytest.raises(TypeError, match="torch.cuda.Stream"):
+        mc.to_csr(np.array([[0, 1], [1, 0]]), 2, stream="cuda:0")
+
+
 @pytest.mark.parametrize("p,q,rule,exc", [
     (0.0, 1.0, "ref_chain", ValueError), (1.0, -2.0, "ref_chain", ValueError),
     (float("nan"), 1.0, "ref_chain", ValueError), (1.0, float("inf"), "ref_chain", ValueError),
