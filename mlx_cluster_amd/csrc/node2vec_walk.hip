@@ -726,13 +726,15 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             n2v_uniforms(a.w.walk_base + n, l, trial, a.key0, a.key1, u0, r);
             e = bv + static_cast<int32_t>(pick_index(u0, dv));
         }
-        if (push) ow_push(ow, nout, g, v);
         if (fill) {
-            ow_fill(ow, nout, g + 1, g0 + L, v);
+            ow_fill(ow, nout, push ? g : g + 1, g0 + L, v);  // v from g on
             if (kEdges) ow_fill(ew, eout, e0 + l, e0 + L - 1, -1);  // l edges buffered
-        } else if (flush) {
-            if (ow.count) ow_flush(ow, nout, g);
-            if (kEdges && ew.count) ow_flush(ew, eout, e0 + L - 1);
+        } else {
+            if (push) ow_push(ow, nout, g, v);
+            if (flush) {
+                if (ow.count) ow_flush(ow, nout, g);
+                if (kEdges && ew.count) ow_flush(ew, eout, e0 + L - 1);
+            }
         }
         if (fill || flush) phase = kN2vIdle;
     }

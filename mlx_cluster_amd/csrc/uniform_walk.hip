@@ -279,15 +279,17 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_rec_kernel(WalkArgs a,
                 const int32_t la = l[s] + (ph[s] == kSlotWalk ? 1 : 0);  // steps taken
                 status |= (deg == kRecBadNode ? MLXC_STATUS_BAD_NODE : 0u) |
                           (deg == kRecBadRow && la < L ? MLXC_STATUS_BAD_ROW : 0u);
-                ow_push(ow[s], nout, g, node);
+                // an absorbing node (the walk stays) or a malformed record
+                // fills the rest of the row, this node included
+                const bool stop = la < L && deg <= 0 && deg != kRecLongRow;
+                if (stop) ow_fill(ow[s], nout, g, g0 + L, node);
+                else ow_push(ow[s], nout, g, node);
                 l[s] = la;
                 if (la == L) {
                     if (ow[s].count) ow_flush(ow[s], nout, g);
                     if (kEdges && ew[s].count) ow_flush(ew[s], eout, e0 + L - 1);
                     phase[s] = kSlotIdle;
-                } else if (deg <= 0 && deg != kRecLongRow) {
-                    // an absorbing node (the walk stays) or a malformed record
-                    ow_fill(ow[s], nout, g + 1, g0 + L, node);
+                } else if (stop) {
                     if (kEdges) ow_fill(ew[s], eout, e0 + la, e0 + L - 1, -1);
                     phase[s] = kSlotIdle;
                 } else if (kPacked && deg == kRecLongRow) {  // read the row's end first
@@ -539,9 +541,8 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                 fr[s] = n[s] * L + l[s] + 1;
                 phase[s] = kSlotCol;
             }
-            if (push) ow_push(ow[s], nout, g, v[s]);
             if (fill) {
-                ow_fill(ow[s], nout, g + 1, g0 + L, v[s]);
+                ow_fill(ow[s], nout, push ? g : g + 1, g0 + L, v[s]);  // v[s] from g on
                 if (kEdges) {
                     if constexpr (kWide) {
                         for (int64_t j = eg; j < e0 + L; ++j) eout[j] = static_cast<OutT>(-1);
@@ -549,9 +550,12 @@ __global__ __launch_bounds__(kBlock) void uniform_walk_csr_kernel(WalkArgs a,
                         ow_fill(ew[s], eout, eg, e0 + L - 1, -1);
                     }
                 }
-            } else if (flush) {
-                if (ow[s].count) ow_flush(ow[s], nout, g);
-                if (kEdges && !kWide && ew[s].count) ow_flush(ew[s], eout, e0 + L - 1);
+            } else {
+                if (push) ow_push(ow[s], nout, g, v[s]);
+                if (flush) {
+                    if (ow[s].count) ow_flush(ow[s], nout, g);
+                    if (kEdges && !kWide && ew[s].count) ow_flush(ew[s], eout, e0 + L - 1);
+                }
             }
             if (fill || flush) phase[s] = kSlotIdle;
         }

@@ -300,16 +300,24 @@ __device__ __forceinline__ float lw_take(float (&area)[RW][kBlock], LdsWindow<RW
 // Output rows are written in blocks of 8 entries, aligned in the output: 64
 // bytes of int64 entries, or 32 bytes with the compact int32 output.  A lane
 // buffers its walk's entries in an OutWin.  The stores of a completed block,
-// and of the run of whole blocks that a walk absorbed by a sink repeats to
-// the end of its row, are deferred to ow_drain, which the whole wavefront
-// executes together: completed blocks are staged through LDS and stored by
-// several lanes per block, one 16-byte non-temporal store each, and runs are
-// stored by the whole wavefront in consecutive 16-byte pieces.  Every store
-// instruction thus covers whole blocks and the L2 sends one full write per
-// block; a lane storing its own 64-byte block in four pieces leaves up to four
-// partial writes of it (measured: 3.6 write requests per block on MI355X,
-// against 1.0 here).  Only the partial blocks at the two ends of a row are
-// stored by the lane itself, entry by entry.
+// and of the run of entries that a walk absorbed by a sink repeats to the end
+// of its row, are deferred to ow_drain, which the whole wavefront executes
+// together: completed blocks are staged through LDS and stored by several
+// lanes per block, one 16-byte non-temporal store each, and the whole blocks
+// of a run are stored by the whole wavefront in consecutive 16-byte pieces.
+// Every such store instruction covers whole blocks and the L2 sends one full
+// write per block; a lane storing its own 64-byte block in four pieces leaves
+// up to four partial writes of it (measured: 3.6 write requests per block on
+// MI355X, against 1.0 here).  The partial blocks at the two ends of a row, and
+// a run's entries before its first block boundary and after its last whole
+// block, are stored the same way, one entry per lane on consecutive lanes, so
+// that each is one write request instead of one per entry: eight partial
+// blocks per store instruction, and a run's two ends in one.  Against the
+// same partial entries stored by their own lanes one at a time (up to eight
+// store instructions, a write request each), on MI355X: configuration 4
+// 6.15 -> 5.80 ms (62% of its walks meet a sink, and its rows of 21 entries
+// have partial blocks at both ends), configuration 2 7.26 -> 7.17, 3 10.01 ->
+// 9.88, 5x 16.60 -> 16.49.
 //
 // Every output store is issued by ow_drain, which the walk loops call right
 // after issuing their reads and before their single wait.  No store is then
@@ -318,8 +326,10 @@ __device__ __forceinline__ float lw_take(float (&area)[RW][kBlock], LdsWindow<RW
 // reads wait for that store.
 //
 // Between a completion and the drain the window is not pushed again: each
-// iteration of the walk loops pushes at most one entry per window, and a run
-// that follows a completed block starts on a block boundary.
+// iteration of the walk loops pushes at most one entry per window, and a fill
+// in the same iteration flushes only what that push left (a push that
+// completes a block leaves nothing), so a window defers at most one block
+// and one run per drain.
 //
 // T is the type the entries are buffered in (int32_t: the windowed walks'
 // node and edge ids fit in it); OutT is the output element type, int64_t (the
@@ -394,9 +404,9 @@ struct OutWin {
     // Deferred stores, written by ow_drain:
     void* blk;           // set: w[i] belongs at blk + i; the last blk_n entries are
     int32_t blk_n;       //   stored (8: a complete aligned block, by the wavefront)
-    void* run;           // set: run_blocks whole blocks of run_val, then tail_n more
-    int32_t run_blocks;  //   entries of run_val, from the aligned position run
-    int32_t tail_n;
+    void* run;           // set: run_n entries of run_val from run, of which the
+    int32_t run_n;       //   first run_head lie before the first block boundary
+    int32_t run_head;
     T run_val;
 };
 
@@ -406,15 +416,16 @@ __device__ __forceinline__ void ow_init(OutWin<T>& o) {
     o.blk = nullptr;
     o.blk_n = 0;
     o.run = nullptr;
-    o.run_blocks = 0;
-    o.tail_n = 0;
+    o.run_n = 0;
+    o.run_head = 0;
     o.run_val = 0;
 }
 
 // Per-wavefront LDS staging of ow_drain.
 struct WaveStage {
-    int32_t vals[kWave][8];  // completed blocks (entries as int32)
+    int32_t vals[kWave][8];  // completed and partial blocks (entries as int32)
     void* dst[kWave];
+    int32_t first[kWave];    // a partial block's first entry written
 };
 
 // Writes (defers to ow_drain) the buffered entries, the newest of which is
@@ -441,19 +452,19 @@ __device__ __forceinline__ void ow_push(OutWin<T>& o, OutT* __restrict__ out, in
 }
 
 // Output indices g .. g_last (inclusive) all hold x; the window holds the
-// entries before g.  The entries up to the first block boundary go through
-// the window; the whole blocks and the entries after the last one are left
-// to ow_drain as a run.
+// entries before g, which are flushed.  The fill is left to ow_drain as a
+// run: its entries before the first block boundary, its whole blocks and the
+// entries after the last one.
 template <typename T, typename OutT>
 __device__ __forceinline__ void ow_fill(OutWin<T>& o, OutT* __restrict__ out, int64_t g,
                                         int64_t g_last, T x) {
-    while (g <= g_last && (g & 7) != 0) ow_push(o, out, g++, x);
     if (o.count) ow_flush(o, out, g - 1);
     if (g <= g_last) {
-        const int64_t blocks = (g_last + 1 - g) >> 3;
+        const int64_t n = g_last + 1 - g;
+        const int64_t head = (8 - (g & 7)) & 7;
         o.run = out + g;
-        o.run_blocks = static_cast<int32_t>(blocks);
-        o.tail_n = static_cast<int32_t>(g_last + 1 - g - 8 * blocks);
+        o.run_n = static_cast<int32_t>(n);
+        o.run_head = static_cast<int32_t>(head < n ? head : n);
         o.run_val = x;
     }
 }
@@ -498,10 +509,13 @@ __device__ __forceinline__ void ow_drain(OutWin<T>& o, WaveStage& st) {
     const int lane = __lane_id();
     const int part = lane % kParts;
     const bool full = o.blk != nullptr && o.blk_n == 8;
+    const bool partial = o.blk != nullptr && !full;  // a partial block at an end of a row
     const uint64_t blocks = __ballot(full);
-    if (blocks) {
-        if (full) {
-            const int rank = lane_rank(blocks);
+    const uint64_t partials = __ballot(partial);
+    if (blocks | partials) {
+        // staged in rank order: the complete blocks, then the partial ones
+        if (o.blk != nullptr) {
+            const int rank = full ? lane_rank(blocks) : __popcll(blocks) + lane_rank(partials);
             *reinterpret_cast<i32x4*>(&st.vals[rank][0]) =
                 i32x4{static_cast<int32_t>(o.w[0]), static_cast<int32_t>(o.w[1]),
                       static_cast<int32_t>(o.w[2]), static_cast<int32_t>(o.w[3])};
@@ -509,6 +523,7 @@ __device__ __forceinline__ void ow_drain(OutWin<T>& o, WaveStage& st) {
                 i32x4{static_cast<int32_t>(o.w[4]), static_cast<int32_t>(o.w[5]),
                       static_cast<int32_t>(o.w[6]), static_cast<int32_t>(o.w[7])};
             st.dst[rank] = o.blk;
+            st.first[rank] = 8 - o.blk_n;
         }
         wave_sync();
         const int c = __popcll(blocks);
@@ -518,35 +533,39 @@ __device__ __forceinline__ void ow_drain(OutWin<T>& o, WaveStage& st) {
                 store_block_part(vec16_from<OutT>(&st.vals[k][kPer * part]),
                                  static_cast<OutT*>(st.dst[k]) + kPer * part);
         }
+        // partial blocks: eight lanes per block, lane i storing entry i when
+        // it is one of the block's, eight blocks per store instruction
+        const int cp = __popcll(partials);
+        for (int r = 0; r < cp; r += kWave / 8) {
+            const int k = c + r + lane / 8;
+            const int i = lane % 8;
+            if (r + lane / 8 < cp && i >= st.first[k])
+                store_partial(static_cast<OutT>(st.vals[k][i]), static_cast<OutT*>(st.dst[k]) + i);
+        }
         wave_sync();
     }
-    if (o.blk != nullptr && !full) {  // partial block at an end of a row: this lane alone
-        OutT* p = static_cast<OutT*>(o.blk);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (i >= 8 - o.blk_n) store_partial(static_cast<OutT>(o.w[i]), p + i);
-    }
     o.blk = nullptr;
-    if (o.tail_n > 0) {  // the entries of a run after its last whole block
-        OutT* p = static_cast<OutT*>(o.run) + 8 * static_cast<int64_t>(o.run_blocks);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (j < o.tail_n) store_partial(static_cast<OutT>(o.run_val), p + j);
-    }
-    uint64_t runs = __ballot(o.run_blocks > 0);
+    uint64_t runs = __ballot(o.run_n > 0);
     while (runs) {  // wave-uniform: one lane's run at a time, the whole wave storing it
         const int src = __builtin_ctzll(runs);
         runs &= runs - 1;
         OutT* dst = static_cast<OutT*>(read_lane_ptr(o.run, src));
-        const int32_t chunks = kParts * __builtin_amdgcn_readlane(o.run_blocks, src);
+        const int32_t n = __builtin_amdgcn_readlane(o.run_n, src);
+        const int32_t head = __builtin_amdgcn_readlane(o.run_head, src);
+        const int32_t blocks_n = (n - head) >> 3;
+        const int32_t tail = n - head - 8 * blocks_n;
         const OutT x = static_cast<OutT>(
             static_cast<T>(__builtin_amdgcn_readlane(static_cast<int32_t>(o.run_val), src)));
         const typename Vec16<OutT>::type xx = vec16_splat(x);
-        for (int c = lane; c < chunks; c += kWave) store_block_part(xx, dst + kPer * c);
+        OutT* body = dst + head;  // a block boundary
+        for (int c = lane; c < kParts * blocks_n; c += kWave) store_block_part(xx, body + kPer * c);
+        // the entries before the first block boundary and after the last
+        // whole block, one per lane
+        if (lane < head + tail)
+            store_partial(x, lane < head ? dst + lane : body + 8 * static_cast<int64_t>(blocks_n) + (lane - head));
     }
     o.run = nullptr;
-    o.run_blocks = 0;
-    o.tail_n = 0;
+    o.run_n = 0;
 }
 
 // ----------------------------------------------------------- edge records
