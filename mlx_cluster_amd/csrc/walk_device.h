@@ -312,12 +312,14 @@ __device__ __forceinline__ float lw_take(float (&area)[RW][kBlock], LdsWindow<RW
 // a run's entries before its first block boundary and after its last whole
 // block, are stored the same way, one entry per lane on consecutive lanes, so
 // that each is one write request instead of one per entry: eight partial
-// blocks per store instruction, and a run's two ends in one.  Against the
-// same partial entries stored by their own lanes one at a time (up to eight
-// store instructions, a write request each), on MI355X: configuration 4
-// 6.15 -> 5.80 ms (62% of its walks meet a sink, and its rows of 21 entries
-// have partial blocks at both ends), configuration 2 7.26 -> 7.17, 3 10.01 ->
-// 9.88, 5x 16.60 -> 16.49.
+// blocks per store instruction, and a run's two ends in one; and a walk
+// absorbed by a sink fills its row from its current entry as one run.
+// Against the same partial entries stored by their own lanes one at a time
+// (up to eight store instructions, a write request each), the fill's first
+// entries pushed through the window, on MI355X: configuration 4 6.15 -> 5.76
+// ms (62% of its walks meet a sink, and its rows of 21 entries have partial
+// blocks at both ends), 2 7.24 -> 7.14, 2 with the int32 output 6.74 -> 6.62,
+// 3 10.00 -> 9.88, 5x 16.57 -> 16.47.
 //
 // Every output store is issued by ow_drain, which the walk loops call right
 // after issuing their reads and before their single wait.  No store is then
@@ -363,16 +365,27 @@ struct Vec16<int32_t> {
     static constexpr int kLanes = 4;
 };
 
+// The output stores go through global-address-space pointers.  The drain's
+// destinations come back from LDS staging or from another lane's registers,
+// where the compiler cannot tell them from LDS addresses, and would emit flat
+// stores, which also count in lgkmcnt: every later wait for an LDS read or a
+// scalar load would then wait for the stores as well.  (No time difference
+// measured on MI355X: the loop's single wait covers the stores either way.)
+template <typename T>
+using GlobalPtr = __attribute__((address_space(1))) T*;
+
 template <typename OutT>
 __device__ __forceinline__ void store_block_part(typename Vec16<OutT>::type v, OutT* p) {
     typedef typename Vec16<OutT>::type V;
-    if (MLXC_BLOCK_NT) __builtin_nontemporal_store(v, reinterpret_cast<V*>(p));
-    else *reinterpret_cast<V*>(p) = v;
+    GlobalPtr<V> q = (GlobalPtr<V>)(p);
+    if (MLXC_BLOCK_NT) __builtin_nontemporal_store(v, q);
+    else *q = v;
 }
 
 template <typename OutT>
 __device__ __forceinline__ void store_partial(OutT v, OutT* p) {
-    if (MLXC_PARTIAL_NT) __builtin_nontemporal_store(v, p); else *p = v;
+    GlobalPtr<OutT> q = (GlobalPtr<OutT>)(p);
+    if (MLXC_PARTIAL_NT) __builtin_nontemporal_store(v, q); else *q = v;
 }
 
 // Entries p[0 .. kLanes-1] (int32) widened to one 16-byte vector of OutT.
