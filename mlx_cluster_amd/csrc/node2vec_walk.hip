@@ -389,11 +389,16 @@ __device__ __forceinline__ void n2v_search_rows(int32_t symmetric, int32_t x, in
     }
 }
 
-// Decision once the search has answered whether t is in row(x).
+// Decision once the search has answered whether t is in row(x).  Both
+// compares are made and the answer selects between them: selecting the
+// threshold instead lets the compiler turn the two argument reads into one
+// per-lane load from the kernel-argument segment, a memory round trip (and a
+// wait for every store in flight) in the middle of the iteration.
 template <int kRule>
 __device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, float r, bool adjacent) {
     if (kRule == MLXC_RULE_REF_CHAIN) return adjacent;  // only searched when r < p1 decides
-    return adjacent ? (r < a.thr1) : (r < a.thr2);
+    const bool lt1 = r < a.thr1, lt2 = r < a.thr2;
+    return adjacent ? lt1 : lt2;
 }
 
 // node2vec walk over edge records (num_nodes, num_edges below 2^31; n_out and
