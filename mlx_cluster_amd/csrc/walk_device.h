@@ -1,7 +1,8 @@
 // Device-side building blocks of the random-walk kernels (gfx950): the
 // Philox4x32-10 generator, the reference's float32 index rule, CSR row reads
-// with bounds checks, the per-wavefront walk queue, the per-lane register
-// windows for the rand and output streams, and the edge-record layout.
+// with bounds checks, the per-wavefront walk queue, the per-lane windows for
+// the rand stream (in LDS) and the output stream (in registers, stored by the
+// wavefront together), and the edge-record layout.
 //
 // Reference semantics (vinayhpandya/mlx_cluster):
 //   uniform walk   /root/reference/random_walks/RandomWalk.cpp:41-60
@@ -189,8 +190,10 @@ struct WalkArgs {
 // Each slot buffers its entries in an 8-entry window aligned to 64 bytes of
 // the output (OutWin below) and the wavefront stores completed windows, and
 // the constant tails of walks that sink in a node of out-degree 0, as whole
-// 64-byte blocks.  The stores are non-temporal: the output is never read
-// back, and streaming it past the caches keeps them for the graph.
+// 64-byte blocks where they can (the partial blocks at the ends of rows and
+// tails from consecutive lanes, one write each).  The whole blocks are
+// non-temporal: the output is never read back, and streaming it past the
+// caches keeps them for the graph.
 // One block of RW uniforms as read or generated, before it is stored.
 template <int RW>
 struct RandWindow {
