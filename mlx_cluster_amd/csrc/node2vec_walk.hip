@@ -344,6 +344,8 @@ struct N2VRecArgs {
     // Row hash tables (record mode; null: none), kSearchBlock slots a bucket:
     // rows without a hub bitmap whose search would take more than one read.
     const int32_t* hash;
+    // LDS walk: the threads of a block that walk (all of them copy the graph)
+    int32_t lds_walkers;
 };
 
 // Smallest float >= p (p > 0), the float threshold of N2VRecArgs.
@@ -806,8 +808,9 @@ __global__ __launch_bounds__(kLdsBlock) void node2vec_lds_kernel(N2VRecArgs a) {
     // step goes on with the next step (or its next walk) in the next
     // iteration, so a wavefront runs as long as its longest walk, not as
     // long as the longest trial run of each step summed over the steps.
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kLdsBlock;
-    int64_t n = static_cast<int64_t>(blockIdx.x) * kLdsBlock + threadIdx.x;
+    const int64_t walkers = a.lds_walkers;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * walkers;
+    int64_t n = threadIdx.x < walkers ? static_cast<int64_t>(blockIdx.x) * walkers + threadIdx.x : N;
     OutT* row = nullptr;
     OutT* erow = nullptr;
     int64_t l = 0;           // steps taken
@@ -1221,7 +1224,22 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         a.thr2 = float_at_or_above(p.prob2);
         a.key0 = p.key0;
         a.key1 = p.key1;
-        const dim3 grid(static_cast<unsigned>((w.num_walks + kLdsBlock - 1) / kLdsBlock));  // <= 1024
+        // Every block copies the graph with all its threads, then walks with
+        // lds_walkers of them: at most one block per compute unit, and down
+        // to one wavefront per SIMD (256 walkers) while the walks allow, since
+        // the walk of a trial is bound by its own instruction latency (a
+        // Philox draw per trial) once a SIMD has no other wavefront to run.
+        DeviceInfo info;
+        if (int rc = device_info(info)) return rc;
+        const int64_t N = w.num_walks;  // 1 .. kLdsWalkSteps (lds_walk_fits)
+        int64_t blocks = (N + kLdsMinWalkers - 1) / kLdsMinWalkers;
+        if (blocks > info.cus) blocks = info.cus;
+        if (blocks < 1) blocks = 1;
+        int64_t walkers = (N + blocks - 1) / blocks;
+        walkers = (walkers + kWave - 1) / kWave * kWave;
+        a.lds_walkers = static_cast<int32_t>(walkers < kLdsMinWalkers ? kLdsMinWalkers
+                                             : walkers > kLdsBlock ? kLdsBlock : walkers);
+        const dim3 grid(static_cast<unsigned>(blocks));
         const dim3 block(kLdsBlock);
         const bool edges = w.e_out != nullptr;
         if (p.rule == MLXC_RULE_REF_CHAIN) {

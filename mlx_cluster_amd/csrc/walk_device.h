@@ -759,6 +759,9 @@ constexpr int kLdsGraphEntries = 14336;              // rowptr + col entries (56
 // times finer than 256 (the reference tests' 2,000 walks of 5 steps on the
 // Cora-like graph: 11.2 -> 6.7 us per launch).
 constexpr int kLdsBlock = 1024;
+// Fewest walking threads per block of the node2vec LDS walk: one wavefront
+// per SIMD of the block's compute unit.
+constexpr int kLdsMinWalkers = 256;
 
 constexpr int64_t kLdsWalkSteps = int64_t{1} << 20;  // calls of 1 .. 2^20 steps
 __host__ __device__ inline bool lds_walk_fits(int64_t num_nodes, int64_t num_edges,
