@@ -538,6 +538,31 @@ def test_lds_walk(rule, cuda):
                               seed=1, rule=RULE_NAME[rule])
 
 
+@pytest.mark.parametrize("rule", [oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT])
+def test_lds_walk_many_walks(rule, cuda):
+    """The LDS walk spreads its walks over at most one block per compute unit,
+    256 to 1,024 walking threads a block: 50,000 walks take about 200 blocks
+    of 256 walkers, 300,000 take a block per compute unit of 1,024 walkers
+    that each run two walks or more.  Bit-exact against the oracle, nodes
+    and edges."""
+    from mlx_cluster_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(11 + rule)
+    V = 900
+    rowptr, col = undirected(V, rng.integers(0, V, (3000, 2)))
+    t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.int64)).to(cuda)
+    for N, L in ((50_000, 4), (300_000, 3)):
+        assert lib.mlxc_rejection_sampling_workspace_bytes(V, col.size, N, L, 0.5, 2.0, rule) == 256
+        start = (np.arange(N) * 7) % V
+        n_ref, e_ref, st, _ = oracle.node2vec_walk(rowptr, col, start, L, 0.5, 2.0, 21, rule=rule,
+                                                   rows_sorted=True, with_edges=True)
+        assert st == 0
+        n, e = mc.rejection_sampling(t(rowptr), t(col), t(start), L, 0.5, 2.0, seed=21,
+                                     rule=RULE_NAME[rule], return_edges=True)
+        np.testing.assert_array_equal(n.cpu().numpy(), n_ref)
+        np.testing.assert_array_equal(e.cpu().numpy(), e_ref)
+
+
 def test_lds_walks_random_sweep(cuda):
     """Random small graphs (directed and undirected, duplicates and
     self-loops kept) under the LDS limit, random walk counts and lengths:
