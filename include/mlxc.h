@@ -9,6 +9,8 @@
  *
  * Return codes: 0 on success, a negative MLXC_ERR_* code otherwise; the
  * message of the calling thread's last failure is in mlxc_last_error().
+ * Every walk_length is in [0, 2^31 - 2]: a walk's row holds walk_length + 1
+ * entries.
  *
  * Ownership: the caller allocates every buffer (inputs, outputs and the small
  * status/work buffers).  The library never allocates or frees device memory.

@@ -53,13 +53,21 @@ int check_workspace(const void* work, size_t work_bytes) {
     return MLXC_OK;
 }
 
+// A walk's row holds walk_length + 1 entries, which the kernels count in int32.
+int check_walk_length(int32_t walk_length) {
+    if (walk_length < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "walk_length must be >= 0");
+    if (walk_length == INT32_MAX)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "walk_length must be below 2^31 - 1");
+    return MLXC_OK;
+}
+
 int check_graph(const int64_t* rowptr, int64_t num_nodes, const int64_t* col, int64_t num_edges,
                 const int64_t* start, int64_t num_walks, int32_t walk_length,
                 const void* n_out) {
     if (num_nodes < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_nodes must be >= 0");
     if (num_edges < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_edges must be >= 0");
     if (num_walks < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "num_walks must be >= 0");
-    if (walk_length < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "walk_length must be >= 0");
+    if (int rc = check_walk_length(walk_length)) return rc;
     if (num_walks > 0) {
         if (!rowptr || !start || !n_out)
             return fail(MLXC_ERR_INVALID_ARGUMENT, "rowptr, start and n_out must not be NULL");
@@ -177,7 +185,7 @@ int check_window_grid(int64_t num_walks, int32_t walk_nodes, int32_t elem_type) 
 
 int check_negative(const int64_t* start, int64_t num_walks, int32_t walk_length, int32_t ctx,
                    int64_t num_nodes, int32_t out_type, const void* out) {
-    if (walk_length < 0) return fail(MLXC_ERR_INVALID_ARGUMENT, "walk_length must be >= 0");
+    if (int rc = check_walk_length(walk_length)) return rc;
     if (int rc = check_windows(start, num_walks, walk_length + 1, ctx, out_type, out)) return rc;
     if (num_nodes < 1 || num_nodes > (int64_t(1) << 32))
         return fail(MLXC_ERR_INVALID_ARGUMENT, "num_nodes must lie in [1, 2^32]");

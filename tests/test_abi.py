@@ -62,6 +62,7 @@ WS = 64  # workspace bytes passed with FAKE
     ((FAKE, 1, FAKE, -1, FAKE, 1, FAKE, 1, FAKE, None, FAKE, WS, None), "num_edges"),
     ((FAKE, 1, FAKE, 0, FAKE, -1, FAKE, 1, FAKE, None, FAKE, WS, None), "num_walks"),
     ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, -2, FAKE, None, FAKE, WS, None), "walk_length"),
+    ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, 2**31 - 1, FAKE, None, FAKE, WS, None), "2^31 - 1"),
     ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, None, WS, None), "workspace"),
     ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, FAKE, 16, None), "MLXC_WORK_WORDS"),
     ((FAKE, 1, FAKE, 0, FAKE, 1, FAKE, 1, FAKE, None, ctypes.c_void_p(0x1008), WS, None),
