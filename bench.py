@@ -332,6 +332,27 @@ def random_footprint(mc, kind, V, E, N, L, extra):
     return None if ws <= 256 else ws - 256 - 16 * N
 
 
+def walk_kernel_event_ms(torch, mc, stream, step, calls):
+    """The walk kernel's own duration in each of `calls` calls, from HIP events
+    the library records around it on `stream` (mlxc_set_walk_events)."""
+    lib = mc._lib.load()
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(calls)]
+    for a, b in pairs:  # torch creates an event's HIP handle at its first record
+        a.record(stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    try:
+        for a, b in pairs:
+            mc._lib.check(lib.mlxc_set_walk_events(a.cuda_event, b.cuda_event),
+                          "mlxc_set_walk_events")
+            step()
+    finally:
+        lib.mlxc_set_walk_events(None, None)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in pairs]
+
+
 def line_roofline(mc, kind, config, V, E, N, L, extra):
     """lines/s of the walk kernel and its fraction of the ceiling at the call's
     random footprint (nulls where a profile or the ceiling is missing)."""
@@ -777,10 +798,12 @@ def main():
     event_ms = [a.elapsed_time(b) for a, b in events]
     kernel_ms = float(np.mean(event_ms))
     kernel_ms_median = float(np.median(event_ms))
+    walk_ms = walk_kernel_event_ms(torch, mc, stream, step, args.steps)
     ms_per_step = wall / args.steps * 1e3
     steps_per_launch = N * L
     value = steps_per_launch / (ms_per_step / 1e3)
-    log(f"{ms_per_step:.3f} ms/step wall, {kernel_ms:.3f} ms/launch (events)")
+    log(f"{ms_per_step:.3f} ms/step wall, {kernel_ms:.3f} ms/launch (events), "
+        f"walk kernel {float(np.mean(walk_ms)):.3f} ms (events)")
 
     # One end-to-end call with allocation: the caching allocator is emptied
     # first, so the output and workspace come from fresh device allocations.
@@ -829,6 +852,7 @@ def main():
     # kernels) against the ceiling's line traffic (128 bytes a line)
     lines["fabric_frac"] = (traffic / (kernel_ms / 1e3) / (lines["line_ceiling_per_s"] * 128)
                             if traffic and lines["line_ceiling_per_s"] else None)
+    walk_kernel_ms = float(np.mean(walk_ms))
     roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": (achieved / PEAK_HBM_GBS) if achieved else None, "traffic": traffic,
                 **lines,
@@ -836,6 +860,13 @@ def main():
                 "kernel_ms": kernel_ms, "kernel_ms_median": kernel_ms_median,
                 "e2e_ms_with_allocation": e2e_alloc_ms,
                 "kernel_ms_source": "HIP events around each call on its stream (mean; median beside it)",
+                "walk_kernel_ms": walk_kernel_ms,
+                "walk_kernel_ms_median": float(np.median(walk_ms)),
+                "walk_kernel_ms_source": "HIP events the library records on the call's stream right "
+                                         "before and after its walk kernel (mlxc_set_walk_events), "
+                                         "mean over as many calls as timed (median beside it)",
+                "frac_walk_kernel": (roof_bytes / (walk_kernel_ms / 1e3) / 1e9 / PEAK_HBM_GBS
+                                     if roof_bytes else None),
                 "useful_gbs": useful_bytes / (kernel_ms / 1e3) / 1e9,
                 "useful_bytes_per_launch": useful_bytes,
                 "fabric_gbs_measured": (traffic / (kernel_ms / 1e3) / 1e9) if traffic else None,

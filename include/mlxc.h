@@ -414,6 +414,21 @@ int mlxc_rejection_sampling_cpu(const int64_t* rowptr, int64_t num_nodes,
                                 int32_t threads, int64_t* status);
 
 /*
+ * Measurement hook: times the walk kernel alone, without the preparation
+ * launches before it (a call's last launch is its walk kernel).  After
+ * mlxc_set_walk_events(start_event, stop_event), with two hipEvent_t handles
+ * created by the caller, every walk call the calling thread makes
+ * (mlxc_random_walk*, mlxc_rejection_sampling) records start_event on its
+ * stream right before its walk kernel and stop_event right after it;
+ * hipEventElapsedTime between them is that kernel's duration.
+ * mlxc_set_walk_events(NULL, NULL) stops the recording.  A call without
+ * walks launches no walk kernel and records neither event.  Returns
+ * MLXC_ERR_INVALID_ARGUMENT if exactly one handle is NULL.  No reference
+ * counterpart.
+ */
+int mlxc_set_walk_events(void* start_event, void* stop_event);
+
+/*
  * Diagnostic: random reads from a device table, the measurement behind the
  * walks' random-read ceiling (a walk step is one or two dependent reads at
  * random addresses, so the walk kernels are bound by how many such reads the

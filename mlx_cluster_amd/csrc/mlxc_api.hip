@@ -20,6 +20,8 @@ namespace {
 thread_local std::string g_last_error;
 }
 
+thread_local hipEvent_t g_walk_events[2] = {nullptr, nullptr};
+
 int fail(int code, const std::string& msg) {
     g_last_error = msg;
     return code;
@@ -229,9 +231,17 @@ using namespace mlxc;
 
 extern "C" {
 
-int mlxc_version(void) { return 300; }
+int mlxc_version(void) { return 301; }
 
 const char* mlxc_last_error(void) { return g_last_error.c_str(); }
+
+int mlxc_set_walk_events(void* start_event, void* stop_event) {
+    if ((start_event == nullptr) != (stop_event == nullptr))
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "set both events or neither");
+    g_walk_events[0] = static_cast<hipEvent_t>(start_event);
+    g_walk_events[1] = static_cast<hipEvent_t>(stop_event);
+    return MLXC_OK;
+}
 
 size_t mlxc_random_walk_workspace_bytes(int64_t num_nodes, int64_t num_edges, int64_t num_walks,
                                         int32_t walk_length) {

@@ -926,9 +926,10 @@ int launch_n2v(const N2VArgs& a, hipStream_t stream) {
     auto kernel = node2vec_walk_kernel<kRule, kEdges, OutT>;
     int grid = 0;
     if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid)) return rc;
+    if (int rc = record_walk_event(0, stream)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
     MLXC_HIP_TRY(hipGetLastError());
-    return MLXC_OK;
+    return record_walk_event(1, stream);
 }
 
 template <int kRule, typename OutT>
@@ -959,9 +960,10 @@ int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
                                                          : MLXC_N2V_ANALYTIC_BLOCKS_PER_CU;
     int grid = 0;
     if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid, per_cu)) return rc;
+    if (int rc = record_walk_event(0, stream)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
     MLXC_HIP_TRY(hipGetLastError());
-    return MLXC_OK;
+    return record_walk_event(1, stream);
 }
 
 // Workspace of the record walk: edge records (record mode only), start
@@ -1242,6 +1244,7 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         const dim3 grid(static_cast<unsigned>(blocks));
         const dim3 block(kLdsBlock);
         const bool edges = w.e_out != nullptr;
+        if (int rc = record_walk_event(0, stream)) return rc;
         if (p.rule == MLXC_RULE_REF_CHAIN) {
             if (edges) hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, true, OutT>), grid, block, 0, stream, a);
             else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_REF_CHAIN, false, OutT>), grid, block, 0, stream, a);
@@ -1250,7 +1253,7 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
             else hipLaunchKernelGGL((node2vec_lds_kernel<MLXC_RULE_NODE2VEC_EXACT, false, OutT>), grid, block, 0, stream, a);
         }
         MLXC_HIP_TRY(hipGetLastError());
-        return MLXC_OK;
+        return record_walk_event(1, stream);
     }
     // Graphs beyond int32, a workspace too small for the records, or output
     // buffers not 16-byte aligned: the direct CSR kernel.  The CSR check

@@ -737,9 +737,10 @@ int launch_walk_kernel(Kernel kernel, int slots, int max_per_cu, const WalkArgs&
                        hipStream_t stream, Extra... extra) {
     int grid = 0;
     if (int rc = persistent_grid(kernel, a.num_walks, slots, grid, max_per_cu)) return rc;
+    if (int rc = record_walk_event(0, stream)) return rc;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a, extra...);
     MLXC_HIP_TRY(hipGetLastError());
-    return MLXC_OK;
+    return record_walk_event(1, stream);
 }
 
 }  // namespace
@@ -812,10 +813,11 @@ int launch_uniform_impl(const WalkArgs& a, void* workspace, size_t workspace_byt
     case UniformMode::kLds: {
         if (int rc = launch_zero_work(a.work, stream)) return rc;
         const int64_t blocks = (a.num_walks + kLdsBlock - 1) / kLdsBlock;  // at most 1024
+        if (int rc = record_walk_event(0, stream)) return rc;
         hipLaunchKernelGGL((uniform_walk_lds_kernel<kGen, kEdges, OutT>), dim3(static_cast<int>(blocks)),
                            dim3(kLdsBlock), 0, stream, a);
         MLXC_HIP_TRY(hipGetLastError());
-        return MLXC_OK;
+        return record_walk_event(1, stream);
     }
     case UniformMode::kPlain:
         break;

@@ -24,6 +24,16 @@ int fail(int code, const std::string& msg);
             return ::mlxc::fail(MLXC_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(err_)); \
     } while (0)
 
+// The events the calling thread set with mlxc_set_walk_events (null: none),
+// recorded on a call's stream right before (0) and right after (1) its walk
+// kernel, the last launch of the call.
+extern thread_local hipEvent_t g_walk_events[2];
+
+inline int record_walk_event(int which, hipStream_t stream) {
+    if (g_walk_events[which]) MLXC_HIP_TRY(hipEventRecord(g_walk_events[which], stream));
+    return MLXC_OK;
+}
+
 struct DeviceInfo {
     int cus = 0;  // compute units of the current device
 };

@@ -48,7 +48,7 @@ def test_header_constants_match_binding():
 
 
 def test_version():
-    assert _lib.load().mlxc_version() == 300
+    assert _lib.load().mlxc_version() == 301
 
 
 FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
@@ -121,6 +121,14 @@ def test_other_entry_points_reject_bad_arguments():
         == _lib.MLXC_ERR_INVALID_ARGUMENT
     assert lib.mlxc_csr_check(FAKE, 1, FAKE, 0, FAKE, 8, ctypes.addressof(flags), None) \
         == _lib.MLXC_ERR_INVALID_ARGUMENT
+
+
+def test_walk_events_are_set_in_pairs():
+    lib = _lib.load()
+    assert lib.mlxc_set_walk_events(FAKE, None) == _lib.MLXC_ERR_INVALID_ARGUMENT
+    assert "both events" in _lib.last_error()
+    assert lib.mlxc_set_walk_events(None, FAKE) == _lib.MLXC_ERR_INVALID_ARGUMENT
+    assert lib.mlxc_set_walk_events(None, None) == _lib.MLXC_OK
 
 
 def test_window_launches_beyond_the_grid_limit_are_rejected():
