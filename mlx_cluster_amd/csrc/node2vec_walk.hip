@@ -344,8 +344,10 @@ struct N2VRecArgs {
     // Row hash tables (record mode; null: none), kSearchBlock slots a bucket:
     // rows without a hub bitmap whose search would take more than one read.
     const int32_t* hash;
-    // LDS walk: the threads of a block that walk (all of them copy the graph)
+    // LDS walk: the walks a block runs at once (all its threads copy the
+    // graph), and the lanes that run each walk (1, 2, 4 or 8)
     int32_t lds_walkers;
+    int32_t lds_group;
 };
 
 // Smallest float >= p (p > 0), the float threshold of N2VRecArgs.
@@ -750,9 +752,10 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
 
 // node2vec walk on a graph small enough for LDS (lds_walk_fits), for calls
 // bound by launch latency (the reference tests' Cora-sized workload): every
-// block copies rowptr and col, as int32, into its LDS; one walk per thread,
-// the same draws and decisions as the record walk, the neighbour test by
-// bisection (sorted rows) or a linear scan (unsorted rows) in LDS.  Every
+// block copies rowptr and col, as int32, into its LDS; each walk runs on a
+// group of lds_group consecutive lanes, with the same draws and decisions as
+// the record walk, the neighbour test by bisection (sorted rows) or a linear
+// scan (unsorted rows) in LDS.  Every
 // block validates its copy of the whole CSR, as the preparation passes of the
 // other layouts do (block 0 reports it); with MLXC_ROWS_DETECT each block
 // also decides the row order of its copy by the preparation passes' rule
@@ -804,13 +807,25 @@ __global__ __launch_bounds__(kLdsBlock) void node2vec_lds_kernel(N2VRecArgs a) {
     uint32_t status = 0;
     if (blockIdx.x == 0 && threadIdx.x == 0)
         status = (any_bad_row ? MLXC_STATUS_BAD_ROW : 0u) | (any_bad_col ? MLXC_STATUS_BAD_NODE : 0u);
-    // One trial per loop iteration and lane: a lane whose walk takes its
-    // step goes on with the next step (or its next walk) in the next
-    // iteration, so a wavefront runs as long as its longest walk, not as
-    // long as the longest trial run of each step summed over the steps.
+    // One round of trials per loop iteration: the G = lds_group lanes of a
+    // walk try trials trial .. trial + G - 1 of its step at once, one each,
+    // and the step takes the first of them, in trial order, that accepts (or
+    // meets a malformed entry), which is where one lane trying them in turn
+    // would have stopped: the same walks, in fewer rounds.  A call with few
+    // walks leaves most of the device idle, and its time is the longest
+    // chain of trials of one walk; G lanes cut that chain about G-fold where
+    // steps take several trials.  A walk that takes its step goes on with
+    // the next step (or its next walk) in the next iteration, so a wavefront
+    // runs as long as its longest walk.  Every lane of a group holds the
+    // walk's whole state; only the trial differs.
+    const int G = a.lds_group;
+    const int k = static_cast<int>(threadIdx.x) & (G - 1);  // this lane's trial offset
+    const int base = __lane_id() & ~(G - 1);                 // the group's first lane
+    const uint32_t group_bits = (G == 32 ? 0xffffffffu : (1u << G) - 1u);
     const int64_t walkers = a.lds_walkers;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * walkers;
-    int64_t n = threadIdx.x < walkers ? static_cast<int64_t>(blockIdx.x) * walkers + threadIdx.x : N;
+    const int64_t gi = threadIdx.x / G;
+    int64_t n = gi < walkers ? static_cast<int64_t>(blockIdx.x) * walkers + gi : N;
     OutT* row = nullptr;
     OutT* erow = nullptr;
     int64_t l = 0;           // steps taken
@@ -818,11 +833,12 @@ __global__ __launch_bounds__(kLdsBlock) void node2vec_lds_kernel(N2VRecArgs a) {
     int32_t b = 0, deg = 0;  // row of v
     uint32_t trial = 0;
     bool walking = false;    // walk n has a trial due
-    // the walk stays at v from step l on; then the lane takes its next walk
+    // the walk stays at v from step l on (the group's lanes share the
+    // stores); then the group takes its next walk
     auto finish = [&]() {
-        for (int64_t j = l + 1; j <= L; ++j) row[j] = static_cast<OutT>(v);
+        for (int64_t j = l + 1 + k; j <= L; j += G) row[j] = static_cast<OutT>(v);
         if (kEdges)
-            for (int64_t j = l; j < L; ++j) erow[j] = static_cast<OutT>(-1);
+            for (int64_t j = l + k; j < L; j += G) erow[j] = static_cast<OutT>(-1);
         walking = false;
         n += stride;
     };
@@ -832,7 +848,7 @@ __global__ __launch_bounds__(kLdsBlock) void node2vec_lds_kernel(N2VRecArgs a) {
             const int64_t s = a.w.start[n];
             row = nout + n * (L + 1);
             erow = kEdges ? eout + n * L : nullptr;
-            row[0] = static_cast<OutT>(s);
+            if (k == 0) row[0] = static_cast<OutT>(s);
             l = 0;
             v = static_cast<int32_t>(s);
             t = v;
@@ -860,24 +876,27 @@ __global__ __launch_bounds__(kLdsBlock) void node2vec_lds_kernel(N2VRecArgs a) {
             trial = 0;
             walking = true;
         }
-        // trial `trial` of step l from v; the first step and forced steps
-        // accept (BiasedRandomWalk.cpp:60-66, 76-78)
+        // trial `trial + k` of step l from v; the first step and forced steps
+        // accept at trial 0 (BiasedRandomWalk.cpp:60-66, 76-78), and the
+        // trial cap keeps the last candidate
+        const uint32_t my = trial + static_cast<uint32_t>(k);
         const bool test = l > 0 && deg > 1;
         float r = 0.0f;
         int32_t e = b;
         if (l == 0 || deg > 1) {
             float u0;
-            n2v_uniforms(a.w.walk_base + n, static_cast<int32_t>(l), trial, a.key0, a.key1, u0, r);
+            n2v_uniforms(a.w.walk_base + n, static_cast<int32_t>(l), my, a.key0, a.key1, u0, r);
             e = b + static_cast<int32_t>(pick_index(u0, deg));
         }
-        const int32_t x = cl[e];
-        const int32_t bx = x >= 0 ? rp[x] : -1, ex = x >= 0 ? rp[x + 1] : -1;
-        if (x < 0 || bx < 0 || ex < bx) {
-            status |= x < 0 ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
-            finish();
-            continue;
-        }
-        if (test) {
+        int32_t x = cl[e];
+        int32_t bx = x >= 0 ? rp[x] : -1, ex = x >= 0 ? rp[x + 1] : -1;
+        // 0: rejected, 1: accepted, else the status bit of a malformed entry
+        uint32_t outcome = 1;
+        if (x < 0) {
+            outcome = MLXC_STATUS_BAD_NODE | 4u;
+        } else if (bx < 0 || ex < bx) {
+            outcome = MLXC_STATUS_BAD_ROW | 4u;
+        } else if (test) {
             int d = n2v_decide<kRule>(a, r, x, t);
             if (d < 0) {  // is t in row(x)?
                 bool adjacent = false;
@@ -898,14 +917,33 @@ __global__ __launch_bounds__(kLdsBlock) void node2vec_lds_kernel(N2VRecArgs a) {
                 }
                 d = n2v_resolve<kRule>(a, r, adjacent) ? 1 : 0;
             }
-            if (d != 1 && trial + 1 < MLXC_MAX_TRIALS) {  // (the cap keeps the last candidate)
-                ++trial;
-                continue;
-            }
+            outcome = d == 1 || my == MLXC_MAX_TRIALS - 1 ? 1u : 0u;
+        }
+        // the group's first trial that does not reject (the group's lanes
+        // reach this point together: their control flow up to here depends
+        // on the walk's state alone, apart from the search above)
+        const uint32_t decided =
+            static_cast<uint32_t>(__ballot(outcome != 0) >> base) & group_bits;
+        if (decided == 0) {
+            trial += static_cast<uint32_t>(G);
+            continue;
+        }
+        const int src = base + __builtin_ctz(decided);
+        outcome = __shfl(outcome, src, kWave);
+        x = __shfl(x, src, kWave);
+        e = __shfl(e, src, kWave);
+        bx = __shfl(bx, src, kWave);
+        ex = __shfl(ex, src, kWave);
+        if (outcome != 1) {
+            status |= outcome & 3u;
+            finish();
+            continue;
         }
         // the step to x, whose row the trial has read and checked
-        row[l + 1] = static_cast<OutT>(x);
-        if (kEdges) erow[l] = static_cast<OutT>(e);
+        if (k == 0) {
+            row[l + 1] = static_cast<OutT>(x);
+            if (kEdges) erow[l] = static_cast<OutT>(e);
+        }
         t = v;
         v = x;
         l += 1;
@@ -946,6 +984,12 @@ int dispatch_n2v(const N2VArgs& a, bool edges, hipStream_t stream) {
 // 16.61.  The reference-chain walk at configuration 3 spends more of each
 // iteration in VALU work (more waves then contend), the analytic walk at 5x
 // more of it waiting on reads (more waves hide them).
+// Most lanes one walk of the node2vec LDS walk runs on (a power of two, at
+// most 32): each tries one trial of the walk's step per round.
+#ifndef MLXC_LDS_MAX_GROUP
+#define MLXC_LDS_MAX_GROUP 16
+#endif
+
 #ifndef MLXC_N2V_BLOCKS_PER_CU
 #define MLXC_N2V_BLOCKS_PER_CU 4
 #endif
@@ -1227,20 +1271,27 @@ int launch_node2vec_typed(const WalkArgs& w, const N2VParams& p, void* workspace
         a.key0 = p.key0;
         a.key1 = p.key1;
         // Every block copies the graph with all its threads, then walks with
-        // lds_walkers of them: at most one block per compute unit, and down
-        // to one wavefront per SIMD (256 walkers) while the walks allow, since
+        // some of them: at most one block per compute unit, and down to one
+        // wavefront per SIMD (256 walking lanes) while the walks allow, since
         // the walk of a trial is bound by its own instruction latency (a
         // Philox draw per trial) once a SIMD has no other wavefront to run.
+        // Each walk gets as many lanes (up to MLXC_LDS_MAX_GROUP) as keep its
+        // call within one wavefront per SIMD of the device.
         DeviceInfo info;
         if (int rc = device_info(info)) return rc;
         const int64_t N = w.num_walks;  // 1 .. kLdsWalkSteps (lds_walk_fits)
-        int64_t blocks = (N + kLdsMinWalkers - 1) / kLdsMinWalkers;
+        int G = 1;
+        while (G < MLXC_LDS_MAX_GROUP && N * G * 2 <= static_cast<int64_t>(info.cus) * kLdsMinWalkers)
+            G *= 2;
+        const int64_t lanes = N * G;
+        int64_t blocks = (lanes + kLdsMinWalkers - 1) / kLdsMinWalkers;
         if (blocks > info.cus) blocks = info.cus;
         if (blocks < 1) blocks = 1;
-        int64_t walkers = (N + blocks - 1) / blocks;
-        walkers = (walkers + kWave - 1) / kWave * kWave;
-        a.lds_walkers = static_cast<int32_t>(walkers < kLdsMinWalkers ? kLdsMinWalkers
-                                             : walkers > kLdsBlock ? kLdsBlock : walkers);
+        int64_t threads = (lanes + blocks - 1) / blocks;
+        threads = (threads + kWave - 1) / kWave * kWave;
+        threads = threads < kLdsMinWalkers ? kLdsMinWalkers : threads > kLdsBlock ? kLdsBlock : threads;
+        a.lds_group = G;
+        a.lds_walkers = static_cast<int32_t>(threads / G);
         const dim3 grid(static_cast<unsigned>(blocks));
         const dim3 block(kLdsBlock);
         const bool edges = w.e_out != nullptr;
