@@ -414,6 +414,22 @@ int mlxc_rejection_sampling_cpu(const int64_t* rowptr, int64_t num_nodes,
                                 int32_t threads, int64_t* status);
 
 /*
+ * Publishes a call's status word to host memory without a device-to-host
+ * copy: enqueues on `stream` a one-thread kernel that stores workspace word 0
+ * (the MLXC_STATUS_* bits of the walk call enqueued before it on the same
+ * stream and workspace) into h_status[1], then 1 into h_status[0], both as
+ * system-scope stores.  Once h_status[0] reads 1 on the host (an acquire
+ * load), h_status[1] holds the bits and the walk call has completed.  The
+ * caller sets h_status[0] to 0 before the call and owns h_status: host
+ * memory of at least 16 bytes, 8-byte aligned, that the device can write
+ * (hipHostMalloc with hipHostMallocCoherent).  For callers that wait for each
+ * call's status (a validated call of a few microseconds, where a copy of the
+ * word back to the host costs more than the walk).  No reference
+ * counterpart.
+ */
+int mlxc_publish_status(const void* d_workspace, int64_t* h_status, void* stream);
+
+/*
  * Measurement hook: times the walk kernel alone, without the preparation
  * launches before it (a call's last launch is its walk kernel).  After
  * mlxc_set_walk_events(start_event, stop_event), with two hipEvent_t handles

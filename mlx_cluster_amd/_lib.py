@@ -101,6 +101,7 @@ SIGNATURES = {
         [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i32, _u64, _i64, _ptr, _ptr, _i32, _i32, _ptr],
     ),
     "mlxc_set_walk_events": (ctypes.c_int, [_ptr, _ptr]),
+    "mlxc_publish_status": (ctypes.c_int, [_ptr, _ptr, _ptr]),
     "mlxc_gather_probe": (
         ctypes.c_int, [_ptr, _i64, _i32, _i32, _i32, _i32, _i64, _u64, _ptr, _ptr, _ptr],
     ),

@@ -224,6 +224,16 @@ HostWalk host_walk(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                     static_cast<uint32_t>(seed >> 32), first_walk};
 }
 
+// The status word of a call (workspace word 0) into host memory, then the
+// flag that it is there: system-scope stores, the flag's with release order.
+__global__ void publish_status_kernel(const int64_t* work, int64_t* h_status) {
+    if (threadIdx.x == 0) {
+        const int64_t bits = work[0];
+        __hip_atomic_store(h_status + 1, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(h_status, int64_t{1}, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 }  // namespace
 }  // namespace mlxc
 
@@ -234,6 +244,23 @@ extern "C" {
 int mlxc_version(void) { return 301; }
 
 const char* mlxc_last_error(void) { return g_last_error.c_str(); }
+
+int mlxc_publish_status(const void* d_workspace, int64_t* h_status, void* stream) {
+    if (int rc = check_workspace(d_workspace, MLXC_WORK_WORDS * sizeof(int64_t))) return rc;
+    if (!h_status || reinterpret_cast<uintptr_t>(h_status) % 8 != 0)
+        return fail(MLXC_ERR_INVALID_ARGUMENT, "h_status must be 8-byte aligned host memory");
+    int64_t* d_status = nullptr;  // the device's address of the host words
+    if (hipHostGetDevicePointer(reinterpret_cast<void**>(&d_status), h_status, 0) != hipSuccess) {
+        (void)hipGetLastError();  // not left for the next call's launch check
+        return fail(MLXC_ERR_INVALID_ARGUMENT,
+                    "h_status is not host memory the device can write (hipHostMalloc)");
+    }
+    hipLaunchKernelGGL(publish_status_kernel, dim3(1), dim3(kWave), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const int64_t*>(d_workspace),
+                       d_status);
+    MLXC_HIP_TRY(hipGetLastError());
+    return MLXC_OK;
+}
 
 int mlxc_set_walk_events(void* start_event, void* stop_event) {
     if ((start_event == nullptr) != (stop_event == nullptr))

@@ -123,6 +123,16 @@ def test_other_entry_points_reject_bad_arguments():
         == _lib.MLXC_ERR_INVALID_ARGUMENT
 
 
+def test_publish_status_checks_its_pointers():
+    lib = _lib.load()
+    assert lib.mlxc_publish_status(None, FAKE, None) == _lib.MLXC_ERR_INVALID_ARGUMENT
+    assert "workspace" in _lib.last_error()
+    assert lib.mlxc_publish_status(FAKE, None, None) == _lib.MLXC_ERR_INVALID_ARGUMENT
+    assert lib.mlxc_publish_status(FAKE, ctypes.c_void_p(0x1004), None) \
+        == _lib.MLXC_ERR_INVALID_ARGUMENT
+    assert "h_status" in _lib.last_error()
+
+
 def test_walk_events_are_set_in_pairs():
     lib = _lib.load()
     assert lib.mlxc_set_walk_events(FAKE, None) == _lib.MLXC_ERR_INVALID_ARGUMENT

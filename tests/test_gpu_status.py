@@ -6,6 +6,9 @@ report the hand-derived bits.  node2vec validates the whole CSR on every
 call, so its bits depend neither on the path nor on the seed; the uniform
 walk reports what its walks read.
 """
+import ctypes
+import time
+
 import numpy as np
 import pytest
 import torch
@@ -103,3 +106,45 @@ def test_uniform_status_same_on_every_path(case, cuda):
         got["host"] = sc.host_uniform_status(lib, rowptr, col, start, L,
                                              seed=5 if seeded else None)
         assert all(v == want for v in got.values()), (name, seeded, got)
+
+
+@pytest.mark.parametrize("case", sc.UNI_CASES, ids=[c[0] for c in sc.UNI_CASES])
+def test_published_status_is_the_workspace_word(case, cuda):
+    """mlxc_publish_status stores the call's status word into host memory and
+    then its flag: the word equals workspace word 0 read back by a copy, and
+    the compiled binding's check (which waits on those host words) raises
+    exactly when it is non-zero."""
+    name, rowptr, col, start, L, want = case
+    lib = _lib.load()
+    hip = ctypes.CDLL("libamdhip64.so")  # the HIP runtime torch has loaded
+    words = ctypes.c_void_p()
+    flags = 0x40000000 | 0x2 | 0x1  # hipHostMallocCoherent | Mapped | Portable
+    assert hip.hipHostMalloc(ctypes.byref(words), ctypes.c_size_t(16), ctypes.c_uint(flags)) == 0
+    try:
+        h = (ctypes.c_int64 * 2).from_address(words.value)
+        start = np.resize(np.asarray(start, np.int64), 16)
+        r, c, s = _t(rowptr, cuda), _t(col, cuda), _t(start, cuda)
+        V, E, N = r.numel() - 1, c.numel(), s.numel()
+        nbytes = 256 + 16 * (E + N)
+        ws = torch.full(((nbytes + 7) // 8,), -1, dtype=torch.int64, device=cuda)
+        n = torch.empty((N, L + 1), dtype=torch.int64, device=cuda)
+        stream = torch.cuda.current_stream().cuda_stream
+        for _ in range(2):  # the second time over the first call's host words
+            h[0], h[1] = 0, -1
+            rc = lib.mlxc_random_walk_seeded(r.data_ptr(), V, c.data_ptr(), E, s.data_ptr(), N, L,
+                                             5, 0, n.data_ptr(), None, _lib.MLXC_OUT_INT64,
+                                             ws.data_ptr(), nbytes, stream)
+            assert rc == 0, _lib.last_error()
+            assert lib.mlxc_publish_status(ws.data_ptr(), words, stream) == 0, _lib.last_error()
+            deadline = time.monotonic() + 30
+            while h[0] == 0:
+                assert time.monotonic() < deadline, "the status was not published"
+            assert h[1] == int(ws[0].item()) == want, (name, h[1], want)
+    finally:
+        torch.cuda.synchronize()
+        hip.hipHostFree(words)
+    if want:
+        with pytest.raises(ValueError):
+            mc.random_walk(r, c, s, None, L, seed=5)
+    else:
+        mc.random_walk(r, c, s, None, L, seed=5)
