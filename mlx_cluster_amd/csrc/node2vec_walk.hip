@@ -405,6 +405,254 @@ __device__ __forceinline__ bool n2v_resolve(const N2VRecArgs& a, float r, bool a
     return adjacent ? lt1 : lt2;
 }
 
+// Walks a wavefront of the record walk still holds when the queue has run
+// dry and at most this many remain (0: no tail phase): the wavefront then
+// finishes them in n2v_tail.  Measured on MI355X at configuration 3 (walk
+// kernel): 8.72 ms without the tail phase, 8.68 / 8.62 / 8.55 ms with 8 / 16
+// / 32; configuration 5x (about one trial per step) unchanged.
+#ifndef MLXC_N2V_TAIL_WALKS
+#define MLXC_N2V_TAIL_WALKS 32
+#endif
+constexpr int kTailWalks = MLXC_N2V_TAIL_WALKS;
+static_assert(kTailWalks <= kWave / 2, "a tail walk gets two lanes at least");
+constexpr int kTailWords = 13;  // one walk's state in the tail table (below)
+static_assert(kTailWalks * kTailWords <= kWave * 8, "the table lives in the wave's staging area");
+
+// Stores, by this lane alone, what a window holds for the output: the block
+// and the run deferred to ow_drain, and the entries it buffers, the newest
+// of which belongs at last.  (Static indices keep the window in registers.)
+template <typename OutT, typename T>
+__device__ __forceinline__ void tail_flush(const OutWin<T>& o, OutT* last) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (o.blk != nullptr && i >= 8 - o.blk_n) static_cast<OutT*>(o.blk)[i] = static_cast<OutT>(o.w[i]);
+        if (i >= 8 - o.count) last[i - 7] = static_cast<OutT>(o.w[i]);
+    }
+    for (int32_t j = 0; j < o.run_n; ++j) static_cast<OutT*>(o.run)[j] = static_cast<OutT>(o.run_val);
+}
+
+// Whether t is in row(x) (or, on a graph declared symmetric, x in row(t)),
+// answered the way the record walk's search phases answer it: a hub bitmap,
+// a row hash table, a scan of an unsorted row or a bisection of a sorted
+// one, here as a chain of dependent reads of this lane.
+__device__ __forceinline__ bool n2v_tail_adjacent(const N2VRecArgs& a, bool sorted, int32_t x,
+                                                  int32_t bx, int32_t dx, int32_t sx, int32_t t,
+                                                  int32_t bt, int32_t dt, int32_t s_t) {
+    int32_t lo, hi, tgt;
+    n2v_search_rows(a.symmetric, x, bx, dx, t, bt, dt, lo, hi, tgt);
+    const bool one_block = ((lo ^ (hi - 1)) >> 4) == 0;
+    if (!one_block && (sx >= 0 || (a.symmetric && s_t >= 0))) {
+        const int32_t blk = sx >= 0 ? sx : s_t;
+        const int32_t bit = sx >= 0 ? t : x;
+        const uint32_t word = a.hub_bits[static_cast<int64_t>(blk) * a.hub_words + (bit >> 5)];
+        return ((word >> (bit & 31)) & 1u) != 0;
+    }
+    const int32_t* col32 = a.index.level[0];
+    if (!one_block && a.hash && hi - lo < kHashMaxDegree) {
+        const int32_t nb = hash_buckets(hi - lo);
+        const int64_t region = hash_region(lo, tgt == t ? x : t);
+        int32_t b = hash_bucket(tgt, nb);
+        for (int32_t i = 0; i < nb; ++i) {
+            const int32_t* bucket = a.hash + static_cast<int64_t>(kSearchBlock) * (region + b);
+            bool found = false, open = false;
+#pragma unroll
+            for (int j = 0; j < kSearchBlock; ++j) {
+                found |= bucket[j] == tgt;
+                open |= bucket[j] < 0;
+            }
+            if (found) return true;
+            if (open) return false;
+            b = b + 1 == nb ? 0 : b + 1;
+        }
+        return false;
+    }
+    if (!sorted) {
+        for (int32_t i = lo; i < hi; ++i)
+            if (col32[i] == tgt) return true;
+        return false;
+    }
+    int32_t count = hi - lo;
+    while (count > 0) {  // lower_bound
+        const int32_t half = count >> 1;
+        if (col32[lo + half] < tgt) {
+            lo += half + 1;
+            count -= half + 1;
+        } else {
+            count = half;
+        }
+    }
+    return lo < hi && col32[lo] == tgt;
+}
+
+// The end of a record-walk call, for one wavefront: the walks left in its
+// table (kTailWords words each: walk id (2 words), steps taken, trial, t and
+// its row and hub slot, v and its row and hub slot, and whether the walk
+// has not started).  Each walk runs on a group of G lanes, G as large as
+// the walks left allow, which try trials trial .. trial + G - 1 of its step
+// at once; the step takes the first of them, in trial order, that accepts
+// or meets a malformed record, as one lane trying them in turn would have
+// stopped there.  The draws are keyed by (walk, step, trial) and the
+// neighbour test has one answer whatever reads it, so the walks are the same
+// as in the main loop.  When a walk ends the others are regrouped.  Without
+// this phase a call's last walks run one lane each while the device is
+// nearly idle: the call's tail is the longest of them.
+template <int kRule, bool kEdges, typename OutT>
+__device__ void n2v_tail(const N2VRecArgs& a, int32_t* tab, int live, bool sorted,
+                         uint32_t& status) {
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    OutT* const nout = static_cast<OutT*>(a.w.n_out);
+    OutT* const eout = static_cast<OutT*>(a.w.e_out);
+    const int64_t L = a.w.walk_length;
+    const int lane = __lane_id();
+    while (live > 0) {  // wave-uniform
+        int G = 2;
+        while (2 * G * live <= kWave) G *= 2;
+        const int w = lane / G, k = lane % G, base = lane & ~(G - 1);
+        const uint64_t group_bits = G == kWave ? ~0ull : (1ull << G) - 1;
+        const bool act = w < live;
+        int64_t n = 0;
+        int32_t l = 0, t = 0, bt = 0, dt = 0, s_t = -1, v = 0, bv = 0, dv = 0, sv = -1;
+        uint32_t trial = 0;
+        bool fresh = false;
+        if (act) {
+            const int32_t* rec = tab + w * kTailWords;
+            n = static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(rec[1])) << 32) |
+                                     static_cast<uint32_t>(rec[0]));
+            l = rec[2];
+            trial = static_cast<uint32_t>(rec[3]);
+            t = rec[4];
+            bt = rec[5];
+            dt = rec[6];
+            s_t = rec[7];
+            v = rec[8];
+            bv = rec[9];
+            dv = rec[10];
+            sv = rec[11];
+            fresh = rec[12] != 0;
+        }
+        wave_sync();
+        const int64_t g0 = n * (L + 1), e0 = n * L;
+        bool fin = false;
+        // the rest of the walk's row stays at v from entry l + 1 on (edges -1)
+        auto fill = [&]() {
+            for (int64_t j = l + 1 + k; j <= L; j += G) nout[g0 + j] = static_cast<OutT>(v);
+            if (kEdges)
+                for (int64_t j = l + k; j < L; j += G) eout[e0 + j] = static_cast<OutT>(-1);
+            fin = true;
+        };
+        if (act && fresh) {
+            const i32x4 r0 = *reinterpret_cast<const i32x4*>(a.init + n);
+            v = r0.x;
+            if (k == 0) nout[g0] = static_cast<OutT>(v);
+            l = 0;
+            trial = 0;
+            if (r0.z < 0) {
+                status |= r0.z == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
+                fill();
+            } else if (L == 0) {
+                fin = true;
+            } else if (r0.z == 0) {
+                fill();  // absorbing start node
+            } else {
+                bv = r0.y;
+                dv = r0.z;
+                sv = r0.w;
+            }
+        }
+        while (!__any(act && fin)) {  // rounds until a walk ends
+            // trial `trial + k` of step l from v: 0 rejected, 1 accepted, else
+            // 4 | the status bit of a malformed record
+            const uint32_t my = trial + static_cast<uint32_t>(k);
+            int32_t e = bv, x = 0, bx = 0, dx = 0, sx = -1;
+            uint32_t outcome = 0;
+            if (act) {
+                float r = 0.0f;
+                if (dv != 1) {  // (a forced step takes its only edge)
+                    float u0;
+                    n2v_uniforms(a.w.walk_base + n, l, my, a.key0, a.key1, u0, r);
+                    e = bv + static_cast<int32_t>(pick_index(u0, dv));
+                }
+                const i32x4 rec = *reinterpret_cast<const i32x4*>(a.recs + e);
+                x = rec.x;
+                bx = rec.y;
+                dx = rec.z;
+                sx = rec.w;
+                if (dx < 0) {
+                    outcome = 4u | (dx == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW);
+                } else if (l == 0 || dv == 1) {
+                    outcome = 1;  // first step, or a forced step (BiasedRandomWalk.cpp:60-66, 76-78)
+                } else {
+                    int d = n2v_decide<kRule>(a, r, x, t);
+                    if (d < 0)
+                        d = n2v_resolve<kRule>(
+                                a, r, dx > 0 && n2v_tail_adjacent(a, sorted, x, bx, dx, sx, t, bt, dt, s_t))
+                                ? 1
+                                : 0;
+                    // the trial cap keeps the last candidate
+                    outcome = d == 1 || my == MLXC_MAX_TRIALS - 1 ? 1u : 0u;
+                }
+            }
+            const uint64_t decided = (__ballot(outcome != 0) >> base) & group_bits;
+            if (!act) continue;
+            if (decided == 0) {
+                trial += static_cast<uint32_t>(G);
+                continue;
+            }
+            const int src = base + __builtin_ctzll(decided);
+            outcome = __shfl(outcome, src, kWave);
+            x = __shfl(x, src, kWave);
+            e = __shfl(e, src, kWave);
+            bx = __shfl(bx, src, kWave);
+            dx = __shfl(dx, src, kWave);
+            sx = __shfl(sx, src, kWave);
+            if (outcome != 1) {
+                status |= outcome & 3u;
+                fill();
+                continue;
+            }
+            if (k == 0) {
+                nout[g0 + l + 1] = static_cast<OutT>(x);
+                if (kEdges) eout[e0 + l] = static_cast<OutT>(e);
+            }
+            l += 1;
+            t = v;
+            bt = bv;
+            dt = dv;
+            s_t = sv;
+            v = x;
+            bv = bx;
+            dv = dx;
+            sv = sx;
+            trial = 0;
+            if (l == L) {
+                fin = true;
+            } else if (dv == 0) {
+                fill();
+            }
+        }
+        // the walks that go on, back into the table in order
+        const uint64_t keep = __ballot(act && !fin && k == 0);
+        if (act && !fin && k == 0) {
+            int32_t* rec = tab + lane_rank(keep) * kTailWords;
+            rec[0] = static_cast<int32_t>(static_cast<uint32_t>(n));
+            rec[1] = static_cast<int32_t>(static_cast<uint32_t>(static_cast<uint64_t>(n) >> 32));
+            rec[2] = l;
+            rec[3] = static_cast<int32_t>(trial);
+            rec[4] = t;
+            rec[5] = bt;
+            rec[6] = dt;
+            rec[7] = s_t;
+            rec[8] = v;
+            rec[9] = bv;
+            rec[10] = dv;
+            rec[11] = sv;
+            rec[12] = 0;
+        }
+        wave_sync();
+        live = __popcll(keep);
+    }
+}
+
 // node2vec walk over edge records (num_nodes, num_edges below 2^31; n_out and
 // e_out 16-byte aligned).  One walk per lane slot from the wave queue.  Every
 // iteration a live slot issues one dependent read: its start record or its
@@ -461,6 +709,8 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     __shared__ WaveStage stage[kBlock / kWave];
     WaveStage& st = stage[threadIdx.x / kWave];
     uint32_t status = 0;
+    bool drained = false;  // the queue has run dry (wave-uniform)
+    bool tail = false;     // the wavefront's last walks go to n2v_tail
 
     while (true) {
         // 1. This iteration's read: 16 bytes (a record, the aligned 16 bytes
@@ -521,231 +771,273 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             phase = id < N ? kN2vStart : kN2vDone;
         }
         if (!__any(phase != kN2vDone)) break;
+        if (!kCsr && kTailWalks > 0) drained = drained || __any(phase == kN2vDone);
         wait_vmem();
-        if (ph == kN2vIdle || ph == kN2vDone) continue;
-        const i32x4 rec = qb[0];
+        if (ph != kN2vIdle && ph != kN2vDone) {
+            const i32x4 rec = qb[0];
 
-        // 3. Consume.
-        bool push = false, fill = false, flush = false, accept = false, next_trial = false;
-        bool draw = false;  // draw trial `trial` of step l from v's row (bv, dv)
-        int64_t g = g0 + l;  // output index of the last buffered entry
-        if (ph == kN2vStart) {
-            ow.count = 0;
-            ew.count = 0;
-            v = rec.x;
-            sv = kCsr ? -1 : rec.w;
-            push = true;
-            if (rec.z < 0) {
-                status |= rec.z == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
-                fill = true;
-            } else if (L == 0) {
-                flush = true;
-            } else if (rec.z == 0) {
-                fill = true;  // absorbing start node
-            } else {
-                // first step: uniform, no acceptance test (BiasedRandomWalk.cpp:60-66)
-                bv = rec.y;
-                dv = rec.z;
-                trial = 0;
-                draw = true;
-                phase = kN2vCand;
-            }
-        } else if (kCsr && ph == kN2vCand) {
-            const int k = e & 3;
-            x = k == 0 ? rec.x : k == 1 ? rec.y : k == 2 ? rec.z : rec.w;
-            int d = 1;  // first step and forced steps accept
-            if (!(l == 0 || dv == 1)) d = n2v_decide<kRule>(a, r, x, t);
-            if (static_cast<uint32_t>(x) >= static_cast<uint32_t>(a.w.num_nodes)) {
-                status |= MLXC_STATUS_BAD_NODE;  // (col32 holds -1 for any bad col)
-                fill = true;
-            } else if (d == 0) {
-                next_trial = true;
-            } else if (d == 1 && x == t && l > 0) {
-                accept = true;  // back to t: its row is known
-                bx = bt;
-                dx = dt;
-            } else {
-                row_then = d == 1 ? kRowAccept : kRowSearch;
-                phase = kN2vRow;
-            }
-        } else if (kCsr && ph == kN2vRow) {
-            // row32[x] and row32[x + 1] (-1 marks an entry outside [0, num_edges])
-            const bool ok = rec.x >= 0 && rec.y >= rec.x;
-            bx = rec.x;
-            dx = rec.y - rec.x;
-            if (!ok) {
-                status |= MLXC_STATUS_BAD_ROW;
-                fill = true;
-            } else if (row_then == kRowAccept) {
-                accept = true;
-            } else if (dx == 0) {
-                accept = n2v_resolve<kRule>(a, r, false);
-                next_trial = !accept;
-            } else {
-                n2v_search_rows(a.symmetric, x, bx, dx, t, bt, dt, lo, hi, tgt);
-                if (!sorted) {
-                    phase = kN2vScan;
+            // 3. Consume.
+            bool push = false, fill = false, flush = false, accept = false, next_trial = false;
+            bool draw = false;  // draw trial `trial` of step l from v's row (bv, dv)
+            int64_t g = g0 + l;  // output index of the last buffered entry
+            if (ph == kN2vStart) {
+                ow.count = 0;
+                ew.count = 0;
+                v = rec.x;
+                sv = kCsr ? -1 : rec.w;
+                push = true;
+                if (rec.z < 0) {
+                    status |= rec.z == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
+                    fill = true;
+                } else if (L == 0) {
+                    flush = true;
+                } else if (rec.z == 0) {
+                    fill = true;  // absorbing start node
                 } else {
-                    const uint32_t diff = static_cast<uint32_t>(lo) ^ static_cast<uint32_t>(hi - 1);
-                    lvl = diff ? (31 - __builtin_clz(diff)) >> 2 : 0;
-                    blk = static_cast<int32_t>(static_cast<int64_t>(lo) >> (4 * (lvl + 1)));
-                    phase = kN2vLevel;
+                    // first step: uniform, no acceptance test (BiasedRandomWalk.cpp:60-66)
+                    bv = rec.y;
+                    dv = rec.z;
+                    trial = 0;
+                    draw = true;
+                    phase = kN2vCand;
                 }
-            }
-        } else if (ph == kN2vCand) {
-            x = rec.x;
-            bx = rec.y;
-            dx = rec.z;
-            sx = rec.w;
-            if (dx < 0) {
-                status |= dx == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
-                fill = true;
-            } else if (l == 0 || dv == 1) {
-                accept = true;  // first step, or a forced step (BiasedRandomWalk.cpp:76-78)
-            } else {
-                const int d = n2v_decide<kRule>(a, r, x, t);
-                if (d == 1) {
-                    accept = true;
+            } else if (kCsr && ph == kN2vCand) {
+                const int k = e & 3;
+                x = k == 0 ? rec.x : k == 1 ? rec.y : k == 2 ? rec.z : rec.w;
+                int d = 1;  // first step and forced steps accept
+                if (!(l == 0 || dv == 1)) d = n2v_decide<kRule>(a, r, x, t);
+                if (static_cast<uint32_t>(x) >= static_cast<uint32_t>(a.w.num_nodes)) {
+                    status |= MLXC_STATUS_BAD_NODE;  // (col32 holds -1 for any bad col)
+                    fill = true;
                 } else if (d == 0) {
                     next_trial = true;
+                } else if (d == 1 && x == t && l > 0) {
+                    accept = true;  // back to t: its row is known
+                    bx = bt;
+                    dx = dt;
+                } else {
+                    row_then = d == 1 ? kRowAccept : kRowSearch;
+                    phase = kN2vRow;
+                }
+            } else if (kCsr && ph == kN2vRow) {
+                // row32[x] and row32[x + 1] (-1 marks an entry outside [0, num_edges])
+                const bool ok = rec.x >= 0 && rec.y >= rec.x;
+                bx = rec.x;
+                dx = rec.y - rec.x;
+                if (!ok) {
+                    status |= MLXC_STATUS_BAD_ROW;
+                    fill = true;
+                } else if (row_then == kRowAccept) {
+                    accept = true;
                 } else if (dx == 0) {
                     accept = n2v_resolve<kRule>(a, r, false);
                     next_trial = !accept;
                 } else {
                     n2v_search_rows(a.symmetric, x, bx, dx, t, bt, dt, lo, hi, tgt);
-                    // a row inside one aligned 16-entry block takes one read
-                    // either way; longer ones take the bitmap's single read
-                    const bool one_block = ((lo ^ (hi - 1)) >> 4) == 0;
-                    if (!one_block && sx >= 0) {
-                        blk = sx;  // bit t of row(x)'s bitmap
-                        tgt = t;
-                        phase = kN2vBit;
-                    } else if (!one_block && a.symmetric && s_t >= 0) {
-                        blk = s_t;  // bit x of row(t)'s bitmap: the same answer on a symmetric graph
-                        tgt = x;
-                        phase = kN2vBit;
-                    } else if (!one_block && a.hash && hi - lo < kHashMaxDegree) {
-                        // the row searched has no bitmap (it would have been
-                        // taken above) and a hash table: lo <- its first
-                        // bucket, hi <- its bucket count, blk <- tgt's bucket
-                        const int32_t node = tgt == t ? x : t;
-                        const int32_t nb = hash_buckets(hi - lo);
-                        lo = static_cast<int32_t>(hash_region(lo, node));
-                        hi = nb;
-                        blk = lo + hash_bucket(tgt, nb);
-                        lvl = 0;  // buckets read
-                        phase = kN2vHash;
-                    } else if (!sorted) {
+                    if (!sorted) {
                         phase = kN2vScan;
                     } else {
-                        // finest level whose aligned blocks (16^(lvl+1) positions)
-                        // hold the whole row in one
                         const uint32_t diff = static_cast<uint32_t>(lo) ^ static_cast<uint32_t>(hi - 1);
                         lvl = diff ? (31 - __builtin_clz(diff)) >> 2 : 0;
                         blk = static_cast<int32_t>(static_cast<int64_t>(lo) >> (4 * (lvl + 1)));
                         phase = kN2vLevel;
                     }
                 }
-            }
-        } else if (!kCsr && ph == kN2vBit) {
-            const uint32_t word = static_cast<uint32_t>(rec[(tgt >> 5) & 3]);
-            accept = n2v_resolve<kRule>(a, r, ((word >> (tgt & 31)) & 1u) != 0);
-            next_trial = !accept;
-        } else if (!kCsr && ph == kN2vHash) {
-            // tgt in the bucket: adjacent; an empty slot (-1): not adjacent;
-            // a full bucket without tgt: the next bucket of the table.  A
-            // table always has an empty slot; the bound on the buckets read
-            // only keeps a malformed CSR (rows that overlap, whose tables
-            // then overwrite each other) from looping.
-            bool found = false, open = false;
-#pragma unroll
-            for (int i = 0; i < kSearchBlock; ++i) {
-                const int32_t v16 = qb[i / 4][i % 4];
-                found |= v16 == tgt;
-                open |= v16 < 0;
-            }
-            lvl += 1;
-            if (found || open || lvl >= hi) {
-                accept = n2v_resolve<kRule>(a, r, found);
-                next_trial = !accept;
-            } else {
-                blk = blk + 1 == lo + hi ? lo : blk + 1;
-            }
-        } else {  // the neighbour search: is t in row(x)?
-            int32_t vals[kSearchBlock];
-#pragma unroll
-            for (int i = 0; i < kSearchBlock; ++i) vals[i] = qb[i / 4][i % 4];
-            const int res = ph == kN2vLevel ? level_step(vals, tgt, lvl, blk, lo, hi)
-                                            : scan_step(vals, tgt, lo, hi);
-            if (res >= 0) {
-                accept = n2v_resolve<kRule>(a, r, res == 1);
-                next_trial = !accept;
-            }
-        }
-        if (next_trial) {
-            trial += 1;
-            if (trial >= MLXC_MAX_TRIALS) {
-                // trial cap: keep the last candidate (CSR mode: read its row
-                // first, unless it is t)
-                if (!kCsr) {
-                    accept = true;
-                } else if (x == t) {
-                    accept = true;
-                    bx = bt;
-                    dx = dt;
+            } else if (ph == kN2vCand) {
+                x = rec.x;
+                bx = rec.y;
+                dx = rec.z;
+                sx = rec.w;
+                if (dx < 0) {
+                    status |= dx == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW;
+                    fill = true;
+                } else if (l == 0 || dv == 1) {
+                    accept = true;  // first step, or a forced step (BiasedRandomWalk.cpp:76-78)
                 } else {
-                    row_then = kRowAccept;
-                    phase = kN2vRow;
+                    const int d = n2v_decide<kRule>(a, r, x, t);
+                    if (d == 1) {
+                        accept = true;
+                    } else if (d == 0) {
+                        next_trial = true;
+                    } else if (dx == 0) {
+                        accept = n2v_resolve<kRule>(a, r, false);
+                        next_trial = !accept;
+                    } else {
+                        n2v_search_rows(a.symmetric, x, bx, dx, t, bt, dt, lo, hi, tgt);
+                        // a row inside one aligned 16-entry block takes one read
+                        // either way; longer ones take the bitmap's single read
+                        const bool one_block = ((lo ^ (hi - 1)) >> 4) == 0;
+                        if (!one_block && sx >= 0) {
+                            blk = sx;  // bit t of row(x)'s bitmap
+                            tgt = t;
+                            phase = kN2vBit;
+                        } else if (!one_block && a.symmetric && s_t >= 0) {
+                            blk = s_t;  // bit x of row(t)'s bitmap: the same answer on a symmetric graph
+                            tgt = x;
+                            phase = kN2vBit;
+                        } else if (!one_block && a.hash && hi - lo < kHashMaxDegree) {
+                            // the row searched has no bitmap (it would have been
+                            // taken above) and a hash table: lo <- its first
+                            // bucket, hi <- its bucket count, blk <- tgt's bucket
+                            const int32_t node = tgt == t ? x : t;
+                            const int32_t nb = hash_buckets(hi - lo);
+                            lo = static_cast<int32_t>(hash_region(lo, node));
+                            hi = nb;
+                            blk = lo + hash_bucket(tgt, nb);
+                            lvl = 0;  // buckets read
+                            phase = kN2vHash;
+                        } else if (!sorted) {
+                            phase = kN2vScan;
+                        } else {
+                            // finest level whose aligned blocks (16^(lvl+1) positions)
+                            // hold the whole row in one
+                            const uint32_t diff = static_cast<uint32_t>(lo) ^ static_cast<uint32_t>(hi - 1);
+                            lvl = diff ? (31 - __builtin_clz(diff)) >> 2 : 0;
+                            blk = static_cast<int32_t>(static_cast<int64_t>(lo) >> (4 * (lvl + 1)));
+                            phase = kN2vLevel;
+                        }
+                    }
                 }
-            } else {
-                draw = true;
-                phase = kN2vCand;
+            } else if (!kCsr && ph == kN2vBit) {
+                const uint32_t word = static_cast<uint32_t>(rec[(tgt >> 5) & 3]);
+                accept = n2v_resolve<kRule>(a, r, ((word >> (tgt & 31)) & 1u) != 0);
+                next_trial = !accept;
+            } else if (!kCsr && ph == kN2vHash) {
+                // tgt in the bucket: adjacent; an empty slot (-1): not adjacent;
+                // a full bucket without tgt: the next bucket of the table.  A
+                // table always has an empty slot; the bound on the buckets read
+                // only keeps a malformed CSR (rows that overlap, whose tables
+                // then overwrite each other) from looping.
+                bool found = false, open = false;
+    #pragma unroll
+                for (int i = 0; i < kSearchBlock; ++i) {
+                    const int32_t v16 = qb[i / 4][i % 4];
+                    found |= v16 == tgt;
+                    open |= v16 < 0;
+                }
+                lvl += 1;
+                if (found || open || lvl >= hi) {
+                    accept = n2v_resolve<kRule>(a, r, found);
+                    next_trial = !accept;
+                } else {
+                    blk = blk + 1 == lo + hi ? lo : blk + 1;
+                }
+            } else {  // the neighbour search: is t in row(x)?
+                int32_t vals[kSearchBlock];
+    #pragma unroll
+                for (int i = 0; i < kSearchBlock; ++i) vals[i] = qb[i / 4][i % 4];
+                const int res = ph == kN2vLevel ? level_step(vals, tgt, lvl, blk, lo, hi)
+                                                : scan_step(vals, tgt, lo, hi);
+                if (res >= 0) {
+                    accept = n2v_resolve<kRule>(a, r, res == 1);
+                    next_trial = !accept;
+                }
             }
-        }
-        if (accept) {
-            if (kEdges) ow_push(ew, eout, e0 + l, e);
-            push = true;
-            g += 1;
-            l += 1;
-            t = v;
-            bt = bv;
-            dt = dv;
-            s_t = sv;
-            v = x;
-            bv = bx;
-            dv = dx;
-            sv = sx;
-            if (l == L) {
-                flush = true;
-            } else if (dv == 0) {
-                fill = true;
-            } else {
-                trial = 0;
-                if (dv == 1)
-                    e = bv;  // forced: no draw
-                else
+            if (next_trial) {
+                trial += 1;
+                if (trial >= MLXC_MAX_TRIALS) {
+                    // trial cap: keep the last candidate (CSR mode: read its row
+                    // first, unless it is t)
+                    if (!kCsr) {
+                        accept = true;
+                    } else if (x == t) {
+                        accept = true;
+                        bx = bt;
+                        dx = dt;
+                    } else {
+                        row_then = kRowAccept;
+                        phase = kN2vRow;
+                    }
+                } else {
                     draw = true;
-                phase = kN2vCand;
+                    phase = kN2vCand;
+                }
             }
-        }
-        // The trial's candidate and r: one Philox call site for the three
-        // places that draw (a wavefront executes each site any lane needs).
-        if (draw) {
-            float u0;
-            n2v_uniforms(a.w.walk_base + n, l, trial, a.key0, a.key1, u0, r);
-            e = bv + static_cast<int32_t>(pick_index(u0, dv));
-        }
-        if (fill) {
-            ow_fill(ow, nout, push ? g : g + 1, g0 + L, v);  // v from g on
-            if (kEdges) ow_fill(ew, eout, e0 + l, e0 + L - 1, -1);  // l edges buffered
-        } else {
-            if (push) ow_push(ow, nout, g, v);
-            if (flush) {
-                if (ow.count) ow_flush(ow, nout, g);
-                if (kEdges && ew.count) ow_flush(ew, eout, e0 + L - 1);
+            if (accept) {
+                if (kEdges) ow_push(ew, eout, e0 + l, e);
+                push = true;
+                g += 1;
+                l += 1;
+                t = v;
+                bt = bv;
+                dt = dv;
+                s_t = sv;
+                v = x;
+                bv = bx;
+                dv = dx;
+                sv = sx;
+                if (l == L) {
+                    flush = true;
+                } else if (dv == 0) {
+                    fill = true;
+                } else {
+                    trial = 0;
+                    if (dv == 1)
+                        e = bv;  // forced: no draw
+                    else
+                        draw = true;
+                    phase = kN2vCand;
+                }
             }
+            // The trial's candidate and r: one Philox call site for the three
+            // places that draw (a wavefront executes each site any lane needs).
+            if (draw) {
+                float u0;
+                n2v_uniforms(a.w.walk_base + n, l, trial, a.key0, a.key1, u0, r);
+                e = bv + static_cast<int32_t>(pick_index(u0, dv));
+            }
+            if (fill) {
+                ow_fill(ow, nout, push ? g : g + 1, g0 + L, v);  // v from g on
+                if (kEdges) ow_fill(ew, eout, e0 + l, e0 + L - 1, -1);  // l edges buffered
+            } else {
+                if (push) ow_push(ow, nout, g, v);
+                if (flush) {
+                    if (ow.count) ow_flush(ow, nout, g);
+                    if (kEdges && ew.count) ow_flush(ew, eout, e0 + L - 1);
+                }
+            }
+            if (fill || flush) phase = kN2vIdle;
         }
-        if (fill || flush) phase = kN2vIdle;
+        // 4. Once the queue has run dry and at most kTailWalks walks are left
+        // to the wavefront (a lane whose walk just ended takes no other),
+        // n2v_tail finishes them.  (Checked here, where every lane has
+        // reconverged and no read is in flight: the register allocation of
+        // the loop then stays as it is without the tail.)
+        if (!kCsr && kTailWalks > 0 && drained &&
+            __popcll(__ballot(phase != kN2vDone && phase != kN2vIdle)) <= kTailWalks) {
+            tail = true;
+            break;
+        }
+    }
+    if (!kCsr && tail) {
+        // The stores this iteration deferred, and the entries the windows
+        // still hold (the walk's newest at g0 + l, its edges' at e0 + l - 1),
+        // stored here by each lane for itself.  A trial in progress is tried
+        // again from its draw in n2v_tail.
+        tail_flush<OutT>(ow, nout + g0 + l);
+        if (kEdges) tail_flush<OutT>(ew, eout + e0 + l - 1);
+        const bool live = phase != kN2vDone && phase != kN2vIdle;
+        const uint64_t mask = __ballot(live);
+        int32_t* tab = &st.vals[0][0];
+        wave_sync();
+        if (live) {
+            int32_t* rec = tab + lane_rank(mask) * kTailWords;
+            rec[0] = static_cast<int32_t>(static_cast<uint32_t>(n));
+            rec[1] = static_cast<int32_t>(static_cast<uint32_t>(static_cast<uint64_t>(n) >> 32));
+            rec[2] = l;
+            rec[3] = static_cast<int32_t>(trial);
+            rec[4] = t;
+            rec[5] = bt;
+            rec[6] = dt;
+            rec[7] = s_t;
+            rec[8] = v;
+            rec[9] = bv;
+            rec[10] = dv;
+            rec[11] = sv;
+            rec[12] = phase == kN2vStart;
+        }
+        wave_sync();
+        n2v_tail<kRule, kEdges, OutT>(a, tab, __popcll(mask), sorted, status);
     }
     if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.w.work), static_cast<unsigned long long>(status));
 }
