@@ -36,8 +36,10 @@ void raise_code(int rc, const char* what) {
     throw std::runtime_error(msg);
 }
 
-// The calling thread's two host words for mlxc_publish_status (allocated
-// once per thread and kept for the process; null if the allocation failed).
+// The calling thread's two host words for mlxc_publish_status: allocated at
+// the thread's first validated call (one pinned page) and kept for the rest
+// of the process, since freeing them at thread exit could run after the HIP
+// runtime has shut down; null if the allocation failed.
 int64_t* status_words() {
     thread_local int64_t* words = [] {
         void* p = nullptr;
