@@ -563,6 +563,31 @@ def test_lds_walk_many_walks(rule, cuda):
         np.testing.assert_array_equal(e.cpu().numpy(), e_ref)
 
 
+@pytest.mark.parametrize("N", [3000, 6000, 12000, 24000, 40000])
+def test_lds_walk_lane_groups(N, cuda):
+    """The LDS walk runs each walk on a group of lanes that try consecutive
+    trials of its step at once: on 256 compute units, 16 lanes up to 4,096
+    walks, then 8, 4 and 2 up to 8,192, 16,384 and 32,768, and one lane
+    beyond.  One call per group size, both rules, and with q = 30 too, where
+    most candidates away from t are rejected and steps take many rounds:
+    bit-exact against the oracle, nodes and edges."""
+    rng = np.random.default_rng(N)
+    V = 700
+    rowptr, col = undirected(V, rng.integers(0, V, (2500, 2)))
+    t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.int64)).to(cuda)
+    start = (np.arange(N) * 13) % V
+    L = 6
+    for rule in (oracle.RULE_REF_CHAIN, oracle.RULE_NODE2VEC_EXACT):
+        for p, q in ((0.5, 2.0), (1.0, 30.0)):
+            n_ref, e_ref, st, _ = oracle.node2vec_walk(rowptr, col, start, L, p, q, 5, rule=rule,
+                                                       rows_sorted=True, with_edges=True)
+            assert st == 0
+            n, e = mc.rejection_sampling(t(rowptr), t(col), t(start), L, p, q, seed=5,
+                                         rule=RULE_NAME[rule], return_edges=True)
+            np.testing.assert_array_equal(n.cpu().numpy(), n_ref, err_msg=f"{rule} {p} {q}")
+            np.testing.assert_array_equal(e.cpu().numpy(), e_ref, err_msg=f"{rule} {p} {q}")
+
+
 def test_lds_walks_random_sweep(cuda):
     """Random small graphs (directed and undirected, duplicates and
     self-loops kept) under the LDS limit, random walk counts and lengths:
