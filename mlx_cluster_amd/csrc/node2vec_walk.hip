@@ -661,7 +661,8 @@ __device__ void n2v_tail(const N2VRecArgs& a, int32_t* tab, int live, bool sorte
 // neighbour search; the read is unconditional (idle slots read the first
 // start record) and the wave waits once.  Sorted rows are searched through
 // the index levels (level_step); unsorted rows are scanned 16 entries per
-// read, as the reference scans them.
+// read, as the reference scans them.  In record mode a wavefront's last
+// walks (queue empty, at most kTailWalks left) finish in n2v_tail.
 //
 // kCsr (CSR mode, for calls with few steps per edge, where building a record
 // per edge costs more than it saves): a candidate is read as its col32 entry
