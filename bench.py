@@ -51,6 +51,10 @@ CONFIGS = {
             "symmetric-graph hint (the neighbour test searches the shorter row; same walks as c3)",
             "node2vec", dict(scale=20, samples=1 << 24, symmetrize=True), 4, 40,
             dict(p=0.5, q=2.0, seed=3, rule="ref_chain", symmetric=True)),
+    "c3b": ("node2vec p=0.5 q=2 on symmetrized R-MAT 2^20 (the graph of c3), 2,000 walks, "
+            "L=40: a call of few walks on a large graph, bound by the walks' chains of dependent "
+            "reads", "node2vec", dict(scale=20, samples=1 << 24, symmetrize=True), 1, 40,
+            dict(num_walks=2000, p=0.5, q=2.0, seed=3, rule="ref_chain")),
     "c4": ("R-MAT 2^24 uniform walk, 1 walk/node, L=20", "uniform",
            dict(scale=24, samples=1 << 28, symmetrize=False), 1, 20, {}),
     "c5": ("node2vec p=4 q=0.25 (reference chain) on BA 4M nodes m=20 + 64 hubs of 500K, "

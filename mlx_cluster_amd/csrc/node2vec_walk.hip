@@ -345,9 +345,12 @@ struct N2VRecArgs {
     // rows without a hub bitmap whose search would take more than one read.
     const int32_t* hash;
     // LDS walk: the walks a block runs at once (all its threads copy the
-    // graph), and the lanes that run each walk (1, 2, 4 or 8)
+    // graph), and the lanes that run each walk (1, 2, 4, 8 or 16)
     int32_t lds_walkers;
     int32_t lds_group;
+    // record walk: walks per wavefront of a call of few walks, which skips
+    // the queue and runs them all in the tail phase (0: the queue)
+    int32_t tail_direct;
 };
 
 // Smallest float >= p (p > 0), the float threshold of N2VRecArgs.
@@ -496,7 +499,7 @@ __device__ __forceinline__ bool n2v_tail_adjacent(const N2VRecArgs& a, bool sort
 // as in the main loop.  When a walk ends the others are regrouped.  Without
 // this phase a call's last walks run one lane each while the device is
 // nearly idle: the call's tail is the longest of them.
-template <int kRule, bool kEdges, typename OutT>
+template <int kRule, bool kEdges, bool kCsr, typename OutT>
 __device__ void n2v_tail(const N2VRecArgs& a, int32_t* tab, int live, bool sorted,
                          uint32_t& status) {
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -556,7 +559,7 @@ __device__ void n2v_tail(const N2VRecArgs& a, int32_t* tab, int live, bool sorte
             } else {
                 bv = r0.y;
                 dv = r0.z;
-                sv = r0.w;
+                sv = kCsr ? -1 : r0.w;
             }
         }
         while (!__any(act && fin)) {  // rounds until a walk ends
@@ -572,24 +575,56 @@ __device__ void n2v_tail(const N2VRecArgs& a, int32_t* tab, int live, bool sorte
                     n2v_uniforms(a.w.walk_base + n, l, my, a.key0, a.key1, u0, r);
                     e = bv + static_cast<int32_t>(pick_index(u0, dv));
                 }
-                const i32x4 rec = *reinterpret_cast<const i32x4*>(a.recs + e);
-                x = rec.x;
-                bx = rec.y;
-                dx = rec.z;
-                sx = rec.w;
-                if (dx < 0) {
-                    outcome = 4u | (dx == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW);
-                } else if (l == 0 || dv == 1) {
-                    outcome = 1;  // first step, or a forced step (BiasedRandomWalk.cpp:60-66, 76-78)
+                const bool cap = my == MLXC_MAX_TRIALS - 1;  // the cap keeps the last candidate
+                if (!kCsr) {
+                    const i32x4 rec = *reinterpret_cast<const i32x4*>(a.recs + e);
+                    x = rec.x;
+                    bx = rec.y;
+                    dx = rec.z;
+                    sx = rec.w;
+                    if (dx < 0) {
+                        outcome = 4u | (dx == kRecBadNode ? MLXC_STATUS_BAD_NODE : MLXC_STATUS_BAD_ROW);
+                    } else if (l == 0 || dv == 1) {
+                        outcome = 1;  // first step, or a forced step (BiasedRandomWalk.cpp:60-66, 76-78)
+                    } else {
+                        int d = n2v_decide<kRule>(a, r, x, t);
+                        if (d < 0)
+                            d = n2v_resolve<kRule>(a, r,
+                                                   dx > 0 && n2v_tail_adjacent(a, sorted, x, bx, dx, sx,
+                                                                               t, bt, dt, s_t))
+                                    ? 1
+                                    : 0;
+                        outcome = d == 1 || cap ? 1u : 0u;
+                    }
                 } else {
-                    int d = n2v_decide<kRule>(a, r, x, t);
-                    if (d < 0)
-                        d = n2v_resolve<kRule>(
-                                a, r, dx > 0 && n2v_tail_adjacent(a, sorted, x, bx, dx, sx, t, bt, dt, s_t))
-                                ? 1
-                                : 0;
-                    // the trial cap keeps the last candidate
-                    outcome = d == 1 || my == MLXC_MAX_TRIALS - 1 ? 1u : 0u;
+                    // CSR mode: the candidate's id from col32 (-1: a bad col
+                    // entry), its row from row32 when the step or the test
+                    // needs it, as the main loop reads them
+                    x = a.index.level[0][e];
+                    const int d = l == 0 || dv == 1 ? 1 : n2v_decide<kRule>(a, r, x, t);
+                    if (static_cast<uint32_t>(x) >= static_cast<uint32_t>(a.w.num_nodes)) {
+                        outcome = 4u | MLXC_STATUS_BAD_NODE;
+                    } else if (d == 0 && !cap) {
+                        outcome = 0;
+                    } else if (d != -1 && x == t && l > 0) {
+                        outcome = 1;  // back to t, whose row the walk keeps
+                        bx = bt;
+                        dx = dt;
+                    } else {
+                        typedef int32_t i32x2 __attribute__((ext_vector_type(2), aligned(4)));
+                        const i32x2 rr = *reinterpret_cast<const i32x2*>(a.row32 + x);
+                        bx = rr.x;
+                        dx = rr.y - rr.x;
+                        if (rr.x < 0 || rr.y < rr.x) {
+                            outcome = 4u | MLXC_STATUS_BAD_ROW;
+                        } else if (d != -1) {
+                            outcome = 1;
+                        } else {
+                            const bool acc = n2v_resolve<kRule>(
+                                a, r, dx > 0 && n2v_tail_adjacent(a, sorted, x, bx, dx, -1, t, bt, dt, -1));
+                            outcome = acc || cap ? 1u : 0u;
+                        }
+                    }
                 }
             }
             const uint64_t decided = (__ballot(outcome != 0) >> base) & group_bits;
@@ -710,6 +745,29 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
     __shared__ WaveStage stage[kBlock / kWave];
     WaveStage& st = stage[threadIdx.x / kWave];
     uint32_t status = 0;
+    if (kTailWalks > 0 && a.tail_direct > 0) {
+        // A call of few walks: wavefront k takes walks [k d, k d + d) with
+        // d = tail_direct and runs them in n2v_tail from their start, a
+        // group of lanes each; no queue.
+        const int64_t wave = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) / kWave;
+        const int64_t w0 = wave * a.tail_direct;
+        const int64_t left = N - w0;
+        const int cnt = left <= 0 ? 0 : left < a.tail_direct ? static_cast<int>(left) : a.tail_direct;
+        int32_t* tab = &st.vals[0][0];
+        const int lane = __lane_id();
+        if (lane < cnt) {
+            int32_t* rec = tab + lane * kTailWords;
+            const int64_t id = w0 + lane;
+            rec[0] = static_cast<int32_t>(static_cast<uint32_t>(id));
+            rec[1] = static_cast<int32_t>(static_cast<uint32_t>(static_cast<uint64_t>(id) >> 32));
+            for (int k = 2; k < kTailWords - 1; ++k) rec[k] = 0;
+            rec[kTailWords - 1] = 1;  // not started
+        }
+        wave_sync();
+        n2v_tail<kRule, kEdges, kCsr, OutT>(a, tab, cnt, sorted, status);
+        if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.w.work), static_cast<unsigned long long>(status));
+        return;
+    }
     bool drained = false;  // the queue has run dry (wave-uniform)
     bool tail = false;     // the wavefront's last walks go to n2v_tail
 
@@ -772,7 +830,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             phase = id < N ? kN2vStart : kN2vDone;
         }
         if (!__any(phase != kN2vDone)) break;
-        if (!kCsr && kTailWalks > 0) drained = drained || __any(phase == kN2vDone);
+        if (kTailWalks > 0) drained = drained || __any(phase == kN2vDone);
         wait_vmem();
         if (ph != kN2vIdle && ph != kN2vDone) {
             const i32x4 rec = qb[0];
@@ -1004,13 +1062,13 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
         // n2v_tail finishes them.  (Checked here, where every lane has
         // reconverged and no read is in flight: the register allocation of
         // the loop then stays as it is without the tail.)
-        if (!kCsr && kTailWalks > 0 && drained &&
+        if (kTailWalks > 0 && drained &&
             __popcll(__ballot(phase != kN2vDone && phase != kN2vIdle)) <= kTailWalks) {
             tail = true;
             break;
         }
     }
-    if (!kCsr && tail) {
+    if (tail) {
         // The stores this iteration deferred, and the entries the windows
         // still hold (the walk's newest at g0 + l, its edges' at e0 + l - 1),
         // stored here by each lane for itself.  A trial in progress is tried
@@ -1038,7 +1096,7 @@ __global__ __launch_bounds__(kBlock) void node2vec_rec_kernel(N2VRecArgs a) {
             rec[12] = phase == kN2vStart;
         }
         wave_sync();
-        n2v_tail<kRule, kEdges, OutT>(a, tab, __popcll(mask), sorted, status);
+        n2v_tail<kRule, kEdges, kCsr, OutT>(a, tab, __popcll(mask), sorted, status);
     }
     if (status) atomicOr(reinterpret_cast<unsigned long long*>(a.w.work), static_cast<unsigned long long>(status));
 }
@@ -1296,9 +1354,27 @@ int launch_n2v_rec(const N2VRecArgs& a, hipStream_t stream) {
     constexpr int per_cu = kRule == MLXC_RULE_REF_CHAIN ? MLXC_N2V_BLOCKS_PER_CU
                                                          : MLXC_N2V_ANALYTIC_BLOCKS_PER_CU;
     int grid = 0;
-    if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid, per_cu)) return rc;
+    N2VRecArgs b = a;
+    b.tail_direct = 0;
+    // A call whose walks fill at most half the device's wavefront slots at
+    // one per SIMD (256 lanes a CU) leaves lanes to spare: each walk then gets
+    // a group of G lanes (the largest power of two, at most 32, that keeps
+    // the call within those slots) in the tail phase, 64 / G walks to a
+    // wavefront, from the start.
+    DeviceInfo info;
+    if (int rc = device_info(info)) return rc;
+    const int64_t N = a.w.num_walks, slots = static_cast<int64_t>(info.cus) * 256;
+    if (kTailWalks > 0 && N > 0 && 2 * N <= slots) {
+        int G = 2;
+        while (G < 32 && 2 * G * N <= slots) G *= 2;
+        b.tail_direct = kWave / G;
+        const int64_t waves = (N + b.tail_direct - 1) / b.tail_direct;
+        grid = static_cast<int>((waves + kBlock / kWave - 1) / (kBlock / kWave));
+    } else if (int rc = persistent_grid(kernel, a.w.num_walks, 1, grid, per_cu)) {
+        return rc;
+    }
     if (int rc = record_walk_event(0, stream)) return rc;
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, a);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kBlock), 0, stream, b);
     MLXC_HIP_TRY(hipGetLastError());
     return record_walk_event(1, stream);
 }
