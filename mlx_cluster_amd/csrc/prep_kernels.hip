@@ -25,7 +25,7 @@ __device__ __forceinline__ uint32_t wave_or(uint32_t x) {
     return x;
 }
 
-// CSR validation, accumulated per thread and reduced per wave.  Rows are
+// CSR validation, accumulated per thread and reduced per block.  Rows are
 // sorted iff every position i >= 1 with col[i] < col[i-1] starts a non-empty
 // row, i.e. iff desc == start_desc.
 struct CsrCheck {
@@ -49,15 +49,32 @@ struct CsrCheck {
         if (!node_ok(c, V)) bad_col = true;
         if (i >= 1 && c < col[i - 1]) ++desc;
     }
-    // adds the wave's totals to the given words (lane 0 of each wave)
+    // Adds the block's totals to the given words, one atomic each from
+    // thread 0: the status bits, and the descents that start no row
+    // (desc - start_desc, zero exactly when the rows are sorted) to
+    // diff_word.  Every thread of the block calls it.  (Atomics on one word
+    // serialize: three per wavefront, 49,000 per call, took 0.3 ms of the
+    // 0.42 ms pass over configuration 3's 31 M entries.)
     __device__ void flush(unsigned long long* bits_word, uint32_t rowptr_bit, uint32_t col_bit,
-                          unsigned long long* desc_word, unsigned long long* start_desc_word) {
+                          unsigned long long* diff_word) {
+        __shared__ uint32_t block_bits[kBlock / kWave];
+        __shared__ int64_t block_diff[kBlock / kWave];
         const uint32_t bits = wave_or((bad_rowptr ? rowptr_bit : 0u) | (bad_col ? col_bit : 0u));
-        const int64_t d = wave_sum(desc), sd = wave_sum(start_desc);
+        const int64_t d = wave_sum(desc - start_desc);
         if (__lane_id() == 0) {
-            if (bits) atomicOr(bits_word, static_cast<unsigned long long>(bits));
-            if (d) atomicAdd(desc_word, static_cast<unsigned long long>(d));
-            if (sd) atomicAdd(start_desc_word, static_cast<unsigned long long>(sd));
+            block_bits[threadIdx.x / kWave] = bits;
+            block_diff[threadIdx.x / kWave] = d;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t b = 0;
+            int64_t t = 0;
+            for (int i = 0; i < kBlock / kWave; ++i) {
+                b |= block_bits[i];
+                t += block_diff[i];
+            }
+            if (b) atomicOr(bits_word, static_cast<unsigned long long>(b));
+            if (t) atomicAdd(diff_word, static_cast<unsigned long long>(t));
         }
     }
 };
@@ -126,9 +143,9 @@ __device__ __forceinline__ int4 with_slot(int4 r, const HubBitmaps& hubs, int64_
 // col32[16^k * i].  With rec == nullptr (the node2vec walk's CSR mode) only
 // the index is written, with -1 for a col value outside [0, num_nodes), and
 // no rowptr is read.  With a non-null work pointer the same pass validates the
-// whole CSR (status bits into work[0]) and counts the row descents into
-// work[2] / work[3], from which the node2vec walk decides whether its rows
-// are sorted.  With hubs.max > 0 every record's pad word holds its node's
+// whole CSR (status bits into work[0]) and counts into work[2] the row
+// descents that start no row (work[3] stays 0): the node2vec walk takes its
+// rows as sorted when work[2] == work[3].  With hubs.max > 0 every record's pad word holds its node's
 // hub slot (hub_assign_kernel ran before), else -1.  With a non-null row32
 // (row32_kernel ran before) the rows are gathered from it instead of rowptr.
 __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __restrict__ rowptr,
@@ -181,7 +198,7 @@ __global__ __launch_bounds__(kBlock) void edge_record_kernel(const int64_t* __re
     if (work) {
         check.nodes(rowptr, num_nodes, col, num_edges, gid, stride);
         unsigned long long* w = reinterpret_cast<unsigned long long*>(work);
-        check.flush(w, MLXC_STATUS_BAD_ROW, MLXC_STATUS_BAD_NODE, w + 2, w + 3);
+        check.flush(w, MLXC_STATUS_BAD_ROW, MLXC_STATUS_BAD_NODE, w + 2);
     }
 }
 
@@ -566,7 +583,7 @@ __global__ __launch_bounds__(kBlock) void edge_index_kernel(const int64_t* __res
     if (work) {
         check.nodes(rowptr, num_nodes, col, num_edges, gid, stride);
         unsigned long long* w = reinterpret_cast<unsigned long long*>(work);
-        check.flush(w, MLXC_STATUS_BAD_ROW, MLXC_STATUS_BAD_NODE, w + 2, w + 3);
+        check.flush(w, MLXC_STATUS_BAD_ROW, MLXC_STATUS_BAD_NODE, w + 2);
     }
 }
 
@@ -613,9 +630,9 @@ __global__ __launch_bounds__(kBlock) void walk_init_kernel(const int64_t* __rest
         *reinterpret_cast<int4*>(init + n) = node_record(rowptr, start[n], num_nodes, num_edges);
 }
 
-// work[0] |= MLXC_CSR_BAD_ROWPTR / MLXC_CSR_BAD_COL bits; work[1] counts
-// positions i >= 1 with col[i] < col[i-1]; work[2] counts those positions
-// that start a non-empty row.  Rows are sorted iff work[1] == work[2].
+// work[0] |= MLXC_CSR_BAD_ROWPTR / MLXC_CSR_BAD_COL bits; work[1] counts the
+// positions i >= 1 with col[i] < col[i-1] that start no non-empty row (work[2]
+// stays 0).  Rows are sorted iff work[1] == work[2].
 __global__ __launch_bounds__(kBlock) void csr_check_kernel(const int64_t* __restrict__ rowptr,
                                                            int64_t V,
                                                            const int64_t* __restrict__ col,
@@ -626,7 +643,7 @@ __global__ __launch_bounds__(kBlock) void csr_check_kernel(const int64_t* __rest
     check.nodes(rowptr, V, col, E, gid, stride);
     for (int64_t i = gid; i < E; i += stride) check.edge(col, V, i, col[i]);
     unsigned long long* w = reinterpret_cast<unsigned long long*>(work);
-    check.flush(w, MLXC_CSR_BAD_ROWPTR, MLXC_CSR_BAD_COL, w + 1, w + 2);
+    check.flush(w, MLXC_CSR_BAD_ROWPTR, MLXC_CSR_BAD_COL, w + 1);
 }
 
 // After csr_check_kernel, on a well-formed graph whose rows are all sorted:
@@ -676,11 +693,12 @@ __global__ __launch_bounds__(kBlock) void csr_symmetry_kernel(const int64_t* __r
 // work[2] = 1 when every row is sorted (else 0), work[3] = 0.
 __global__ void csr_status_kernel(int64_t* work) {
     if (threadIdx.x != 0) return;
-    const int64_t bits = work[0], desc = work[1], start_desc = work[2];
+    const int64_t bits = work[0];
+    const bool sorted = work[1] == work[2];
     work[0] = ((bits & MLXC_CSR_BAD_ROWPTR) ? MLXC_STATUS_BAD_ROW : 0) |
               ((bits & MLXC_CSR_BAD_COL) ? MLXC_STATUS_BAD_NODE : 0);
     work[1] = 0;
-    work[2] = desc == start_desc ? 1 : 0;
+    work[2] = sorted ? 1 : 0;
     work[3] = 0;
 }
 

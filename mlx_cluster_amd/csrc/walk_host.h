@@ -123,8 +123,9 @@ int launch_edge_index(const int64_t* rowptr, const int64_t* col, int64_t num_nod
 int launch_walk_init(const int64_t* rowptr, const int64_t* start, int64_t num_nodes,
                      int64_t num_edges, int64_t num_walks, EdgeRecord* init, int64_t* work,
                      hipStream_t stream);
-// work[0] |= MLXC_CSR_* bits, work[1] / work[2] += row descents (all
-// descents / those at a row start); the words must start at zero.
+// work[0] |= MLXC_CSR_* bits, work[1] += the row descents that start no row
+// (rows sorted iff work[1] == work[2], which stays 0); the words must start
+// at zero.
 int launch_csr_check(const int64_t* rowptr, int64_t num_nodes, const int64_t* col,
                      int64_t num_edges, int64_t* d_work, hipStream_t stream);
 // After launch_csr_check, on a well-formed graph with sorted rows: work[3] = 1
