@@ -1,7 +1,7 @@
 """Randomized parity sweep: every kernel path of both walks against the oracle.
 
 Each case draws a graph, a walk count around the 64-walk wavefront and queue
-chunk (1 .. 20,000), a walk length around the rand-window and long-walk
+chunk and the record walk's few-walks mode (1 .. 40,000), a walk length around the rand-window and long-walk
 boundaries (0 .. 129), generated or caller uniforms, a walk offset, int32 or
 int64 output, with or without edge ids, and a workspace that selects one
 kernel path: for the uniform walk the query's size, edge records, start
@@ -24,7 +24,9 @@ from mlx_cluster_amd import _lib, synth
 
 pytestmark = pytest.mark.gpu
 
-N_CHOICES = [1, 2, 63, 64, 65, 127, 129, 1000, 4097, 20000]
+# up to 32,768 node2vec walks (on 256 compute units) run in the record walk's
+# tail phase from the start; 33,000 and 40,000 take its queue and main loop
+N_CHOICES = [1, 2, 63, 64, 65, 127, 129, 1000, 4097, 20000, 33000, 40000]
 L_UNIFORM = [0, 1, 2, 3, 4, 5, 7, 8, 15, 16, 17, 31, 32, 33, 40, 63, 64, 65, 80, 127, 128, 129]
 L_N2V = [0, 1, 2, 3, 5, 8, 16, 17, 30, 33, 40]
 PQ = [(0.5, 2.0), (4.0, 0.25), (1.0, 3.0), (2.0, 0.5), (1.0, 1.0), (0.25, 4.0)]
