@@ -271,6 +271,7 @@ __global__ __launch_bounds__(kBlock) void hub_assign_kernel(const int64_t* __res
 // outside [0, num_nodes) are left out (the preparation pass reports them).
 constexpr int kHubChunkWords = 8192;  // 32 KB of LDS: 2^18 nodes per chunk
 constexpr int64_t kHubScanEntries = 16 * kBlock;  // rows up to this are scanned by every chunk
+constexpr int kHubLoads = 8;
 
 // lower_bound of v in the sorted a[lo, hi), by the whole block: each round
 // every thread compares one of kBlock evenly spaced samples, and the count of
@@ -316,11 +317,21 @@ __global__ __launch_bounds__(kBlock) void hub_build_kernel(const int64_t* __rest
             first = block_lower_bound(col, rb.begin, rb.end, 32 * w0);
             last = block_lower_bound(col, first, rb.end, 32 * (w0 + nw));
         }
-        for (int64_t i = first + threadIdx.x; i < last; i += kBlock) {
-            const int64_t c = col[i];
-            const int64_t wi = (c >> 5) - w0;
-            if (node_ok(c, num_nodes) && wi >= 0 && wi < nw)
-                atomicOr(&lw[wi], 1u << (c & 31));
+        // kHubLoads loads per thread issued before any is used (indices past
+        // the range clamped to its last entry), one memory round trip each
+        for (int64_t i0 = first + threadIdx.x; i0 < last; i0 += kHubLoads * kBlock) {
+            int64_t c[kHubLoads];
+#pragma unroll
+            for (int u = 0; u < kHubLoads; ++u) {
+                const int64_t i = i0 + u * kBlock;
+                c[u] = col[i < last ? i : last - 1];
+            }
+#pragma unroll
+            for (int u = 0; u < kHubLoads; ++u) {
+                const int64_t wi = (c[u] >> 5) - w0;
+                if (i0 + u * kBlock < last && node_ok(c[u], num_nodes) && wi >= 0 && wi < nw)
+                    atomicOr(&lw[wi], 1u << (c[u] & 31));
+            }
         }
         __syncthreads();
         u32x4* out = reinterpret_cast<u32x4*>(hubs.bits + slot * hubs.words + w0);
